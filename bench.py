@@ -1,0 +1,361 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X layer kernels (one GPU).
+
+Headline (the JSON line's `value`): achieved HBM bandwidth of the fused
+residual-add + RMSNorm kernel at Qwen2.5-7B prefill, x / residual fp16
+[8192, 3584].  One step = one launch over that batch;
+inputs are resident in HBM before the timed region.  Buffer sets are rotated
+so the working set of consecutive launches exceeds the 256 MB Infinity Cache
+and every launch streams from HBM.
+
+Also reported, under "kernels": every BASELINE config, each kernel timed the
+same way (average over back-to-back launches with HIP events on the launch
+stream), as algorithmic GB/s, fraction of the 8 TB/s HBM peak and tokens/s.
+
+`cpu_baseline` times the CPU oracle (a C restatement of the reference's
+test arithmetic, oracle/libmi_oracle.so) on the host, on a bounded sample of
+the same workload.  The oracle is the checker, never the thing measured on
+the GPU.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-kernels] [--no-cpu]
+"""
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "mini-infer_amd"))
+
+HBM_PEAK = 8.0e12          # MI355X HBM3E, bytes/s
+MALL_BYTES = 256 << 20     # Infinity Cache
+METRIC = "achieved HBM GB/s (% of 8 TB/s peak) per layer kernel at Qwen2.5-7B shapes"
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def rotations(set_bytes, min_sets=2, max_sets=16):
+    """Enough buffer sets that a full rotation is >= 3x the Infinity Cache."""
+    return int(min(max_sets, max(min_sets, math.ceil(3 * MALL_BYTES / max(set_bytes, 1)))))
+
+
+def time_launches(launch, nsets, iters, warmup):
+    """Average seconds per launch over `iters` back-to-back launches cycling
+    through `nsets` buffer sets, timed with events on the current stream."""
+    import torch
+    for i in range(warmup):
+        launch(i % nsets)
+    torch.cuda.synchronize()
+    s = torch.cuda.current_stream()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record(s)
+    for i in range(iters):
+        launch(i % nsets)
+    t1.record(s)
+    torch.cuda.synchronize()
+    return t0.elapsed_time(t1) * 1e-3 / iters
+
+
+def randn16(shape, gen, dev, mean=0.0, std=1.0):
+    import torch
+    return (torch.randn(shape, generator=gen, device=dev, dtype=torch.float32) * std + mean).half()
+
+
+def report(name, cfg, nbytes, seconds, tokens):
+    return {
+        "kernel": name,
+        "config": cfg,
+        "bytes": int(nbytes),
+        "us": round(seconds * 1e6, 3),
+        "GBps": round(nbytes / seconds / 1e9, 1),
+        "frac": round(nbytes / seconds / HBM_PEAK, 4),
+        "tokens_per_s": round(tokens / seconds, 1),
+    }
+
+
+# ---------------------------------------------------------------------------
+# Headline: fused residual-add + RMSNorm [8192, 3584]
+# ---------------------------------------------------------------------------
+
+def fused_sets(mk, dev, gen, T, D, nsets):
+    w = randn16((D,), gen, dev, 1.0, 0.1)
+    sets = [(randn16((T, D), gen, dev), randn16((T, D), gen, dev),
+             __import__("torch").empty((T, D), dtype=__import__("torch").float16, device=dev))
+            for _ in range(nsets)]
+    return w, sets
+
+
+def headline(mk, dev, steps, warmup):
+    import torch
+    gen = torch.Generator(device=dev).manual_seed(0)
+    T, D = 8192, 3584
+    nbytes = 4 * T * D * 2 + D * 2
+    nsets = rotations(3 * T * D * 2)
+    w, sets = fused_sets(mk, dev, gen, T, D, nsets)
+
+    def launch(i):
+        x, r, y = sets[i]
+        mk.fused_add_rmsnorm(x, r, w, y=y, eps=1e-6)
+
+    sec = time_launches(launch, nsets, steps, warmup)
+    return T, D, nbytes, sec
+
+
+# ---------------------------------------------------------------------------
+# Every BASELINE config
+# ---------------------------------------------------------------------------
+
+def config3_positions(gen_np, total, nseq, max_start):
+    import numpy as np
+    cuts = np.sort(gen_np.choice(np.arange(1, total), nseq - 1, replace=False))
+    lengths = np.diff(np.concatenate([[0], cuts, [total]]))
+    starts = gen_np.integers(0, max_start, nseq)
+    return np.concatenate([s + np.arange(n) for s, n in zip(starts, lengths)]).astype(np.int64)
+
+
+def chain_positions(gen_np):
+    """64 decode tokens at random offsets, then two 3000-token prefills."""
+    import numpy as np
+    dec = gen_np.integers(0, 28000, 64)
+    pre = [s + np.arange(3000) for s in gen_np.integers(0, 28000, 2)]
+    return np.concatenate([dec] + pre).astype(np.int64)
+
+
+def all_kernels(mk, dev, iters, warmup):
+    import numpy as np
+    import torch
+    gen = torch.Generator(device=dev).manual_seed(1)
+    rng = np.random.default_rng(1)
+    out = []
+    f16 = torch.float16
+
+    rope_inv = mk.rope_inv_freq
+
+    # 1. RMSNorm [16, 3584]: launch-latency bound; back-to-back average.
+    T, D = 16, 3584
+    nb = 2 * T * D * 2 + D * 2
+    w = randn16((D,), gen, dev, 1.0, 0.1)
+    xs = [randn16((T, D), gen, dev) for _ in range(4)]
+    ys = [torch.empty_like(xs[0]) for _ in range(4)]
+    sec = time_launches(lambda i: mk.rmsnorm(xs[i], w, y=ys[i]), 4, iters * 10, warmup)
+    out.append(report("rmsnorm", "[16,3584]", nb, sec, T))
+    del xs, ys
+
+    # 2. fused residual-add + RMSNorm [8192, 3584]
+    T, D = 8192, 3584
+    nb = 4 * T * D * 2 + D * 2
+    ns = rotations(3 * T * D * 2)
+    w, sets = fused_sets(mk, dev, gen, T, D, ns)
+    sec = time_launches(lambda i: mk.fused_add_rmsnorm(sets[i][0], sets[i][1], w, y=sets[i][2]),
+                        ns, iters, warmup)
+    out.append(report("fused_add_rmsnorm", "[8192,3584]", nb, sec, T))
+    del sets
+
+    # 3. RoPE in place, Q [4096,28,128] + K [4096,4,128], theta 1e6
+    T, Hq, Hkv, hd = 4096, 28, 4, 128
+    nb = 2 * (T * Hq * hd + T * Hkv * hd) * 2 + T * 8
+    ns = rotations((T * (Hq + Hkv) * hd) * 2)
+    inv = rope_inv(hd)
+    pos = torch.from_numpy(config3_positions(rng, T, 8, 28000)).to(dev)
+    qs = [randn16((T, Hq, hd), gen, dev) for _ in range(ns)]
+    ks = [randn16((T, Hkv, hd), gen, dev) for _ in range(ns)]
+    sec = time_launches(lambda i: mk.rope_neox_qk(qs[i], ks[i], pos, inv), ns, iters, warmup)
+    out.append(report("rope_neox_qk", "Q[4096,28,128]+K[4096,4,128]", nb, sec, T))
+    del qs, ks
+
+    # 4a/4b. SwiGLU [4096,18944], GeGLU [4096,14336]
+    for name, fn, I in (("swiglu", mk.swiglu, 18944), ("geglu", mk.geglu, 14336)):
+        T = 4096
+        nb = 3 * T * I * 2
+        ns = rotations(3 * T * I * 2)
+        sets = [(randn16((T, I), gen, dev), randn16((T, I), gen, dev),
+                 torch.empty((T, I), dtype=f16, device=dev)) for _ in range(ns)]
+        sec = time_launches(lambda i: fn(sets[i][0], sets[i][1], out=sets[i][2]), ns, iters, warmup)
+        out.append(report(name, f"[4096,{I}]", nb, sec, T))
+        del sets
+
+    # 5. the decoder chain at T = 64 decode + 2 x 3000 prefill = 6064 tokens
+    T, D, I, V = 6064, 3584, 18944, 152064
+    # 5a. embedding gather from [152064, 3584]
+    table = randn16((V, D), gen, dev, 0.0, 0.02)
+    nb = T * 8 + 2 * T * D * 2
+    ns = 8
+    ids = [torch.from_numpy(rng.integers(0, V, T).astype(np.int64)).to(dev) for _ in range(ns)]
+    outs = [torch.empty((T, D), dtype=f16, device=dev) for _ in range(ns)]
+    sec = time_launches(lambda i: mk.embedding_gather(ids[i], table, out=outs[i]), ns, iters,
+                        warmup)
+    out.append(report("embedding_gather", "T=6064 from [152064,3584]", nb, sec, T))
+    del table, ids, outs
+    # 5b. residual + RMSNorm
+    nb = 4 * T * D * 2 + D * 2
+    ns = rotations(3 * T * D * 2)
+    w, sets = fused_sets(mk, dev, gen, T, D, ns)
+    sec = time_launches(lambda i: mk.fused_add_rmsnorm(sets[i][0], sets[i][1], w, y=sets[i][2]),
+                        ns, iters, warmup)
+    out.append(report("fused_add_rmsnorm", "chain [6064,3584]", nb, sec, T))
+    del sets
+    # 5c. Q/K RMSNorm, head_dim 128, in place (two launches: Q rows, K rows)
+    nb = 2 * (T * 32 * 128) * 2 + 2 * 128 * 2
+    ns = rotations(T * 32 * 128 * 2)
+    wq = randn16((128,), gen, dev, 1.0, 0.1)
+    wk = randn16((128,), gen, dev, 1.0, 0.1)
+    qs = [randn16((T * 28, 128), gen, dev) for _ in range(ns)]
+    ks = [randn16((T * 4, 128), gen, dev) for _ in range(ns)]
+
+    def qk(i):
+        mk.rmsnorm(qs[i], wq, y=qs[i])
+        mk.rmsnorm(ks[i], wk, y=ks[i])
+    sec = time_launches(qk, ns, iters, warmup)
+    out.append(report("qk_rmsnorm", "chain Q[6064*28,128]+K[6064*4,128]", nb, sec, T))
+    # 5d. RoPE on the same Q/K (fused Q+K launch)
+    nb = 2 * T * 32 * 128 * 2 + T * 8
+    pos = torch.from_numpy(chain_positions(rng)).to(dev)
+    inv = rope_inv(128)
+    sec = time_launches(lambda i: mk.rope_neox_qk(qs[i].view(T, 28, 128), ks[i].view(T, 4, 128),
+                                                  pos, inv), ns, iters, warmup)
+    out.append(report("rope_neox_qk", "chain Q[6064,28,128]+K[6064,4,128]", nb, sec, T))
+    del qs, ks
+    # 5e. SwiGLU [6064, 18944]
+    nb = 3 * T * I * 2
+    ns = rotations(3 * T * I * 2)
+    sets = [(randn16((T, I), gen, dev), randn16((T, I), gen, dev),
+             torch.empty((T, I), dtype=f16, device=dev)) for _ in range(ns)]
+    sec = time_launches(lambda i: mk.swiglu(sets[i][0], sets[i][1], out=sets[i][2]), ns, iters,
+                        warmup)
+    out.append(report("swiglu", "chain [6064,18944]", nb, sec, T))
+    del sets
+    # 5f. softmax over logits [64, 152064] ~N(0,4)
+    N = 64
+    nb = 2 * N * V * 2
+    ns = rotations(2 * N * V * 2)
+    sets = [(randn16((N, V), gen, dev, 0.0, 4.0), torch.empty((N, V), dtype=f16, device=dev))
+            for _ in range(ns)]
+    sec = time_launches(lambda i: mk.softmax(sets[i][0], y=sets[i][1]), ns, iters, warmup)
+    out.append(report("softmax", "[64,152064]", nb, sec, N))
+    del sets
+    torch.cuda.synchronize()
+    return out
+
+
+# ---------------------------------------------------------------------------
+# CPU baseline: the oracle on the host, bounded sample of the headline config
+# ---------------------------------------------------------------------------
+
+def cpu_baseline(budget_s=10.0):
+    import numpy as np
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import oracle  # the checker, timed here as the CPU reference implementation
+    T, D = 8192, 3584
+    cores = max(1, min(16, os.cpu_count() or 1))
+    rng = np.random.default_rng(0)
+    x = rng.standard_normal((T, D), dtype=np.float32).astype(np.float16)
+    r = rng.standard_normal((T, D), dtype=np.float32).astype(np.float16)
+    w = (rng.standard_normal(D, dtype=np.float32) * 0.1 + 1).astype(np.float16)
+    oracle.fused_add_rmsnorm(x, r, w, 1e-6, nthreads=cores)  # warm
+    n = 0
+    t0 = time.perf_counter()
+    while True:
+        oracle.fused_add_rmsnorm(x, r, w, 1e-6, nthreads=cores)
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s:
+            break
+    sec = el / n
+    nbytes = 4 * T * D * 2 + D * 2
+    return {
+        "value": round(nbytes / sec / 1e9, 3),
+        "unit": "GB/s",
+        "cores": cores,
+        "kind": "port",
+        "sample": (f"oracle fused residual-add + RMSNorm (fp32 math) on the full [8192,3584] "
+                   f"workload, {n} passes in {el:.1f} s with {cores} threads over rows; "
+                   f"{sec * 1e3:.1f} ms/pass, {T / sec:.0f} tokens/s"),
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawTextHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-kernels", action="store_true", help="skip the per-config table")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: these layer kernels are row-independent and run "
+              "without communication; multi-GPU sharding is described in DESIGN.md, not "
+              "benchmarked.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import mi_kernels as mk
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(1)
+    mk.load_library()
+    dev = torch.device("cuda:0")
+
+    log("[bench] headline: fused residual-add + RMSNorm [8192,3584]")
+    T, D, nbytes, sec = headline(mk, dev, args.steps, args.warmup)
+    gbps = nbytes / sec / 1e9
+
+    kernels = None
+    if not args.no_kernels:
+        log("[bench] per-config kernel table")
+        kernels = all_kernels(mk, dev, max(20, args.steps // 2), max(5, args.warmup // 2))
+        for k in kernels:
+            log(f"[bench]   {k['kernel']:<18} {k['config']:<38} {k['us']:>9.2f} us "
+                f"{k['GBps']:>8.1f} GB/s  {100 * k['frac']:5.1f}%")
+
+    cpu = None
+    if not args.no_cpu:
+        log("[bench] CPU baseline (oracle on host cores)")
+        cpu = cpu_baseline(args.cpu_seconds)
+
+    traffic = None
+    tf = ROOT / "profiles" / "fused_add_rmsnorm_8192x3584_traffic.json"
+    if tf.exists():
+        traffic = json.loads(tf.read_text()).get("hbm_bytes_per_launch")
+
+    line = {
+        "metric": METRIC,
+        "value": round(gbps, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(sec * 1e3, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16",
+        "data": "synthetic (seeded N(0,1) fp16 inputs, N(1,0.1) weight)",
+        "config": {
+            "workload": "fused residual-add + RMSNorm, Qwen2.5-7B prefill (BASELINE config 2)",
+            "tokens": T, "hidden": D, "eps": 1e-6,
+            "global_batch": T, "parallelism": "none (1 GPU)",
+        },
+        "tokens_per_s": round(T / sec, 1),
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(gbps, 1),
+            "peak": HBM_PEAK / 1e9,
+            "unit": "GB/s",
+            "frac": round(nbytes / sec / HBM_PEAK, 4),
+            "traffic": traffic,
+        },
+        "cpu_baseline": cpu,
+        "kernels": kernels,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

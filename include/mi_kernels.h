@@ -1,0 +1,136 @@
+/*
+ * mi_kernels.h -- C ABI of the MI355X (gfx950) layer-kernel library
+ * (libmi_kernels.so).
+ *
+ * This is the drop-in boundary for mini-infer's non-GEMM layer kernels.  The
+ * reference exposes them as C++ free functions in namespace
+ * mini_infer::kernels (src/kernels/<name>_kernel.cuh); each entry point below names the
+ * reference function it replaces.  The C++ launch_* wrappers with the
+ * reference's exact names and argument order forward to these entry points
+ * (mini-infer_amd/host/kernels/).
+ *
+ * Conventions (all entry points):
+ *   - every tensor pointer is a DEVICE pointer owned by the caller; fp16
+ *     tensors are IEEE binary16, row-major, contiguous;
+ *   - sizes are int64_t element counts;
+ *   - `stream` is a hipStream_t passed as void* (NULL = the null stream); the
+ *     call only enqueues work and returns without synchronising;
+ *   - the return value is 0 on success, a negative MI_ERR_* code for an
+ *     argument error (nothing is launched), or a positive hipError_t when the
+ *     HIP runtime refused the launch;
+ *   - a size of zero is a successful no-op;
+ *   - math is fp32 with fp16 storage; outputs are rounded to nearest even.
+ * No entry point allocates device memory, except mi_softmax_f16 on its
+ * split-row path (N < 512 rows of D >= 8192), which takes 8 bytes per row
+ * chunk (<= 256 KiB) from the device's stream-ordered pool (hipMallocAsync /
+ * hipFreeAsync on `stream`) for the duration of the call's kernels.
+ */
+#ifndef MI_KERNELS_H
+#define MI_KERNELS_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MI_OK 0
+#define MI_ERR_INVALID_ARGUMENT (-1) /* null pointer, negative or too-large size */
+#define MI_ERR_UNSUPPORTED (-2)      /* shape outside what the kernels support */
+#define MI_ERR_ALIASING (-3)         /* buffers overlap where they must not */
+
+/* Human-readable text for a status code (never NULL). */
+const char* mi_status_string(int status);
+
+/* ABI version of this header; bumped on any incompatible change. */
+#define MI_KERNELS_ABI_VERSION 1
+int mi_abi_version(void);
+
+/* RMSNorm: y = x * rsqrt(sum(x^2)/D + eps) * (add_one ? 1 + w : w).
+ * x, y: [N, D]; weight: [D].  y may equal x (in place, as the Q/K-norm call
+ * sites do, src/layers/attention.cpp:757-768); any other overlap is an error.
+ * Replaces launch_rmsnorm (src/kernels/rmsnorm_kernel.cuh:19-20). */
+int mi_rmsnorm_f16(const void* x, const void* weight, void* y, int64_t N,
+                   int64_t D, float eps, int add_one, void* stream);
+
+/* Residual add fused with RMSNorm, in one pass over each row:
+ *   residual = half(residual + x);  y = rmsnorm(residual).
+ * Replaces the pair launch_add_inplace(residual, x) + launch_rmsnorm that the
+ * model chain issues (src/model/transformer_model.cpp:608-615 and :637;
+ * src/kernels/model_utils_kernel.cuh:12, rmsnorm_kernel.cuh:19).  y may equal
+ * x; residual must not overlap x or y. */
+int mi_fused_add_rmsnorm_f16(const void* x, void* residual, const void* weight,
+                             void* y, int64_t N, int64_t D, float eps,
+                             int add_one, void* stream);
+
+/* NeoX half-rotation RoPE from per-token cos/sin tables.
+ * x, y: [B, S, H, D]; cos_t, sin_t: [B*S, D/2].  y may equal x.
+ * Replaces launch_rope (src/kernels/rope_kernel.cuh:11). */
+int mi_rope_neox_f16(const void* x, const void* cos_t, const void* sin_t,
+                     void* y, int64_t B, int64_t S, int64_t H, int64_t D,
+                     void* stream);
+
+/* cos/sin tables [N, half] for the positions in DEVICE memory:
+ * cos_t[n, i] = half(cos(float(positions[n]) * inv_freq[i])), likewise sin.
+ * inv_freq is a HOST array of `half` floats (<= 256), passed to the kernel by
+ * value, so nothing is allocated or copied.  Device part of
+ * launch_rope_precompute / launch_rope_precompute_batched
+ * (src/kernels/rope_kernel.cuh:16-28), which take host positions. */
+int mi_rope_tables_f16(const float* inv_freq_host, const int64_t* positions,
+                       void* cos_t, void* sin_t, int64_t N, int64_t half,
+                       void* stream);
+
+/* Fused, in-place NeoX RoPE over the Q and K of T tokens with cos/sin
+ * generated in registers from DEVICE positions[T] and HOST inv_freq[hd/2]:
+ * q: [T, Hq, hd], k: [T, Hkv, hd] (k may be NULL when Hkv == 0).  The result
+ * equals mi_rope_tables_f16 followed by mi_rope_neox_f16 on q and on k.
+ * Replaces the RoPE::forward_batched pair at src/layers/attention.cpp:779-780
+ * (src/layers/rope.cpp:89-131): no table round trip, no host-to-device copy,
+ * no allocation. */
+int mi_rope_neox_qk_f16(void* q, void* k, const int64_t* positions,
+                        const float* inv_freq_host, int64_t T, int64_t Hq,
+                        int64_t Hkv, int64_t head_dim, void* stream);
+
+/* out = silu(gate) * up, elementwise over n.
+ * Replaces launch_swiglu (src/kernels/swiglu_kernel.cuh:9). */
+int mi_swiglu_f16(const void* gate, const void* up, void* out, int64_t n,
+                  void* stream);
+
+/* y = gelu_tanh(x) (y may equal x).
+ * Replaces launch_gelu_tanh (src/kernels/gelu_kernel.cuh:15). */
+int mi_gelu_tanh_f16(const void* x, void* y, int64_t n, void* stream);
+
+/* out = gelu_tanh(gate) * up in one pass.  Replaces the pair
+ * launch_gelu_tanh + launch_mul_inplace at src/layers/mlp.cpp:282-291. */
+int mi_geglu_f16(const void* gate, const void* up, void* out, int64_t n,
+                 void* stream);
+
+/* y = half(y + x).  Replaces launch_add_inplace
+ * (src/kernels/model_utils_kernel.cuh:12). */
+int mi_add_inplace_f16(void* y, const void* x, int64_t n, void* stream);
+
+/* y = half(y * x).  Replaces launch_mul_inplace
+ * (src/kernels/model_utils_kernel.cuh:29). */
+int mi_mul_inplace_f16(void* y, const void* x, int64_t n, void* stream);
+
+/* y = half(y * scale).  Replaces launch_scale_inplace
+ * (src/kernels/model_utils_kernel.cuh:23). */
+int mi_scale_inplace_f16(void* y, float scale, int64_t n, void* stream);
+
+/* Row softmax, fp32 math: y = exp(x - max) / sum(exp(x - max)).
+ * x, y: [N, D]; y may equal x.  Replaces launch_softmax
+ * (src/kernels/softmax_kernel.cuh:12). */
+int mi_softmax_f16(const void* x, void* y, int64_t N, int64_t D, void* stream);
+
+/* out[t, :] = table[ids[t], :] for t < T; table: [vocab, H], ids: int64 [T].
+ * Bit-exact copy.  When vocab > 0, an id outside [0, vocab) yields a zero
+ * row instead of an out-of-bounds read; vocab <= 0 disables that check
+ * (the reference's behaviour).  Replaces launch_embedding_gather
+ * (src/kernels/model_utils_kernel.cuh:14), where T = B*S. */
+int mi_embedding_gather_f16(const int64_t* ids, const void* table, void* out,
+                            int64_t T, int64_t H, int64_t vocab, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* MI_KERNELS_H */

@@ -1,0 +1,153 @@
+// elementwise.hip -- gated activations (SwiGLU, GeGLU), gelu_tanh and the
+// in-place add / mul / scale used by the model chain, for gfx950.
+//
+// Arithmetic (fp32 math, one fp16 rounding of each output):
+//   swiglu : out = half(silu(g) * u),  silu(g) = g / (1 + exp(-g))
+//            (src/kernels/swiglu_kernel.cu:16-26)
+//   gelu   : y = half(0.5 x (1 + tanh(sqrt(2/pi)(x + 0.044715 x^3))))
+//            (src/kernels/gelu_kernel.cu:23-35), evaluated as x / (1 + exp(-2u)),
+//            which is the same function since 0.5 (1 + tanh(u)) = sigmoid(2u)
+//   geglu  : out = half(gelu(g) * u) -- the reference runs gelu then
+//            mul_inplace (src/layers/mlp.cpp:282-291), rounding twice
+//   add    : y = half(y + x)   (src/kernels/model_utils_kernel.cu:31-35)
+//   mul    : y = half(y * x)   (:82-86)
+//   scale  : y = half(y * s)   (:68-72)
+//
+// Design (HBM-bound; 6 bytes/element for the binary ops, 4 for unary): each
+// 256-lane workgroup owns a contiguous tile of 4 x 256 16-byte vectors per
+// operand; a lane issues all 4 (or 8, binary) loads before any math, so
+// every wave keeps 4-8 KiB in flight.  Outputs are written with non-temporal
+// stores since nothing re-reads them inside the kernel.  A scalar kernel takes
+// the n % 8 tail and any unaligned buffer.
+#include "mi_device.h"
+#include "mi_host.h"
+
+namespace mi {
+namespace {
+
+enum Op { kSwiglu = 0, kGelu = 1, kGeglu = 2, kAdd = 3, kMul = 4, kScale = 5 };
+
+template <int OP>
+__device__ __forceinline__ float apply(float a, float b, float scale) {
+    if constexpr (OP == kSwiglu) return silu_mul(a, b);
+    if constexpr (OP == kGelu) return gelu_tanh(a);
+    if constexpr (OP == kGeglu) return gelu_tanh(a) * b;
+    if constexpr (OP == kAdd) return a + b;
+    if constexpr (OP == kMul) return a * b;
+    if constexpr (OP == kScale) return a * scale;
+    return 0.0f;
+}
+
+template <int OP>
+constexpr bool binary() {
+    return OP == kSwiglu || OP == kGeglu || OP == kAdd || OP == kMul;
+}
+
+constexpr int kUnroll = 4;
+constexpr int kThreads = 256;
+constexpr int64_t kTileVec = kUnroll * kThreads;  // 16-byte vectors per workgroup
+
+template <int OP>
+__global__ __launch_bounds__(kThreads) void ew_vec_kernel(const half_t* a, const half_t* b,
+                                                          half_t* out, int64_t nvec, float scale) {
+    const int64_t base = static_cast<int64_t>(blockIdx.x) * kTileVec + threadIdx.x;
+    h8 va[kUnroll], vb[kUnroll];
+#pragma unroll
+    for (int j = 0; j < kUnroll; ++j) {
+        const int64_t v = base + j * kThreads;
+        if (v < nvec) {
+            va[j] = ld8(a + v * 8);
+            if constexpr (binary<OP>()) vb[j] = ld8(b + v * 8);
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < kUnroll; ++j) {
+        const int64_t v = base + j * kThreads;
+        if (v < nvec) {
+            h8 o;
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const float bb = binary<OP>() ? (float)vb[j][k] : 0.0f;
+                o[k] = to_half(apply<OP>((float)va[j][k], bb, scale));
+            }
+            st8_stream(out + v * 8, o);
+        }
+    }
+}
+
+template <int OP>
+__global__ __launch_bounds__(kThreads) void ew_scalar_kernel(const half_t* a, const half_t* b,
+                                                             half_t* out, int64_t begin,
+                                                             int64_t n, float scale) {
+    const int64_t i = begin + static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+    if (i >= n) return;
+    const float bb = binary<OP>() ? (float)b[i] : 0.0f;
+    out[i] = to_half(apply<OP>((float)a[i], bb, scale));
+}
+
+// Elementwise over n: out[i] = op(a[i], b[i]).  For the in-place ops the
+// caller passes out == a.  Each element is read and written by one lane, so
+// out may equal a or b.
+template <int OP>
+int ew_launch(const void* av, const void* bv, void* outv, int64_t n, float scale, void* stream) {
+    if (n < 0) return MI_ERR_INVALID_ARGUMENT;
+    if (n == 0) return MI_OK;
+    if (!av || !outv || (binary<OP>() && !bv)) return MI_ERR_INVALID_ARGUMENT;
+    const int64_t bytes = n * 2;
+    if (outv != av && overlaps(outv, bytes, av, bytes)) return MI_ERR_ALIASING;
+    if (binary<OP>() && outv != bv && overlaps(outv, bytes, bv, bytes)) return MI_ERR_ALIASING;
+
+    const half_t* a = static_cast<const half_t*>(av);
+    const half_t* b = static_cast<const half_t*>(bv);
+    half_t* out = static_cast<half_t*>(outv);
+    const hipStream_t s = as_stream(stream);
+
+    const bool vec = aligned16(a) && aligned16(out) && (!binary<OP>() || aligned16(b));
+    int64_t done = 0;
+    if (vec) {
+        const int64_t nvec = n / 8;
+        if (nvec > 0) {
+            const int64_t grid = ceil_div(nvec, kTileVec);
+            if (grid > kMaxGridX) return MI_ERR_UNSUPPORTED;
+            ew_vec_kernel<OP><<<dim3(static_cast<unsigned>(grid)), dim3(kThreads), 0, s>>>(
+                a, b, out, nvec, scale);
+            done = nvec * 8;
+        }
+    }
+    if (done < n) {
+        const int64_t grid = ceil_div(n - done, kThreads);
+        if (grid > kMaxGridX) return MI_ERR_UNSUPPORTED;
+        ew_scalar_kernel<OP><<<dim3(static_cast<unsigned>(grid)), dim3(kThreads), 0, s>>>(
+            a, b, out, done, n, scale);
+    }
+    return launch_status();
+}
+
+}  // namespace
+}  // namespace mi
+
+extern "C" int mi_swiglu_f16(const void* gate, const void* up, void* out, int64_t n,
+                             void* stream) {
+    return mi::ew_launch<mi::kSwiglu>(gate, up, out, n, 0.0f, stream);
+}
+
+extern "C" int mi_gelu_tanh_f16(const void* x, void* y, int64_t n, void* stream) {
+    return mi::ew_launch<mi::kGelu>(x, nullptr, y, n, 0.0f, stream);
+}
+
+extern "C" int mi_geglu_f16(const void* gate, const void* up, void* out, int64_t n,
+                            void* stream) {
+    return mi::ew_launch<mi::kGeglu>(gate, up, out, n, 0.0f, stream);
+}
+
+extern "C" int mi_add_inplace_f16(void* y, const void* x, int64_t n, void* stream) {
+    return mi::ew_launch<mi::kAdd>(y, x, y, n, 0.0f, stream);
+}
+
+extern "C" int mi_mul_inplace_f16(void* y, const void* x, int64_t n, void* stream) {
+    return mi::ew_launch<mi::kMul>(y, x, y, n, 0.0f, stream);
+}
+
+extern "C" int mi_scale_inplace_f16(void* y, float scale, int64_t n, void* stream) {
+    return mi::ew_launch<mi::kScale>(y, nullptr, y, n, scale, stream);
+}

@@ -1,0 +1,121 @@
+// mi_device.h -- device-side building blocks shared by the gfx950 kernels.
+//
+// fp16 streams are moved as 16-byte vectors (8 halves, one global_load_dwordx4
+// per lane), math is fp32, reductions are wave64: DPP within a 16-lane row,
+// cross-row shuffles for lanes 16/32, and one LDS slot per wave for a
+// workgroup total.  Nothing here allocates.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mi {
+
+typedef _Float16 half_t;
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+
+constexpr int kWave = 64;
+
+__device__ __forceinline__ h8 ld8(const half_t* p) {
+    return *reinterpret_cast<const h8*>(p);
+}
+__device__ __forceinline__ void st8(half_t* p, h8 v) {
+    *reinterpret_cast<h8*>(p) = v;
+}
+// Streaming variants: the data is touched exactly once, so ask the cache
+// hierarchy not to keep it (slc/nt bits on the access).
+__device__ __forceinline__ h8 ld8_stream(const half_t* p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const h8*>(p));
+}
+__device__ __forceinline__ void st8_stream(half_t* p, h8 v) {
+    __builtin_nontemporal_store(v, reinterpret_cast<h8*>(p));
+}
+
+// Round-to-nearest-even fp32 -> fp16 (v_cvt_f16_f32 under the default mode).
+__device__ __forceinline__ half_t to_half(float f) { return (half_t)f; }
+
+// --- DPP helpers ------------------------------------------------------------
+// dpp_ctrl encodings (GFX9 DPP): quad_perm = 8-bit lane map within a quad,
+// 0x141 = row_half_mirror (lane i of 8 reads 7-i), 0x140 = row_mirror (lane i
+// of 16 reads 15-i).
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __builtin_bit_cast(
+        float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+
+// Sum across aligned groups of G lanes (G a power of two, 1..64); every lane
+// of a group receives the group total.
+template <int G>
+__device__ __forceinline__ float group_sum(float v) {
+    static_assert(G >= 1 && G <= 64 && (G & (G - 1)) == 0, "G must be a power of two <= 64");
+    if constexpr (G >= 2) v += dpp_f<0xB1>(v);    // quad_perm [1,0,3,2]: xor 1
+    if constexpr (G >= 4) v += dpp_f<0x4E>(v);    // quad_perm [2,3,0,1]: xor 2
+    if constexpr (G >= 8) v += dpp_f<0x141>(v);   // other quad of the 8-lane half row
+    if constexpr (G >= 16) v += dpp_f<0x140>(v);  // other half of the 16-lane row
+    if constexpr (G >= 32) v += __shfl_xor(v, 16, kWave);
+    if constexpr (G >= 64) v += __shfl_xor(v, 32, kWave);
+    return v;
+}
+
+template <int G>
+__device__ __forceinline__ float group_max(float v) {
+    static_assert(G >= 1 && G <= 64 && (G & (G - 1)) == 0, "G must be a power of two <= 64");
+    if constexpr (G >= 2) v = fmaxf(v, dpp_f<0xB1>(v));
+    if constexpr (G >= 4) v = fmaxf(v, dpp_f<0x4E>(v));
+    if constexpr (G >= 8) v = fmaxf(v, dpp_f<0x141>(v));
+    if constexpr (G >= 16) v = fmaxf(v, dpp_f<0x140>(v));
+    if constexpr (G >= 32) v = fmaxf(v, __shfl_xor(v, 16, kWave));
+    if constexpr (G >= 64) v = fmaxf(v, __shfl_xor(v, 32, kWave));
+    return v;
+}
+
+// Workgroup-wide sum with a single barrier: each wave reduces in registers,
+// lane 0 publishes to LDS, then every lane folds the per-wave partials in the
+// same fixed order (so all lanes agree bit for bit).  `slots` needs one float
+// per wave; blockDim.x must be a multiple of 64.
+__device__ __forceinline__ float block_sum(float v, float* slots) {
+    v = group_sum<kWave>(v);
+    const int wave = threadIdx.x / kWave;
+    if ((threadIdx.x & (kWave - 1)) == 0) slots[wave] = v;
+    __syncthreads();
+    const int nwaves = blockDim.x / kWave;
+    float t = 0.0f;
+    for (int i = 0; i < nwaves; ++i) t += slots[i];
+    return t;
+}
+
+__device__ __forceinline__ float block_max(float v, float* slots) {
+    v = group_max<kWave>(v);
+    const int wave = threadIdx.x / kWave;
+    if ((threadIdx.x & (kWave - 1)) == 0) slots[wave] = v;
+    __syncthreads();
+    const int nwaves = blockDim.x / kWave;
+    float t = -INFINITY;
+    for (int i = 0; i < nwaves; ++i) t = fmaxf(t, slots[i]);
+    return t;
+}
+
+// exp(x) through the hardware base-2 exponential (v_exp_f32, ~1 ulp).
+__device__ __forceinline__ float fast_exp(float x) {
+    return __builtin_amdgcn_exp2f(x * 1.4426950408889634f);
+}
+
+// x / (1 + exp(-y)): shared tail of silu (y = x) and of gelu_tanh, which is
+// exactly x * sigmoid(2u) since 0.5 (1 + tanh(u)) = 1 / (1 + exp(-2u)).
+// exp overflow to +inf gives x / inf = 0, the correct limit.
+__device__ __forceinline__ float x_sigmoid(float x, float y) {
+    return x * __builtin_amdgcn_rcpf(1.0f + fast_exp(-y));
+}
+
+__device__ __forceinline__ float silu_mul(float g, float u) { return x_sigmoid(g, g) * u; }
+
+__device__ __forceinline__ float gelu_tanh(float x) {
+    const float k0 = 0.7978845608028654f;  // sqrt(2/pi)
+    const float k1 = 0.044715f;
+    const float inner = k0 * (x + k1 * x * x * x);
+    return x_sigmoid(x, 2.0f * inner);
+}
+
+}  // namespace mi

@@ -1,0 +1,254 @@
+// rmsnorm.hip -- RMSNorm, Gemma (1 + w) RMSNorm, per-head Q/K RMSNorm and
+// residual-add + RMSNorm for gfx950.
+//
+// Arithmetic follows the reference kernel (src/kernels/rmsnorm_kernel.cu:30-67):
+// fp32 sum of squares, rrms = rsqrt(sum / D + eps), y = half(x * rrms * f(w))
+// with f(w) = w or 1 + w.  The fused variant first forms
+// residual = half(residual + x) exactly as launch_add_inplace does
+// (src/kernels/model_utils_kernel.cu:31-35) and normalises that rounded sum.
+//
+// Design (HBM-bound; 4 bytes/element for the plain norm, 8 for the fused one):
+//   * the whole row stays in registers, so x is read from HBM once (the
+//     reference reads it twice) and, fused, residual is read and written once;
+//   * 16-byte vector accesses (8 halves per lane per access);
+//   * rows of <= 512 elements (Q/K-norm, head_dim 128) are handled by a
+//     G-lane slice of a wave (G = 16 for 128), so a 256-lane workgroup
+//     normalises 16 heads with DPP-only reductions and no LDS or barrier;
+//   * longer rows (hidden 3584) get one workgroup each, ceil(D/8) lanes (448
+//     for 3584), a wave64 DPP/shuffle reduction and one LDS barrier.
+//   * shapes the vector path cannot take (D % 8 != 0, unaligned pointers,
+//     D > 65536) use a scalar two-pass kernel.
+#include "mi_device.h"
+#include "mi_host.h"
+
+namespace mi {
+namespace {
+
+// ---------------------------------------------------------------------------
+// Row-per-workgroup kernel: VPT 16-byte vectors per lane.
+// ---------------------------------------------------------------------------
+template <int VPT, bool FUSED>
+__global__ __launch_bounds__(1024) void rms_row_kernel(const half_t* x, half_t* residual,
+                                                       const half_t* __restrict__ w, half_t* y,
+                                                       int64_t D, float eps, float w_bias) {
+    __shared__ float slots[1024 / kWave];
+    const int64_t row = blockIdx.x;
+    const int64_t chunks = D >> 3;
+    const int nthr = blockDim.x;
+    const half_t* xr = x + row * D;
+    half_t* rr = FUSED ? residual + row * D : nullptr;
+    half_t* yr = y + row * D;
+
+    h8 v[VPT];
+    h8 wv[VPT];
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+        const int64_t c = threadIdx.x + static_cast<int64_t>(j) * nthr;
+        if (c < chunks) {
+            h8 a = ld8(xr + c * 8);
+            if constexpr (FUSED) {
+                const h8 r = ld8(rr + c * 8);
+#pragma unroll
+                for (int k = 0; k < 8; ++k) a[k] = to_half((float)r[k] + (float)a[k]);
+                st8(rr + c * 8, a);
+            }
+            v[j] = a;
+            wv[j] = ld8(w + c * 8);
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const float f = (float)a[k];
+                ss = fmaf(f, f, ss);
+            }
+        } else {
+            v[j] = h8(0);
+            wv[j] = h8(0);
+        }
+    }
+    ss = block_sum(ss, slots);
+    const float rrms = rsqrtf(ss / static_cast<float>(D) + eps);
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+        const int64_t c = threadIdx.x + static_cast<int64_t>(j) * nthr;
+        if (c < chunks) {
+            h8 o;
+#pragma unroll
+            for (int k = 0; k < 8; ++k)
+                o[k] = to_half((float)v[j][k] * rrms * ((float)wv[j][k] + w_bias));
+            st8(yr + c * 8, o);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Short rows: G lanes per row, one 16-byte vector per lane (D <= 8*G).
+// ---------------------------------------------------------------------------
+template <int G, bool FUSED>
+__global__ __launch_bounds__(256) void rms_small_kernel(const half_t* x, half_t* residual,
+                                                        const half_t* __restrict__ w, half_t* y,
+                                                        int64_t N, int D, float eps, float w_bias) {
+    const int lane = threadIdx.x & (G - 1);
+    const int64_t row = static_cast<int64_t>(blockIdx.x) * (blockDim.x / G) + threadIdx.x / G;
+    const int chunks = D >> 3;
+    const bool active = row < N && lane < chunks;
+    const int64_t off = row * D + lane * 8;
+
+    h8 a = h8(0);
+    h8 wv = h8(0);
+    float ss = 0.0f;
+    if (active) {
+        a = ld8(x + off);
+        if constexpr (FUSED) {
+            const h8 r = ld8(residual + off);
+#pragma unroll
+            for (int k = 0; k < 8; ++k) a[k] = to_half((float)r[k] + (float)a[k]);
+            st8(residual + off, a);
+        }
+        wv = ld8(w + lane * 8);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const float f = (float)a[k];
+            ss = fmaf(f, f, ss);
+        }
+    }
+    // every lane takes part in the DPP reduction (no lane has exited)
+    ss = group_sum<G>(ss);
+    const float rrms = rsqrtf(ss / static_cast<float>(D) + eps);
+    if (active) {
+        h8 o;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) o[k] = to_half((float)a[k] * rrms * ((float)wv[k] + w_bias));
+        st8(y + off, o);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Scalar fallback: one 256-lane workgroup per row, two passes.  Each lane
+// revisits only the elements it produced in pass 1, so in-place use is safe.
+// ---------------------------------------------------------------------------
+template <bool FUSED>
+__global__ __launch_bounds__(256) void rms_scalar_kernel(const half_t* x, half_t* residual,
+                                                         const half_t* __restrict__ w, half_t* y,
+                                                         int64_t D, float eps, float w_bias) {
+    __shared__ float slots[256 / kWave];
+    const int64_t row = blockIdx.x;
+    const half_t* xr = x + row * D;
+    half_t* rr = FUSED ? residual + row * D : nullptr;
+    half_t* yr = y + row * D;
+    float ss = 0.0f;
+    for (int64_t i = threadIdx.x; i < D; i += blockDim.x) {
+        float v = (float)xr[i];
+        if constexpr (FUSED) {
+            const half_t s = to_half((float)rr[i] + v);
+            rr[i] = s;
+            v = (float)s;
+        }
+        ss = fmaf(v, v, ss);
+    }
+    ss = block_sum(ss, slots);
+    const float rrms = rsqrtf(ss / static_cast<float>(D) + eps);
+    for (int64_t i = threadIdx.x; i < D; i += blockDim.x) {
+        const float v = FUSED ? (float)rr[i] : (float)xr[i];
+        yr[i] = to_half(v * rrms * ((float)w[i] + w_bias));
+    }
+}
+
+template <bool FUSED>
+int launch_small(const half_t* x, half_t* r, const half_t* w, half_t* y, int64_t N, int D,
+                 float eps, float bias, hipStream_t s) {
+    const int chunks = D >> 3;
+    int G = 1;
+    while (G < chunks) G <<= 1;
+    const int rows_per_wg = 256 / G;
+    const int64_t grid = ceil_div(N, rows_per_wg);
+    if (grid > kMaxGridX) return MI_ERR_UNSUPPORTED;
+    const dim3 g(static_cast<unsigned>(grid)), b(256);
+    switch (G) {
+#define MI_SMALL_CASE(GG) \
+    case GG: rms_small_kernel<GG, FUSED><<<g, b, 0, s>>>(x, r, w, y, N, D, eps, bias); break;
+        MI_SMALL_CASE(1)
+        MI_SMALL_CASE(2)
+        MI_SMALL_CASE(4)
+        MI_SMALL_CASE(8)
+        MI_SMALL_CASE(16)
+        MI_SMALL_CASE(32)
+        MI_SMALL_CASE(64)
+#undef MI_SMALL_CASE
+        default: return MI_ERR_UNSUPPORTED;
+    }
+    return launch_status();
+}
+
+template <bool FUSED>
+int launch_row(const half_t* x, half_t* r, const half_t* w, half_t* y, int64_t N, int64_t D,
+               float eps, float bias, hipStream_t s) {
+    const int64_t chunks = D >> 3;
+    const int vpt = static_cast<int>(ceil_div(chunks, 512));
+    const int threads = static_cast<int>(ceil_div(ceil_div(chunks, vpt), kWave) * kWave);
+    const dim3 g(static_cast<unsigned>(N)), b(threads);
+    switch (vpt) {
+#define MI_ROW_CASE(V) \
+    case V: rms_row_kernel<V, FUSED><<<g, b, 0, s>>>(x, r, w, y, D, eps, bias); break;
+        MI_ROW_CASE(1)
+        MI_ROW_CASE(2)
+        MI_ROW_CASE(3)
+        MI_ROW_CASE(4)
+        MI_ROW_CASE(5)
+        MI_ROW_CASE(6)
+        MI_ROW_CASE(7)
+        MI_ROW_CASE(8)
+        MI_ROW_CASE(9)
+        MI_ROW_CASE(10)
+        MI_ROW_CASE(11)
+        MI_ROW_CASE(12)
+        MI_ROW_CASE(13)
+        MI_ROW_CASE(14)
+        MI_ROW_CASE(15)
+        MI_ROW_CASE(16)
+#undef MI_ROW_CASE
+        default: return MI_ERR_UNSUPPORTED;
+    }
+    return launch_status();
+}
+
+template <bool FUSED>
+int rmsnorm_dispatch(const void* xv, void* rv, const void* wv, void* yv, int64_t N, int64_t D,
+                     float eps, int add_one, void* stream) {
+    if (N < 0 || D < 0) return MI_ERR_INVALID_ARGUMENT;
+    if (N == 0 || D == 0) return MI_OK;
+    if (!xv || !wv || !yv || (FUSED && !rv)) return MI_ERR_INVALID_ARGUMENT;
+    if (N > kMaxGridX) return MI_ERR_UNSUPPORTED;
+    const int64_t bytes = N * D * 2;
+    if (xv != yv && overlaps(xv, bytes, yv, bytes)) return MI_ERR_ALIASING;
+    if (FUSED && (overlaps(rv, bytes, xv, bytes) || overlaps(rv, bytes, yv, bytes)))
+        return MI_ERR_ALIASING;
+
+    const half_t* x = static_cast<const half_t*>(xv);
+    half_t* r = static_cast<half_t*>(rv);
+    const half_t* w = static_cast<const half_t*>(wv);
+    half_t* y = static_cast<half_t*>(yv);
+    const float bias = add_one ? 1.0f : 0.0f;
+    const hipStream_t s = as_stream(stream);
+
+    const bool vec = (D % 8 == 0) && aligned16(x) && aligned16(w) && aligned16(y) &&
+                     (!FUSED || aligned16(r));
+    if (vec && D <= 512) return launch_small<FUSED>(x, r, w, y, N, static_cast<int>(D), eps, bias, s);
+    if (vec && D <= 16 * 512 * 8) return launch_row<FUSED>(x, r, w, y, N, D, eps, bias, s);
+    rms_scalar_kernel<FUSED><<<dim3(static_cast<unsigned>(N)), dim3(256), 0, s>>>(x, r, w, y, D, eps,
+                                                                                  bias);
+    return launch_status();
+}
+
+}  // namespace
+}  // namespace mi
+
+extern "C" int mi_rmsnorm_f16(const void* x, const void* weight, void* y, int64_t N, int64_t D,
+                              float eps, int add_one, void* stream) {
+    return mi::rmsnorm_dispatch<false>(x, nullptr, weight, y, N, D, eps, add_one, stream);
+}
+
+extern "C" int mi_fused_add_rmsnorm_f16(const void* x, void* residual, const void* weight, void* y,
+                                        int64_t N, int64_t D, float eps, int add_one,
+                                        void* stream) {
+    return mi::rmsnorm_dispatch<true>(x, residual, weight, y, N, D, eps, add_one, stream);
+}

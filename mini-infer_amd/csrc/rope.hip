@@ -1,0 +1,281 @@
+// rope.hip -- NeoX half-rotation RoPE for gfx950: table-driven rotation,
+// table generation, and the fused in-place Q+K rotation with cos/sin made in
+// registers.
+//
+// Arithmetic follows the reference (src/kernels/rope_kernel.cu:27-54, 65-77;
+// src/layers/rope.cpp:20-28):
+//   angle  = float(pos) * inv_freq[i]           (fp32 product)
+//   c, s   = half(cos(angle)), half(sin(angle))  (fp16-rounded table values)
+//   y[i]   = x[i] * c - x[i + h] * s,  y[i + h] = x[i + h] * c + x[i] * s
+// Both products in a rotation are exact in fp32 (11-bit x 11-bit
+// significands), so the output is the single rounding of the fp32 result.
+//
+// cos/sin: the fp32 sincosf result (a few ulp) is rounded to fp16; when the
+// value lies within 2^-20 (relative) of an fp16 rounding boundary the angle is
+// re-evaluated in fp64, so the fp16 value always equals half(RN32(cos(angle)))
+// computed from the exact cosine.  This makes the tables independent of the
+// fp32 sincos implementation.
+//
+// Design (HBM-bound: 8 bytes/element in place, + 8 bytes/token of positions):
+//   one 256-lane workgroup per token; lanes 0..hd/2-1 build the token's cos/sin
+//   row in LDS once (instead of once per head), while every lane has already
+//   issued its first pair of 16-byte loads (x[i..i+7], x[h+i..h+i+7]); after a
+//   single barrier each lane rotates one (head, 8-element) unit.  For Qwen2.5
+//   (28 + 4 heads x 64 pairs) that is exactly 256 units = one per lane.
+#include <math.h>
+
+#include "mi_device.h"
+#include "mi_host.h"
+
+namespace mi {
+namespace {
+
+constexpr int kMaxHalf = 256;  // head_dim <= 512
+
+// Host-computed inverse frequencies travel by value in the kernel arguments.
+struct InvFreq {
+    float v[kMaxHalf];
+};
+
+__device__ __forceinline__ bool near_half_boundary(float v) {
+    const float d = v * 9.5367431640625e-07f;  // 2^-20 relative
+    return to_half(v - d) != to_half(v + d);
+}
+
+// fp16 cos/sin of an fp32 angle, equal to half(RN32(exact)) (see file header).
+__device__ __forceinline__ void cos_sin_half(float ang, half_t& hc, half_t& hs) {
+    float s, c;
+    sincosf(ang, &s, &c);
+    if (near_half_boundary(c) || near_half_boundary(s)) {
+        double sd, cd;
+        sincos(static_cast<double>(ang), &sd, &cd);
+        c = static_cast<float>(cd);
+        s = static_cast<float>(sd);
+    }
+    hc = to_half(c);
+    hs = to_half(s);
+}
+
+template <int VEC>
+struct HVec;
+template <>
+struct HVec<8> {
+    typedef h8 T;
+    __device__ static T load(const half_t* p) { return ld8(p); }
+    __device__ static void store(half_t* p, T v) { st8(p, v); }
+};
+template <>
+struct HVec<1> {
+    typedef half_t T;
+    __device__ static T load(const half_t* p) { return *p; }
+    __device__ static void store(half_t* p, T v) { *p = v; }
+};
+
+template <int VEC>
+__device__ __forceinline__ float elem(const typename HVec<VEC>::T& v, int k) {
+    if constexpr (VEC == 1) return (float)v; else return (float)v[k];
+}
+template <int VEC>
+__device__ __forceinline__ void set_elem(typename HVec<VEC>::T& v, int k, float f) {
+    if constexpr (VEC == 1) v = to_half(f); else v[k] = to_half(f);
+}
+
+// One workgroup per token.  Sources: q_in/k_in; destinations q_out/k_out (may
+// equal the sources).  FROM_POS: cos/sin from positions + inv_freq, else from
+// fp16 tables [T, half].
+template <int VEC, bool FROM_POS>
+__global__ __launch_bounds__(256) void rope_kernel(const half_t* q_in, half_t* q_out, int Hq,
+                                                   const half_t* k_in, half_t* k_out, int Hkv,
+                                                   const int64_t* __restrict__ positions,
+                                                   const half_t* __restrict__ cos_t,
+                                                   const half_t* __restrict__ sin_t, int hd,
+                                                   InvFreq inv) {
+    typedef HVec<VEC> V;
+    __shared__ float cs[2 * kMaxHalf];
+    const int64_t tok = blockIdx.x;
+    const int half = hd >> 1;
+    const int cph = half / VEC;  // vector units per half head
+    const int units = (Hq + Hkv) * cph;
+
+    auto locate = [&](int u, const half_t*& src, half_t*& dst) {
+        const int h = u / cph;
+        const int c = u - h * cph;
+        if (h < Hq) {
+            const int64_t base = (tok * Hq + h) * static_cast<int64_t>(hd) + c * VEC;
+            src = q_in + base;
+            dst = q_out + base;
+        } else {
+            const int64_t base = (tok * Hkv + (h - Hq)) * static_cast<int64_t>(hd) + c * VEC;
+            src = k_in + base;
+            dst = k_out + base;
+        }
+        return c;
+    };
+
+    // Issue this lane's first loads before the table work so HBM latency
+    // overlaps the sincos evaluation.
+    int u = threadIdx.x;
+    typename V::T x1{}, x2{};
+    if (u < units) {
+        const half_t* src;
+        half_t* dst;
+        locate(u, src, dst);
+        x1 = V::load(src);
+        x2 = V::load(src + half);
+    }
+
+    for (int i = threadIdx.x; i < half; i += blockDim.x) {
+        half_t hc, hs;
+        if constexpr (FROM_POS) {
+            const float ang = static_cast<float>(positions[tok]) * inv.v[i];
+            cos_sin_half(ang, hc, hs);
+        } else {
+            hc = cos_t[tok * half + i];
+            hs = sin_t[tok * half + i];
+        }
+        cs[i] = (float)hc;
+        cs[kMaxHalf + i] = (float)hs;
+    }
+    __syncthreads();
+
+    for (; u < units; u += blockDim.x) {
+        const half_t* src;
+        half_t* dst;
+        const int c = locate(u, src, dst);
+        if (u != static_cast<int>(threadIdx.x)) {
+            x1 = V::load(src);
+            x2 = V::load(src + half);
+        }
+        typename V::T y1, y2;
+#pragma unroll
+        for (int k = 0; k < VEC; ++k) {
+            const float cv = cs[c * VEC + k];
+            const float sv = cs[kMaxHalf + c * VEC + k];
+            const float a = elem<VEC>(x1, k), b = elem<VEC>(x2, k);
+            set_elem<VEC>(y1, k, a * cv - b * sv);
+            set_elem<VEC>(y2, k, b * cv + a * sv);
+        }
+        V::store(dst, y1);
+        V::store(dst + half, y2);
+    }
+}
+
+__global__ __launch_bounds__(256) void rope_table_kernel(const int64_t* __restrict__ positions,
+                                                         half_t* __restrict__ cos_t,
+                                                         half_t* __restrict__ sin_t, int64_t N,
+                                                         int half, InvFreq inv) {
+    const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (idx >= N * half) return;
+    const int64_t n = idx / half;
+    const int i = static_cast<int>(idx - n * half);
+    half_t hc, hs;
+    cos_sin_half(static_cast<float>(positions[n]) * inv.v[i], hc, hs);
+    cos_t[idx] = hc;
+    sin_t[idx] = hs;
+}
+
+bool load_inv_freq(const float* host, int64_t half, InvFreq& out) {
+    if (!host || half <= 0 || half > kMaxHalf) return false;
+    for (int64_t i = 0; i < half; ++i) out.v[i] = host[i];
+    for (int64_t i = half; i < kMaxHalf; ++i) out.v[i] = 0.0f;
+    return true;
+}
+
+int launch_rope(const half_t* q_in, half_t* q_out, int64_t Hq, const half_t* k_in, half_t* k_out,
+                int64_t Hkv, const int64_t* positions, const half_t* cos_t, const half_t* sin_t,
+                int64_t T, int64_t hd, const InvFreq& inv, hipStream_t s) {
+    if (T > kMaxGridX) return MI_ERR_UNSUPPORTED;
+    const int64_t half = hd / 2;
+    bool vec = (half % 8 == 0) && aligned16(q_in) && aligned16(q_out);
+    if (Hkv > 0) vec = vec && aligned16(k_in) && aligned16(k_out);
+    const dim3 g(static_cast<unsigned>(T)), b(256);
+    const int hq = static_cast<int>(Hq), hk = static_cast<int>(Hkv), d = static_cast<int>(hd);
+    if (positions) {
+        if (vec)
+            rope_kernel<8, true><<<g, b, 0, s>>>(q_in, q_out, hq, k_in, k_out, hk, positions,
+                                                 nullptr, nullptr, d, inv);
+        else
+            rope_kernel<1, true><<<g, b, 0, s>>>(q_in, q_out, hq, k_in, k_out, hk, positions,
+                                                 nullptr, nullptr, d, inv);
+    } else {
+        if (vec)
+            rope_kernel<8, false><<<g, b, 0, s>>>(q_in, q_out, hq, k_in, k_out, hk, nullptr,
+                                                  cos_t, sin_t, d, inv);
+        else
+            rope_kernel<1, false><<<g, b, 0, s>>>(q_in, q_out, hq, k_in, k_out, hk, nullptr,
+                                                  cos_t, sin_t, d, inv);
+    }
+    return launch_status();
+}
+
+// (Hq + Hkv) * hd/2 must fit the int lane arithmetic of rope_kernel.
+bool heads_ok(int64_t Hq, int64_t Hkv, int64_t hd) {
+    return Hq >= 0 && Hkv >= 0 && hd > 0 && hd % 2 == 0 && hd / 2 <= kMaxHalf &&
+           (Hq + Hkv) * hd < (int64_t{1} << 30);
+}
+
+}  // namespace
+}  // namespace mi
+
+using mi::half_t;
+
+extern "C" int mi_rope_neox_f16(const void* x, const void* cos_t, const void* sin_t, void* y,
+                                int64_t B, int64_t S, int64_t H, int64_t D, void* stream) {
+    if (B < 0 || S < 0 || H < 0 || D < 0) return MI_ERR_INVALID_ARGUMENT;
+    const int64_t T = B * S;
+    if (T == 0 || H == 0) return MI_OK;
+    if (!x || !y || !cos_t || !sin_t) return MI_ERR_INVALID_ARGUMENT;
+    if (!mi::heads_ok(H, 0, D)) return MI_ERR_UNSUPPORTED;
+    const int64_t bytes = T * H * D * 2;
+    if (x != y && mi::overlaps(x, bytes, y, bytes)) return MI_ERR_ALIASING;
+    mi::InvFreq unused{};
+    return mi::launch_rope(static_cast<const half_t*>(x), static_cast<half_t*>(y), H, nullptr,
+                           nullptr, 0, nullptr, static_cast<const half_t*>(cos_t),
+                           static_cast<const half_t*>(sin_t), T, D, unused,
+                           mi::as_stream(stream));
+}
+
+extern "C" int mi_rope_tables_f16(const float* inv_freq_host, const int64_t* positions,
+                                  void* cos_t, void* sin_t, int64_t N, int64_t half,
+                                  void* stream) {
+    if (N < 0 || half < 0) return MI_ERR_INVALID_ARGUMENT;
+    if (N == 0 || half == 0) return MI_OK;
+    if (!positions || !cos_t || !sin_t) return MI_ERR_INVALID_ARGUMENT;
+    mi::InvFreq inv;
+    if (!mi::load_inv_freq(inv_freq_host, half, inv)) return MI_ERR_INVALID_ARGUMENT;
+    const int64_t total = N * half;
+    const int64_t grid = mi::ceil_div(total, 256);
+    if (grid > mi::kMaxGridX) return MI_ERR_UNSUPPORTED;
+    const int64_t bytes = total * 2;
+    if (mi::overlaps(cos_t, bytes, sin_t, bytes)) return MI_ERR_ALIASING;
+    mi::rope_table_kernel<<<dim3(static_cast<unsigned>(grid)), dim3(256), 0,
+                            mi::as_stream(stream)>>>(positions, static_cast<half_t*>(cos_t),
+                                                     static_cast<half_t*>(sin_t), N,
+                                                     static_cast<int>(half), inv);
+    return mi::launch_status();
+}
+
+extern "C" int mi_rope_neox_qk_f16(void* q, void* k, const int64_t* positions,
+                                   const float* inv_freq_host, int64_t T, int64_t Hq,
+                                   int64_t Hkv, int64_t head_dim, void* stream) {
+    if (T < 0 || Hq < 0 || Hkv < 0 || head_dim < 0) return MI_ERR_INVALID_ARGUMENT;
+    if (T == 0 || Hq + Hkv == 0) return MI_OK;
+    if (!positions || (Hq > 0 && !q) || (Hkv > 0 && !k)) return MI_ERR_INVALID_ARGUMENT;
+    if (!mi::heads_ok(Hq, Hkv, head_dim)) return MI_ERR_UNSUPPORTED;
+    if (Hq > 0 && Hkv > 0 &&
+        mi::overlaps(q, T * Hq * head_dim * 2, k, T * Hkv * head_dim * 2))
+        return MI_ERR_ALIASING;
+    mi::InvFreq inv;
+    if (!mi::load_inv_freq(inv_freq_host, head_dim / 2, inv)) return MI_ERR_INVALID_ARGUMENT;
+    // With no Q heads, run K through the Q slot (the kernel has one code path).
+    if (Hq == 0) {
+        q = k;
+        Hq = Hkv;
+        k = nullptr;
+        Hkv = 0;
+    }
+    return mi::launch_rope(static_cast<const half_t*>(q), static_cast<half_t*>(q), Hq,
+                           static_cast<const half_t*>(k), static_cast<half_t*>(k), Hkv,
+                           positions, nullptr, nullptr, T, head_dim, inv,
+                           mi::as_stream(stream));
+}

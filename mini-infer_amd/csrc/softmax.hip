@@ -1,0 +1,181 @@
+// softmax.hip -- row softmax for gfx950, fp16 in/out, fp32 math.
+//
+// Arithmetic follows the reference (src/kernels/softmax_kernel.cu:26-58):
+// m = max(x), S = sum(exp(x - m)), y = half(exp(x - m) * (1 / S)).
+//
+// Design (HBM-bound: 4 bytes/element):
+//   * Each lane keeps an online (max, sum) pair over its 16-byte vectors,
+//     rescaling the sum when the max grows, so statistics need ONE read of x
+//     (the reference makes separate max and sum passes, then a third to write).
+//   * Many rows (N >= 512): one workgroup per row; the write pass re-reads the
+//     row, which the workgroup has just streamed through L2.
+//   * Few long rows (the LM-head case, 64 x 152064): one workgroup per row
+//     would light up 64 of 256 CUs, so each row is cut into `splits` chunks.
+//     Kernel 1 writes a (max, sum) pair per chunk to a small stream-ordered
+//     workspace (8 bytes per chunk);
+//     kernel 2, on the same grid, merges the row's pairs (one lane per
+//     chunk, wave reductions, no barrier) and writes its chunk.  Both grids
+//     map block (split, row) to the same XCD, so kernel 2's re-read of the
+//     chunk hits the L2 / Infinity Cache that kernel 1 filled.
+#include "mi_device.h"
+#include "mi_host.h"
+
+namespace mi {
+namespace {
+
+constexpr int kSplitMaxRows = 512;  // below this many rows, split each row
+constexpr int kMaxSplits = 64;      // chunk pairs of a row fit one wave
+
+// Accumulate elements [begin, end) of a row into this lane's (m, s).
+template <int VEC>
+__device__ __forceinline__ void lane_stats(const half_t* xr, int64_t begin, int64_t end, float& m,
+                                           float& s) {
+    for (int64_t i = begin + static_cast<int64_t>(threadIdx.x) * VEC; i < end;
+         i += static_cast<int64_t>(blockDim.x) * VEC) {
+        float v[VEC];
+        if constexpr (VEC == 8) {
+            const h8 h = ld8(xr + i);
+#pragma unroll
+            for (int k = 0; k < 8; ++k) v[k] = (float)h[k];
+        } else {
+            v[0] = (float)xr[i];
+        }
+        float vm = v[0];
+#pragma unroll
+        for (int k = 1; k < VEC; ++k) vm = fmaxf(vm, v[k]);
+        const float mn = fmaxf(m, vm);
+        if (mn == -INFINITY) continue;
+        float acc = s * fast_exp(m - mn);
+#pragma unroll
+        for (int k = 0; k < VEC; ++k) acc += fast_exp(v[k] - mn);
+        s = acc;
+        m = mn;
+    }
+}
+
+template <int VEC>
+__device__ __forceinline__ void write_range(const half_t* xr, half_t* yr, int64_t begin,
+                                            int64_t end, float m, float inv) {
+    for (int64_t i = begin + static_cast<int64_t>(threadIdx.x) * VEC; i < end;
+         i += static_cast<int64_t>(blockDim.x) * VEC) {
+        if constexpr (VEC == 8) {
+            const h8 h = ld8(xr + i);
+            h8 o;
+#pragma unroll
+            for (int k = 0; k < 8; ++k) o[k] = to_half(fast_exp((float)h[k] - m) * inv);
+            st8_stream(yr + i, o);
+        } else {
+            yr[i] = to_half(fast_exp((float)xr[i] - m) * inv);
+        }
+    }
+}
+
+// Workgroup-wide merge of per-lane (m, s): max first, then rescaled sums.
+__device__ __forceinline__ void block_merge(float& m, float& s, float* slots) {
+    const float M = block_max(m, slots);
+    const float part = (m == -INFINITY) ? 0.0f : s * fast_exp(m - M);
+    __syncthreads();  // slots are reused by the sum
+    s = block_sum(part, slots);
+    m = M;
+}
+
+template <int VEC>
+__global__ __launch_bounds__(1024) void softmax_row_kernel(const half_t* x, half_t* y, int64_t D) {
+    __shared__ float slots[1024 / kWave];
+    const int64_t row = blockIdx.x;
+    const half_t* xr = x + row * D;
+    half_t* yr = y + row * D;
+    float m = -INFINITY, s = 0.0f;
+    lane_stats<VEC>(xr, 0, D, m, s);
+    block_merge(m, s, slots);
+    write_range<VEC>(xr, yr, 0, D, m, 1.0f / s);
+}
+
+template <int VEC>
+__global__ __launch_bounds__(256) void softmax_partial_kernel(const half_t* x, float* ws,
+                                                              int64_t D, int64_t chunk) {
+    __shared__ float slots[256 / kWave];
+    const int split = blockIdx.x, splits = gridDim.x;
+    const int64_t row = blockIdx.y;
+    const int64_t b = split * chunk;
+    const int64_t e = b + chunk < D ? b + chunk : D;
+    float m = -INFINITY, s = 0.0f;
+    lane_stats<VEC>(x + row * D, b, e, m, s);
+    block_merge(m, s, slots);
+    if (threadIdx.x == 0) {
+        float* p = ws + (row * splits + split) * 2;
+        p[0] = m;
+        p[1] = s;
+    }
+}
+
+template <int VEC>
+__global__ __launch_bounds__(256) void softmax_finish_kernel(const half_t* x, half_t* y,
+                                                             const float* __restrict__ ws,
+                                                             int64_t D, int64_t chunk) {
+    const int split = blockIdx.x, splits = gridDim.x;
+    const int64_t row = blockIdx.y;
+    const int lane = threadIdx.x & (kWave - 1);
+    // Every wave merges the row's pairs itself: lane j holds chunk j.
+    float m = -INFINITY, s = 0.0f;
+    if (lane < splits) {
+        const float* p = ws + (row * splits + lane) * 2;
+        m = p[0];
+        s = p[1];
+    }
+    const float M = group_max<kWave>(m);
+    const float S = group_sum<kWave>(m == -INFINITY ? 0.0f : s * fast_exp(m - M));
+    const int64_t b = split * chunk;
+    const int64_t e = b + chunk < D ? b + chunk : D;
+    write_range<VEC>(x + row * D, y + row * D, b, e, M, 1.0f / S);
+}
+
+template <int VEC>
+int launch_softmax(const half_t* x, half_t* y, int64_t N, int64_t D, hipStream_t s) {
+    if (N >= kSplitMaxRows || D < 8192) {
+        const int64_t want = ceil_div(D, VEC);
+        int threads = static_cast<int>(ceil_div(want < 1024 ? want : 1024, kWave) * kWave);
+        softmax_row_kernel<VEC><<<dim3(static_cast<unsigned>(N)), dim3(threads), 0, s>>>(x, y, D);
+        return launch_status();
+    }
+    // Split rows: aim for >= 2048 workgroups, chunks of >= 2048 elements,
+    // chunk a multiple of 8 so vector accesses stay aligned.
+    int64_t splits = ceil_div(2048, N);
+    if (splits > kMaxSplits) splits = kMaxSplits;
+    const int64_t max_by_len = D / 2048 > 1 ? D / 2048 : 1;
+    if (splits > max_by_len) splits = max_by_len;
+    const int64_t chunk = ceil_div(ceil_div(D, splits), 8) * 8;
+    splits = ceil_div(D, chunk);
+    // The (max, sum) pairs live in a stream-ordered allocation from the
+    // device's default pool: concurrent calls on other streams get their own,
+    // and after the first call the pool hands back cached memory.
+    void* ws = nullptr;
+    hipError_t e = hipMallocAsync(&ws, static_cast<size_t>(N * splits) * 2 * sizeof(float), s);
+    if (e != hipSuccess) return static_cast<int>(e);
+    const dim3 g(static_cast<unsigned>(splits), static_cast<unsigned>(N));
+    softmax_partial_kernel<VEC><<<g, dim3(256), 0, s>>>(x, static_cast<float*>(ws), D, chunk);
+    softmax_finish_kernel<VEC><<<g, dim3(256), 0, s>>>(x, y, static_cast<const float*>(ws), D,
+                                                       chunk);
+    const int st = launch_status();
+    e = hipFreeAsync(ws, s);
+    if (st != MI_OK) return st;
+    return e == hipSuccess ? MI_OK : static_cast<int>(e);
+}
+
+}  // namespace
+}  // namespace mi
+
+extern "C" int mi_softmax_f16(const void* x, void* y, int64_t N, int64_t D, void* stream) {
+    if (N < 0 || D < 0) return MI_ERR_INVALID_ARGUMENT;
+    if (N == 0 || D == 0) return MI_OK;
+    if (!x || !y) return MI_ERR_INVALID_ARGUMENT;
+    if (N > mi::kMaxGridX) return MI_ERR_UNSUPPORTED;
+    const int64_t bytes = N * D * 2;
+    if (x != y && mi::overlaps(x, bytes, y, bytes)) return MI_ERR_ALIASING;
+    const auto* xh = static_cast<const mi::half_t*>(x);
+    auto* yh = static_cast<mi::half_t*>(y);
+    const hipStream_t s = mi::as_stream(stream);
+    if (D % 8 == 0 && mi::aligned16(x) && mi::aligned16(y))
+        return mi::launch_softmax<8>(xh, yh, N, D, s);
+    return mi::launch_softmax<1>(xh, yh, N, D, s);
+}

@@ -1,0 +1,18 @@
+// status.cpp -- status strings and ABI version of libmi_kernels.so.
+#include <hip/hip_runtime.h>
+
+#include "mi_kernels.h"
+
+extern "C" const char* mi_status_string(int status) {
+    switch (status) {
+        case MI_OK: return "ok";
+        case MI_ERR_INVALID_ARGUMENT: return "invalid argument (null pointer or bad size)";
+        case MI_ERR_UNSUPPORTED: return "shape not supported by the kernels";
+        case MI_ERR_ALIASING: return "buffers overlap where they must not";
+        default: break;
+    }
+    if (status > 0) return hipGetErrorString(static_cast<hipError_t>(status));
+    return "unknown status";
+}
+
+extern "C" int mi_abi_version(void) { return MI_KERNELS_ABI_VERSION; }

@@ -1,0 +1,338 @@
+"""ctypes binding of libmi_kernels.so (the C ABI in include/mi_kernels.h).
+
+PyTorch is used here only for device memory and streams: every function takes
+torch CUDA (HIP) tensors, checks dtype / contiguity / shape on the host, and
+enqueues the HIP kernel on the current torch stream through the C ABI.  There
+is no fallback: if the shared library is missing, or the call's status is not
+0, a RuntimeError is raised.
+
+The functions mirror the reference's ``mini_infer::kernels::launch_*`` entry
+points (src/kernels/<name>_kernel.cuh in the reference tree); the two fused
+ops (``fused_add_rmsnorm``, ``geglu``) and the positions-driven
+``rope_neox_qk`` are additions named after what they fuse.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+
+_HERE = Path(__file__).resolve().parent
+LIB_PATH = _HERE / "libmi_kernels.so"
+
+_c_void_p = ctypes.c_void_p
+_i64 = ctypes.c_int64
+_f32 = ctypes.c_float
+_int = ctypes.c_int
+
+# name -> argtypes (restype is int for every entry point)
+SIGNATURES = {
+    "mi_rmsnorm_f16": [_c_void_p, _c_void_p, _c_void_p, _i64, _i64, _f32, _int, _c_void_p],
+    "mi_fused_add_rmsnorm_f16": [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _f32,
+                                 _int, _c_void_p],
+    "mi_rope_neox_f16": [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64, _i64,
+                         _c_void_p],
+    "mi_rope_tables_f16": [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _c_void_p],
+    "mi_rope_neox_qk_f16": [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64, _i64,
+                            _c_void_p],
+    "mi_swiglu_f16": [_c_void_p, _c_void_p, _c_void_p, _i64, _c_void_p],
+    "mi_gelu_tanh_f16": [_c_void_p, _c_void_p, _i64, _c_void_p],
+    "mi_geglu_f16": [_c_void_p, _c_void_p, _c_void_p, _i64, _c_void_p],
+    "mi_add_inplace_f16": [_c_void_p, _c_void_p, _i64, _c_void_p],
+    "mi_mul_inplace_f16": [_c_void_p, _c_void_p, _i64, _c_void_p],
+    "mi_scale_inplace_f16": [_c_void_p, _f32, _i64, _c_void_p],
+    "mi_softmax_f16": [_c_void_p, _c_void_p, _i64, _i64, _c_void_p],
+    "mi_embedding_gather_f16": [_c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64, _c_void_p],
+    "mi_abi_version": [],
+}
+
+_lib = None
+
+
+def load_library(path: os.PathLike | str | None = None) -> ctypes.CDLL:
+    """Load (once) and type the kernel library; raise if it is not built."""
+    global _lib
+    if _lib is not None and path is None:
+        return _lib
+    p = Path(path) if path is not None else LIB_PATH
+    if not p.exists():
+        raise RuntimeError(
+            f"{p} is not built; run __graft_entry__.build() (or `make -C mini-infer_amd`)")
+    lib = ctypes.CDLL(str(p))
+    for name, argtypes in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.argtypes = argtypes
+        fn.restype = _int
+    lib.mi_status_string.argtypes = [_int]
+    lib.mi_status_string.restype = ctypes.c_char_p
+    if path is None:
+        _lib = lib
+    return lib
+
+
+def _check(status: int, what: str) -> None:
+    if status != 0:
+        msg = load_library().mi_status_string(status).decode()
+        raise RuntimeError(f"{what} failed: status {status} ({msg})")
+
+
+def _torch():
+    import torch  # noqa: PLC0415  (imported lazily so CPU-only users can load the ABI)
+    return torch
+
+
+def _stream(stream):
+    torch = _torch()
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return ctypes.c_void_p(s.cuda_stream)
+
+
+def _ptr(t) -> ctypes.c_void_p:
+    return ctypes.c_void_p(t.data_ptr())
+
+
+def _need(t, dtype, name: str) -> None:
+    torch = _torch()
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a torch.Tensor")
+    if t.device.type != "cuda":
+        raise ValueError(f"{name} must be on the GPU, got {t.device}")
+    if t.dtype != dtype:
+        raise TypeError(f"{name} must be {dtype}, got {t.dtype}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+
+
+def _f16():
+    return _torch().float16
+
+
+# ---------------------------------------------------------------------------
+# RMSNorm family (reference: launch_rmsnorm, src/kernels/rmsnorm_kernel.cuh:19)
+# ---------------------------------------------------------------------------
+
+def rmsnorm(x, weight, y=None, eps: float = 1e-6, add_one: bool = False, stream=None):
+    """y = x * rsqrt(mean(x^2) + eps) * (1 + w if add_one else w); x: [N, D]."""
+    _need(x, _f16(), "x"); _need(weight, _f16(), "weight")
+    if x.dim() != 2:
+        raise ValueError("x must be 2-D [N, D]")
+    N, D = x.shape
+    if weight.numel() != D:
+        raise ValueError("weight size must equal D")
+    if y is None:
+        y = _torch().empty_like(x)
+    _need(y, _f16(), "y")
+    if y.shape != x.shape:
+        raise ValueError("y must have x's shape")
+    _check(load_library().mi_rmsnorm_f16(_ptr(x), _ptr(weight), _ptr(y), N, D, eps,
+                                         int(bool(add_one)), _stream(stream)), "mi_rmsnorm_f16")
+    return y
+
+
+def fused_add_rmsnorm(x, residual, weight, y=None, eps: float = 1e-6, add_one: bool = False,
+                      stream=None):
+    """residual <- half(residual + x); y = rmsnorm(residual).  Returns y."""
+    _need(x, _f16(), "x"); _need(residual, _f16(), "residual"); _need(weight, _f16(), "weight")
+    if x.dim() != 2 or residual.shape != x.shape:
+        raise ValueError("x and residual must be 2-D [N, D] of the same shape")
+    N, D = x.shape
+    if weight.numel() != D:
+        raise ValueError("weight size must equal D")
+    if y is None:
+        y = _torch().empty_like(x)
+    _need(y, _f16(), "y")
+    if y.shape != x.shape:
+        raise ValueError("y must have x's shape")
+    _check(load_library().mi_fused_add_rmsnorm_f16(_ptr(x), _ptr(residual), _ptr(weight), _ptr(y),
+                                                   N, D, eps, int(bool(add_one)),
+                                                   _stream(stream)), "mi_fused_add_rmsnorm_f16")
+    return y
+
+
+# ---------------------------------------------------------------------------
+# RoPE (reference: launch_rope / launch_rope_precompute*, rope_kernel.cuh:11-28)
+# ---------------------------------------------------------------------------
+
+def _inv_freq_buffer(inv_freq):
+    """inv_freq as a host float32 ctypes array (the ABI reads it on the host)."""
+    import numpy as np  # noqa: PLC0415
+    a = np.ascontiguousarray(np.asarray(inv_freq, dtype=np.float32))
+    return a, a.ctypes.data_as(ctypes.c_void_p)
+
+
+def rope_neox(x, cos_t, sin_t, y=None, stream=None):
+    """Table-driven NeoX RoPE; x: [B, S, H, D], tables [B*S, D/2]; y may be x."""
+    _need(x, _f16(), "x"); _need(cos_t, _f16(), "cos_t"); _need(sin_t, _f16(), "sin_t")
+    if x.dim() != 4:
+        raise ValueError("x must be 4-D [B, S, H, D]")
+    B, S, H, D = x.shape
+    if cos_t.numel() != B * S * (D // 2) or sin_t.numel() != B * S * (D // 2):
+        raise ValueError("cos/sin tables must be [B*S, D/2]")
+    if y is None:
+        y = _torch().empty_like(x)
+    _need(y, _f16(), "y")
+    _check(load_library().mi_rope_neox_f16(_ptr(x), _ptr(cos_t), _ptr(sin_t), _ptr(y), B, S, H, D,
+                                           _stream(stream)), "mi_rope_neox_f16")
+    return y
+
+
+def rope_inv_freq(head_dim: int, theta: float = 1e6):
+    """inv_freq[i] = 1 / powf(theta, 2i/head_dim) in fp32, computed on the host
+    with the C library's powf, as RoPE::recompute_inv_freq_ does
+    (src/layers/rope.cpp:20-28)."""
+    import ctypes.util  # noqa: PLC0415
+    import numpy as np  # noqa: PLC0415
+    libm = ctypes.CDLL(ctypes.util.find_library("m"))
+    libm.powf.argtypes = [ctypes.c_float, ctypes.c_float]
+    libm.powf.restype = ctypes.c_float
+    hd = np.float32(head_dim)
+    return np.array([np.float32(1.0) / np.float32(libm.powf(theta, float(np.float32(2.0 * i) / hd)))
+                     for i in range(head_dim // 2)], dtype=np.float32)
+
+
+def rope_tables(inv_freq, positions, cos_t=None, sin_t=None, stream=None):
+    """fp16 cos/sin tables [N, half] for device int64 positions [N]."""
+    torch = _torch()
+    _need(positions, torch.int64, "positions")
+    arr, p = _inv_freq_buffer(inv_freq)
+    half = arr.size
+    N = positions.numel()
+    if cos_t is None:
+        cos_t = torch.empty((N, half), dtype=torch.float16, device=positions.device)
+    if sin_t is None:
+        sin_t = torch.empty((N, half), dtype=torch.float16, device=positions.device)
+    _need(cos_t, _f16(), "cos_t"); _need(sin_t, _f16(), "sin_t")
+    if cos_t.numel() != N * half or sin_t.numel() != N * half:
+        raise ValueError("tables must hold N * half elements")
+    _check(load_library().mi_rope_tables_f16(p, _ptr(positions), _ptr(cos_t), _ptr(sin_t), N, half,
+                                             _stream(stream)), "mi_rope_tables_f16")
+    return cos_t, sin_t
+
+
+def rope_neox_qk(q, k, positions, inv_freq, stream=None):
+    """In-place NeoX RoPE of q [T, Hq, hd] and k [T, Hkv, hd] (k may be None)."""
+    torch = _torch()
+    _need(q, _f16(), "q"); _need(positions, torch.int64, "positions")
+    if q.dim() != 3:
+        raise ValueError("q must be 3-D [T, Hq, hd]")
+    T, Hq, hd = q.shape
+    Hkv = 0
+    if k is not None:
+        _need(k, _f16(), "k")
+        if k.dim() != 3 or k.shape[0] != T or k.shape[2] != hd:
+            raise ValueError("k must be [T, Hkv, hd]")
+        Hkv = k.shape[1]
+    if positions.numel() != T:
+        raise ValueError("positions must hold T entries")
+    arr, p = _inv_freq_buffer(inv_freq)
+    if arr.size != hd // 2:
+        raise ValueError("inv_freq must hold head_dim/2 entries")
+    kp = _ptr(k) if k is not None else ctypes.c_void_p(0)
+    _check(load_library().mi_rope_neox_qk_f16(_ptr(q), kp, _ptr(positions), p, T, Hq, Hkv, hd,
+                                              _stream(stream)), "mi_rope_neox_qk_f16")
+    return q, k
+
+
+# ---------------------------------------------------------------------------
+# Elementwise (reference: swiglu_kernel.cuh:9, gelu_kernel.cuh:15,
+# model_utils_kernel.cuh:12-29)
+# ---------------------------------------------------------------------------
+
+def _binary(fn_name, a, b, out, stream):
+    _need(a, _f16(), "a"); _need(b, _f16(), "b")
+    if a.numel() != b.numel():
+        raise ValueError("operands must have the same number of elements")
+    if out is None:
+        out = _torch().empty_like(a)
+    _need(out, _f16(), "out")
+    if out.numel() != a.numel():
+        raise ValueError("out must have the operands' size")
+    _check(getattr(load_library(), fn_name)(_ptr(a), _ptr(b), _ptr(out), a.numel(),
+                                            _stream(stream)), fn_name)
+    return out
+
+
+def swiglu(gate, up, out=None, stream=None):
+    return _binary("mi_swiglu_f16", gate, up, out, stream)
+
+
+def geglu(gate, up, out=None, stream=None):
+    return _binary("mi_geglu_f16", gate, up, out, stream)
+
+
+def gelu_tanh(x, y=None, stream=None):
+    _need(x, _f16(), "x")
+    if y is None:
+        y = _torch().empty_like(x)
+    _need(y, _f16(), "y")
+    if y.numel() != x.numel():
+        raise ValueError("y must have x's size")
+    _check(load_library().mi_gelu_tanh_f16(_ptr(x), _ptr(y), x.numel(), _stream(stream)),
+           "mi_gelu_tanh_f16")
+    return y
+
+
+def add_inplace(y, x, stream=None):
+    _need(y, _f16(), "y"); _need(x, _f16(), "x")
+    if y.numel() != x.numel():
+        raise ValueError("size mismatch")
+    _check(load_library().mi_add_inplace_f16(_ptr(y), _ptr(x), y.numel(), _stream(stream)),
+           "mi_add_inplace_f16")
+    return y
+
+
+def mul_inplace(y, x, stream=None):
+    _need(y, _f16(), "y"); _need(x, _f16(), "x")
+    if y.numel() != x.numel():
+        raise ValueError("size mismatch")
+    _check(load_library().mi_mul_inplace_f16(_ptr(y), _ptr(x), y.numel(), _stream(stream)),
+           "mi_mul_inplace_f16")
+    return y
+
+
+def scale_inplace(y, scale: float, stream=None):
+    _need(y, _f16(), "y")
+    _check(load_library().mi_scale_inplace_f16(_ptr(y), float(scale), y.numel(),
+                                               _stream(stream)), "mi_scale_inplace_f16")
+    return y
+
+
+# ---------------------------------------------------------------------------
+# Softmax (reference: launch_softmax, softmax_kernel.cuh:12)
+# ---------------------------------------------------------------------------
+
+def softmax(x, y=None, stream=None):
+    _need(x, _f16(), "x")
+    if x.dim() != 2:
+        raise ValueError("x must be 2-D [N, D]")
+    if y is None:
+        y = _torch().empty_like(x)
+    _need(y, _f16(), "y")
+    if y.shape != x.shape:
+        raise ValueError("y must have x's shape")
+    _check(load_library().mi_softmax_f16(_ptr(x), _ptr(y), x.shape[0], x.shape[1],
+                                         _stream(stream)), "mi_softmax_f16")
+    return y
+
+
+# ---------------------------------------------------------------------------
+# Embedding gather (reference: launch_embedding_gather, model_utils_kernel.cuh:14)
+# ---------------------------------------------------------------------------
+
+def embedding_gather(ids, table, out=None, check_range: bool = True, stream=None):
+    """out[t] = table[ids[t]]; ids int64 (any shape), table [V, H]."""
+    torch = _torch()
+    _need(ids, torch.int64, "ids"); _need(table, _f16(), "table")
+    if table.dim() != 2:
+        raise ValueError("table must be 2-D [V, H]")
+    V, H = table.shape
+    T = ids.numel()
+    if out is None:
+        out = torch.empty((*ids.shape, H), dtype=torch.float16, device=table.device)
+    _need(out, _f16(), "out")
+    if out.numel() != T * H:
+        raise ValueError("out must hold T * H elements")
+    vocab = V if check_range else 0
+    _check(load_library().mi_embedding_gather_f16(_ptr(ids), _ptr(table), _ptr(out), T, H, vocab,
+                                                  _stream(stream)), "mi_embedding_gather_f16")
+    return out

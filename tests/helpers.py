@@ -1,0 +1,47 @@
+"""Test helpers: seeded inputs, host<->device copies, tolerance checks."""
+import numpy as np
+
+RTOL = 1e-3  # tests/verify/verify.py:142 (torch.allclose rtol=1e-3, atol=1e-3)
+ATOL = 1e-3
+
+
+def normal_f16(rng, shape, mean=0.0, std=1.0):
+    return (rng.standard_normal(shape, dtype=np.float32) * np.float32(std)
+            + np.float32(mean)).astype(np.float16)
+
+
+def to_dev(a, dev):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def to_host(t):
+    import torch
+    torch.cuda.synchronize()
+    return t.detach().cpu().numpy()
+
+
+def assert_close(ours_f16, ref_f32, rtol=RTOL, atol=ATOL, what=""):
+    """allclose(ours, ref) as verify.py checks it, with a useful message."""
+    ours = np.asarray(ours_f16).astype(np.float32)
+    ref = np.asarray(ref_f32, dtype=np.float32)
+    assert ours.shape == ref.shape, f"{what}: shape {ours.shape} vs {ref.shape}"
+    diff = np.abs(ours - ref)
+    bad = diff > atol + rtol * np.abs(ref)
+    if bad.any():
+        i = np.unravel_index(np.argmax(diff - (atol + rtol * np.abs(ref))), diff.shape)
+        raise AssertionError(
+            f"{what}: {int(bad.sum())} of {bad.size} outside rtol={rtol} atol={atol}; "
+            f"worst at {i}: ours={ours[i]} ref={ref[i]} max_abs={diff.max():.3e}")
+
+
+def assert_bits_equal(a, b, what=""):
+    a = np.ascontiguousarray(a); b = np.ascontiguousarray(b)
+    assert a.shape == b.shape, f"{what}: shape {a.shape} vs {b.shape}"
+    av = a.view(np.uint16 if a.dtype.itemsize == 2 else np.uint8)
+    bv = b.view(np.uint16 if b.dtype.itemsize == 2 else np.uint8)
+    ne = av != bv
+    if ne.any():
+        i = np.argwhere(ne)[0]
+        raise AssertionError(f"{what}: {int(ne.sum())} of {ne.size} differ; first at {tuple(i)}: "
+                             f"{a[tuple(i)]} vs {b[tuple(i)]}")

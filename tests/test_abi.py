@@ -1,0 +1,104 @@
+"""CPU checks of the C ABI library and the Python binding (no kernel runs).
+
+The library must load without a GPU, export every entry point that
+include/mi_kernels.h declares, and reject bad arguments on the host before
+touching the HIP runtime.
+"""
+import ctypes
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+import mi_kernels
+
+ROOT = Path(__file__).resolve().parent.parent
+HEADER = ROOT / "include" / "mi_kernels.h"
+
+
+def declared_symbols():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(mi_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return mi_kernels.load_library()
+
+
+def test_library_exports_every_declared_symbol(lib):
+    names = declared_symbols()
+    assert len(names) >= 15
+    for n in names:
+        assert hasattr(lib, n), f"{n} declared in mi_kernels.h but not exported"
+
+
+def test_binding_covers_header():
+    names = set(declared_symbols()) - {"mi_status_string"}
+    assert names == set(mi_kernels.SIGNATURES), names ^ set(mi_kernels.SIGNATURES)
+
+
+def test_abi_version_and_status_strings(lib):
+    m = re.search(r"#define MI_KERNELS_ABI_VERSION (\d+)", HEADER.read_text())
+    assert lib.mi_abi_version() == int(m.group(1))
+    assert lib.mi_status_string(0) == b"ok"
+    for code in (-1, -2, -3):
+        assert lib.mi_status_string(code)
+    assert lib.mi_status_string(-99) == b"unknown status"
+
+
+def P(v):
+    return ctypes.c_void_p(v)
+
+
+def test_host_side_argument_rejection(lib):
+    """Every check here returns before any HIP call (fake pointers)."""
+    a, b, c, r = P(0x10000), P(0x20000), P(0x30000), P(0x40000)
+    # negative sizes
+    assert lib.mi_rmsnorm_f16(a, b, c, -1, 64, 1e-6, 0, None) == -1
+    assert lib.mi_swiglu_f16(a, b, c, -5, None) == -1
+    assert lib.mi_softmax_f16(a, c, 4, -1, None) == -1
+    assert lib.mi_embedding_gather_f16(a, b, c, -1, 8, 0, None) == -1
+    # zero sizes are successful no-ops
+    assert lib.mi_rmsnorm_f16(a, b, c, 0, 64, 1e-6, 0, None) == 0
+    assert lib.mi_swiglu_f16(a, b, c, 0, None) == 0
+    assert lib.mi_rope_neox_qk_f16(a, b, c, None, 0, 28, 4, 128, None) == 0
+    # null pointers
+    assert lib.mi_rmsnorm_f16(None, b, c, 4, 64, 1e-6, 0, None) == -1
+    assert lib.mi_geglu_f16(a, None, c, 16, None) == -1
+    assert lib.mi_fused_add_rmsnorm_f16(a, None, b, c, 4, 64, 1e-6, 0, None) == -1
+    # overlap rules
+    assert lib.mi_rmsnorm_f16(a, b, P(0x10000 + 8), 4, 64, 1e-6, 0, None) == -3
+    assert lib.mi_fused_add_rmsnorm_f16(a, a, b, c, 4, 64, 1e-6, 0, None) == -3
+    assert lib.mi_fused_add_rmsnorm_f16(a, c, b, c, 4, 64, 1e-6, 0, None) == -3
+    assert lib.mi_swiglu_f16(a, b, P(0x10000 + 2), 64, None) == -3
+    assert lib.mi_rope_neox_f16(a, b, c, P(0x10000 + 2), 1, 2, 4, 64, None) == -3
+    # unsupported shapes
+    inv = (ctypes.c_float * 512)()
+    assert lib.mi_rope_neox_qk_f16(a, r, c, inv, 4, 1, 1, 1024, None) == -2  # head_dim > 512
+    assert lib.mi_rope_neox_qk_f16(a, r, c, inv, 4, 1, 1, 7, None) == -2     # odd head_dim
+    assert lib.mi_rope_neox_qk_f16(a, r, c, None, 4, 1, 1, 64, None) == -1   # no inv_freq
+    assert lib.mi_rope_tables_f16(None, a, b, c, 4, 32, None) == -1
+
+
+def test_binding_validates_on_host():
+    import torch
+    x = torch.zeros(4, 8, dtype=torch.float16)
+    w = torch.zeros(8, dtype=torch.float16)
+    with pytest.raises(ValueError, match="GPU"):
+        mi_kernels.rmsnorm(x, w)
+    with pytest.raises(TypeError):
+        mi_kernels.rmsnorm(np.zeros((4, 8)), w)
+
+
+def test_product_path_has_no_oracle_dependency():
+    """The shipped package must not import, link or load the oracle."""
+    pkg = ROOT / "mini-infer_amd"
+    files = [f for ext in ("*.py", "*.hip", "*.cpp", "*.h", "Makefile") for f in pkg.rglob(ext)]
+    assert files
+    for f in files:
+        text = f.read_text()
+        for needle in ("import oracle", "libmi_oracle", "mi_oracle.h", "mio_"):
+            assert needle not in text, f"{f} references the oracle ({needle})"

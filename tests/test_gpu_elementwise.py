@@ -1,0 +1,130 @@
+"""GPU parity: SwiGLU, GeGLU, gelu_tanh and the in-place add / mul / scale.
+
+Tolerances: activations within rtol = atol = 1e-3 of the fp32 oracle
+(tests/verify/verify.py:142); add / mul / scale are one fp32 operation
+rounded to fp16, so they are bit-exact.  GeGLU is additionally held within
+1 fp16 ulp of the reference's two-kernel composition (gelu, then mul).
+"""
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from helpers import assert_bits_equal, assert_close, normal_f16, to_dev, to_host
+
+pytestmark = pytest.mark.gpu
+GOLD = np.load(Path(__file__).resolve().parent / "golden" / "ref_cases.npz")
+
+
+def _case(msg):
+    print(f"[case] {msg}", flush=True)
+
+
+def test_reference_cases(mk, orc, dev):
+    """tests/test_swiglu/main.cpp:63-68 and tests/test_gelu/main.cpp:64-67."""
+    _case("swiglu/gelu reference n=4096")
+    g, u = GOLD["swiglu_g"], GOLD["swiglu_u"]
+    y = to_host(mk.swiglu(to_dev(g, dev), to_dev(u, dev)))
+    assert_close(y, GOLD["swiglu_y"], what="swiglu vs golden")
+    assert_close(y, orc.swiglu(g, u), what="swiglu vs oracle")
+    gx = GOLD["gelu_x"]
+    y = to_host(mk.gelu_tanh(to_dev(gx, dev)))
+    assert_close(y, GOLD["gelu_y"], what="gelu vs golden")
+    assert_close(y, orc.gelu_tanh(gx), what="gelu vs oracle")
+
+
+def test_config4_swiglu_full(mk, orc, dev):
+    """BASELINE config 4a: gate/up [4096, 18944] ~N(0,1)."""
+    _case("swiglu [4096,18944]")
+    rng = np.random.default_rng(41)
+    g = normal_f16(rng, (4096, 18944))
+    u = normal_f16(rng, (4096, 18944))
+    y = to_host(mk.swiglu(to_dev(g, dev), to_dev(u, dev)))
+    assert_close(y, orc.swiglu(g, u, nthreads=8), what="swiglu cfg4a")
+
+
+def test_config4_geglu_full(mk, orc, dev):
+    """BASELINE config 4b: gate/up [4096, 14336] ~N(0,1)."""
+    _case("geglu [4096,14336]")
+    rng = np.random.default_rng(42)
+    g = normal_f16(rng, (4096, 14336))
+    u = normal_f16(rng, (4096, 14336))
+    y = to_host(mk.geglu(to_dev(g, dev), to_dev(u, dev)))
+    assert_close(y, orc.geglu(g, u, nthreads=8), what="geglu cfg4b")
+
+
+def test_geglu_vs_reference_composition(mk, orc, dev):
+    _case("geglu vs gelu+mul composition")
+    rng = np.random.default_rng(43)
+    g = normal_f16(rng, (300_000,), 0, 3)
+    u = normal_f16(rng, (300_000,))
+    y = to_host(mk.geglu(to_dev(g, dev), to_dev(u, dev)))
+    comp = orc.geglu_composed(g, u)
+    d = np.abs(y.view(np.int16).astype(np.int32) - comp.view(np.int16).astype(np.int32))
+    same_sign = np.sign(y) == np.sign(comp)
+    assert (d[same_sign] <= 1).all()
+    # and the GPU's own two-kernel path (gelu then mul) is the composition
+    a = mk.gelu_tanh(to_dev(g, dev))
+    mk.mul_inplace(a, to_dev(u, dev))
+    assert_close(to_host(a), orc.geglu(g, u), what="gelu+mul")
+
+
+@pytest.mark.parametrize("n", [1, 7, 8, 9, 255, 8192, 8193, 1_000_003])
+def test_odd_sizes(mk, orc, dev, n):
+    _case(f"elementwise n={n}")
+    rng = np.random.default_rng(n)
+    g = normal_f16(rng, (n,), 0, 4)
+    u = normal_f16(rng, (n,))
+    gd, ud = to_dev(g, dev), to_dev(u, dev)
+    assert_close(to_host(mk.swiglu(gd, ud)), orc.swiglu(g, u), what="swiglu")
+    assert_close(to_host(mk.geglu(gd, ud)), orc.geglu(g, u), what="geglu")
+    assert_close(to_host(mk.gelu_tanh(gd)), orc.gelu_tanh(g), what="gelu")
+
+
+def test_extreme_inputs(mk, orc, dev):
+    _case("activations at extremes")
+    g = np.array([0, -0.0, 1e-7, -1e-7, 10, -10, 20, -20, 88, -88, 1000, -1000, 65504, -65504,
+                  3.0, -3.0], dtype=np.float16)
+    u = np.ones_like(g)
+    gd, ud = to_dev(g, dev), to_dev(u, dev)
+    assert_close(to_host(mk.swiglu(gd, ud)), orc.swiglu(g, u), what="swiglu")
+    assert_close(to_host(mk.gelu_tanh(gd)), orc.gelu_tanh(g), what="gelu")
+
+
+def test_unaligned(mk, orc, dev):
+    _case("elementwise unaligned")
+    import torch
+    rng = np.random.default_rng(44)
+    n = 5000
+    g = normal_f16(rng, (n,))
+    u = normal_f16(rng, (n,))
+    buf = torch.empty(n + 1, dtype=torch.float16, device=dev)
+    gv = buf[1:]
+    gv.copy_(to_dev(g, dev))
+    assert_close(to_host(mk.swiglu(gv, to_dev(u, dev))), orc.swiglu(g, u), what="swiglu")
+
+
+def test_add_mul_scale_bit_exact(mk, orc, dev):
+    _case("add/mul/scale")
+    rng = np.random.default_rng(45)
+    n = 1_000_001
+    a = normal_f16(rng, (n,), 0, 50)
+    b = normal_f16(rng, (n,), 0, 50)
+    bd = to_dev(b, dev)
+    y = to_dev(a, dev); mk.add_inplace(y, bd)
+    assert_bits_equal(to_host(y), orc.add(a, b), what="add")
+    y = to_dev(a, dev); mk.mul_inplace(y, bd)
+    assert_bits_equal(to_host(y), orc.mul(a, b), what="mul")
+    s = float(np.float32(np.sqrt(3584.0)))
+    y = to_dev(a, dev); mk.scale_inplace(y, s)
+    assert_bits_equal(to_host(y), orc.scale(a, s), what="scale")
+
+
+def test_in_place_activation(mk, orc, dev):
+    _case("swiglu out == gate")
+    rng = np.random.default_rng(46)
+    g = normal_f16(rng, (4096,))
+    u = normal_f16(rng, (4096,))
+    gd = to_dev(g, dev)
+    mk.swiglu(gd, to_dev(u, dev), out=gd)
+    assert_close(to_host(gd), orc.swiglu(g, u), what="in place")

@@ -1,0 +1,135 @@
+"""GPU parity: NeoX RoPE (table-driven, table generation, fused Q+K from
+positions) vs the CPU oracle.
+
+Tables are compared bit for bit: both sides produce half(RN32(cos(angle))) of
+the fp32 angle float(pos) * inv_freq[i] (src/kernels/rope_kernel.cu:74-76).
+Rotated outputs are compared bit for bit as well: each output is one fp32
+rounding of x1*c - x2*s whose products are exact, so any FMA contraction or
+evaluation order gives the same fp32 value.  (The north-star tolerance,
+rtol = atol = 1e-3, is therefore met with zero error.)
+"""
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from helpers import assert_bits_equal, assert_close, normal_f16, to_dev, to_host
+
+pytestmark = pytest.mark.gpu
+GOLD = np.load(Path(__file__).resolve().parent / "golden" / "ref_cases.npz")
+
+
+def _case(msg):
+    print(f"[case] {msg}", flush=True)
+
+
+def config3_positions(rng, total=4096, nseq=8, max_start=28000):
+    """8 sequences of uniform-random lengths summing to `total`, each starting
+    at a uniform offset in [0, max_start)."""
+    cuts = np.sort(rng.choice(np.arange(1, total), nseq - 1, replace=False))
+    lengths = np.diff(np.concatenate([[0], cuts, [total]]))
+    starts = rng.integers(0, max_start, nseq)
+    return np.concatenate([s + np.arange(n) for s, n in zip(starts, lengths)]).astype(np.int64)
+
+
+def test_reference_case(mk, orc, dev):
+    """tests/test_rope/main.cpp:63-80: x [2,16,4,64] seed 101, positions seed
+    2024 in [0, 4096] (replicated over the batch, src/layers/rope.cpp:66-71)."""
+    _case("rope reference [2,16,4,64]")
+    x = GOLD["rope_x"]
+    B, S, H, D = x.shape
+    inv = orc.rope_inv_freq(D, 1e6)
+    assert (inv == GOLD["rope_inv_freq"]).all()
+    pos = np.tile(GOLD["rope_pos"], B)
+    c, s = mk.rope_tables(inv, to_dev(pos, dev))
+    assert_bits_equal(to_host(c)[:S], GOLD["rope_cos"], what="cos table")
+    assert_bits_equal(to_host(s)[:S], GOLD["rope_sin"], what="sin table")
+    y = to_host(mk.rope_neox(to_dev(x, dev), c, s))
+    assert_close(y, GOLD["rope_y"], what="rope vs golden")
+    c_ref, s_ref = orc.rope_tables(inv, pos)
+    assert_bits_equal(y, orc.rope_neox(x, c_ref, s_ref).astype(np.float16), what="rope vs oracle")
+
+
+def test_tables_large_positions(mk, orc, dev):
+    """Every position 0..32767 for head_dim 128: the fp16 tables are exact."""
+    _case("rope tables 32768 x 64")
+    inv = orc.rope_inv_freq(128, 1e6)
+    pos = np.arange(32768, dtype=np.int64)
+    c, s = mk.rope_tables(inv, to_dev(pos, dev))
+    c_ref, s_ref = orc.rope_tables(inv, pos)
+    assert_bits_equal(to_host(c), c_ref, what="cos")
+    assert_bits_equal(to_host(s), s_ref, what="sin")
+
+
+def test_config3_fused_qk(mk, orc, dev):
+    """Q [4096,28,128], K [4096,4,128] in place, theta 1e6."""
+    _case("rope fused qk [4096,28|4,128]")
+    rng = np.random.default_rng(33)
+    T, Hq, Hkv, hd = 4096, 28, 4, 128
+    q = normal_f16(rng, (T, Hq, hd))
+    k = normal_f16(rng, (T, Hkv, hd))
+    pos = config3_positions(rng)
+    inv = orc.rope_inv_freq(hd, 1e6)
+    qd, kd = to_dev(q, dev), to_dev(k, dev)
+    mk.rope_neox_qk(qd, kd, to_dev(pos, dev), inv)
+    c, s = orc.rope_tables(inv, pos)
+    assert_bits_equal(to_host(qd), orc.rope_neox(q, c, s, nthreads=8).astype(np.float16), what="q")
+    assert_bits_equal(to_host(kd), orc.rope_neox(k, c, s, nthreads=8).astype(np.float16), what="k")
+
+
+def test_fused_equals_tables_plus_rotation(mk, dev, orc):
+    _case("rope fused == tables + rope_neox")
+    rng = np.random.default_rng(34)
+    T, Hq, Hkv, hd = 300, 28, 4, 128
+    q = normal_f16(rng, (T, Hq, hd))
+    k = normal_f16(rng, (T, Hkv, hd))
+    pos = rng.integers(0, 32000, T).astype(np.int64)
+    inv = orc.rope_inv_freq(hd, 1e6)
+    qd, kd, pd = to_dev(q, dev), to_dev(k, dev), to_dev(pos, dev)
+    c, s = mk.rope_tables(inv, pd)
+    yq = mk.rope_neox(to_dev(q, dev).view(1, T, Hq, hd), c, s)
+    yk = mk.rope_neox(to_dev(k, dev).view(1, T, Hkv, hd), c, s)
+    mk.rope_neox_qk(qd, kd, pd, inv)
+    assert_bits_equal(to_host(qd), to_host(yq).reshape(T, Hq, hd), what="q")
+    assert_bits_equal(to_host(kd), to_host(yk).reshape(T, Hkv, hd), what="k")
+
+
+@pytest.mark.parametrize("T,Hq,Hkv,hd", [(1, 1, 0, 2), (7, 3, 1, 6), (5, 2, 2, 64), (64, 28, 4, 128),
+                                         (3, 8, 1, 256), (2, 4, 2, 512), (9, 0, 3, 128)])
+def test_shapes(mk, orc, dev, T, Hq, Hkv, hd):
+    _case(f"rope fused T={T} Hq={Hq} Hkv={Hkv} hd={hd}")
+    rng = np.random.default_rng(T * 1000 + hd)
+    q = normal_f16(rng, (T, Hq, hd))
+    k = normal_f16(rng, (T, Hkv, hd))
+    pos = rng.integers(0, 32000, T).astype(np.int64)
+    inv = orc.rope_inv_freq(hd, 1e6)
+    qd, kd = to_dev(q, dev), to_dev(k, dev)
+    mk.rope_neox_qk(qd, kd if Hkv else None, to_dev(pos, dev), inv)
+    c, s = orc.rope_tables(inv, pos)
+    if Hq:
+        assert_bits_equal(to_host(qd), orc.rope_neox(q, c, s).astype(np.float16), what="q")
+    if Hkv:
+        assert_bits_equal(to_host(kd), orc.rope_neox(k, c, s).astype(np.float16), what="k")
+
+
+def test_out_of_place_table_path(mk, orc, dev):
+    _case("rope table path out of place")
+    rng = np.random.default_rng(35)
+    B, S, H, D = 3, 50, 5, 96
+    x = normal_f16(rng, (B, S, H, D))
+    pos = rng.integers(0, 10000, B * S).astype(np.int64)
+    inv = orc.rope_inv_freq(D, 10000.0)
+    c, s = orc.rope_tables(inv, pos)
+    xd = to_dev(x, dev)
+    y = mk.rope_neox(xd, to_dev(c, dev), to_dev(s, dev))
+    assert_bits_equal(to_host(xd), x, what="input untouched")
+    assert_bits_equal(to_host(y), orc.rope_neox(x, c, s).astype(np.float16), what="y")
+
+
+def test_position_zero_is_identity(mk, orc, dev):
+    _case("rope pos 0")
+    rng = np.random.default_rng(36)
+    q = normal_f16(rng, (4, 2, 128))
+    qd = to_dev(q, dev)
+    mk.rope_neox_qk(qd, None, to_dev(np.zeros(4, np.int64), dev), orc.rope_inv_freq(128, 1e6))
+    assert_bits_equal(to_host(qd), q, what="identity")

@@ -1,0 +1,88 @@
+"""GPU parity: row softmax (row-per-workgroup and split-row paths) and the
+token-embedding gather.
+
+Softmax outputs are held within rtol = atol = 1e-3 of the fp32 oracle
+(tests/verify/verify.py:142); the gather is a copy and must be bit-exact.
+"""
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from helpers import assert_bits_equal, assert_close, normal_f16, to_dev, to_host
+
+pytestmark = pytest.mark.gpu
+GOLD = np.load(Path(__file__).resolve().parent / "golden" / "ref_cases.npz")
+
+
+def _case(msg):
+    print(f"[case] {msg}", flush=True)
+
+
+def test_softmax_reference_case(mk, orc, dev):
+    """tests/test_softmax/main.cpp:63-66: [8, 1024], seed 555 x4."""
+    _case("softmax reference [8,1024]")
+    x = GOLD["softmax_x"]
+    y = to_host(mk.softmax(to_dev(x, dev)))
+    assert_close(y, GOLD["softmax_y"], what="vs golden")
+    assert_close(y, orc.softmax(x), what="vs oracle")
+
+
+def test_softmax_lm_head_config(mk, orc, dev):
+    """BASELINE config 5 softmax: logits [64, 152064] ~N(0,4) (split-row path)."""
+    _case("softmax [64,152064]")
+    rng = np.random.default_rng(51)
+    x = normal_f16(rng, (64, 152064), 0, 4)
+    y = to_host(mk.softmax(to_dev(x, dev)))
+    ref = orc.softmax(x, nthreads=8)
+    assert_close(y, ref, what="cfg5")
+    np.testing.assert_allclose(y.astype(np.float64).sum(-1), 1.0, rtol=2e-3)
+
+
+@pytest.mark.parametrize("N,D", [(1, 1), (3, 7), (57344, 512), (600, 10000), (2, 8192),
+                                 (5, 100003), (511, 9000), (1, 300000), (130, 24)])
+def test_softmax_shapes(mk, orc, dev, N, D):
+    _case(f"softmax [{N},{D}]")
+    rng = np.random.default_rng(N * 31 + D)
+    x = normal_f16(rng, (N, D), 0, 4)
+    y = to_host(mk.softmax(to_dev(x, dev)))
+    assert_close(y, orc.softmax(x, nthreads=8), what=f"[{N},{D}]")
+
+
+def test_softmax_in_place_and_neg_inf(mk, orc, dev):
+    _case("softmax in place, -inf entries")
+    rng = np.random.default_rng(52)
+    for N, D in ((64, 152064), (16, 2048)):
+        x = normal_f16(rng, (N, D), 0, 4)
+        x[:, ::3] = -np.inf  # masked logits
+        xd = to_dev(x, dev)
+        mk.softmax(xd, y=xd)
+        assert_close(to_host(xd), orc.softmax(x, nthreads=8), what=f"in place [{N},{D}]")
+
+
+def test_gather_chain_config(mk, orc, dev):
+    """BASELINE config 5 gather: table [152064, 3584] ~N(0, 0.02), 6064 uniform ids."""
+    _case("gather [6064] from [152064,3584]")
+    import torch
+    g = torch.Generator(device=dev).manual_seed(53)
+    table = (torch.randn(152064, 3584, generator=g, device=dev) * 0.02).half()
+    rng = np.random.default_rng(53)
+    ids = rng.integers(0, 152064, 6064).astype(np.int64)
+    out = to_host(mk.embedding_gather(to_dev(ids, dev), table))
+    table_h = to_host(table)
+    assert_bits_equal(out, orc.embedding_gather(ids, table_h, nthreads=8), what="gather")
+
+
+@pytest.mark.parametrize("H", [3584, 3585, 8, 1, 1000])
+def test_gather_shapes_and_bad_ids(mk, orc, dev, H):
+    _case(f"gather H={H}")
+    rng = np.random.default_rng(H)
+    V = 300
+    table = normal_f16(rng, (V, H), 0, 0.02)
+    ids = rng.integers(0, V, (3, 37)).astype(np.int64)
+    ids[0, 0] = -1
+    ids[1, 5] = V
+    ids[2, 7] = V - 1
+    out = to_host(mk.embedding_gather(to_dev(ids, dev), to_dev(table, dev)))
+    assert_bits_equal(out, orc.embedding_gather(ids, table), what=f"H={H}")
+    assert (out[0, 0] == 0).all() and (out[1, 5] == 0).all()

@@ -1,0 +1,299 @@
+"""Pins the CPU oracle (CPU only).
+
+Each oracle function is checked against something it does not share code
+with: the golden vectors of the reference's own test cases (outputs computed
+by torch, tests/golden/make_golden.py), library routines (numpy's IEEE fp16
+cast, torch's rms_norm / softmax / silu / gelu, libm powf), closed forms and
+invariants, and brute force.  A dropped term, wrong sign, swapped half or
+transposed operand in the oracle fails at least one of these.
+"""
+import ctypes
+import ctypes.util
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+import oracle as O
+from helpers import normal_f16
+
+GOLD = np.load(Path(__file__).resolve().parent / "golden" / "ref_cases.npz")
+
+
+def _wide_floats(n, seed):
+    rng = np.random.default_rng(seed)
+    mant = rng.standard_normal(n).astype(np.float64)
+    expo = rng.integers(-30, 18, n)
+    x = (mant * np.power(2.0, expo)).astype(np.float32)
+    specials = np.array([0.0, -0.0, np.inf, -np.inf, np.nan, 65504, 65519.99, 65520, -65520,
+                         6.1035156e-05, 5.9604645e-08, 2.9802322e-08, 2.9802326e-08, 1e-9,
+                         1.0 + 2**-11, 1.0 + 3 * 2**-11, 1.0 + 2**-11 + 2**-20],
+                        dtype=np.float32)
+    return np.concatenate([x, specials])
+
+
+# ---------------------------------------------------------------------------
+# conversions and generators
+# ---------------------------------------------------------------------------
+
+def test_f32_to_f16_is_ieee_rne():
+    x = _wide_floats(400_000, 0)
+    with np.errstate(over="ignore"):
+        ref = x.astype(np.float16)
+    ours = O.f32_to_f16(x)
+    same = (ours.view(np.uint16) == ref.view(np.uint16)) | (np.isnan(ours) & np.isnan(ref))
+    assert same.all()
+
+
+def test_f16_to_f32_exhaustive():
+    h = np.arange(65536, dtype=np.uint16).view(np.float16)
+    ours = O.f16_to_f32(h)
+    ref = h.astype(np.float32)
+    same = (ours.view(np.uint32) == ref.view(np.uint32)) | (np.isnan(ours) & np.isnan(ref))
+    assert same.all()
+
+
+def test_reftest_converter_quirks():
+    """The reference tests' converter equals IEEE RNE except where its two
+    documented quirks apply: in the normal range it truncates instead of
+    rounding up when the kept LSB is even; below 2^-14 it over-shifts."""
+    x = _wide_floats(200_000, 1)
+    x = x[np.isfinite(x) & (np.abs(x) < 65504)]
+    with np.errstate(over="ignore"):
+        rne = x.astype(np.float16)
+    trunc = x.astype(np.float32)  # truncation toward zero to 10 mantissa bits
+    tb = (trunc.view(np.uint32) & np.uint32(0xFFFFE000)).view(np.float32)
+    with np.errstate(over="ignore"):
+        trunc16 = tb.astype(np.float16)
+    ours = O.reftest_f32_to_f16(x)
+    normal = np.abs(x) >= 2.0 ** -14
+    kept_lsb_odd = ((x.view(np.uint32) >> 13) & 1).astype(bool)
+    # odd kept LSB: identical to RNE
+    m = normal & kept_lsb_odd
+    assert (ours[m].view(np.uint16) == rne[m].view(np.uint16)).all()
+    # even kept LSB: truncation
+    m = normal & ~kept_lsb_odd
+    assert (ours[m].view(np.uint16) == trunc16[m].view(np.uint16)).all()
+    # it does differ from RNE somewhere (so the quirk is real)
+    assert (ours[normal].view(np.uint16) != rne[normal].view(np.uint16)).any()
+
+
+def test_xorshift32_known_answer():
+    # Marsaglia xorshift32 (13, 17, 5) from state 1 yields 270369 first.
+    v = O.fill_uniform(1, 1.0, 1)[0]
+    assert v == np.float32((270369 >> 1) / 2.0 ** 31 * 2.0 - 1.0)
+    # seed 0 falls back to the golden-ratio constant (tests/test_helpers.h:50)
+    assert (O.fill_uniform(4, 1.0, 0) == O.fill_uniform(4, 1.0, 0x9E3779B9)).all()
+
+
+def test_xorshift32_brute_force_sequence():
+    s = 42
+    ref = []
+    for _ in range(1000):
+        s ^= (s << 13) & 0xFFFFFFFF
+        s ^= s >> 17
+        s ^= (s << 5) & 0xFFFFFFFF
+        # fp32 arithmetic throughout, as tests/test_helpers.h:53-55 writes it
+        q = np.float32((s >> 1) & 0x7FFFFFFF) / np.float32(2.0 ** 31)
+        ref.append((q * np.float32(2.0) - np.float32(1.0)) * np.float32(3.0))
+    assert (O.fill_uniform(1000, 3.0, 42) == np.array(ref, dtype=np.float32)).all()
+
+
+def test_uniform_int64_range():
+    v = O.fill_uniform_int64(10_000, 2024, 0, 4096)
+    assert v.min() >= 0 and v.max() <= 4096
+    assert len(np.unique(v)) > 3000
+
+
+# ---------------------------------------------------------------------------
+# RMSNorm family
+# ---------------------------------------------------------------------------
+
+def test_rmsnorm_golden():
+    y = O.rmsnorm(GOLD["rms_x"], GOLD["rms_w"], 1e-6)
+    np.testing.assert_allclose(y, GOLD["rms_y"], rtol=1e-5, atol=1e-6)
+    y = O.rmsnorm(GOLD["rms_x"], GOLD["rms_w"], 1e-6, add_one=True)
+    np.testing.assert_allclose(y, GOLD["rms_y_gemma"], rtol=1e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize("shape", [(16, 3584), (7, 128), (3, 1000)])
+def test_rmsnorm_vs_torch_rms_norm(shape):
+    rng = np.random.default_rng(5)
+    x = normal_f16(rng, shape)
+    w = normal_f16(rng, shape[1:], 1.0, 0.1)
+    ref = F.rms_norm(torch.from_numpy(x.astype(np.float32)), (shape[1],),
+                     torch.from_numpy(w.astype(np.float32)), eps=1e-6).numpy()
+    np.testing.assert_allclose(O.rmsnorm(x, w, 1e-6), ref, rtol=2e-6, atol=1e-6)
+
+
+def test_rmsnorm_constant_row_and_gemma_identity():
+    D = 256
+    w = normal_f16(np.random.default_rng(1), (D,))
+    x = np.full((2, D), 3.0, dtype=np.float16)
+    x[1] = -0.5
+    y = O.rmsnorm(x, w, eps=0.0)
+    wf = w.astype(np.float32)
+    np.testing.assert_allclose(y[0], wf, rtol=1e-6)
+    np.testing.assert_allclose(y[1], -wf, rtol=1e-6)
+    # Gemma variant == standard variant with weight 1 + w (fp32)
+    yg = O.rmsnorm(x, w, eps=0.0, add_one=True)
+    np.testing.assert_allclose(yg[0], 1.0 + wf, rtol=1e-6)
+
+
+def test_fused_add_rmsnorm_composition():
+    rng = np.random.default_rng(2)
+    x = normal_f16(rng, (9, 384))
+    r = normal_f16(rng, (9, 384))
+    w = normal_f16(rng, (384,), 1.0, 0.1)
+    new_r, y = O.fused_add_rmsnorm(x, r, w, 1e-6)
+    # fp16 sum: numpy's IEEE cast of the fp32 sum, and the direct rounding of
+    # the exact (float64) sum -- equal because fp32 keeps >= 2*11+2 bits.
+    s32 = (x.astype(np.float32) + r.astype(np.float32)).astype(np.float16)
+    s64 = (x.astype(np.float64) + r.astype(np.float64)).astype(np.float16)
+    assert (new_r.view(np.uint16) == s32.view(np.uint16)).all()
+    assert (new_r.view(np.uint16) == s64.view(np.uint16)).all()
+    np.testing.assert_allclose(y, O.rmsnorm(s32, w, 1e-6), rtol=0, atol=0)
+
+
+# ---------------------------------------------------------------------------
+# RoPE
+# ---------------------------------------------------------------------------
+
+def test_inv_freq_matches_libm_powf_and_closed_form():
+    libm = ctypes.CDLL(ctypes.util.find_library("m"))
+    libm.powf.argtypes = [ctypes.c_float, ctypes.c_float]
+    libm.powf.restype = ctypes.c_float
+    for hd in (64, 128, 256):
+        inv = O.rope_inv_freq(hd, 1e6)
+        ref = np.array([np.float32(1.0) / np.float32(libm.powf(1e6, float(np.float32(2.0 * i)
+                                                                          / np.float32(hd))))
+                        for i in range(hd // 2)], dtype=np.float32)
+        assert (inv == ref).all()
+        exact = 1e6 ** (-2.0 * np.arange(hd // 2) / hd)
+        np.testing.assert_allclose(inv, exact, rtol=1e-6)
+        assert inv[0] == 1.0 and (np.diff(inv) < 0).all()
+
+
+def test_rope_tables_definition():
+    inv = O.rope_inv_freq(128, 1e6)
+    pos = np.array([0, 1, 7, 4095, 27999, 31999], dtype=np.int64)
+    c, s = O.rope_tables(inv, pos)
+    ang = (pos.astype(np.float32)[:, None] * inv[None, :]).astype(np.float32)
+    assert (c == np.cos(ang.astype(np.float64)).astype(np.float32).astype(np.float16)).all()
+    assert (s == np.sin(ang.astype(np.float64)).astype(np.float32).astype(np.float16)).all()
+    assert (c[0] == 1).all() and (s[0] == 0).all()
+
+
+def test_rope_golden():
+    B, S, H, D = GOLD["rope_x"].shape
+    c, s = O.rope_tables(GOLD["rope_inv_freq"], np.tile(GOLD["rope_pos"], B))
+    assert (c[:S] == GOLD["rope_cos"]).all() and (s[:S] == GOLD["rope_sin"]).all()
+    y = O.rope_neox(GOLD["rope_x"], c, s)
+    np.testing.assert_allclose(y, GOLD["rope_y"], rtol=0, atol=0)
+
+
+def test_rope_complex_formulation_and_invariants():
+    """NeoX rotation == complex multiply of (x1 + i x2) by (c + i s)."""
+    rng = np.random.default_rng(3)
+    T, H, hd = 5, 3, 16
+    x = normal_f16(rng, (T, H, hd))
+    pos = np.array([0, 3, 100, 5000, 31000], dtype=np.int64)
+    c, s = O.rope_tables(O.rope_inv_freq(hd, 1e6), pos)
+    y = O.rope_neox(x, c, s)
+    xf = x.astype(np.float64)
+    z = (xf[..., :hd // 2] + 1j * xf[..., hd // 2:]) * (
+        c.astype(np.float64) + 1j * s.astype(np.float64))[:, None, :]
+    np.testing.assert_allclose(y[..., :hd // 2], z.real, rtol=1e-6, atol=1e-6)
+    np.testing.assert_allclose(y[..., hd // 2:], z.imag, rtol=1e-6, atol=1e-6)
+    assert (y[0] == x[0].astype(np.float32)).all()  # position 0 is the identity
+    n_in = xf[1:, :, :hd // 2] ** 2 + xf[1:, :, hd // 2:] ** 2
+    n_out = y[1:, :, :hd // 2].astype(np.float64) ** 2 + y[1:, :, hd // 2:].astype(np.float64) ** 2
+    np.testing.assert_allclose(n_out, n_in, rtol=2e-3, atol=1e-6)  # fp16 cos/sin -> ~1e-3
+
+
+# ---------------------------------------------------------------------------
+# Activations, elementwise, softmax, gather
+# ---------------------------------------------------------------------------
+
+def test_swiglu_gelu_softmax_golden():
+    np.testing.assert_allclose(O.swiglu(GOLD["swiglu_g"], GOLD["swiglu_u"]), GOLD["swiglu_y"],
+                               rtol=1e-6, atol=1e-6)
+    np.testing.assert_allclose(O.gelu_tanh(GOLD["gelu_x"]), GOLD["gelu_y"], rtol=1e-6, atol=1e-6)
+    np.testing.assert_allclose(O.softmax(GOLD["softmax_x"]), GOLD["softmax_y"], rtol=1e-5,
+                               atol=1e-8)
+
+
+def test_activations_vs_torch_wide_range():
+    rng = np.random.default_rng(4)
+    g = normal_f16(rng, (100_000,), 0.0, 6.0)
+    u = normal_f16(rng, (100_000,))
+    gt, ut = torch.from_numpy(g.astype(np.float32)), torch.from_numpy(u.astype(np.float32))
+    np.testing.assert_allclose(O.swiglu(g, u), (F.silu(gt) * ut).numpy(), rtol=1e-6, atol=1e-6)
+    np.testing.assert_allclose(O.gelu_tanh(g), F.gelu(gt, approximate="tanh").numpy(),
+                               rtol=1e-6, atol=1e-6)
+    np.testing.assert_allclose(O.geglu(g, u), (F.gelu(gt, approximate="tanh") * ut).numpy(),
+                               rtol=1e-6, atol=1e-6)
+    assert O.swiglu(np.zeros(3, np.float16), np.ones(3, np.float16)).tolist() == [0, 0, 0]
+    assert O.gelu_tanh(np.zeros(3, np.float16)).tolist() == [0, 0, 0]
+
+
+def test_geglu_composed_within_one_ulp_of_fused():
+    rng = np.random.default_rng(6)
+    g = normal_f16(rng, (50_000,))
+    u = normal_f16(rng, (50_000,))
+    fused = O.geglu(g, u).astype(np.float16)
+    comp = O.geglu_composed(g, u)
+    ulp = np.abs(fused.view(np.int16).astype(np.int32) - comp.view(np.int16).astype(np.int32))
+    same_sign = np.sign(fused) == np.sign(comp)
+    assert (ulp[same_sign] <= 1).all()
+
+
+def test_elementwise_bit_exact_vs_numpy():
+    rng = np.random.default_rng(7)
+    a = normal_f16(rng, (10_000,), 0, 100)
+    b = normal_f16(rng, (10_000,), 0, 100)
+    assert (O.add(a, b) == (a.astype(np.float32) + b.astype(np.float32)).astype(np.float16)).all()
+    with np.errstate(over="ignore"):
+        assert (O.mul(a, b).view(np.uint16) ==
+                (a.astype(np.float32) * b.astype(np.float32)).astype(np.float16).view(np.uint16)).all()
+    s = np.float32(np.sqrt(3584.0))
+    with np.errstate(over="ignore"):
+        assert (O.scale(a, s).view(np.uint16) ==
+                (a.astype(np.float32) * s).astype(np.float16).view(np.uint16)).all()
+
+
+def test_softmax_vs_torch_and_invariants():
+    rng = np.random.default_rng(8)
+    x = normal_f16(rng, (4, 5000), 0, 4)
+    y = O.softmax(x)
+    np.testing.assert_allclose(y, torch.softmax(torch.from_numpy(x.astype(np.float32)), -1).numpy(),
+                               rtol=1e-5, atol=1e-9)
+    np.testing.assert_allclose(y.sum(-1), 1.0, rtol=1e-6)
+    # shift invariance on a grid where the shift is exact in fp16
+    # (multiples of 2^-6 in [-8, 8) plus 8 need at most 10 significant bits)
+    g = (rng.integers(-512, 512, (3, 700)) / 64.0).astype(np.float16)
+    y1 = O.softmax(g)
+    y2 = O.softmax((g.astype(np.float32) + 8.0).astype(np.float16))
+    np.testing.assert_allclose(y2, y1, rtol=1e-6, atol=1e-12)
+
+
+def test_embedding_gather_brute_force():
+    rng = np.random.default_rng(9)
+    table = normal_f16(rng, (1000, 72), 0, 0.02)
+    ids = rng.integers(0, 1000, (3, 11))
+    out = O.embedding_gather(ids, table, nthreads=4)
+    assert (out.view(np.uint16) == table[ids].view(np.uint16)).all()
+    bad = np.array([0, -1, 1000, 999], dtype=np.int64)
+    out = O.embedding_gather(bad, table)
+    assert (out[1] == 0).all() and (out[2] == 0).all()
+    assert (out[3] == table[999]).all()
+
+
+def test_threaded_matches_single_thread():
+    rng = np.random.default_rng(10)
+    x = normal_f16(rng, (64, 512))
+    w = normal_f16(rng, (512,), 1.0, 0.1)
+    assert (O.rmsnorm(x, w, nthreads=1) == O.rmsnorm(x, w, nthreads=8)).all()
+    assert (O.softmax(x, nthreads=1) == O.softmax(x, nthreads=8)).all()
