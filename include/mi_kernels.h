@@ -122,6 +122,17 @@ int mi_scale_inplace_f16(void* y, float scale, int64_t n, void* stream);
  * (src/kernels/softmax_kernel.cuh:12). */
 int mi_softmax_f16(const void* x, void* y, int64_t N, int64_t D, void* stream);
 
+/* Bytes of device workspace mi_softmax_ws_f16 needs for [N, D]: 0 when rows
+ * are processed one workgroup each, else 8 bytes per row chunk (<= 256 KiB). */
+int64_t mi_softmax_workspace_bytes(int64_t N, int64_t D);
+
+/* mi_softmax_f16 with a caller-provided device workspace of at least
+ * mi_softmax_workspace_bytes(N, D) bytes (may be NULL when that is 0), so the
+ * call allocates nothing and can be captured into a HIP graph.  Calls that
+ * share one workspace must not overlap in time. */
+int mi_softmax_ws_f16(const void* x, void* y, int64_t N, int64_t D, void* workspace,
+                      int64_t workspace_bytes, void* stream);
+
 /* out[t, :] = table[ids[t], :] for t < T; table: [vocab, H], ids: int64 [T].
  * Bit-exact copy.  When vocab > 0, an id outside [0, vocab) yields a zero
  * row instead of an out-of-bounds read; vocab <= 0 disables that check

@@ -37,12 +37,12 @@ __global__ __launch_bounds__(256) void gather_kernel(const int64_t* __restrict__
 #pragma unroll
             for (int j = 0; j < kBatch; ++j) {
                 const int64_t c = c0 + j * kWave + lane;
-                v[j] = (valid && c < nv) ? ld8(src + c * 8) : h8(0);
+                v[j] = (valid && c < nv) ? ld8_stream(src + c * 8) : h8(0);
             }
 #pragma unroll
             for (int j = 0; j < kBatch; ++j) {
                 const int64_t c = c0 + j * kWave + lane;
-                if (c < nv) st8(dst + c * 8, v[j]);
+                if (c < nv) st8_stream(dst + c * 8, v[j]);
             }
         } else {
             half_t v[kBatch];

@@ -8,117 +8,164 @@
 // (src/kernels/model_utils_kernel.cu:31-35) and normalises that rounded sum.
 //
 // Design (HBM-bound; 4 bytes/element for the plain norm, 8 for the fused one):
-//   * the whole row stays in registers, so x is read from HBM once (the
-//     reference reads it twice) and, fused, residual is read and written once;
-//   * 16-byte vector accesses (8 halves per lane per access);
-//   * rows of <= 512 elements (Q/K-norm, head_dim 128) are handled by a
-//     G-lane slice of a wave (G = 16 for 128), so a 256-lane workgroup
-//     normalises 16 heads with DPP-only reductions and no LDS or barrier;
-//   * longer rows (hidden 3584) get one workgroup each, ceil(D/8) lanes (448
-//     for 3584), a wave64 DPP/shuffle reduction and one LDS barrier.
+//   * rows stay in registers, so x is read from HBM once (the reference reads
+//     it twice) and, fused, residual is read and written once;
+//   * 16-byte vector accesses (8 halves per lane per access), non-temporal
+//     for the streamed rows, cached for the weight every workgroup re-reads;
+//   * long rows (hidden 3584): a workgroup of ceil(D/8) lanes (448 for 3584)
+//     takes kRowsPerWg rows (1 by default: measured fastest at [8192, 3584];
+//     with more, every row's loads are issued before the first reduction),
+//     one wave64 DPP reduction per row and ONE barrier for all of them;
+//   * short rows (Q/K-norm, head_dim 128): a G-lane slice of a wave owns a
+//     row (G = 16 for 128), each slice takes kRowsPerGroup rows, and the
+//     reduction is DPP-only: no LDS, no barrier;
 //   * shapes the vector path cannot take (D % 8 != 0, unaligned pointers,
 //     D > 65536) use a scalar two-pass kernel.
 #include "mi_device.h"
 #include "mi_host.h"
 
+#ifndef MI_RMS_ROWS_PER_WG
+#define MI_RMS_ROWS_PER_WG 1
+#endif
+#ifndef MI_RMS_ROWS_PER_GROUP
+#define MI_RMS_ROWS_PER_GROUP 1
+#endif
+#ifndef MI_RMS_MAX_THREADS
+#define MI_RMS_MAX_THREADS 512
+#endif
+
 namespace mi {
 namespace {
 
+constexpr int kRowsPerWg = MI_RMS_ROWS_PER_WG;
+constexpr int kRowsPerGroup = MI_RMS_ROWS_PER_GROUP;
+constexpr int kMaxThreads = MI_RMS_MAX_THREADS;
+
 // ---------------------------------------------------------------------------
-// Row-per-workgroup kernel: VPT 16-byte vectors per lane.
+// Long rows: RPW rows per workgroup, VPT 16-byte vectors per lane per row.
 // ---------------------------------------------------------------------------
-template <int VPT, bool FUSED>
+template <int VPT, int RPW, bool FUSED>
 __global__ __launch_bounds__(1024) void rms_row_kernel(const half_t* x, half_t* residual,
                                                        const half_t* __restrict__ w, half_t* y,
-                                                       int64_t D, float eps, float w_bias) {
-    __shared__ float slots[1024 / kWave];
-    const int64_t row = blockIdx.x;
+                                                       int64_t N, int64_t D, float eps,
+                                                       float w_bias) {
+    __shared__ float slots[(1024 / kWave) * RPW];
+    const int64_t row0 = static_cast<int64_t>(blockIdx.x) * RPW;
     const int64_t chunks = D >> 3;
     const int nthr = blockDim.x;
-    const half_t* xr = x + row * D;
-    half_t* rr = FUSED ? residual + row * D : nullptr;
-    half_t* yr = y + row * D;
 
-    h8 v[VPT];
-    h8 wv[VPT];
-    float ss = 0.0f;
+    h8 v[RPW][VPT];
+    h8 r[FUSED ? RPW : 1][VPT];
+    // 1. issue every load of every row
 #pragma unroll
-    for (int j = 0; j < VPT; ++j) {
-        const int64_t c = threadIdx.x + static_cast<int64_t>(j) * nthr;
-        if (c < chunks) {
-            h8 a = ld8(xr + c * 8);
-            if constexpr (FUSED) {
-                const h8 r = ld8(rr + c * 8);
+    for (int q = 0; q < RPW; ++q) {
+        const int64_t row = row0 + q;
 #pragma unroll
-                for (int k = 0; k < 8; ++k) a[k] = to_half((float)r[k] + (float)a[k]);
-                st8(rr + c * 8, a);
-            }
-            v[j] = a;
-            wv[j] = ld8(w + c * 8);
-#pragma unroll
-            for (int k = 0; k < 8; ++k) {
-                const float f = (float)a[k];
-                ss = fmaf(f, f, ss);
-            }
-        } else {
-            v[j] = h8(0);
-            wv[j] = h8(0);
+        for (int j = 0; j < VPT; ++j) {
+            const int64_t c = threadIdx.x + static_cast<int64_t>(j) * nthr;
+            const bool ok = row < N && c < chunks;
+            v[q][j] = ok ? ld8_stream(x + row * D + c * 8) : h8(0);
+            if constexpr (FUSED) r[q][j] = ok ? ld8_stream(residual + row * D + c * 8) : h8(0);
         }
     }
-    ss = block_sum(ss, slots);
-    const float rrms = rsqrtf(ss / static_cast<float>(D) + eps);
+    h8 wv[VPT];
 #pragma unroll
     for (int j = 0; j < VPT; ++j) {
         const int64_t c = threadIdx.x + static_cast<int64_t>(j) * nthr;
-        if (c < chunks) {
-            h8 o;
+        wv[j] = c < chunks ? ld8(w + c * 8) : h8(0);
+    }
+    // 2. residual sums (stored back) and sums of squares
+    float ss[RPW];
 #pragma unroll
-            for (int k = 0; k < 8; ++k)
-                o[k] = to_half((float)v[j][k] * rrms * ((float)wv[j][k] + w_bias));
-            st8(yr + c * 8, o);
+    for (int q = 0; q < RPW; ++q) {
+        const int64_t row = row0 + q;
+        ss[q] = 0.0f;
+#pragma unroll
+        for (int j = 0; j < VPT; ++j) {
+            if constexpr (FUSED) {
+                const int64_t c = threadIdx.x + static_cast<int64_t>(j) * nthr;
+#pragma unroll
+                for (int k = 0; k < 8; ++k) v[q][j][k] = to_half((float)r[q][j][k] + (float)v[q][j][k]);
+                if (row < N && c < chunks) st8_stream(residual + row * D + c * 8, v[q][j]);
+            }
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const float f = (float)v[q][j][k];
+                ss[q] = fmaf(f, f, ss[q]);
+            }
+        }
+    }
+    // 3. one barrier for all rows
+    block_sum_n<RPW>(ss, slots);
+    // 4. normalise and write
+#pragma unroll
+    for (int q = 0; q < RPW; ++q) {
+        const int64_t row = row0 + q;
+        if (row >= N) break;
+        const float rrms = rsqrtf(ss[q] / static_cast<float>(D) + eps);
+#pragma unroll
+        for (int j = 0; j < VPT; ++j) {
+            const int64_t c = threadIdx.x + static_cast<int64_t>(j) * nthr;
+            if (c < chunks) {
+                h8 o;
+#pragma unroll
+                for (int k = 0; k < 8; ++k)
+                    o[k] = to_half((float)v[q][j][k] * rrms * ((float)wv[j][k] + w_bias));
+                st8_stream(y + row * D + c * 8, o);
+            }
         }
     }
 }
 
 // ---------------------------------------------------------------------------
-// Short rows: G lanes per row, one 16-byte vector per lane (D <= 8*G).
+// Short rows: a G-lane group owns a row (one 16-byte vector per lane,
+// D <= 8*G); the 256/G groups of a workgroup cover a contiguous block of rows
+// and each group takes RPG such blocks, all loads issued first.
 // ---------------------------------------------------------------------------
-template <int G, bool FUSED>
+template <int G, int RPG, bool FUSED>
 __global__ __launch_bounds__(256) void rms_small_kernel(const half_t* x, half_t* residual,
                                                         const half_t* __restrict__ w, half_t* y,
                                                         int64_t N, int D, float eps, float w_bias) {
+    constexpr int kGroups = 256 / G;
     const int lane = threadIdx.x & (G - 1);
-    const int64_t row = static_cast<int64_t>(blockIdx.x) * (blockDim.x / G) + threadIdx.x / G;
+    const int64_t base = static_cast<int64_t>(blockIdx.x) * (kGroups * RPG) + threadIdx.x / G;
     const int chunks = D >> 3;
-    const bool active = row < N && lane < chunks;
-    const int64_t off = row * D + lane * 8;
+    const bool lane_ok = lane < chunks;
 
-    h8 a = h8(0);
-    h8 wv = h8(0);
-    float ss = 0.0f;
-    if (active) {
-        a = ld8(x + off);
-        if constexpr (FUSED) {
-            const h8 r = ld8(residual + off);
+    h8 a[RPG];
+    h8 r[FUSED ? RPG : 1];
 #pragma unroll
-            for (int k = 0; k < 8; ++k) a[k] = to_half((float)r[k] + (float)a[k]);
-            st8(residual + off, a);
+    for (int q = 0; q < RPG; ++q) {
+        const int64_t row = base + q * kGroups;
+        const bool ok = lane_ok && row < N;
+        a[q] = ok ? ld8_stream(x + row * D + lane * 8) : h8(0);
+        if constexpr (FUSED) r[q] = ok ? ld8_stream(residual + row * D + lane * 8) : h8(0);
+    }
+    const h8 wv = lane_ok ? ld8(w + lane * 8) : h8(0);
+#pragma unroll
+    for (int q = 0; q < RPG; ++q) {
+        const int64_t row = base + q * kGroups;
+        const bool ok = lane_ok && row < N;
+        if constexpr (FUSED) {
+#pragma unroll
+            for (int k = 0; k < 8; ++k) a[q][k] = to_half((float)r[q][k] + (float)a[q][k]);
+            if (ok) st8_stream(residual + row * D + lane * 8, a[q]);
         }
-        wv = ld8(w + lane * 8);
+        float ss = 0.0f;
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
-            const float f = (float)a[k];
+            const float f = (float)a[q][k];
             ss = fmaf(f, f, ss);
         }
-    }
-    // every lane takes part in the DPP reduction (no lane has exited)
-    ss = group_sum<G>(ss);
-    const float rrms = rsqrtf(ss / static_cast<float>(D) + eps);
-    if (active) {
-        h8 o;
+        // every lane takes part in the DPP reduction (no lane has exited)
+        ss = group_sum<G>(ss);
+        const float rrms = rsqrtf(ss / static_cast<float>(D) + eps);
+        if (ok) {
+            h8 o;
 #pragma unroll
-        for (int k = 0; k < 8; ++k) o[k] = to_half((float)a[k] * rrms * ((float)wv[k] + w_bias));
-        st8(y + off, o);
+            for (int k = 0; k < 8; ++k) o[k] = to_half((float)a[q][k] * rrms * ((float)wv[k] + w_bias));
+            st8_stream(y + row * D + lane * 8, o);
+        }
     }
 }
 
@@ -159,13 +206,15 @@ int launch_small(const half_t* x, half_t* r, const half_t* w, half_t* y, int64_t
     const int chunks = D >> 3;
     int G = 1;
     while (G < chunks) G <<= 1;
-    const int rows_per_wg = 256 / G;
+    const int64_t rows_per_wg = (256 / G) * kRowsPerGroup;
     const int64_t grid = ceil_div(N, rows_per_wg);
     if (grid > kMaxGridX) return MI_ERR_UNSUPPORTED;
     const dim3 g(static_cast<unsigned>(grid)), b(256);
     switch (G) {
-#define MI_SMALL_CASE(GG) \
-    case GG: rms_small_kernel<GG, FUSED><<<g, b, 0, s>>>(x, r, w, y, N, D, eps, bias); break;
+#define MI_SMALL_CASE(GG)                                                                       \
+    case GG:                                                                                    \
+        rms_small_kernel<GG, kRowsPerGroup, FUSED><<<g, b, 0, s>>>(x, r, w, y, N, D, eps, bias); \
+        break;
         MI_SMALL_CASE(1)
         MI_SMALL_CASE(2)
         MI_SMALL_CASE(4)
@@ -179,16 +228,18 @@ int launch_small(const half_t* x, half_t* r, const half_t* w, half_t* y, int64_t
     return launch_status();
 }
 
-template <bool FUSED>
-int launch_row(const half_t* x, half_t* r, const half_t* w, half_t* y, int64_t N, int64_t D,
-               float eps, float bias, hipStream_t s) {
+template <int RPW, bool FUSED>
+int launch_row_rpw(const half_t* x, half_t* r, const half_t* w, half_t* y, int64_t N, int64_t D,
+                   float eps, float bias, hipStream_t s) {
     const int64_t chunks = D >> 3;
-    const int vpt = static_cast<int>(ceil_div(chunks, 512));
+    const int vpt = static_cast<int>(ceil_div(chunks, kMaxThreads));
     const int threads = static_cast<int>(ceil_div(ceil_div(chunks, vpt), kWave) * kWave);
-    const dim3 g(static_cast<unsigned>(N)), b(threads);
+    const int64_t grid = ceil_div(N, RPW);
+    if (grid > kMaxGridX) return MI_ERR_UNSUPPORTED;
+    const dim3 g(static_cast<unsigned>(grid)), b(threads);
     switch (vpt) {
 #define MI_ROW_CASE(V) \
-    case V: rms_row_kernel<V, FUSED><<<g, b, 0, s>>>(x, r, w, y, D, eps, bias); break;
+    case V: rms_row_kernel<V, RPW, FUSED><<<g, b, 0, s>>>(x, r, w, y, N, D, eps, bias); break;
         MI_ROW_CASE(1)
         MI_ROW_CASE(2)
         MI_ROW_CASE(3)
@@ -197,18 +248,21 @@ int launch_row(const half_t* x, half_t* r, const half_t* w, half_t* y, int64_t N
         MI_ROW_CASE(6)
         MI_ROW_CASE(7)
         MI_ROW_CASE(8)
-        MI_ROW_CASE(9)
-        MI_ROW_CASE(10)
-        MI_ROW_CASE(11)
-        MI_ROW_CASE(12)
-        MI_ROW_CASE(13)
-        MI_ROW_CASE(14)
-        MI_ROW_CASE(15)
-        MI_ROW_CASE(16)
 #undef MI_ROW_CASE
         default: return MI_ERR_UNSUPPORTED;
     }
     return launch_status();
+}
+
+template <bool FUSED>
+int launch_row(const half_t* x, half_t* r, const half_t* w, half_t* y, int64_t N, int64_t D,
+               float eps, float bias, hipStream_t s) {
+    // Several rows per workgroup only pay off with enough rows to fill the
+    // GPU; large-VPT rows already keep many bytes in flight per lane.
+    const int vpt = static_cast<int>(ceil_div(D >> 3, kMaxThreads));
+    if (kRowsPerWg > 1 && vpt <= 2 && N >= 2048)
+        return launch_row_rpw<kRowsPerWg, FUSED>(x, r, w, y, N, D, eps, bias, s);
+    return launch_row_rpw<1, FUSED>(x, r, w, y, N, D, eps, bias, s);
 }
 
 template <bool FUSED>
@@ -233,7 +287,8 @@ int rmsnorm_dispatch(const void* xv, void* rv, const void* wv, void* yv, int64_t
     const bool vec = (D % 8 == 0) && aligned16(x) && aligned16(w) && aligned16(y) &&
                      (!FUSED || aligned16(r));
     if (vec && D <= 512) return launch_small<FUSED>(x, r, w, y, N, static_cast<int>(D), eps, bias, s);
-    if (vec && D <= 16 * 512 * 8) return launch_row<FUSED>(x, r, w, y, N, D, eps, bias, s);
+    if (vec && D <= int64_t{8} * kMaxThreads * 8)
+        return launch_row<FUSED>(x, r, w, y, N, D, eps, bias, s);
     rms_scalar_kernel<FUSED><<<dim3(static_cast<unsigned>(N)), dim3(256), 0, s>>>(x, r, w, y, D, eps,
                                                                                   bias);
     return launch_status();

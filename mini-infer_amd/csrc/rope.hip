@@ -8,7 +8,9 @@
 //   c, s   = half(cos(angle)), half(sin(angle))  (fp16-rounded table values)
 //   y[i]   = x[i] * c - x[i + h] * s,  y[i + h] = x[i + h] * c + x[i] * s
 // Both products in a rotation are exact in fp32 (11-bit x 11-bit
-// significands), so the output is the single rounding of the fp32 result.
+// significands), so the fp32 result is one rounding of the exact value, which
+// is then rounded to fp16 -- the same two roundings the reference performs, so
+// outputs match it bit for bit given equal tables.
 //
 // cos/sin: the fp32 sincosf result (a few ulp) is rounded to fp16; when the
 // value lies within 2^-20 (relative) of an fp16 rounding boundary the angle is
@@ -17,11 +19,12 @@
 // fp32 sincos implementation.
 //
 // Design (HBM-bound: 8 bytes/element in place, + 8 bytes/token of positions):
-//   one 256-lane workgroup per token; lanes 0..hd/2-1 build the token's cos/sin
-//   row in LDS once (instead of once per head), while every lane has already
-//   issued its first pair of 16-byte loads (x[i..i+7], x[h+i..h+i+7]); after a
-//   single barrier each lane rotates one (head, 8-element) unit.  For Qwen2.5
-//   (28 + 4 heads x 64 pairs) that is exactly 256 units = one per lane.
+//   a 256-lane workgroup takes kTokensPerWg tokens.  Every lane first issues
+//   the 16-byte loads of its (token, head, 8-element) units -- x[i..i+7] and
+//   x[h+i..h+i+7] -- then the workgroup builds each token's cos/sin row in LDS
+//   once (instead of once per head), and after a single barrier each lane
+//   rotates its units.  For Qwen2.5 (28 + 4 heads x 8 units) a token is 256
+//   units, so with 2 tokens per workgroup each lane has two units in flight.
 #include <math.h>
 
 #include "mi_device.h"
@@ -80,26 +83,38 @@ __device__ __forceinline__ void set_elem(typename HVec<VEC>::T& v, int k, float 
     if constexpr (VEC == 1) v = to_half(f); else v[k] = to_half(f);
 }
 
-// One workgroup per token.  Sources: q_in/k_in; destinations q_out/k_out (may
-// equal the sources).  FROM_POS: cos/sin from positions + inv_freq, else from
-// fp16 tables [T, half].
-template <int VEC, bool FROM_POS>
+#ifndef MI_ROPE_TOKENS_PER_WG
+#define MI_ROPE_TOKENS_PER_WG 4
+#endif
+constexpr int kTokensPerWg = MI_ROPE_TOKENS_PER_WG;
+constexpr int kPrefetch = 4;  // units per lane whose loads are issued up front
+
+// TPW tokens per 256-lane workgroup.  Sources q_in/k_in, destinations
+// q_out/k_out (may equal the sources).  FROM_POS: cos/sin from positions +
+// inv_freq, else from fp16 tables [T, half].  A unit is one (token, head,
+// VEC-element slice) pair: x[i..i+VEC) and x[h+i..h+i+VEC).
+template <int VEC, bool FROM_POS, int TPW>
 __global__ __launch_bounds__(256) void rope_kernel(const half_t* q_in, half_t* q_out, int Hq,
                                                    const half_t* k_in, half_t* k_out, int Hkv,
                                                    const int64_t* __restrict__ positions,
                                                    const half_t* __restrict__ cos_t,
-                                                   const half_t* __restrict__ sin_t, int hd,
-                                                   InvFreq inv) {
+                                                   const half_t* __restrict__ sin_t, int64_t T,
+                                                   int hd, InvFreq inv) {
     typedef HVec<VEC> V;
-    __shared__ float cs[2 * kMaxHalf];
-    const int64_t tok = blockIdx.x;
+    __shared__ float cs[TPW][2 * kMaxHalf];
+    const int64_t tok0 = static_cast<int64_t>(blockIdx.x) * TPW;
+    const int ntok = static_cast<int>(T - tok0 < TPW ? T - tok0 : TPW);
     const int half = hd >> 1;
-    const int cph = half / VEC;  // vector units per half head
-    const int units = (Hq + Hkv) * cph;
+    const int cph = half / VEC;                // units per head
+    const int upt = (Hq + Hkv) * cph;          // units per token
+    const int units = ntok * upt;
 
     auto locate = [&](int u, const half_t*& src, half_t*& dst) {
-        const int h = u / cph;
-        const int c = u - h * cph;
+        const int t = u / upt;
+        const int rem = u - t * upt;
+        const int h = rem / cph;
+        const int c = rem - h * cph;
+        const int64_t tok = tok0 + t;
         if (h < Hq) {
             const int64_t base = (tok * Hq + h) * static_cast<int64_t>(hd) + c * VEC;
             src = q_in + base;
@@ -109,22 +124,34 @@ __global__ __launch_bounds__(256) void rope_kernel(const half_t* q_in, half_t* q
             src = k_in + base;
             dst = k_out + base;
         }
-        return c;
+        return t * (2 * kMaxHalf) + c * VEC;  // offset of this unit's cos in cs
     };
 
-    // Issue this lane's first loads before the table work so HBM latency
-    // overlaps the sincos evaluation.
-    int u = threadIdx.x;
-    typename V::T x1{}, x2{};
-    if (u < units) {
-        const half_t* src;
-        half_t* dst;
-        locate(u, src, dst);
-        x1 = V::load(src);
-        x2 = V::load(src + half);
+    // 1. issue up to kPrefetch units' loads per lane before the table work,
+    //    so HBM latency overlaps the sincos evaluation
+    typename V::T x1[kPrefetch], x2[kPrefetch];
+#pragma unroll
+    for (int p = 0; p < kPrefetch; ++p) {
+        const int u = threadIdx.x + p * 256;
+        if (u < units) {
+            const half_t* src;
+            half_t* dst;
+            locate(u, src, dst);
+            if constexpr (VEC == 8) {
+                x1[p] = ld8_stream(src);
+                x2[p] = ld8_stream(src + half);
+            } else {
+                x1[p] = V::load(src);
+                x2[p] = V::load(src + half);
+            }
+        }
     }
 
-    for (int i = threadIdx.x; i < half; i += blockDim.x) {
+    // 2. each token's cos/sin row, once per token (not once per head)
+    for (int idx = threadIdx.x; idx < ntok * half; idx += 256) {
+        const int t = idx / half;
+        const int i = idx - t * half;
+        const int64_t tok = tok0 + t;
         half_t hc, hs;
         if constexpr (FROM_POS) {
             const float ang = static_cast<float>(positions[tok]) * inv.v[i];
@@ -133,30 +160,44 @@ __global__ __launch_bounds__(256) void rope_kernel(const half_t* q_in, half_t* q
             hc = cos_t[tok * half + i];
             hs = sin_t[tok * half + i];
         }
-        cs[i] = (float)hc;
-        cs[kMaxHalf + i] = (float)hs;
+        cs[t][i] = (float)hc;
+        cs[t][kMaxHalf + i] = (float)hs;
     }
     __syncthreads();
 
-    for (; u < units; u += blockDim.x) {
+    // 3. rotate: y1 = x1 c - x2 s, y2 = x2 c + x1 s
+    const float* csf = &cs[0][0];
+    auto rotate = [&](int u, const typename V::T& a1, const typename V::T& a2) {
         const half_t* src;
         half_t* dst;
-        const int c = locate(u, src, dst);
-        if (u != static_cast<int>(threadIdx.x)) {
-            x1 = V::load(src);
-            x2 = V::load(src + half);
-        }
+        const int off = locate(u, src, dst);
         typename V::T y1, y2;
 #pragma unroll
         for (int k = 0; k < VEC; ++k) {
-            const float cv = cs[c * VEC + k];
-            const float sv = cs[kMaxHalf + c * VEC + k];
-            const float a = elem<VEC>(x1, k), b = elem<VEC>(x2, k);
-            set_elem<VEC>(y1, k, a * cv - b * sv);
-            set_elem<VEC>(y2, k, b * cv + a * sv);
+            const float cv = csf[off + k];
+            const float sv = csf[off + kMaxHalf + k];
+            const float a = elem<VEC>(a1, k), b = elem<VEC>(a2, k);
+            set_elem<VEC>(y1, k, fp32_rounded(a * cv - b * sv));
+            set_elem<VEC>(y2, k, fp32_rounded(b * cv + a * sv));
         }
-        V::store(dst, y1);
-        V::store(dst + half, y2);
+        if constexpr (VEC == 8) {
+            st8_stream(dst, y1);
+            st8_stream(dst + half, y2);
+        } else {
+            V::store(dst, y1);
+            V::store(dst + half, y2);
+        }
+    };
+#pragma unroll
+    for (int p = 0; p < kPrefetch; ++p) {
+        const int u = threadIdx.x + p * 256;
+        if (u < units) rotate(u, x1[p], x2[p]);
+    }
+    for (int u = threadIdx.x + kPrefetch * 256; u < units; u += 256) {
+        const half_t* src;
+        half_t* dst;
+        locate(u, src, dst);
+        rotate(u, V::load(src), V::load(src + half));
     }
 }
 
@@ -184,26 +225,28 @@ bool load_inv_freq(const float* host, int64_t half, InvFreq& out) {
 int launch_rope(const half_t* q_in, half_t* q_out, int64_t Hq, const half_t* k_in, half_t* k_out,
                 int64_t Hkv, const int64_t* positions, const half_t* cos_t, const half_t* sin_t,
                 int64_t T, int64_t hd, const InvFreq& inv, hipStream_t s) {
-    if (T > kMaxGridX) return MI_ERR_UNSUPPORTED;
+    const int64_t grid = ceil_div(T, kTokensPerWg);
+    if (grid > kMaxGridX) return MI_ERR_UNSUPPORTED;
     const int64_t half = hd / 2;
     bool vec = (half % 8 == 0) && aligned16(q_in) && aligned16(q_out);
     if (Hkv > 0) vec = vec && aligned16(k_in) && aligned16(k_out);
-    const dim3 g(static_cast<unsigned>(T)), b(256);
+    const dim3 g(static_cast<unsigned>(grid)), b(256);
     const int hq = static_cast<int>(Hq), hk = static_cast<int>(Hkv), d = static_cast<int>(hd);
+    constexpr int P = kTokensPerWg;
     if (positions) {
         if (vec)
-            rope_kernel<8, true><<<g, b, 0, s>>>(q_in, q_out, hq, k_in, k_out, hk, positions,
-                                                 nullptr, nullptr, d, inv);
+            rope_kernel<8, true, P><<<g, b, 0, s>>>(q_in, q_out, hq, k_in, k_out, hk, positions,
+                                                    nullptr, nullptr, T, d, inv);
         else
-            rope_kernel<1, true><<<g, b, 0, s>>>(q_in, q_out, hq, k_in, k_out, hk, positions,
-                                                 nullptr, nullptr, d, inv);
+            rope_kernel<1, true, P><<<g, b, 0, s>>>(q_in, q_out, hq, k_in, k_out, hk, positions,
+                                                    nullptr, nullptr, T, d, inv);
     } else {
         if (vec)
-            rope_kernel<8, false><<<g, b, 0, s>>>(q_in, q_out, hq, k_in, k_out, hk, nullptr,
-                                                  cos_t, sin_t, d, inv);
+            rope_kernel<8, false, P><<<g, b, 0, s>>>(q_in, q_out, hq, k_in, k_out, hk, nullptr,
+                                                     cos_t, sin_t, T, d, inv);
         else
-            rope_kernel<1, false><<<g, b, 0, s>>>(q_in, q_out, hq, k_in, k_out, hk, nullptr,
-                                                  cos_t, sin_t, d, inv);
+            rope_kernel<1, false, P><<<g, b, 0, s>>>(q_in, q_out, hq, k_in, k_out, hk, nullptr,
+                                                     cos_t, sin_t, T, d, inv);
     }
     return launch_status();
 }

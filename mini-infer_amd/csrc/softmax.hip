@@ -26,46 +26,83 @@ namespace {
 constexpr int kSplitMaxRows = 512;  // below this many rows, split each row
 constexpr int kMaxSplits = 64;      // chunk pairs of a row fit one wave
 
-// Accumulate elements [begin, end) of a row into this lane's (m, s).
+// Fold one loaded value group into the lane's online (m, s).
+template <int VEC>
+__device__ __forceinline__ void fold(const float (&v)[VEC], float& m, float& s) {
+    float vm = v[0];
+#pragma unroll
+    for (int k = 1; k < VEC; ++k) vm = fmaxf(vm, v[k]);
+    const float mn = fmaxf(m, vm);
+    if (mn == -INFINITY) return;  // nothing but -inf so far
+    float acc = s * fast_exp(m - mn);
+#pragma unroll
+    for (int k = 0; k < VEC; ++k) acc += fast_exp(v[k] - mn);
+    s = acc;
+    m = mn;
+}
+
+// Accumulate elements [begin, end) of a row into this lane's (m, s).  Loads
+// are issued kStatUnroll groups at a time, before the math that consumes them.
+constexpr int kStatUnroll = 4;
 template <int VEC>
 __device__ __forceinline__ void lane_stats(const half_t* xr, int64_t begin, int64_t end, float& m,
                                            float& s) {
-    for (int64_t i = begin + static_cast<int64_t>(threadIdx.x) * VEC; i < end;
-         i += static_cast<int64_t>(blockDim.x) * VEC) {
-        float v[VEC];
-        if constexpr (VEC == 8) {
-            const h8 h = ld8(xr + i);
+    const int64_t step = static_cast<int64_t>(blockDim.x) * VEC;
+    for (int64_t i0 = begin + static_cast<int64_t>(threadIdx.x) * VEC; i0 < end;
+         i0 += step * kStatUnroll) {
+        float v[kStatUnroll][VEC];
 #pragma unroll
-            for (int k = 0; k < 8; ++k) v[k] = (float)h[k];
-        } else {
-            v[0] = (float)xr[i];
+        for (int j = 0; j < kStatUnroll; ++j) {
+            const int64_t i = i0 + j * step;
+            if (i < end) {
+                if constexpr (VEC == 8) {
+                    const h8 h = ld8(xr + i);
+#pragma unroll
+                    for (int k = 0; k < 8; ++k) v[j][k] = (float)h[k];
+                } else {
+                    v[j][0] = (float)xr[i];
+                }
+            } else {
+#pragma unroll
+                for (int k = 0; k < VEC; ++k) v[j][k] = -INFINITY;
+            }
         }
-        float vm = v[0];
 #pragma unroll
-        for (int k = 1; k < VEC; ++k) vm = fmaxf(vm, v[k]);
-        const float mn = fmaxf(m, vm);
-        if (mn == -INFINITY) continue;
-        float acc = s * fast_exp(m - mn);
-#pragma unroll
-        for (int k = 0; k < VEC; ++k) acc += fast_exp(v[k] - mn);
-        s = acc;
-        m = mn;
+        for (int j = 0; j < kStatUnroll; ++j) fold<VEC>(v[j], m, s);
     }
 }
 
+// y = exp(x - m) * inv over [begin, end): the last use of x and the only
+// write of y, both streamed.
 template <int VEC>
 __device__ __forceinline__ void write_range(const half_t* xr, half_t* yr, int64_t begin,
                                             int64_t end, float m, float inv) {
-    for (int64_t i = begin + static_cast<int64_t>(threadIdx.x) * VEC; i < end;
-         i += static_cast<int64_t>(blockDim.x) * VEC) {
+    const int64_t step = static_cast<int64_t>(blockDim.x) * VEC;
+    for (int64_t i0 = begin + static_cast<int64_t>(threadIdx.x) * VEC; i0 < end;
+         i0 += step * kStatUnroll) {
         if constexpr (VEC == 8) {
-            const h8 h = ld8(xr + i);
-            h8 o;
+            h8 h[kStatUnroll];
 #pragma unroll
-            for (int k = 0; k < 8; ++k) o[k] = to_half(fast_exp((float)h[k] - m) * inv);
-            st8_stream(yr + i, o);
+            for (int j = 0; j < kStatUnroll; ++j) {
+                const int64_t i = i0 + j * step;
+                if (i < end) h[j] = ld8_stream(xr + i);
+            }
+#pragma unroll
+            for (int j = 0; j < kStatUnroll; ++j) {
+                const int64_t i = i0 + j * step;
+                if (i < end) {
+                    h8 o;
+#pragma unroll
+                    for (int k = 0; k < 8; ++k) o[k] = to_half(fast_exp((float)h[j][k] - m) * inv);
+                    st8_stream(yr + i, o);
+                }
+            }
         } else {
-            yr[i] = to_half(fast_exp((float)xr[i] - m) * inv);
+#pragma unroll
+            for (int j = 0; j < kStatUnroll; ++j) {
+                const int64_t i = i0 + j * step;
+                if (i < end) yr[i] = to_half(fast_exp((float)xr[i] - m) * inv);
+            }
         }
     }
 }
@@ -130,52 +167,92 @@ __global__ __launch_bounds__(256) void softmax_finish_kernel(const half_t* x, ha
     write_range<VEC>(x + row * D, y + row * D, b, e, M, 1.0f / S);
 }
 
-template <int VEC>
-int launch_softmax(const half_t* x, half_t* y, int64_t N, int64_t D, hipStream_t s) {
-    if (N >= kSplitMaxRows || D < 8192) {
-        const int64_t want = ceil_div(D, VEC);
-        int threads = static_cast<int>(ceil_div(want < 1024 ? want : 1024, kWave) * kWave);
-        softmax_row_kernel<VEC><<<dim3(static_cast<unsigned>(N)), dim3(threads), 0, s>>>(x, y, D);
-        return launch_status();
-    }
-    // Split rows: aim for >= 2048 workgroups, chunks of >= 2048 elements,
-    // chunk a multiple of 8 so vector accesses stay aligned.
+// Split plan for few long rows: aim for >= 2048 workgroups and chunks of
+// >= 2048 elements, chunk a multiple of 8 so vector accesses stay aligned.
+// Returns the number of chunks per row (1 = one workgroup per row, no
+// workspace).
+int64_t split_plan(int64_t N, int64_t D, int64_t& chunk) {
+    chunk = D;
+    if (N >= kSplitMaxRows || D < 8192) return 1;
     int64_t splits = ceil_div(2048, N);
     if (splits > kMaxSplits) splits = kMaxSplits;
     const int64_t max_by_len = D / 2048 > 1 ? D / 2048 : 1;
     if (splits > max_by_len) splits = max_by_len;
-    const int64_t chunk = ceil_div(ceil_div(D, splits), 8) * 8;
-    splits = ceil_div(D, chunk);
-    // The (max, sum) pairs live in a stream-ordered allocation from the
-    // device's default pool: concurrent calls on other streams get their own,
-    // and after the first call the pool hands back cached memory.
-    void* ws = nullptr;
-    hipError_t e = hipMallocAsync(&ws, static_cast<size_t>(N * splits) * 2 * sizeof(float), s);
-    if (e != hipSuccess) return static_cast<int>(e);
+    chunk = ceil_div(ceil_div(D, splits), 8) * 8;
+    return ceil_div(D, chunk);
+}
+
+int64_t workspace_bytes(int64_t N, int64_t D) {
+    int64_t chunk;
+    const int64_t splits = split_plan(N, D, chunk);
+    return splits > 1 ? N * splits * 2 * static_cast<int64_t>(sizeof(float)) : 0;
+}
+
+template <int VEC>
+void launch_softmax(const half_t* x, half_t* y, int64_t N, int64_t D, float* ws, hipStream_t s) {
+    int64_t chunk;
+    const int64_t splits = split_plan(N, D, chunk);
+    if (splits == 1) {
+        const int64_t want = ceil_div(D, VEC);
+        int threads = static_cast<int>(ceil_div(want < 1024 ? want : 1024, kWave) * kWave);
+        softmax_row_kernel<VEC><<<dim3(static_cast<unsigned>(N)), dim3(threads), 0, s>>>(x, y, D);
+        return;
+    }
     const dim3 g(static_cast<unsigned>(splits), static_cast<unsigned>(N));
-    softmax_partial_kernel<VEC><<<g, dim3(256), 0, s>>>(x, static_cast<float*>(ws), D, chunk);
-    softmax_finish_kernel<VEC><<<g, dim3(256), 0, s>>>(x, y, static_cast<const float*>(ws), D,
-                                                       chunk);
-    const int st = launch_status();
-    e = hipFreeAsync(ws, s);
-    if (st != MI_OK) return st;
-    return e == hipSuccess ? MI_OK : static_cast<int>(e);
+    softmax_partial_kernel<VEC><<<g, dim3(256), 0, s>>>(x, ws, D, chunk);
+    softmax_finish_kernel<VEC><<<g, dim3(256), 0, s>>>(x, y, ws, D, chunk);
+}
+
+int softmax_checked(const void* x, void* y, int64_t N, int64_t D, void* ws, int64_t ws_bytes,
+                    void* stream) {
+    if (N < 0 || D < 0 || ws_bytes < 0) return MI_ERR_INVALID_ARGUMENT;
+    if (N == 0 || D == 0) return MI_OK;
+    if (!x || !y) return MI_ERR_INVALID_ARGUMENT;
+    if (N > kMaxGridX) return MI_ERR_UNSUPPORTED;
+    const int64_t bytes = N * D * 2;
+    if (x != y && overlaps(x, bytes, y, bytes)) return MI_ERR_ALIASING;
+    const int64_t need = workspace_bytes(N, D);
+    if (need > 0) {
+        if (!ws || ws_bytes < need) return MI_ERR_INVALID_ARGUMENT;
+        if (overlaps(ws, need, x, bytes) || overlaps(ws, need, y, bytes)) return MI_ERR_ALIASING;
+    }
+    const auto* xh = static_cast<const half_t*>(x);
+    auto* yh = static_cast<half_t*>(y);
+    auto* w = static_cast<float*>(ws);
+    const hipStream_t s = as_stream(stream);
+    if (D % 8 == 0 && aligned16(x) && aligned16(y))
+        launch_softmax<8>(xh, yh, N, D, w, s);
+    else
+        launch_softmax<1>(xh, yh, N, D, w, s);
+    return launch_status();
 }
 
 }  // namespace
 }  // namespace mi
 
+extern "C" int64_t mi_softmax_workspace_bytes(int64_t N, int64_t D) {
+    if (N <= 0 || D <= 0) return 0;
+    return mi::workspace_bytes(N, D);
+}
+
+extern "C" int mi_softmax_ws_f16(const void* x, void* y, int64_t N, int64_t D, void* workspace,
+                                 int64_t workspace_bytes, void* stream) {
+    return mi::softmax_checked(x, y, N, D, workspace, workspace_bytes, stream);
+}
+
 extern "C" int mi_softmax_f16(const void* x, void* y, int64_t N, int64_t D, void* stream) {
-    if (N < 0 || D < 0) return MI_ERR_INVALID_ARGUMENT;
-    if (N == 0 || D == 0) return MI_OK;
+    const int64_t need = (N > 0 && D > 0) ? mi::workspace_bytes(N, D) : 0;
+    if (need == 0) return mi::softmax_checked(x, y, N, D, nullptr, 0, stream);
+    // The (max, sum) pairs live in a stream-ordered allocation from the
+    // device's default pool: concurrent calls on other streams get their own,
+    // and after the first call the pool hands back cached memory.
     if (!x || !y) return MI_ERR_INVALID_ARGUMENT;
-    if (N > mi::kMaxGridX) return MI_ERR_UNSUPPORTED;
-    const int64_t bytes = N * D * 2;
-    if (x != y && mi::overlaps(x, bytes, y, bytes)) return MI_ERR_ALIASING;
-    const auto* xh = static_cast<const mi::half_t*>(x);
-    auto* yh = static_cast<mi::half_t*>(y);
     const hipStream_t s = mi::as_stream(stream);
-    if (D % 8 == 0 && mi::aligned16(x) && mi::aligned16(y))
-        return mi::launch_softmax<8>(xh, yh, N, D, s);
-    return mi::launch_softmax<1>(xh, yh, N, D, s);
+    void* ws = nullptr;
+    hipError_t e = hipMallocAsync(&ws, static_cast<size_t>(need), s);
+    if (e != hipSuccess) return static_cast<int>(e);
+    const int st = mi::softmax_checked(x, y, N, D, ws, need, stream);
+    e = hipFreeAsync(ws, s);
+    if (st != MI_OK) return st;
+    return e == hipSuccess ? MI_OK : static_cast<int>(e);
 }

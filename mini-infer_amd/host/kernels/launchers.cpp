@@ -1,0 +1,125 @@
+// launchers.cpp -- the reference-named C++ launchers, forwarding to the C ABI.
+//
+// The reference's launchers return void and never check for errors; these
+// keep the void signatures but throw std::runtime_error when the library
+// rejects a launch, so a bad shape or a failed launch cannot pass silently.
+#include <hip/hip_runtime.h>
+
+#include <stdexcept>
+#include <string>
+
+#include "kernels/gelu_kernel.h"
+#include "kernels/model_utils_kernel.h"
+#include "kernels/rmsnorm_kernel.h"
+#include "kernels/rope_kernel.h"
+#include "kernels/softmax_kernel.h"
+#include "kernels/swiglu_kernel.h"
+#include "mi_kernels.h"
+
+namespace mini_infer {
+namespace kernels {
+namespace {
+
+void check(int status, const char* what) {
+    if (status != MI_OK)
+        throw std::runtime_error(std::string(what) + ": " + mi_status_string(status));
+}
+
+void hip_check(hipError_t e, const char* what) {
+    if (e != hipSuccess) throw std::runtime_error(std::string(what) + ": " + hipGetErrorString(e));
+}
+
+void* sv(hipStream_t s) { return reinterpret_cast<void*>(s); }
+
+}  // namespace
+
+void launch_rmsnorm(const __half* x, const __half* weight, __half* y, int N, int D, float eps,
+                    int add_one, hipStream_t stream) {
+    check(mi_rmsnorm_f16(x, weight, y, N, D, eps, add_one, sv(stream)), "launch_rmsnorm");
+}
+
+void launch_fused_add_rmsnorm(const __half* x, __half* residual, const __half* weight, __half* y,
+                              int N, int D, float eps, int add_one, hipStream_t stream) {
+    check(mi_fused_add_rmsnorm_f16(x, residual, weight, y, N, D, eps, add_one, sv(stream)),
+          "launch_fused_add_rmsnorm");
+}
+
+void launch_rope(const __half* x, const __half* cos_t, const __half* sin_t, __half* y, int B,
+                 int S, int H, int D, hipStream_t stream) {
+    check(mi_rope_neox_f16(x, cos_t, sin_t, y, B, S, H, D, sv(stream)), "launch_rope");
+}
+
+void launch_rope_precompute_batched(const float* inv_freq_h, const int64_t* positions_h,
+                                    __half* cos_d, __half* sin_d, int B, int S, int half,
+                                    hipStream_t stream) {
+    // The reference takes host positions; they are staged to the device in a
+    // stream-ordered allocation (the table kernel reads device positions, and
+    // inv_freq travels by value in the kernel arguments).
+    const int64_t n = static_cast<int64_t>(B) * S;
+    if (n <= 0 || half <= 0) return;
+    if (!positions_h) throw std::runtime_error("launch_rope_precompute: null positions");
+    void* pos_d = nullptr;
+    const size_t bytes = static_cast<size_t>(n) * sizeof(int64_t);
+    hip_check(hipMallocAsync(&pos_d, bytes, stream), "launch_rope_precompute: hipMallocAsync");
+    hipError_t e = hipMemcpyAsync(pos_d, positions_h, bytes, hipMemcpyHostToDevice, stream);
+    // the caller's host buffer may be released on return: wait for the copy
+    if (e == hipSuccess) e = hipStreamSynchronize(stream);
+    const int st = e == hipSuccess
+                       ? mi_rope_tables_f16(inv_freq_h, static_cast<const int64_t*>(pos_d), cos_d,
+                                            sin_d, n, half, sv(stream))
+                       : MI_OK;
+    const hipError_t fe = hipFreeAsync(pos_d, stream);
+    hip_check(e, "launch_rope_precompute: positions upload");
+    check(st, "launch_rope_precompute");
+    hip_check(fe, "launch_rope_precompute: hipFreeAsync");
+}
+
+void launch_rope_precompute(const float* inv_freq_h, const int64_t* positions_h, __half* cos_d,
+                            __half* sin_d, int S, int half, hipStream_t stream) {
+    launch_rope_precompute_batched(inv_freq_h, positions_h, cos_d, sin_d, 1, S, half, stream);
+}
+
+void launch_rope_qk(__half* q, __half* k, const int64_t* positions_d, const float* inv_freq_h,
+                    int T, int Hq, int Hkv, int head_dim, hipStream_t stream) {
+    check(mi_rope_neox_qk_f16(q, k, positions_d, inv_freq_h, T, Hq, Hkv, head_dim, sv(stream)),
+          "launch_rope_qk");
+}
+
+void launch_swiglu(const __half* gate, const __half* up, __half* out, int n, hipStream_t stream) {
+    check(mi_swiglu_f16(gate, up, out, n, sv(stream)), "launch_swiglu");
+}
+
+void launch_gelu_tanh(const __half* x, __half* y, int64_t n, hipStream_t stream) {
+    check(mi_gelu_tanh_f16(x, y, n, sv(stream)), "launch_gelu_tanh");
+}
+
+void launch_geglu(const __half* gate, const __half* up, __half* out, int64_t n,
+                  hipStream_t stream) {
+    check(mi_geglu_f16(gate, up, out, n, sv(stream)), "launch_geglu");
+}
+
+void launch_softmax(const __half* x, __half* y, int N, int D, hipStream_t stream) {
+    check(mi_softmax_f16(x, y, N, D, sv(stream)), "launch_softmax");
+}
+
+void launch_add_inplace(__half* y, const __half* x, int64_t n, hipStream_t s) {
+    check(mi_add_inplace_f16(y, x, n, sv(s)), "launch_add_inplace");
+}
+
+void launch_embedding_gather(const int64_t* token_ids, const __half* embed_table, __half* out,
+                             int B, int S, int H, hipStream_t stream) {
+    check(mi_embedding_gather_f16(token_ids, embed_table, out, static_cast<int64_t>(B) * S, H, 0,
+                                  sv(stream)),
+          "launch_embedding_gather");
+}
+
+void launch_scale_inplace(__half* y, float scale, int64_t n, hipStream_t stream) {
+    check(mi_scale_inplace_f16(y, scale, n, sv(stream)), "launch_scale_inplace");
+}
+
+void launch_mul_inplace(__half* y, const __half* x, int64_t n, hipStream_t stream) {
+    check(mi_mul_inplace_f16(y, x, n, sv(stream)), "launch_mul_inplace");
+}
+
+}  // namespace kernels
+}  // namespace mini_infer

@@ -1,0 +1,35 @@
+// rope_kernel.h -- RoPE launchers with the reference's signatures
+// (src/kernels/rope_kernel.cuh:11-28), plus the fused positions-driven Q+K
+// rotation.  All forward to the C ABI (include/mi_kernels.h) and throw
+// std::runtime_error if a launch is rejected.
+#pragma once
+
+#include <cstdint>
+
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+
+namespace mini_infer {
+namespace kernels {
+
+// NeoX RoPE: x, y [B, S, H, D] (y may equal x), cos_t / sin_t [B*S, D/2].
+void launch_rope(const __half* x, const __half* cos_t, const __half* sin_t, __half* y, int B,
+                 int S, int H, int D, hipStream_t stream);
+
+// cos/sin tables [S, half] from HOST inv_freq [half] and HOST positions [S].
+void launch_rope_precompute(const float* inv_freq_h, const int64_t* positions_h, __half* cos_d,
+                            __half* sin_d, int S, int half, hipStream_t stream);
+
+// cos/sin tables [B*S, half] from HOST inv_freq [half] and HOST positions [B*S].
+void launch_rope_precompute_batched(const float* inv_freq_h, const int64_t* positions_h,
+                                    __half* cos_d, __half* sin_d, int B, int S, int half,
+                                    hipStream_t stream);
+
+// In-place NeoX RoPE of q [T, Hq, hd] and k [T, Hkv, hd] with cos/sin made in
+// registers from DEVICE positions [T] and HOST inv_freq [hd/2]: no table, no
+// copy, no allocation.  k may be null when Hkv == 0.
+void launch_rope_qk(__half* q, __half* k, const int64_t* positions_d, const float* inv_freq_h,
+                    int T, int Hq, int Hkv, int head_dim, hipStream_t stream);
+
+}  // namespace kernels
+}  // namespace mini_infer

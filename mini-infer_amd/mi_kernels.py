@@ -43,6 +43,7 @@ SIGNATURES = {
     "mi_scale_inplace_f16": [_c_void_p, _f32, _i64, _c_void_p],
     "mi_softmax_f16": [_c_void_p, _c_void_p, _i64, _i64, _c_void_p],
     "mi_embedding_gather_f16": [_c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64, _c_void_p],
+    "mi_softmax_ws_f16": [_c_void_p, _c_void_p, _i64, _i64, _c_void_p, _i64, _c_void_p],
     "mi_abi_version": [],
 }
 
@@ -63,6 +64,8 @@ def load_library(path: os.PathLike | str | None = None) -> ctypes.CDLL:
         fn = getattr(lib, name)
         fn.argtypes = argtypes
         fn.restype = _int
+    lib.mi_softmax_workspace_bytes.argtypes = [_i64, _i64]
+    lib.mi_softmax_workspace_bytes.restype = _i64
     lib.mi_status_string.argtypes = [_int]
     lib.mi_status_string.restype = ctypes.c_char_p
     if path is None:
@@ -301,7 +304,13 @@ def scale_inplace(y, scale: float, stream=None):
 # Softmax (reference: launch_softmax, softmax_kernel.cuh:12)
 # ---------------------------------------------------------------------------
 
-def softmax(x, y=None, stream=None):
+def softmax_workspace_bytes(N: int, D: int) -> int:
+    return int(load_library().mi_softmax_workspace_bytes(N, D))
+
+
+def softmax(x, y=None, workspace=None, stream=None):
+    """Row softmax of x [N, D].  With `workspace` (a device tensor of at least
+    softmax_workspace_bytes(N, D) bytes) nothing is allocated per call."""
     _need(x, _f16(), "x")
     if x.dim() != 2:
         raise ValueError("x must be 2-D [N, D]")
@@ -310,8 +319,16 @@ def softmax(x, y=None, stream=None):
     _need(y, _f16(), "y")
     if y.shape != x.shape:
         raise ValueError("y must have x's shape")
-    _check(load_library().mi_softmax_f16(_ptr(x), _ptr(y), x.shape[0], x.shape[1],
-                                         _stream(stream)), "mi_softmax_f16")
+    if workspace is None:
+        _check(load_library().mi_softmax_f16(_ptr(x), _ptr(y), x.shape[0], x.shape[1],
+                                             _stream(stream)), "mi_softmax_f16")
+        return y
+    if workspace.device.type != "cuda" or not workspace.is_contiguous():
+        raise ValueError("workspace must be a contiguous GPU tensor")
+    nbytes = workspace.numel() * workspace.element_size()
+    _check(load_library().mi_softmax_ws_f16(_ptr(x), _ptr(y), x.shape[0], x.shape[1],
+                                            _ptr(workspace), nbytes, _stream(stream)),
+           "mi_softmax_ws_f16")
     return y
 
 

@@ -1,0 +1,289 @@
+// test_layers -- parity of the C++ host layer (Tensor, RMSNorm, RoPE, gated
+// activation, reference-named launchers) against the CPU oracle, in the shape
+// of the reference's kernel tests (tests/test_rmsnorm/main.cpp,
+// tests/test_rope/main.cpp, ...): seeded xorshift inputs converted to fp16
+// the way those tests do, run through the layer, compared with
+// |ours - ref| <= 1e-3 + 1e-3 |ref| (tests/verify/verify.py:142).
+//
+// `test_layers --cpu` runs only the host-side Tensor checks (no GPU needed).
+// Links oracle/libmi_oracle.so as the checker.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <functional>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "core/tensor.h"
+#include "kernels/gelu_kernel.h"
+#include "kernels/model_utils_kernel.h"
+#include "kernels/rmsnorm_kernel.h"
+#include "kernels/rope_kernel.h"
+#include "kernels/softmax_kernel.h"
+#include "kernels/swiglu_kernel.h"
+#include "layers/mlp_activation.h"
+#include "layers/rmsnorm.h"
+#include "layers/rope.h"
+#include "mi_oracle.h"
+
+using mini_infer::DType;
+using mini_infer::Device;
+using mini_infer::Tensor;
+
+static int g_failures = 0;
+#define EXPECT(cond, msg)                                                           \
+    do {                                                                            \
+        if (!(cond)) {                                                              \
+            std::fprintf(stderr, "FAIL [%s:%d] %s\n", __FILE__, __LINE__, (msg));   \
+            ++g_failures;                                                           \
+        }                                                                           \
+    } while (0)
+
+namespace {
+
+// fp16 CPU tensor built like the reference tests build theirs.
+Tensor reftest_f16(std::vector<int64_t> shape, float scale, uint32_t seed) {
+    Tensor t(shape, DType::FP16, Device::cpu());
+    std::vector<float> f(static_cast<size_t>(t.numel()));
+    mio_fill_uniform(f.data(), t.numel(), scale, seed);
+    mio_reftest_f32_to_f16_array(f.data(), static_cast<uint16_t*>(t.data()), t.numel());
+    return t;
+}
+
+const uint16_t* bits(const Tensor& t) { return static_cast<const uint16_t*>(t.data()); }
+
+bool close(const Tensor& ours_dev, const std::vector<float>& ref, const char* what) {
+    Tensor h = ours_dev.to(Device::cpu());
+    int bad = 0;
+    double worst = 0;
+    for (int64_t i = 0; i < h.numel(); ++i) {
+        const double o = mio_f16_to_f32(bits(h)[i]);
+        const double d = std::fabs(o - ref[i]);
+        if (d > 1e-3 + 1e-3 * std::fabs(ref[i])) ++bad;
+        worst = std::max(worst, d);
+    }
+    std::printf("  %-40s %s  max_abs=%.3e\n", what, bad ? "FAIL" : "OK  ", worst);
+    return bad == 0;
+}
+
+bool bit_equal(const Tensor& ours_dev, const uint16_t* ref, const char* what) {
+    Tensor h = ours_dev.to(Device::cpu());
+    const bool ok = std::memcmp(h.data(), ref, h.nbytes()) == 0;
+    std::printf("  %-40s %s\n", what, ok ? "OK   (bit-exact)" : "FAIL (bits differ)");
+    return ok;
+}
+
+bool throws(const std::function<void()>& fn) {
+    try {
+        fn();
+    } catch (const std::runtime_error&) {
+        return true;
+    }
+    return false;
+}
+
+void cpu_checks() {
+    std::printf("[cpu] Tensor\n");
+    Tensor t({2, 3, 4}, DType::FP16, Device::cpu());
+    EXPECT(t.numel() == 24 && t.nbytes() == 48 && t.ndim() == 3, "shape bookkeeping");
+    EXPECT(t.is_contiguous(), "default stride is contiguous");
+    EXPECT(t.stride()[0] == 12 && t.stride()[1] == 4 && t.stride()[2] == 1, "row-major strides");
+    t.fill(1.5f);
+    EXPECT(mio_f16_to_f32(bits(t)[23]) == 1.5f, "fill fp16 on host");
+    Tensor c = t;  // deep copy
+    EXPECT(c.data() != t.data() && std::memcmp(c.data(), t.data(), t.nbytes()) == 0, "deep copy");
+    Tensor m = std::move(c);
+    EXPECT(c.data() == nullptr && m.numel() == 24, "move leaves the source empty");
+    EXPECT(std::string(mini_infer::dtype_name(DType::INT64)) == "int64", "dtype_name");
+    EXPECT(throws([] { Tensor bad({-1}, DType::FP32, Device::cpu()); }), "negative dim throws");
+}
+
+void gpu_checks() {
+    const float eps = 1e-6f;
+    // --- RMSNorm layer, tests/test_rmsnorm/main.cpp:83-124 ---------------
+    std::printf("[gpu] RMSNorm layer\n");
+    {
+        const int N = 4, D = 4096;
+        Tensor x = reftest_f16({N, D}, 1.0f, 42), w = reftest_f16({D}, 0.5f, 7);
+        std::vector<float> ref(N * D), refg(N * D);
+        mio_rmsnorm(bits(x), bits(w), ref.data(), N, D, eps, 0, 1);
+        mio_rmsnorm(bits(x), bits(w), refg.data(), N, D, eps, 1, 1);
+        mini_infer::RMSNorm norm(D, eps, 0), gemma(D, eps, 0, true);
+        norm.set_weight(w);
+        gemma.set_weight(w);
+        Tensor xd = x.to(Device::cuda(0));
+        EXPECT(close(norm.forward(xd), ref, "RMSNorm [4,4096]"), "rmsnorm std");
+        EXPECT(close(gemma.forward(xd), refg, "RMSNorm Gemma (1+w) [4,4096]"), "rmsnorm gemma");
+        norm.forward_inplace(xd);
+        EXPECT(close(xd, ref, "RMSNorm in place"), "rmsnorm in place");
+        EXPECT(throws([&] { norm.forward(x); }), "host tensor rejected");
+        Tensor wrong = Tensor::empty({N, D + 8}, DType::FP16, Device::cuda(0));
+        EXPECT(throws([&] { norm.forward(wrong); }), "hidden dim mismatch rejected");
+        Tensor f32 = Tensor::empty({N, D}, DType::FP32, Device::cuda(0));
+        EXPECT(throws([&] { norm.forward(f32); }), "fp32 rejected");
+        EXPECT(throws([&] { norm.set_weight(reftest_f16({D + 1}, 1.f, 1)); }), "bad weight size");
+    }
+    // --- fused residual add + RMSNorm -------------------------------------
+    {
+        const int N = 37, D = 3584;
+        Tensor x = reftest_f16({N, D}, 1.0f, 11), r = reftest_f16({N, D}, 1.0f, 12);
+        Tensor w = reftest_f16({D}, 0.5f, 13);
+        std::vector<uint16_t> r_ref(bits(r), bits(r) + N * D);
+        std::vector<float> ref(N * D);
+        mio_fused_add_rmsnorm(bits(x), r_ref.data(), bits(w), ref.data(), N, D, eps, 0, 1);
+        mini_infer::RMSNorm norm(D, eps, 0);
+        norm.set_weight(w);
+        Tensor xd = x.to(Device::cuda(0)), rd = r.to(Device::cuda(0));
+        EXPECT(close(norm.forward_fused_add(xd, rd), ref, "RMSNorm forward_fused_add"), "fused y");
+        EXPECT(bit_equal(rd, r_ref.data(), "  updated residual"), "fused residual");
+    }
+    // --- RoPE layer, tests/test_rope/main.cpp:63-80 ------------------------
+    std::printf("[gpu] RoPE layer\n");
+    {
+        const int B = 2, S = 16, Hh = 4, D = 64, half = D / 2;
+        mini_infer::RoPE rope(D, 1e6f, 0);
+        std::vector<float> inv(half);
+        mio_rope_inv_freq(inv.data(), D, 1e6f);
+        EXPECT(std::memcmp(inv.data(), rope.inv_freq().data(), half * 4) == 0, "inv_freq");
+        Tensor x = reftest_f16({B, S, Hh, D}, 1.0f, 101);
+        std::vector<int64_t> pos(S);
+        mio_fill_uniform_int64(pos.data(), S, 2024, 0, 4096);
+        std::vector<int64_t> rep(B * S);
+        for (int b = 0; b < B; ++b)
+            for (int s = 0; s < S; ++s) rep[b * S + s] = pos[s];
+        std::vector<uint16_t> c(B * S * half), sn(B * S * half);
+        mio_rope_tables(inv.data(), rep.data(), c.data(), sn.data(), B * S, half);
+        std::vector<float> ref(B * S * Hh * D);
+        mio_rope_neox(bits(x), c.data(), sn.data(), ref.data(), B * S, Hh, D, 1);
+        std::vector<uint16_t> ref16(ref.size());
+        mio_f32_to_f16_array(ref.data(), ref16.data(), static_cast<int64_t>(ref.size()));
+        Tensor xd = x.to(Device::cuda(0));
+        EXPECT(bit_equal(rope.forward(xd, pos), ref16.data(), "RoPE::forward [2,16,4,64]"),
+               "rope forward");
+        EXPECT(bit_equal(rope.forward_batched(xd, rep), ref16.data(), "RoPE::forward_batched"),
+               "rope batched");
+        Tensor pt(std::vector<int64_t>{B * S}, DType::INT64, Device::cpu());
+        std::memcpy(pt.data(), rep.data(), rep.size() * 8);
+        Tensor pd = pt.to(Device::cuda(0));
+        Tensor q = x.to(Device::cuda(0));
+        Tensor k = Tensor::empty({B * S, 0, D}, DType::FP16, Device::cuda(0));
+        rope.forward_qk_inplace(q, k, pd);
+        EXPECT(bit_equal(q, ref16.data(), "RoPE::forward_qk_inplace"), "rope fused");
+        EXPECT(throws([&] { rope.forward(xd, std::vector<int64_t>(S + 1)); }), "bad positions");
+        EXPECT(throws([] { mini_infer::RoPE bad(7); }), "odd head_dim");
+    }
+    // --- gated activations (src/layers/mlp.cpp:270-292) --------------------
+    std::printf("[gpu] MLP gated activation\n");
+    {
+        const int n = 4096;
+        Tensor g = reftest_f16({n}, 2.0f, 11), u = reftest_f16({n}, 2.0f, 22);
+        std::vector<float> rs(n), rg(n);
+        mio_swiglu(bits(g), bits(u), rs.data(), n, 1);
+        mio_geglu(bits(g), bits(u), rg.data(), n, 1);
+        Tensor gd = g.to(Device::cuda(0)), ud = u.to(Device::cuda(0));
+        Tensor out = Tensor::empty({n}, DType::FP16, Device::cuda(0));
+        mini_infer::apply_gated_activation(mini_infer::ActKind::Silu, gd, ud, out);
+        EXPECT(close(out, rs, "SwiGLU n=4096 (seeds 11/22)"), "swiglu");
+        mini_infer::apply_gated_activation(mini_infer::ActKind::GeluTanh, gd, ud, out);
+        EXPECT(close(out, rg, "GeGLU n=4096"), "geglu");
+    }
+    // --- remaining reference-named launchers -------------------------------
+    std::printf("[gpu] launchers\n");
+    {
+        const int N = 8, D = 1024;
+        Tensor x = reftest_f16({N, D}, 4.0f, 555);  // tests/test_softmax/main.cpp:63-66
+        std::vector<float> ref(N * D);
+        mio_softmax(bits(x), ref.data(), N, D, 1);
+        Tensor xd = x.to(Device::cuda(0));
+        Tensor yd = Tensor::empty({N, D}, DType::FP16, Device::cuda(0));
+        mini_infer::kernels::launch_softmax(static_cast<const __half*>(xd.data()),
+                                            static_cast<__half*>(yd.data()), N, D, 0);
+        EXPECT(close(yd, ref, "launch_softmax [8,1024]"), "softmax");
+
+        Tensor gx = reftest_f16({4096}, 2.0f, 13);  // tests/test_gelu/main.cpp:64-67
+        std::vector<float> gref(4096);
+        mio_gelu_tanh(bits(gx), gref.data(), 4096, 1);
+        Tensor gxd = gx.to(Device::cuda(0));
+        mini_infer::kernels::launch_gelu_tanh(static_cast<const __half*>(gxd.data()),
+                                              static_cast<__half*>(gxd.data()), 4096, 0);
+        EXPECT(close(gxd, gref, "launch_gelu_tanh n=4096 (in place)"), "gelu");
+
+        Tensor a = reftest_f16({5000}, 50.0f, 1), b = reftest_f16({5000}, 50.0f, 2);
+        std::vector<uint16_t> ra(bits(a), bits(a) + 5000), rm(ra), rsc(ra);
+        mio_add_inplace(ra.data(), bits(b), 5000);
+        mio_mul_inplace(rm.data(), bits(b), 5000);
+        mio_scale_inplace(rsc.data(), 59.866518f, 5000);
+        Tensor bd = b.to(Device::cuda(0));
+        Tensor ad = a.to(Device::cuda(0));
+        mini_infer::kernels::launch_add_inplace(static_cast<__half*>(ad.data()),
+                                                static_cast<const __half*>(bd.data()), 5000, 0);
+        EXPECT(bit_equal(ad, ra.data(), "launch_add_inplace"), "add");
+        ad = a.to(Device::cuda(0));
+        mini_infer::kernels::launch_mul_inplace(static_cast<__half*>(ad.data()),
+                                                static_cast<const __half*>(bd.data()), 5000, 0);
+        EXPECT(bit_equal(ad, rm.data(), "launch_mul_inplace"), "mul");
+        ad = a.to(Device::cuda(0));
+        mini_infer::kernels::launch_scale_inplace(static_cast<__half*>(ad.data()), 59.866518f, 5000,
+                                                  0);
+        EXPECT(bit_equal(ad, rsc.data(), "launch_scale_inplace"), "scale");
+
+        const int V = 500, Hd = 3584, B = 2, S = 33;
+        Tensor table = reftest_f16({V, Hd}, 0.02f, 9);
+        std::vector<int64_t> ids(B * S);
+        mio_fill_uniform_int64(ids.data(), B * S, 77, 0, V - 1);
+        std::vector<uint16_t> gref16(static_cast<size_t>(B) * S * Hd);
+        mio_embedding_gather(ids.data(), bits(table), gref16.data(), B * S, Hd, V, 1);
+        Tensor it(std::vector<int64_t>{B, S}, DType::INT64, Device::cpu());
+        std::memcpy(it.data(), ids.data(), ids.size() * 8);
+        Tensor itd = it.to(Device::cuda(0)), td = table.to(Device::cuda(0));
+        Tensor od = Tensor::empty({B, S, Hd}, DType::FP16, Device::cuda(0));
+        mini_infer::kernels::launch_embedding_gather(static_cast<const int64_t*>(itd.data()),
+                                                     static_cast<const __half*>(td.data()),
+                                                     static_cast<__half*>(od.data()), B, S, Hd, 0);
+        EXPECT(bit_equal(od, gref16.data(), "launch_embedding_gather [2,33]x3584"), "gather");
+
+        EXPECT(throws([&] {
+                   mini_infer::kernels::launch_rmsnorm(static_cast<const __half*>(xd.data()),
+                                                       nullptr, static_cast<__half*>(yd.data()), N,
+                                                       D, 1e-6f, 0, 0);
+               }),
+               "launcher rejects a null weight");
+    }
+    // --- device Tensor round trip --------------------------------------------
+    {
+        Tensor h = reftest_f16({3, 5}, 1.0f, 3);
+        Tensor d = h.to(Device::cuda(0));
+        Tensor d2 = d;  // device deep copy
+        Tensor back = d2.to(Device::cpu());
+        EXPECT(std::memcmp(back.data(), h.data(), h.nbytes()) == 0, "device round trip");
+        d2.fill(2.0f);
+        back = d2.to(Device::cpu());
+        EXPECT(mio_f16_to_f32(bits(back)[14]) == 2.0f, "device fill");
+    }
+}
+
+}  // namespace
+
+int main(int argc, char** argv) {
+    std::printf("mini-infer MI355X :: C++ layer parity\n");
+    cpu_checks();
+    if (!(argc > 1 && std::strcmp(argv[1], "--cpu") == 0)) {
+        try {
+            gpu_checks();
+        } catch (const std::exception& e) {
+            std::fprintf(stderr, "FAIL: exception %s\n", e.what());
+            ++g_failures;
+        }
+        const hipError_t e = hipDeviceSynchronize();
+        EXPECT(e == hipSuccess, "device synchronize");
+    }
+    if (g_failures == 0) {
+        std::printf("\nALL OK\n");
+        return 0;
+    }
+    std::fprintf(stderr, "\n%d failures\n", g_failures);
+    return 1;
+}

@@ -45,3 +45,11 @@ def assert_bits_equal(a, b, what=""):
         i = np.argwhere(ne)[0]
         raise AssertionError(f"{what}: {int(ne.sum())} of {ne.size} differ; first at {tuple(i)}: "
                              f"{a[tuple(i)]} vs {b[tuple(i)]}")
+
+
+def ulp_diff(a, b):
+    """Distance in fp16 units in the last place (+0 and -0 coincide)."""
+    def ordered(x):
+        v = np.ascontiguousarray(x, dtype=np.float16).view(np.uint16).astype(np.int32)
+        return np.where(v & 0x8000, -(v & 0x7FFF), v)
+    return np.abs(ordered(a) - ordered(b))

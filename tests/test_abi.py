@@ -36,7 +36,7 @@ def test_library_exports_every_declared_symbol(lib):
 
 
 def test_binding_covers_header():
-    names = set(declared_symbols()) - {"mi_status_string"}
+    names = set(declared_symbols()) - {"mi_status_string", "mi_softmax_workspace_bytes"}
     assert names == set(mi_kernels.SIGNATURES), names ^ set(mi_kernels.SIGNATURES)
 
 
@@ -102,3 +102,13 @@ def test_product_path_has_no_oracle_dependency():
         text = f.read_text()
         for needle in ("import oracle", "libmi_oracle", "mi_oracle.h", "mio_"):
             assert needle not in text, f"{f} references the oracle ({needle})"
+
+
+def test_softmax_workspace_sizes(lib):
+    lib.mi_softmax_workspace_bytes.argtypes = [ctypes.c_int64, ctypes.c_int64]
+    lib.mi_softmax_workspace_bytes.restype = ctypes.c_int64
+    assert lib.mi_softmax_workspace_bytes(64, 152064) == 64 * 32 * 8
+    assert lib.mi_softmax_workspace_bytes(57344, 512) == 0
+    assert lib.mi_softmax_workspace_bytes(8, 1024) == 0
+    assert lib.mi_softmax_workspace_bytes(0, 5) == 0
+    assert 0 < lib.mi_softmax_workspace_bytes(511, 10**6) <= 256 * 1024

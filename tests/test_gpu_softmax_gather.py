@@ -86,3 +86,19 @@ def test_gather_shapes_and_bad_ids(mk, orc, dev, H):
     out = to_host(mk.embedding_gather(to_dev(ids, dev), to_dev(table, dev)))
     assert_bits_equal(out, orc.embedding_gather(ids, table), what=f"H={H}")
     assert (out[0, 0] == 0).all() and (out[1, 5] == 0).all()
+
+
+def test_softmax_workspace_variant(mk, orc, dev):
+    _case("softmax with caller workspace")
+    import torch
+    rng = np.random.default_rng(54)
+    x = normal_f16(rng, (64, 152064), 0, 4)
+    xd = to_dev(x, dev)
+    nb = mk.softmax_workspace_bytes(64, 152064)
+    assert nb > 0
+    ws = torch.empty(nb, dtype=torch.uint8, device=dev)
+    y1 = to_host(mk.softmax(xd, workspace=ws))
+    y2 = to_host(mk.softmax(xd))
+    assert_bits_equal(y1, y2, what="ws vs pool")
+    with pytest.raises(RuntimeError, match="status -1"):
+        mk.softmax(xd, workspace=ws[: nb - 8])
