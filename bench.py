@@ -44,12 +44,27 @@ def rotations(set_bytes, min_sets=2, max_sets=16):
     return int(min(max_sets, max(min_sets, math.ceil(3 * MALL_BYTES / max(set_bytes, 1)))))
 
 
+EAGER = False  # --eager: plain launches (for counter collection), no graph
+
+
 def time_launches(launch, nsets, iters, warmup):
     """Average seconds per launch over `iters` back-to-back launches cycling
     through `nsets` buffer sets.  The launches are captured into one HIP
     graph and replayed, so host-side launch cost (Python, ctypes) is not in
     the figure; events on the replay stream bracket the timed replay."""
     import torch
+    if EAGER:
+        for i in range(warmup):
+            launch(i % nsets)
+        torch.cuda.synchronize()
+        s = torch.cuda.current_stream()
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0.record(s)
+        for i in range(iters):
+            launch(i % nsets)
+        t1.record(s)
+        torch.cuda.synchronize()
+        return t0.elapsed_time(t1) * 1e-3 / iters
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(side):
@@ -312,7 +327,11 @@ def main():
     ap.add_argument("--no-kernels", action="store_true", help="skip the per-config table")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--eager", action="store_true",
+                    help="launch eagerly instead of replaying a HIP graph (profiler counter runs)")
     args = ap.parse_args()
+    global EAGER
+    EAGER = args.eager
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: these layer kernels are row-independent and run "
@@ -381,7 +400,8 @@ def main():
             "traffic": traffic,
         },
         "cpu_baseline": cpu,
-        "timing": "HIP graph replay of back-to-back launches; HIP events on the replay stream",
+        "timing": ("eager launches; HIP events on the launch stream" if EAGER else
+                   "HIP graph replay of back-to-back launches; HIP events on the replay stream"),
         "copy_calibration_GBps": round(copy_gbps, 1),
         "kernels": kernels,
     }
