@@ -258,6 +258,11 @@ def all_kernels(mk, dev, iters, warmup):
     sec = time_launches(lambda i: mk.rope_neox_qk(qs[i].view(T, 28, 128), ks[i].view(T, 4, 128),
                                                   pos, inv), ns, iters, warmup)
     out.append(report("rope_neox_qk", "chain Q[6064,28,128]+K[6064,4,128]", nb, sec, T))
+    # 5c+5d fused: Q/K RMSNorm + RoPE in one pass (replaces the two rows above)
+    nb = 2 * T * 32 * 128 * 2 + T * 8 + 2 * 128 * 2
+    sec = time_launches(lambda i: mk.qk_norm_rope(qs[i].view(T, 28, 128), ks[i].view(T, 4, 128),
+                                                  wq, wk, pos, inv), ns, iters, warmup)
+    out.append(report("qk_norm_rope", "chain Q[6064,28,128]+K[6064,4,128]", nb, sec, T))
     del qs, ks
     # 5e. SwiGLU [6064, 18944]
     nb = 3 * T * I * 2
@@ -274,7 +279,7 @@ def all_kernels(mk, dev, iters, warmup):
     ns = rotations(2 * N * V * 2)
     sets = [(randn16((N, V), gen, dev, 0.0, 4.0), torch.empty((N, V), dtype=f16, device=dev))
             for _ in range(ns)]
-    ws = torch.empty(max(1, mk.softmax_workspace_bytes(N, V)), dtype=torch.uint8, device=dev)
+    ws = torch.zeros(max(1, mk.softmax_workspace_bytes(N, V)), dtype=torch.uint8, device=dev)
     sec = time_launches(lambda i: mk.softmax(sets[i][0], y=sets[i][1], workspace=ws), ns, iters,
                         warmup)
     out.append(report("softmax", "[64,152064]", nb, sec, N))

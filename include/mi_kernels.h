@@ -23,7 +23,7 @@
  * No entry point allocates device memory, except mi_softmax_f16 on its
  * split-row path (N < 512 rows of D >= 8192), which takes 8 bytes per row
  * chunk (<= 256 KiB) from the device's stream-ordered pool (hipMallocAsync /
- * hipFreeAsync on `stream`) for the duration of the call's kernels.
+ * hipFreeAsync on `stream`) for the duration of the call.
  */
 #ifndef MI_KERNELS_H
 #define MI_KERNELS_H
@@ -91,6 +91,21 @@ int mi_rope_neox_qk_f16(void* q, void* k, const int64_t* positions,
                         const float* inv_freq_host, int64_t T, int64_t Hq,
                         int64_t Hkv, int64_t head_dim, void* stream);
 
+/* Fused per-head RMSNorm + NeoX RoPE, in place, for Q [T, Hq, hd] and
+ * K [T, Hkv, hd]: each head is normalised with its weight (q_weight or
+ * k_weight, [hd]; f(w) = w, or 1 + w when add_one), rounded to fp16, then
+ * rotated with cos/sin made from DEVICE positions[T] and HOST inv_freq
+ * [hd/2].  Equals mi_rmsnorm_f16 on the Q rows and on the K rows followed by
+ * mi_rope_neox_qk_f16, in one pass.  hd must be 16, 32, 64, 128, 256 or 512
+ * and the buffers 16-byte aligned (else MI_ERR_UNSUPPORTED).  Replaces the
+ * Q/K-norm + RoPE sequence at src/layers/attention.cpp:754-780 (two
+ * launch_rmsnorm calls, src/kernels/rmsnorm_kernel.cuh:19, then two
+ * RoPE::forward_batched calls). */
+int mi_qk_norm_rope_f16(void* q, void* k, const void* q_weight, const void* k_weight,
+                        const int64_t* positions, const float* inv_freq_host, int64_t T,
+                        int64_t Hq, int64_t Hkv, int64_t head_dim, float eps, int add_one,
+                        void* stream);
+
 /* out = silu(gate) * up, elementwise over n.
  * Replaces launch_swiglu (src/kernels/swiglu_kernel.cuh:9). */
 int mi_swiglu_f16(const void* gate, const void* up, void* out, int64_t n,
@@ -123,7 +138,8 @@ int mi_scale_inplace_f16(void* y, float scale, int64_t n, void* stream);
 int mi_softmax_f16(const void* x, void* y, int64_t N, int64_t D, void* stream);
 
 /* Bytes of device workspace mi_softmax_ws_f16 needs for [N, D]: 0 when rows
- * are processed one workgroup each, else 8 bytes per row chunk (<= 256 KiB). */
+ * are processed one workgroup each (N >= 512 or D < 8192), else one fp32
+ * (max, sum) pair per row chunk, at most 64 chunks per row (<= 256 KiB). */
 int64_t mi_softmax_workspace_bytes(int64_t N, int64_t D);
 
 /* mi_softmax_f16 with a caller-provided device workspace of at least

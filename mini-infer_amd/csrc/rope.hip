@@ -201,6 +201,123 @@ __global__ __launch_bounds__(256) void rope_kernel(const half_t* q_in, half_t* q
     }
 }
 
+// ---------------------------------------------------------------------------
+// Fused per-head RMSNorm + RoPE, in place, for Q and K: the reference runs
+// launch_rmsnorm on the Q rows and the K rows (D = head_dim, in place,
+// src/layers/attention.cpp:757-768) and then RoPE on both (:779-780).  Here
+// a head's elements are held by CPH = head_dim/16 lanes -- each lane owns
+// x[i..i+7] and x[h+i..h+i+7] -- so the sum of squares is a CPH-lane DPP
+// reduction, the normalised value is rounded to fp16 exactly where the
+// reference writes it, and the rotation consumes it from registers: one HBM
+// read and one write of Q and K instead of two of each.
+// ---------------------------------------------------------------------------
+template <int CPH, int TPW>
+__global__ __launch_bounds__(256) void qk_norm_rope_kernel(half_t* q, int Hq, half_t* k, int Hkv,
+                                                           const half_t* __restrict__ wq,
+                                                           const half_t* __restrict__ wk,
+                                                           const int64_t* __restrict__ positions,
+                                                           int64_t T, float eps, float w_bias,
+                                                           InvFreq inv) {
+    constexpr int HALF = CPH * 8;
+    constexpr int HD = 2 * HALF;
+    __shared__ float cs[TPW][2 * kMaxHalf];
+    const int64_t tok0 = static_cast<int64_t>(blockIdx.x) * TPW;
+    const int ntok = static_cast<int>(T - tok0 < TPW ? T - tok0 : TPW);
+    const int upt = (Hq + Hkv) * CPH;  // units per token
+    const int units = ntok * upt;
+    const int c = threadIdx.x & (CPH - 1);  // a lane's slice is the same for every unit
+
+    // this lane's weight slices, for a Q head and for a K head
+    const h8 wq1 = ld8(wq + c * 8), wq2 = ld8(wq + HALF + c * 8);
+    h8 wk1 = h8(0), wk2 = h8(0);
+    if (Hkv > 0) {
+        wk1 = ld8(wk + c * 8);
+        wk2 = ld8(wk + HALF + c * 8);
+    }
+
+    // unit u -> (token, head); returns the head's base pointer
+    auto head_ptr = [&](int u, bool& is_k, int& t) -> half_t* {
+        t = u / upt;
+        const int h = (u - t * upt) / CPH;
+        const int64_t tok = tok0 + t;
+        is_k = h >= Hq;
+        return is_k ? k + (tok * Hkv + (h - Hq)) * static_cast<int64_t>(HD)
+                    : q + (tok * Hq + h) * static_cast<int64_t>(HD);
+    };
+
+    h8 x1[kPrefetch], x2[kPrefetch];
+#pragma unroll
+    for (int p = 0; p < kPrefetch; ++p) {
+        const int u = threadIdx.x + p * 256;
+        x1[p] = h8(0);
+        x2[p] = h8(0);
+        if (u < units) {
+            bool is_k;
+            int t;
+            half_t* hp = head_ptr(u, is_k, t);
+            x1[p] = ld8_stream(hp + c * 8);
+            x2[p] = ld8_stream(hp + HALF + c * 8);
+        }
+    }
+
+    for (int idx = threadIdx.x; idx < ntok * HALF; idx += 256) {
+        const int t = idx / HALF;
+        const int i = idx - t * HALF;
+        half_t hc, hs;
+        cos_sin_half(static_cast<float>(positions[tok0 + t]) * inv.v[i], hc, hs);
+        cs[t][i] = (float)hc;
+        cs[t][kMaxHalf + i] = (float)hs;
+    }
+    __syncthreads();
+
+    // Every lane runs process() for every step (the DPP reduction needs the
+    // whole wave); lanes past `units` contribute zeros and store nothing.
+    auto process = [&](int u, const h8& a1, const h8& a2) {
+        const bool valid = u < units;
+        float ss = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const float f1 = (float)a1[e], f2 = (float)a2[e];
+            ss = fmaf(f1, f1, ss);
+            ss = fmaf(f2, f2, ss);
+        }
+        ss = group_sum<CPH>(ss);
+        if (!valid) return;
+        bool is_k;
+        int t;
+        half_t* hp = head_ptr(u, is_k, t);
+        const float rrms = rsqrtf(ss / static_cast<float>(HD) + eps);
+        const h8 w1 = is_k ? wk1 : wq1, w2 = is_k ? wk2 : wq2;
+        const float* cst = &cs[t][0];
+        h8 y1, y2;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            // the normalised value as the reference stores it (fp16)
+            const float n1 = (float)to_half((float)a1[e] * rrms * ((float)w1[e] + w_bias));
+            const float n2 = (float)to_half((float)a2[e] * rrms * ((float)w2[e] + w_bias));
+            const float cv = cst[c * 8 + e], sv = cst[kMaxHalf + c * 8 + e];
+            y1[e] = to_half(fp32_rounded(n1 * cv - n2 * sv));
+            y2[e] = to_half(fp32_rounded(n2 * cv + n1 * sv));
+        }
+        st8_stream(hp + c * 8, y1);
+        st8_stream(hp + HALF + c * 8, y2);
+    };
+#pragma unroll
+    for (int p = 0; p < kPrefetch; ++p) process(threadIdx.x + p * 256, x1[p], x2[p]);
+    for (int base = kPrefetch * 256; base < units; base += 256) {
+        const int u = base + threadIdx.x;
+        h8 a1 = h8(0), a2 = h8(0);
+        if (u < units) {
+            bool is_k;
+            int t;
+            half_t* hp = head_ptr(u, is_k, t);
+            a1 = ld8_stream(hp + c * 8);
+            a2 = ld8_stream(hp + HALF + c * 8);
+        }
+        process(u, a1, a2);
+    }
+}
+
 __global__ __launch_bounds__(256) void rope_table_kernel(const int64_t* __restrict__ positions,
                                                          half_t* __restrict__ cos_t,
                                                          half_t* __restrict__ sin_t, int64_t N,
@@ -247,6 +364,32 @@ int launch_rope(const half_t* q_in, half_t* q_out, int64_t Hq, const half_t* k_i
         else
             rope_kernel<1, false, P><<<g, b, 0, s>>>(q_in, q_out, hq, k_in, k_out, hk, nullptr,
                                                      cos_t, sin_t, T, d, inv);
+    }
+    return launch_status();
+}
+
+int launch_qk_norm_rope(half_t* q, int64_t Hq, half_t* k, int64_t Hkv, const half_t* wq,
+                        const half_t* wk, const int64_t* positions, int64_t T, int64_t hd,
+                        float eps, float w_bias, const InvFreq& inv, hipStream_t s) {
+    const int64_t grid = ceil_div(T, kTokensPerWg);
+    if (grid > kMaxGridX) return MI_ERR_UNSUPPORTED;
+    const dim3 g(static_cast<unsigned>(grid)), b(256);
+    const int hq = static_cast<int>(Hq), hk = static_cast<int>(Hkv);
+    constexpr int P = kTokensPerWg;
+    switch (hd) {
+#define MI_QKN_CASE(HD)                                                                         \
+    case HD:                                                                                    \
+        qk_norm_rope_kernel<HD / 16, P><<<g, b, 0, s>>>(q, hq, k, hk, wq, wk, positions, T, eps, \
+                                                       w_bias, inv);                            \
+        break;
+        MI_QKN_CASE(16)
+        MI_QKN_CASE(32)
+        MI_QKN_CASE(64)
+        MI_QKN_CASE(128)
+        MI_QKN_CASE(256)
+        MI_QKN_CASE(512)
+#undef MI_QKN_CASE
+        default: return MI_ERR_UNSUPPORTED;
     }
     return launch_status();
 }
@@ -321,4 +464,36 @@ extern "C" int mi_rope_neox_qk_f16(void* q, void* k, const int64_t* positions,
                            static_cast<const half_t*>(k), static_cast<half_t*>(k), Hkv,
                            positions, nullptr, nullptr, T, head_dim, inv,
                            mi::as_stream(stream));
+}
+
+extern "C" int mi_qk_norm_rope_f16(void* q, void* k, const void* q_weight, const void* k_weight,
+                                   const int64_t* positions, const float* inv_freq_host,
+                                   int64_t T, int64_t Hq, int64_t Hkv, int64_t head_dim,
+                                   float eps, int add_one, void* stream) {
+    if (T < 0 || Hq < 0 || Hkv < 0 || head_dim < 0) return MI_ERR_INVALID_ARGUMENT;
+    if (T == 0 || Hq + Hkv == 0) return MI_OK;
+    if (!positions || (Hq > 0 && (!q || !q_weight)) || (Hkv > 0 && (!k || !k_weight)))
+        return MI_ERR_INVALID_ARGUMENT;
+    if (!mi::heads_ok(Hq, Hkv, head_dim)) return MI_ERR_UNSUPPORTED;
+    if (Hq > 0 && Hkv > 0 &&
+        mi::overlaps(q, T * Hq * head_dim * 2, k, T * Hkv * head_dim * 2))
+        return MI_ERR_ALIASING;
+    mi::InvFreq inv;
+    if (!mi::load_inv_freq(inv_freq_host, head_dim / 2, inv)) return MI_ERR_INVALID_ARGUMENT;
+    const bool aligned = (Hq == 0 || (mi::aligned16(q) && mi::aligned16(q_weight))) &&
+                         (Hkv == 0 || (mi::aligned16(k) && mi::aligned16(k_weight)));
+    if (!aligned) return MI_ERR_UNSUPPORTED;
+    // With no Q heads, run K through the Q slot (the kernel has one code path).
+    if (Hq == 0) {
+        q = k;
+        q_weight = k_weight;
+        Hq = Hkv;
+        k = nullptr;
+        k_weight = nullptr;
+        Hkv = 0;
+    }
+    return mi::launch_qk_norm_rope(static_cast<half_t*>(q), Hq, static_cast<half_t*>(k), Hkv,
+                                   static_cast<const half_t*>(q_weight),
+                                   static_cast<const half_t*>(k_weight), positions, T, head_dim,
+                                   eps, add_one ? 1.0f : 0.0f, inv, mi::as_stream(stream));
 }

@@ -167,40 +167,28 @@ __global__ __launch_bounds__(256) void softmax_finish_kernel(const half_t* x, ha
     write_range<VEC>(x + row * D, y + row * D, b, e, M, 1.0f / S);
 }
 
-// Split plan for few long rows: aim for >= 2048 workgroups and chunks of
-// >= 2048 elements, chunk a multiple of 8 so vector accesses stay aligned.
-// Returns the number of chunks per row (1 = one workgroup per row, no
-// workspace).
-int64_t split_plan(int64_t N, int64_t D, int64_t& chunk) {
+enum class Plan { kRow, kTwoPass };
+
+// Few long rows are split into chunks: aim for >= 2048 workgroups and chunks
+// of >= 2048 elements, chunk a multiple of 8 so vector accesses stay aligned.
+Plan plan(int64_t N, int64_t D, int64_t& splits, int64_t& chunk) {
+    splits = 1;
     chunk = D;
-    if (N >= kSplitMaxRows || D < 8192) return 1;
-    int64_t splits = ceil_div(2048, N);
-    if (splits > kMaxSplits) splits = kMaxSplits;
+    if (N >= kSplitMaxRows || D < 8192) return Plan::kRow;
+    int64_t sp = ceil_div(2048, N);
+    if (sp > kMaxSplits) sp = kMaxSplits;
     const int64_t max_by_len = D / 2048 > 1 ? D / 2048 : 1;
-    if (splits > max_by_len) splits = max_by_len;
-    chunk = ceil_div(ceil_div(D, splits), 8) * 8;
-    return ceil_div(D, chunk);
+    if (sp > max_by_len) sp = max_by_len;
+    chunk = ceil_div(ceil_div(D, sp), 8) * 8;
+    splits = ceil_div(D, chunk);
+    return Plan::kTwoPass;
 }
 
+// Workspace of a split plan: one (max, sum) pair per chunk.
 int64_t workspace_bytes(int64_t N, int64_t D) {
-    int64_t chunk;
-    const int64_t splits = split_plan(N, D, chunk);
-    return splits > 1 ? N * splits * 2 * static_cast<int64_t>(sizeof(float)) : 0;
-}
-
-template <int VEC>
-void launch_softmax(const half_t* x, half_t* y, int64_t N, int64_t D, float* ws, hipStream_t s) {
-    int64_t chunk;
-    const int64_t splits = split_plan(N, D, chunk);
-    if (splits == 1) {
-        const int64_t want = ceil_div(D, VEC);
-        int threads = static_cast<int>(ceil_div(want < 1024 ? want : 1024, kWave) * kWave);
-        softmax_row_kernel<VEC><<<dim3(static_cast<unsigned>(N)), dim3(threads), 0, s>>>(x, y, D);
-        return;
-    }
-    const dim3 g(static_cast<unsigned>(splits), static_cast<unsigned>(N));
-    softmax_partial_kernel<VEC><<<g, dim3(256), 0, s>>>(x, ws, D, chunk);
-    softmax_finish_kernel<VEC><<<g, dim3(256), 0, s>>>(x, y, ws, D, chunk);
+    int64_t splits, chunk;
+    if (plan(N, D, splits, chunk) == Plan::kRow) return 0;
+    return N * splits * 2 * static_cast<int64_t>(sizeof(float));
 }
 
 int softmax_checked(const void* x, void* y, int64_t N, int64_t D, void* ws, int64_t ws_bytes,
@@ -218,12 +206,32 @@ int softmax_checked(const void* x, void* y, int64_t N, int64_t D, void* ws, int6
     }
     const auto* xh = static_cast<const half_t*>(x);
     auto* yh = static_cast<half_t*>(y);
-    auto* w = static_cast<float*>(ws);
+    auto* part = static_cast<float*>(ws);
     const hipStream_t s = as_stream(stream);
-    if (D % 8 == 0 && aligned16(x) && aligned16(y))
-        launch_softmax<8>(xh, yh, N, D, w, s);
-    else
-        launch_softmax<1>(xh, yh, N, D, w, s);
+    const bool vec = D % 8 == 0 && aligned16(x) && aligned16(y);
+    int64_t splits, chunk;
+    switch (plan(N, D, splits, chunk)) {
+        case Plan::kRow: {
+            const int64_t want = ceil_div(D, vec ? 8 : 1);
+            const int threads = static_cast<int>(ceil_div(want < 1024 ? want : 1024, kWave) * kWave);
+            if (vec)
+                softmax_row_kernel<8><<<dim3(static_cast<unsigned>(N)), dim3(threads), 0, s>>>(xh, yh, D);
+            else
+                softmax_row_kernel<1><<<dim3(static_cast<unsigned>(N)), dim3(threads), 0, s>>>(xh, yh, D);
+            break;
+        }
+        case Plan::kTwoPass: {
+            const dim3 g(static_cast<unsigned>(splits), static_cast<unsigned>(N));
+            if (vec) {
+                softmax_partial_kernel<8><<<g, dim3(256), 0, s>>>(xh, part, D, chunk);
+                softmax_finish_kernel<8><<<g, dim3(256), 0, s>>>(xh, yh, part, D, chunk);
+            } else {
+                softmax_partial_kernel<1><<<g, dim3(256), 0, s>>>(xh, part, D, chunk);
+                softmax_finish_kernel<1><<<g, dim3(256), 0, s>>>(xh, yh, part, D, chunk);
+            }
+            break;
+        }
+    }
     return launch_status();
 }
 
@@ -243,9 +251,8 @@ extern "C" int mi_softmax_ws_f16(const void* x, void* y, int64_t N, int64_t D, v
 extern "C" int mi_softmax_f16(const void* x, void* y, int64_t N, int64_t D, void* stream) {
     const int64_t need = (N > 0 && D > 0) ? mi::workspace_bytes(N, D) : 0;
     if (need == 0) return mi::softmax_checked(x, y, N, D, nullptr, 0, stream);
-    // The (max, sum) pairs live in a stream-ordered allocation from the
-    // device's default pool: concurrent calls on other streams get their own,
-    // and after the first call the pool hands back cached memory.
+    // Few long rows: a stream-ordered workspace from the device's default
+    // pool (concurrent calls on other streams get their own).
     if (!x || !y) return MI_ERR_INVALID_ARGUMENT;
     const hipStream_t s = mi::as_stream(stream);
     void* ws = nullptr;

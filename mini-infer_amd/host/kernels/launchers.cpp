@@ -85,6 +85,14 @@ void launch_rope_qk(__half* q, __half* k, const int64_t* positions_d, const floa
           "launch_rope_qk");
 }
 
+void launch_qk_norm_rope(__half* q, __half* k, const __half* q_weight, const __half* k_weight,
+                         const int64_t* positions_d, const float* inv_freq_h, int T, int Hq,
+                         int Hkv, int head_dim, float eps, int add_one, hipStream_t stream) {
+    check(mi_qk_norm_rope_f16(q, k, q_weight, k_weight, positions_d, inv_freq_h, T, Hq, Hkv,
+                              head_dim, eps, add_one, sv(stream)),
+          "launch_qk_norm_rope");
+}
+
 void launch_swiglu(const __half* gate, const __half* up, __half* out, int n, hipStream_t stream) {
     check(mi_swiglu_f16(gate, up, out, n, sv(stream)), "launch_swiglu");
 }

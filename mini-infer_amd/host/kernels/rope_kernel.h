@@ -31,5 +31,13 @@ void launch_rope_precompute_batched(const float* inv_freq_h, const int64_t* posi
 void launch_rope_qk(__half* q, __half* k, const int64_t* positions_d, const float* inv_freq_h,
                     int T, int Hq, int Hkv, int head_dim, hipStream_t stream);
 
+// In place: per-head RMSNorm of q / k with q_weight / k_weight [head_dim]
+// (f(w) = w, or 1 + w when add_one), rounded to fp16, then the NeoX rotation
+// of launch_rope_qk -- the Q/K-norm + RoPE sequence in one pass.
+// head_dim must be 16, 32, 64, 128, 256 or 512.
+void launch_qk_norm_rope(__half* q, __half* k, const __half* q_weight, const __half* k_weight,
+                         const int64_t* positions_d, const float* inv_freq_h, int T, int Hq,
+                         int Hkv, int head_dim, float eps, int add_one, hipStream_t stream);
+
 }  // namespace kernels
 }  // namespace mini_infer

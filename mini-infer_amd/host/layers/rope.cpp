@@ -85,9 +85,10 @@ Tensor RoPE::forward_batched(const Tensor& x, const std::vector<int64_t>& positi
     return rotate_(x, positions, "RoPE::forward_batched");
 }
 
-void RoPE::forward_qk_inplace(Tensor& q, Tensor& k, const Tensor& positions) const {
+void RoPE::check_qk_(const Tensor& q, const Tensor& k, const Tensor& positions, const char* who,
+                     int64_t& Tq, int64_t& Hq, int64_t& Hk) const {
     auto split = [&](const Tensor& t, const char* name, int64_t& T, int64_t& H) {
-        const std::string w = std::string("RoPE::forward_qk_inplace(") + name + ")";
+        const std::string w = std::string(who) + "(" + name + ")";
         if (t.dtype() != DType::FP16) throw std::runtime_error(w + ": only FP16 supported");
         if (t.ndim() < 3) throw std::runtime_error(w + ": expect [..., H, head_dim]");
         if (t.shape().back() != head_dim_) throw std::runtime_error(w + ": head_dim mismatch");
@@ -98,18 +99,40 @@ void RoPE::forward_qk_inplace(Tensor& q, Tensor& k, const Tensor& positions) con
         T = 1;
         for (int i = 0; i < t.ndim() - 2; ++i) T *= t.shape()[i];
     };
-    int64_t Tq, Hq, Tk, Hk;
+    int64_t Tk;
     split(q, "q", Tq, Hq);
     split(k, "k", Tk, Hk);
-    if (Tq != Tk) throw std::runtime_error("RoPE::forward_qk_inplace: q and k token counts differ");
+    if (Tq != Tk) throw std::runtime_error(std::string(who) + ": q and k token counts differ");
     if (positions.dtype() != DType::INT64 || positions.numel() != Tq ||
         !positions.device().is_cuda() || positions.device().index != device_index_)
-        throw std::runtime_error(
-            "RoPE::forward_qk_inplace: positions must be int64 [T] on the layer's GPU");
+        throw std::runtime_error(std::string(who) +
+                                 ": positions must be int64 [T] on the layer's GPU");
+}
+
+void RoPE::forward_qk_inplace(Tensor& q, Tensor& k, const Tensor& positions) const {
+    int64_t T, Hq, Hk;
+    check_qk_(q, k, positions, "RoPE::forward_qk_inplace", T, Hq, Hk);
     kernels::launch_rope_qk(static_cast<__half*>(q.data()), static_cast<__half*>(k.data()),
                             static_cast<const int64_t*>(positions.data()), inv_freq_.data(),
-                            static_cast<int>(Tq), static_cast<int>(Hq), static_cast<int>(Hk),
+                            static_cast<int>(T), static_cast<int>(Hq), static_cast<int>(Hk),
                             head_dim_, 0);
+}
+
+void RoPE::forward_qk_norm_inplace(Tensor& q, Tensor& k, const RMSNorm& q_norm,
+                                   const RMSNorm& k_norm, const Tensor& positions) const {
+    int64_t T, Hq, Hk;
+    check_qk_(q, k, positions, "RoPE::forward_qk_norm_inplace", T, Hq, Hk);
+    if (q_norm.dim() != head_dim_ || k_norm.dim() != head_dim_)
+        throw std::runtime_error("RoPE::forward_qk_norm_inplace: norm dim must equal head_dim");
+    if (q_norm.add_one() != k_norm.add_one() || q_norm.eps() != k_norm.eps())
+        throw std::runtime_error(
+            "RoPE::forward_qk_norm_inplace: q and k norms must share eps and add_one");
+    kernels::launch_qk_norm_rope(static_cast<__half*>(q.data()), static_cast<__half*>(k.data()),
+                                 static_cast<const __half*>(q_norm.weight().data()),
+                                 static_cast<const __half*>(k_norm.weight().data()),
+                                 static_cast<const int64_t*>(positions.data()), inv_freq_.data(),
+                                 static_cast<int>(T), static_cast<int>(Hq), static_cast<int>(Hk),
+                                 head_dim_, q_norm.eps(), q_norm.add_one() ? 1 : 0, 0);
 }
 
 }  // namespace mini_infer

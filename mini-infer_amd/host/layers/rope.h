@@ -10,6 +10,7 @@
 #include <vector>
 
 #include "core/tensor.h"
+#include "layers/rmsnorm.h"
 
 namespace mini_infer {
 
@@ -28,6 +29,12 @@ public:
     // on the same GPU.
     void forward_qk_inplace(Tensor& q, Tensor& k, const Tensor& positions) const;
 
+    // Gemma-3 style Q/K RMSNorm fused in front of the rotation, in place:
+    // q = rope(q_norm(q)), k = rope(k_norm(k)), per head, in one pass.  The
+    // norms' dim must equal head_dim (shapes as forward_qk_inplace).
+    void forward_qk_norm_inplace(Tensor& q, Tensor& k, const RMSNorm& q_norm,
+                                 const RMSNorm& k_norm, const Tensor& positions) const;
+
     void set_theta_base(float theta_base);
 
     int head_dim() const { return head_dim_; }
@@ -38,6 +45,8 @@ public:
 private:
     void recompute_inv_freq_();
     Tensor rotate_(const Tensor& x, const std::vector<int64_t>& flat_positions, const char* who);
+    void check_qk_(const Tensor& q, const Tensor& k, const Tensor& positions, const char* who,
+                   int64_t& T, int64_t& Hq, int64_t& Hk) const;
 
     int head_dim_;
     float theta_base_;

@@ -35,6 +35,8 @@ SIGNATURES = {
     "mi_rope_tables_f16": [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _c_void_p],
     "mi_rope_neox_qk_f16": [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64, _i64,
                             _c_void_p],
+    "mi_qk_norm_rope_f16": [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+                            _i64, _i64, _i64, _i64, _f32, _int, _c_void_p],
     "mi_swiglu_f16": [_c_void_p, _c_void_p, _c_void_p, _i64, _c_void_p],
     "mi_gelu_tanh_f16": [_c_void_p, _c_void_p, _i64, _c_void_p],
     "mi_geglu_f16": [_c_void_p, _c_void_p, _c_void_p, _i64, _c_void_p],
@@ -233,6 +235,37 @@ def rope_neox_qk(q, k, positions, inv_freq, stream=None):
     kp = _ptr(k) if k is not None else ctypes.c_void_p(0)
     _check(load_library().mi_rope_neox_qk_f16(_ptr(q), kp, _ptr(positions), p, T, Hq, Hkv, hd,
                                               _stream(stream)), "mi_rope_neox_qk_f16")
+    return q, k
+
+
+def qk_norm_rope(q, k, q_weight, k_weight, positions, inv_freq, eps: float = 1e-6,
+                 add_one: bool = False, stream=None):
+    """In place: per-head RMSNorm of q [T, Hq, hd] / k [T, Hkv, hd] (k may be
+    None) with q_weight / k_weight [hd], then NeoX RoPE at device positions."""
+    torch = _torch()
+    _need(q, _f16(), "q"); _need(q_weight, _f16(), "q_weight")
+    _need(positions, torch.int64, "positions")
+    if q.dim() != 3:
+        raise ValueError("q must be 3-D [T, Hq, hd]")
+    T, Hq, hd = q.shape
+    if q_weight.numel() != hd:
+        raise ValueError("q_weight must hold head_dim entries")
+    Hkv = 0
+    if k is not None:
+        _need(k, _f16(), "k"); _need(k_weight, _f16(), "k_weight")
+        if k.dim() != 3 or k.shape[0] != T or k.shape[2] != hd or k_weight.numel() != hd:
+            raise ValueError("k must be [T, Hkv, hd] with k_weight [hd]")
+        Hkv = k.shape[1]
+    if positions.numel() != T:
+        raise ValueError("positions must hold T entries")
+    arr, p = _inv_freq_buffer(inv_freq)
+    if arr.size != hd // 2:
+        raise ValueError("inv_freq must hold head_dim/2 entries")
+    kp = _ptr(k) if k is not None else ctypes.c_void_p(0)
+    kw = _ptr(k_weight) if k is not None else ctypes.c_void_p(0)
+    _check(load_library().mi_qk_norm_rope_f16(_ptr(q), kp, _ptr(q_weight), kw, _ptr(positions), p,
+                                              T, Hq, Hkv, hd, eps, int(bool(add_one)),
+                                              _stream(stream)), "mi_qk_norm_rope_f16")
     return q, k
 
 

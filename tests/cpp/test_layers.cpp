@@ -175,6 +175,36 @@ void gpu_checks() {
         EXPECT(throws([&] { rope.forward(xd, std::vector<int64_t>(S + 1)); }), "bad positions");
         EXPECT(throws([] { mini_infer::RoPE bad(7); }), "odd head_dim");
     }
+    // --- fused Q/K RMSNorm + RoPE (src/layers/attention.cpp:754-780) -------
+    {
+        const int T = 40, Hq = 28, Hk = 4, D = 128, half = D / 2;
+        mini_infer::RoPE rope(D, 1e6f, 0);
+        mini_infer::RMSNorm qn(D, eps, 0), kn(D, eps, 0);
+        Tensor wq = reftest_f16({D}, 0.5f, 31), wk = reftest_f16({D}, 0.5f, 32);
+        qn.set_weight(wq);
+        kn.set_weight(wk);
+        Tensor q = reftest_f16({T, Hq, D}, 1.0f, 33), k = reftest_f16({T, Hk, D}, 1.0f, 34);
+        std::vector<int64_t> pos(T);
+        mio_fill_uniform_int64(pos.data(), T, 35, 0, 31000);
+        std::vector<uint16_t> c(T * half), sn(T * half);
+        mio_rope_tables(rope.inv_freq().data(), pos.data(), c.data(), sn.data(), T, half);
+        auto ref_of = [&](const Tensor& x, const Tensor& w, int H) {
+            std::vector<float> n(static_cast<size_t>(T) * H * D), y(n.size());
+            mio_rmsnorm(bits(x), bits(w), n.data(), static_cast<int64_t>(T) * H, D, eps, 0, 1);
+            std::vector<uint16_t> n16(n.size());
+            mio_f32_to_f16_array(n.data(), n16.data(), static_cast<int64_t>(n.size()));
+            mio_rope_neox(n16.data(), c.data(), sn.data(), y.data(), T, H, D, 1);
+            return y;
+        };
+        const std::vector<float> rq = ref_of(q, wq, Hq), rk = ref_of(k, wk, Hk);
+        Tensor pt(std::vector<int64_t>{T}, DType::INT64, Device::cpu());
+        std::memcpy(pt.data(), pos.data(), pos.size() * 8);
+        Tensor pd = pt.to(Device::cuda(0));
+        Tensor qd = q.to(Device::cuda(0)), kd = k.to(Device::cuda(0));
+        rope.forward_qk_norm_inplace(qd, kd, qn, kn, pd);
+        EXPECT(close(qd, rq, "RoPE::forward_qk_norm_inplace (q)"), "qk-norm rope q");
+        EXPECT(close(kd, rk, "RoPE::forward_qk_norm_inplace (k)"), "qk-norm rope k");
+    }
     // --- gated activations (src/layers/mlp.cpp:270-292) --------------------
     std::printf("[gpu] MLP gated activation\n");
     {

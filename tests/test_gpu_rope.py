@@ -133,3 +133,59 @@ def test_position_zero_is_identity(mk, orc, dev):
     qd = to_dev(q, dev)
     mk.rope_neox_qk(qd, None, to_dev(np.zeros(4, np.int64), dev), orc.rope_inv_freq(128, 1e6))
     assert_bits_equal(to_host(qd), q, what="identity")
+
+
+def _qk_norm_rope_ref(orc, x, w, pos, inv, eps=1e-6, add_one=False):
+    """Reference composition: per-head RMSNorm written as fp16, then RoPE."""
+    T, H, hd = x.shape
+    n = orc.rmsnorm(x.reshape(T * H, hd), w, eps, add_one, nthreads=8)
+    n16 = orc.f32_to_f16(n).reshape(T, H, hd)
+    c, s = orc.rope_tables(inv, pos)
+    return orc.rope_neox(n16, c, s, nthreads=8), n16
+
+
+@pytest.mark.parametrize("T,Hq,Hkv,hd", [(6064, 28, 4, 128), (37, 8, 2, 64), (5, 3, 1, 256),
+                                         (9, 2, 2, 16), (3, 4, 0, 128), (4, 0, 2, 128),
+                                         (2, 2, 1, 512), (11, 5, 3, 32)])
+def test_qk_norm_rope(mk, orc, dev, T, Hq, Hkv, hd):
+    """Fused Q/K RMSNorm + RoPE == the reference's norm-then-rope composition
+    (src/layers/attention.cpp:754-780), within rtol = atol = 1e-3."""
+    _case(f"qk_norm_rope T={T} Hq={Hq} Hkv={Hkv} hd={hd}")
+    rng = np.random.default_rng(T * 7 + hd)
+    q = normal_f16(rng, (T, Hq, hd))
+    k = normal_f16(rng, (T, Hkv, hd))
+    wq = normal_f16(rng, (hd,), 1.0, 0.1)
+    wk = normal_f16(rng, (hd,), 1.0, 0.1)
+    pos = rng.integers(0, 32000, T).astype(np.int64)
+    inv = orc.rope_inv_freq(hd, 1e6)
+    qd, kd = to_dev(q, dev), to_dev(k, dev)
+    mk.qk_norm_rope(qd, kd if Hkv else None, to_dev(wq, dev), to_dev(wk, dev), to_dev(pos, dev), inv)
+    if Hq:
+        ref, _ = _qk_norm_rope_ref(orc, q, wq, pos, inv)
+        assert_close(to_host(qd), ref, what="q")
+    if Hkv:
+        ref, _ = _qk_norm_rope_ref(orc, k, wk, pos, inv)
+        assert_close(to_host(kd), ref, what="k")
+
+
+def test_qk_norm_rope_vs_two_launches(mk, orc, dev):
+    """Against this library's own two-launch sequence (rmsnorm then rope):
+    identical except where the normalised fp16 value sits on a rounding
+    boundary (different fp32 summation order), never more than 1 ulp there."""
+    _case("qk_norm_rope vs rmsnorm + rope_neox_qk")
+    rng = np.random.default_rng(71)
+    T, Hq, Hkv, hd = 512, 28, 4, 128
+    q = normal_f16(rng, (T, Hq, hd)); k = normal_f16(rng, (T, Hkv, hd))
+    wq = normal_f16(rng, (hd,), 1.0, 0.1); wk = normal_f16(rng, (hd,), 1.0, 0.1)
+    pos = rng.integers(0, 32000, T).astype(np.int64)
+    inv = orc.rope_inv_freq(hd, 1e6)
+    wqd, wkd, pd = to_dev(wq, dev), to_dev(wk, dev), to_dev(pos, dev)
+    q1, k1 = to_dev(q, dev), to_dev(k, dev)
+    mk.qk_norm_rope(q1, k1, wqd, wkd, pd, inv)
+    q2, k2 = to_dev(q, dev), to_dev(k, dev)
+    mk.rmsnorm(q2.view(T * Hq, hd), wqd, y=q2.view(T * Hq, hd))
+    mk.rmsnorm(k2.view(T * Hkv, hd), wkd, y=k2.view(T * Hkv, hd))
+    mk.rope_neox_qk(q2, k2, pd, inv)
+    a, b = to_host(q1), to_host(q2)
+    assert_close(a, b.astype(np.float32), what="q vs two launches")
+    assert (a.view(np.uint16) == b.view(np.uint16)).mean() > 0.99

@@ -40,7 +40,8 @@ def test_softmax_lm_head_config(mk, orc, dev):
 
 
 @pytest.mark.parametrize("N,D", [(1, 1), (3, 7), (57344, 512), (600, 10000), (2, 8192),
-                                 (5, 100003), (511, 9000), (1, 300000), (130, 24)])
+                                 (5, 100003), (511, 9000), (1, 300000), (130, 24), (2, 600000),
+                                 (3, 8200), (64, 16384)])
 def test_softmax_shapes(mk, orc, dev, N, D):
     _case(f"softmax [{N},{D}]")
     rng = np.random.default_rng(N * 31 + D)
@@ -100,5 +101,36 @@ def test_softmax_workspace_variant(mk, orc, dev):
     y1 = to_host(mk.softmax(xd, workspace=ws))
     y2 = to_host(mk.softmax(xd))
     assert_bits_equal(y1, y2, what="ws vs pool")
+    for _ in range(3):
+        assert_bits_equal(to_host(mk.softmax(xd, workspace=ws)), y1, what="repeat")
     with pytest.raises(RuntimeError, match="status -1"):
         mk.softmax(xd, workspace=ws[: nb - 8])
+
+
+def test_softmax_graph_replay(mk, orc, dev):
+    """The split-row kernels inside a captured graph, replayed several times
+    with eager work in between; every replay matches the eager call."""
+    _case("softmax graph replay [64,152064]")
+    import torch
+    rng = np.random.default_rng(55)
+    x = normal_f16(rng, (64, 152064), 0, 4)
+    xd = to_dev(x, dev)
+    ws = torch.zeros(mk.softmax_workspace_bytes(64, 152064), dtype=torch.uint8, device=dev)
+    y = torch.empty_like(xd)
+    ref = to_host(mk.softmax(xd, workspace=ws))
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        mk.softmax(xd, y=y, workspace=ws)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        mk.softmax(xd, y=y, workspace=ws)
+    for i in range(4):
+        y.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        assert_bits_equal(to_host(y), ref, what=f"replay {i}")
+        mk.softmax(xd, workspace=ws)  # eager call between replays
+    assert_close(ref, orc.softmax(x, nthreads=8), what="vs oracle")
