@@ -5,6 +5,10 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <map>
+#include <mutex>
+#include <utility>
+
 #include "mi_kernels.h"
 
 namespace mi {
@@ -28,5 +32,34 @@ inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s);
 constexpr int64_t kMaxGridX = 2147483647;  // HIP grid.x limit (2^31 - 1)
 
 inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// Workgroups of `kernel` (launched with `threads` lanes) the current device
+// holds at once: occupancy per CU x CU count, queried once per
+// (kernel, device) and cached.  0 if the runtime cannot say.
+inline int64_t resident_workgroups(const void* kernel, int threads) {
+    static std::mutex mu;
+    static std::map<std::pair<const void*, int>, int64_t> cache;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 0;
+    std::lock_guard<std::mutex> lock(mu);
+    const auto key = std::make_pair(kernel, dev * 4096 + threads);
+    auto it = cache.find(key);
+    if (it != cache.end()) return it->second;
+    int per_cu = 0, cus = 0;
+    int64_t cap = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads, 0) == hipSuccess &&
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess)
+        cap = static_cast<int64_t>(per_cu) * cus;
+    cache[key] = cap;
+    return cap;
+}
+
+// How full the GPU's last round of workgroups is when `groups` workgroups
+// run `cap` at a time: groups / (rounds * cap), 1.0 = no idle tail.
+inline double round_fill(int64_t groups, int64_t cap) {
+    if (cap <= 0 || groups <= 0) return 0.0;
+    const int64_t rounds = (groups + cap - 1) / cap;
+    return static_cast<double>(groups) / static_cast<double>(rounds * cap);
+}
 
 }  // namespace mi

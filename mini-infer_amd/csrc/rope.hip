@@ -19,7 +19,7 @@
 // fp32 sincos implementation.
 //
 // Design (HBM-bound: 8 bytes/element in place, + 8 bytes/token of positions):
-//   a 256-lane workgroup takes kTokensPerWg tokens.  Every lane first issues
+//   a 256-lane workgroup takes 1-8 tokens.  Every lane first issues
 //   the 16-byte loads of its (token, head, 8-element) units -- x[i..i+7] and
 //   x[h+i..h+i+7] -- then the workgroup builds each token's cos/sin row in LDS
 //   once (instead of once per head), and after a single barrier each lane
@@ -40,8 +40,11 @@ struct InvFreq {
     float v[kMaxHalf];
 };
 
+#ifndef MI_ROPE_GUARD
+#define MI_ROPE_GUARD 9.5367431640625e-07f  // 2^-20
+#endif
 __device__ __forceinline__ bool near_half_boundary(float v) {
-    const float d = v * 9.5367431640625e-07f;  // 2^-20 relative
+    const float d = v * MI_ROPE_GUARD;  // relative half-width of the guard window
     return to_half(v - d) != to_half(v + d);
 }
 
@@ -83,11 +86,9 @@ __device__ __forceinline__ void set_elem(typename HVec<VEC>::T& v, int k, float 
     if constexpr (VEC == 1) v = to_half(f); else v[k] = to_half(f);
 }
 
-#ifndef MI_ROPE_TOKENS_PER_WG
-#define MI_ROPE_TOKENS_PER_WG 4
-#endif
-constexpr int kTokensPerWg = MI_ROPE_TOKENS_PER_WG;
-constexpr int kPrefetch = 4;  // units per lane whose loads are issued up front
+// Tokens per 256-lane workgroup, chosen per launch from {1, 2, 4, 8} (see
+// pick_tokens_per_wg); each lane issues the loads of TPW units (one per
+// token for a 256-unit token, the Qwen2.5 case) before the table work.
 
 // TPW tokens per 256-lane workgroup.  Sources q_in/k_in, destinations
 // q_out/k_out (may equal the sources).  FROM_POS: cos/sin from positions +
@@ -127,11 +128,11 @@ __global__ __launch_bounds__(256) void rope_kernel(const half_t* q_in, half_t* q
         return t * (2 * kMaxHalf) + c * VEC;  // offset of this unit's cos in cs
     };
 
-    // 1. issue up to kPrefetch units' loads per lane before the table work,
+    // 1. issue up to TPW units' loads per lane before the table work,
     //    so HBM latency overlaps the sincos evaluation
-    typename V::T x1[kPrefetch], x2[kPrefetch];
+    typename V::T x1[TPW], x2[TPW];
 #pragma unroll
-    for (int p = 0; p < kPrefetch; ++p) {
+    for (int p = 0; p < TPW; ++p) {
         const int u = threadIdx.x + p * 256;
         if (u < units) {
             const half_t* src;
@@ -189,11 +190,11 @@ __global__ __launch_bounds__(256) void rope_kernel(const half_t* q_in, half_t* q
         }
     };
 #pragma unroll
-    for (int p = 0; p < kPrefetch; ++p) {
+    for (int p = 0; p < TPW; ++p) {
         const int u = threadIdx.x + p * 256;
         if (u < units) rotate(u, x1[p], x2[p]);
     }
-    for (int u = threadIdx.x + kPrefetch * 256; u < units; u += 256) {
+    for (int u = threadIdx.x + TPW * 256; u < units; u += 256) {
         const half_t* src;
         half_t* dst;
         locate(u, src, dst);
@@ -245,9 +246,9 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(half_t* q, int Hq, ha
                     : q + (tok * Hq + h) * static_cast<int64_t>(HD);
     };
 
-    h8 x1[kPrefetch], x2[kPrefetch];
+    h8 x1[TPW], x2[TPW];
 #pragma unroll
-    for (int p = 0; p < kPrefetch; ++p) {
+    for (int p = 0; p < TPW; ++p) {
         const int u = threadIdx.x + p * 256;
         x1[p] = h8(0);
         x2[p] = h8(0);
@@ -303,8 +304,8 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(half_t* q, int Hq, ha
         st8_stream(hp + HALF + c * 8, y2);
     };
 #pragma unroll
-    for (int p = 0; p < kPrefetch; ++p) process(threadIdx.x + p * 256, x1[p], x2[p]);
-    for (int base = kPrefetch * 256; base < units; base += 256) {
+    for (int p = 0; p < TPW; ++p) process(threadIdx.x + p * 256, x1[p], x2[p]);
+    for (int base = TPW * 256; base < units; base += 256) {
         const int u = base + threadIdx.x;
         h8 a1 = h8(0), a2 = h8(0);
         if (u < units) {
@@ -339,31 +340,99 @@ bool load_inv_freq(const float* host, int64_t half, InvFreq& out) {
     return true;
 }
 
+// Tokens per workgroup: the candidate whose grid leaves the least idle tail
+// in the GPU's last round of resident workgroups, with a small charge per
+// extra round (each round repeats the load-latency / table / barrier ramp).
+// Measured on MI355X: T = 4096 -> 4 tokens (1024 workgroups, one round);
+// T = 6064 -> 8 (758 workgroups, one round) instead of 4 (1516, a second
+// round 18% full: 58% -> 68% of HBM peak).
+template <typename K1, typename K2, typename K4, typename K8>
+int pick_tokens_per_wg(int64_t T, K1 k1, K2 k2, K4 k4, K8 k8) {
+    const void* ks[4] = {reinterpret_cast<const void*>(k1), reinterpret_cast<const void*>(k2),
+                         reinterpret_cast<const void*>(k4), reinterpret_cast<const void*>(k8)};
+    int best = 1;
+    double best_fill = -1.0;
+    for (int i = 0, tpw = 1; i < 4; ++i, tpw *= 2) {
+        const int64_t groups = ceil_div(T, tpw), cap = resident_workgroups(ks[i], 256);
+        const double f = round_fill(groups, cap) -
+                         (cap > 0 ? 0.05 * static_cast<double>(ceil_div(groups, cap) - 1) : 0.0);
+        if (f > best_fill + 1e-9) {
+            best_fill = f;
+            best = tpw;
+        }
+    }
+    return best;
+}
+
+template <int VEC, bool FROM_POS>
+int launch_rope_t(const half_t* q_in, half_t* q_out, int hq, const half_t* k_in, half_t* k_out,
+                  int hk, const int64_t* positions, const half_t* cos_t, const half_t* sin_t,
+                  int64_t T, int d, const InvFreq& inv, hipStream_t s) {
+    const int tpw = pick_tokens_per_wg(T, rope_kernel<VEC, FROM_POS, 1>,
+                                       rope_kernel<VEC, FROM_POS, 2>,
+                                       rope_kernel<VEC, FROM_POS, 4>,
+                                       rope_kernel<VEC, FROM_POS, 8>);
+    const int64_t grid = ceil_div(T, tpw);
+    if (grid > kMaxGridX) return MI_ERR_UNSUPPORTED;
+    const dim3 g(static_cast<unsigned>(grid)), b(256);
+    switch (tpw) {
+#define MI_ROPE_CASE(P)                                                                        \
+    case P:                                                                                    \
+        rope_kernel<VEC, FROM_POS, P><<<g, b, 0, s>>>(q_in, q_out, hq, k_in, k_out, hk,        \
+                                                      positions, cos_t, sin_t, T, d, inv);     \
+        break;
+        MI_ROPE_CASE(1)
+        MI_ROPE_CASE(2)
+        MI_ROPE_CASE(4)
+        MI_ROPE_CASE(8)
+#undef MI_ROPE_CASE
+        default: return MI_ERR_UNSUPPORTED;
+    }
+    return launch_status();
+}
+
 int launch_rope(const half_t* q_in, half_t* q_out, int64_t Hq, const half_t* k_in, half_t* k_out,
                 int64_t Hkv, const int64_t* positions, const half_t* cos_t, const half_t* sin_t,
                 int64_t T, int64_t hd, const InvFreq& inv, hipStream_t s) {
-    const int64_t grid = ceil_div(T, kTokensPerWg);
-    if (grid > kMaxGridX) return MI_ERR_UNSUPPORTED;
     const int64_t half = hd / 2;
     bool vec = (half % 8 == 0) && aligned16(q_in) && aligned16(q_out);
     if (Hkv > 0) vec = vec && aligned16(k_in) && aligned16(k_out);
-    const dim3 g(static_cast<unsigned>(grid)), b(256);
     const int hq = static_cast<int>(Hq), hk = static_cast<int>(Hkv), d = static_cast<int>(hd);
-    constexpr int P = kTokensPerWg;
     if (positions) {
         if (vec)
-            rope_kernel<8, true, P><<<g, b, 0, s>>>(q_in, q_out, hq, k_in, k_out, hk, positions,
-                                                    nullptr, nullptr, T, d, inv);
-        else
-            rope_kernel<1, true, P><<<g, b, 0, s>>>(q_in, q_out, hq, k_in, k_out, hk, positions,
-                                                    nullptr, nullptr, T, d, inv);
-    } else {
-        if (vec)
-            rope_kernel<8, false, P><<<g, b, 0, s>>>(q_in, q_out, hq, k_in, k_out, hk, nullptr,
-                                                     cos_t, sin_t, T, d, inv);
-        else
-            rope_kernel<1, false, P><<<g, b, 0, s>>>(q_in, q_out, hq, k_in, k_out, hk, nullptr,
-                                                     cos_t, sin_t, T, d, inv);
+            return launch_rope_t<8, true>(q_in, q_out, hq, k_in, k_out, hk, positions, nullptr,
+                                          nullptr, T, d, inv, s);
+        return launch_rope_t<1, true>(q_in, q_out, hq, k_in, k_out, hk, positions, nullptr,
+                                      nullptr, T, d, inv, s);
+    }
+    if (vec)
+        return launch_rope_t<8, false>(q_in, q_out, hq, k_in, k_out, hk, nullptr, cos_t, sin_t, T,
+                                       d, inv, s);
+    return launch_rope_t<1, false>(q_in, q_out, hq, k_in, k_out, hk, nullptr, cos_t, sin_t, T, d,
+                                   inv, s);
+}
+
+template <int CPH>
+int launch_qk_norm_rope_t(half_t* q, int hq, half_t* k, int hk, const half_t* wq,
+                          const half_t* wk, const int64_t* positions, int64_t T, float eps,
+                          float w_bias, const InvFreq& inv, hipStream_t s) {
+    const int tpw = pick_tokens_per_wg(T, qk_norm_rope_kernel<CPH, 1>, qk_norm_rope_kernel<CPH, 2>,
+                                       qk_norm_rope_kernel<CPH, 4>, qk_norm_rope_kernel<CPH, 8>);
+    const int64_t grid = ceil_div(T, tpw);
+    if (grid > kMaxGridX) return MI_ERR_UNSUPPORTED;
+    const dim3 g(static_cast<unsigned>(grid)), b(256);
+    switch (tpw) {
+#define MI_QKN_CASE(P)                                                                          \
+    case P:                                                                                     \
+        qk_norm_rope_kernel<CPH, P><<<g, b, 0, s>>>(q, hq, k, hk, wq, wk, positions, T, eps,     \
+                                                    w_bias, inv);                               \
+        break;
+        MI_QKN_CASE(1)
+        MI_QKN_CASE(2)
+        MI_QKN_CASE(4)
+        MI_QKN_CASE(8)
+#undef MI_QKN_CASE
+        default: return MI_ERR_UNSUPPORTED;
     }
     return launch_status();
 }
@@ -371,27 +440,16 @@ int launch_rope(const half_t* q_in, half_t* q_out, int64_t Hq, const half_t* k_i
 int launch_qk_norm_rope(half_t* q, int64_t Hq, half_t* k, int64_t Hkv, const half_t* wq,
                         const half_t* wk, const int64_t* positions, int64_t T, int64_t hd,
                         float eps, float w_bias, const InvFreq& inv, hipStream_t s) {
-    const int64_t grid = ceil_div(T, kTokensPerWg);
-    if (grid > kMaxGridX) return MI_ERR_UNSUPPORTED;
-    const dim3 g(static_cast<unsigned>(grid)), b(256);
     const int hq = static_cast<int>(Hq), hk = static_cast<int>(Hkv);
-    constexpr int P = kTokensPerWg;
     switch (hd) {
-#define MI_QKN_CASE(HD)                                                                         \
-    case HD:                                                                                    \
-        qk_norm_rope_kernel<HD / 16, P><<<g, b, 0, s>>>(q, hq, k, hk, wq, wk, positions, T, eps, \
-                                                       w_bias, inv);                            \
-        break;
-        MI_QKN_CASE(16)
-        MI_QKN_CASE(32)
-        MI_QKN_CASE(64)
-        MI_QKN_CASE(128)
-        MI_QKN_CASE(256)
-        MI_QKN_CASE(512)
-#undef MI_QKN_CASE
+        case 16: return launch_qk_norm_rope_t<1>(q, hq, k, hk, wq, wk, positions, T, eps, w_bias, inv, s);
+        case 32: return launch_qk_norm_rope_t<2>(q, hq, k, hk, wq, wk, positions, T, eps, w_bias, inv, s);
+        case 64: return launch_qk_norm_rope_t<4>(q, hq, k, hk, wq, wk, positions, T, eps, w_bias, inv, s);
+        case 128: return launch_qk_norm_rope_t<8>(q, hq, k, hk, wq, wk, positions, T, eps, w_bias, inv, s);
+        case 256: return launch_qk_norm_rope_t<16>(q, hq, k, hk, wq, wk, positions, T, eps, w_bias, inv, s);
+        case 512: return launch_qk_norm_rope_t<32>(q, hq, k, hk, wq, wk, positions, T, eps, w_bias, inv, s);
         default: return MI_ERR_UNSUPPORTED;
     }
-    return launch_status();
 }
 
 // (Hq + Hkv) * hd/2 must fit the int lane arithmetic of rope_kernel.
