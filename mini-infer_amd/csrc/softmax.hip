@@ -25,6 +25,14 @@ namespace {
 
 constexpr int kSplitMaxRows = 512;  // below this many rows, split each row
 constexpr int kMaxSplits = 64;      // chunk pairs of a row fit one wave
+#ifndef MI_SOFTMAX_TARGET_WGS
+#define MI_SOFTMAX_TARGET_WGS 2048
+#endif
+#ifndef MI_SOFTMAX_MIN_CHUNK
+#define MI_SOFTMAX_MIN_CHUNK 2048
+#endif
+constexpr int64_t kSplitTargetWgs = MI_SOFTMAX_TARGET_WGS;
+constexpr int64_t kMinChunk = MI_SOFTMAX_MIN_CHUNK;
 
 // Fold one loaded value group into the lane's online (m, s).
 template <int VEC>
@@ -171,13 +179,16 @@ enum class Plan { kRow, kTwoPass };
 
 // Few long rows are split into chunks: aim for >= 2048 workgroups and chunks
 // of >= 2048 elements, chunk a multiple of 8 so vector accesses stay aligned.
+// (Keeping a whole row in one workgroup's registers instead measured 2x
+// slower at [64, 152064]: a single CU sustains only ~12 GB/s, so 64 busy CUs
+// cannot feed HBM.)
 Plan plan(int64_t N, int64_t D, int64_t& splits, int64_t& chunk) {
     splits = 1;
     chunk = D;
     if (N >= kSplitMaxRows || D < 8192) return Plan::kRow;
-    int64_t sp = ceil_div(2048, N);
+    int64_t sp = ceil_div(kSplitTargetWgs, N);
     if (sp > kMaxSplits) sp = kMaxSplits;
-    const int64_t max_by_len = D / 2048 > 1 ? D / 2048 : 1;
+    const int64_t max_by_len = D / kMinChunk > 1 ? D / kMinChunk : 1;
     if (sp > max_by_len) sp = max_by_len;
     chunk = ceil_div(ceil_div(D, sp), 8) * 8;
     splits = ceil_div(D, chunk);
