@@ -105,8 +105,32 @@ def randn16(shape, gen, dev, mean=0.0, std=1.0):
     return (torch.randn(shape, generator=gen, device=dev, dtype=torch.float32) * std + mean).half()
 
 
-def report(name, cfg, nbytes, seconds, tokens):
-    return {
+_FLOOR = {}
+
+
+def copy_floor(mk, dev, nbytes, iters=50):
+    """Seconds for a plain device copy moving the same bytes (half read, half
+    written), through the library's gather kernel with identity ids, buffers
+    rotated past the Infinity Cache like the kernel under test.  Small
+    transfers pay a fixed launch / ramp cost, so this is the practical floor
+    for a kernel of that size."""
+    import torch
+    H = 3584
+    rows = max(1, int(round(nbytes / (4 * H))))
+    if rows in _FLOOR:
+        return _FLOOR[rows]
+    ns = rotations(2 * rows * H * 2)
+    ids = torch.arange(rows, dtype=torch.int64, device=dev)
+    src = [torch.zeros((rows, H), dtype=torch.float16, device=dev) for _ in range(ns)]
+    dst = [torch.empty((rows, H), dtype=torch.float16, device=dev) for _ in range(ns)]
+    sec = time_launches(lambda i: mk.embedding_gather(ids, src[i], out=dst[i]), ns, iters, 5)
+    del src, dst
+    _FLOOR[rows] = sec
+    return sec
+
+
+def report(name, cfg, nbytes, seconds, tokens, floor=None):
+    r = {
         "kernel": name,
         "config": cfg,
         "bytes": int(nbytes),
@@ -115,6 +139,10 @@ def report(name, cfg, nbytes, seconds, tokens):
         "frac": round(nbytes / seconds / HBM_PEAK, 4),
         "tokens_per_s": round(tokens / seconds, 1),
     }
+    if floor is not None:
+        r["copy_floor_us"] = round(floor * 1e6, 3)
+        r["frac_of_copy_floor"] = round(floor / seconds, 4)
+    return r
 
 
 # ---------------------------------------------------------------------------
@@ -285,6 +313,11 @@ def all_kernels(mk, dev, iters, warmup):
     out.append(report("softmax", "[64,152064]", nb, sec, N))
     del sets
     torch.cuda.synchronize()
+    for r in out:
+        if r["bytes"] >= 8 << 20:
+            f = copy_floor(mk, dev, r["bytes"])
+            r["copy_floor_us"] = round(f * 1e6, 3)
+            r["frac_of_copy_floor"] = round(f / (r["us"] * 1e-6), 4)
     return out
 
 
@@ -364,8 +397,10 @@ def main():
         log("[bench] per-config kernel table")
         kernels = all_kernels(mk, dev, max(20, args.steps // 2), max(5, args.warmup // 2))
         for k in kernels:
+            floor = (f"  copy floor {k['copy_floor_us']:7.2f} us ({100 * k['frac_of_copy_floor']:5.1f}%)"
+                     if "copy_floor_us" in k else "")
             log(f"[bench]   {k['kernel']:<18} {k['config']:<38} {k['us']:>9.2f} us "
-                f"{k['GBps']:>8.1f} GB/s  {100 * k['frac']:5.1f}%")
+                f"{k['GBps']:>8.1f} GB/s  {100 * k['frac']:5.1f}%{floor}")
 
     cpu = None
     if not args.no_cpu:
