@@ -311,7 +311,30 @@ def all_kernels(mk, dev, iters, warmup):
     sec = time_launches(lambda i: mk.softmax(sets[i][0], y=sets[i][1], workspace=ws), ns, iters,
                         warmup)
     out.append(report("softmax", "[64,152064]", nb, sec, N))
+    # 5g. greedy argmax over the same logits (the step after the LM head)
+    nb = N * V * 2 + N * 4
+    wsa = torch.empty(max(1, mk.greedy_argmax_workspace_bytes(N, V)), dtype=torch.uint8, device=dev)
+    outi = torch.empty(N, dtype=torch.int32, device=dev)
+    sec = time_launches(lambda i: mk.greedy_argmax(sets[i][0], out=outi, workspace=wsa), ns, iters,
+                        warmup)
+    out.append(report("greedy_argmax", "[64,152064]", nb, sec, N))
     del sets
+    # 5h. paged KV scatter of the chain's K and V [6064, 4, 128], block size
+    # 16, as one 6064-token sequence into shuffled physical blocks
+    H, hd, bs = 4, 128, 16
+    mb = -(-T // bs)
+    bt = torch.from_numpy(rng.permutation(mb).astype(np.int32)).to(dev).view(1, mb)
+    sl = torch.tensor([T], dtype=torch.int32, device=dev)
+    sp = torch.tensor([0], dtype=torch.int32, device=dev)
+    ksrc = randn16((1, T, H, hd), gen, dev)
+    vsrc = randn16((1, T, H, hd), gen, dev)
+    kc = torch.empty((1, mb, H, bs, hd), dtype=f16, device=dev)
+    vc = torch.empty_like(kc)
+    nb = 2 * 2 * T * H * hd * 2 + (mb + 2) * 4
+    sec = time_launches(lambda i: mk.paged_kv_scatter(ksrc, kc, bt, sl, sp, 0, bs, v_src=vsrc,
+                                                      v_cache=vc), 1, iters, warmup)
+    out.append(report("paged_kv_scatter_kv", "chain K+V [6064,4,128] bs=16", nb, sec, T))
+    del ksrc, vsrc, kc, vc
     torch.cuda.synchronize()
     for r in out:
         if r["bytes"] >= 8 << 20:

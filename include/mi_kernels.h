@@ -20,7 +20,8 @@
  *     HIP runtime refused the launch;
  *   - a size of zero is a successful no-op;
  *   - math is fp32 with fp16 storage; outputs are rounded to nearest even.
- * No entry point allocates device memory, except mi_softmax_f16 on its
+ * No entry point allocates device memory, except mi_softmax_f16 and
+ * mi_greedy_argmax_f16 on their
  * split-row path (N < 512 rows of D >= 8192), which takes 8 bytes per row
  * chunk (<= 256 KiB) from the device's stream-ordered pool (hipMallocAsync /
  * hipFreeAsync on `stream`) for the duration of the call.
@@ -156,6 +157,47 @@ int mi_softmax_ws_f16(const void* x, void* y, int64_t N, int64_t D, void* worksp
  * (src/kernels/model_utils_kernel.cuh:14), where T = B*S. */
 int mi_embedding_gather_f16(const int64_t* ids, const void* table, void* out,
                             int64_t T, int64_t H, int64_t vocab, void* stream);
+
+/* Paged KV-cache scatter: token (b, s) of src [B, S, H_kv, D] at global
+ * position p = start_pos[b] + s is copied, when p < seq_len[b], into physical
+ * block block_table[b * max_blocks_per_seq + p / block_size], slot
+ * p % block_size, of layer `layer` in cache [L, num_blocks, H_kv, block_size, D]
+ * (bit-exact).  block_table, seq_len and start_pos are int32 DEVICE arrays.
+ * Tokens whose block index or physical block falls outside the cache are
+ * skipped.  Replaces launch_paged_kv_scatter
+ * (src/kernels/model_utils_kernel.cuh:55-67, called at
+ * src/layers/attention.cpp:600-623 and :823-846). */
+int mi_paged_kv_scatter_f16(const void* src, void* cache, const int* block_table,
+                            const int* seq_len, const int* start_pos, int64_t B, int64_t S,
+                            int64_t layer, int64_t num_blocks, int64_t H_kv, int64_t D,
+                            int64_t block_size, int64_t max_blocks_per_seq, void* stream);
+
+/* K and V scattered in one launch with the same block table (the reference
+ * issues two launch_paged_kv_scatter calls, src/layers/attention.cpp:823-846). */
+int mi_paged_kv_scatter_kv_f16(const void* k_src, const void* v_src, void* k_cache,
+                               void* v_cache, const int* block_table, const int* seq_len,
+                               const int* start_pos, int64_t B, int64_t S, int64_t layer,
+                               int64_t num_blocks, int64_t H_kv, int64_t D, int64_t block_size,
+                               int64_t max_blocks_per_seq, void* stream);
+
+/* Greedy sampling: out[b] = argmax over logits[b, 0:V) (fp16 [B, V]; out int32
+ * [B], DEVICE).  Ties resolve exactly as the reference's 256-thread kernel
+ * does: among maximal entries, the one whose i mod 256 has the smallest 8-bit
+ * bit reversal, then the smallest i; NaN is never chosen; -0 equals +0; a row
+ * with nothing above -inf gives -1.
+ * Replaces launch_greedy_sample / launch_greedy_sample_batched
+ * (src/kernels/sampling_kernel.cuh:17-30; src/kernels/sampling_kernel.cu:14-76).
+ * For B < 512 rows of V >= 8192 it takes <= 256 KiB of stream-ordered
+ * workspace for the call, as mi_softmax_f16 does. */
+int mi_greedy_argmax_f16(const void* logits, int64_t B, int64_t V, int32_t* out, void* stream);
+
+/* Workspace bytes mi_greedy_argmax_ws_f16 needs (0 when rows are not split). */
+int64_t mi_greedy_argmax_workspace_bytes(int64_t B, int64_t V);
+
+/* mi_greedy_argmax_f16 with a caller-provided device workspace (allocates
+ * nothing; graph-capturable).  Calls sharing a workspace must not overlap. */
+int mi_greedy_argmax_ws_f16(const void* logits, int64_t B, int64_t V, int32_t* out,
+                            void* workspace, int64_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -1,0 +1,323 @@
+// kv_argmax.hip -- the two steps either side of the layer chain: scattering
+// the rotated K / V into the paged KV cache, and greedy (argmax) sampling
+// over the LM-head logits.  Both are HBM-bound with no arithmetic to speak of.
+//
+// Paged KV scatter (src/kernels/model_utils_kernel.cu:108-164): token (b, s)
+// of src [B, S, H_kv, D] sits at global position p = start_pos[b] + s and,
+// if p < seq_len[b], is copied to block block_table[b, p / BS], slot p % BS
+// of the cache laid out [L, num_blocks, H_kv, BS, D].  Bit-exact copy.  One
+// wave per token moves its H_kv * D halves as 16-byte vectors (H_kv = 4,
+// D = 128: 64 vectors = one per lane); block-table reads are wave-uniform.
+// Entries that would leave the cache (block index past max_blocks_per_seq,
+// physical block outside [0, num_blocks)) are skipped, where the reference
+// would write out of bounds.  A K+V form moves both tensors in one launch.
+//
+// Greedy argmax (src/kernels/sampling_kernel.cu:14-38, :52-76): the reference
+// lets each of 256 threads keep its first strict maximum over a stride-256
+// slice (thread u = i mod 256), then tree-reduces pairs (t, t + offset) for
+// offset = 128 .. 1, keeping the lower slot on ties.  Slot t at offset o holds
+// the best of the threads congruent to t mod 2o, so among tied threads the
+// one whose index has the smallest 8-bit bit reversal wins (low bits decide
+// first).  NaN is never chosen (comparisons are false); only values above
+// -inf are (the result is -1 when none is); -0 and +0 compare equal.  Here
+// that order is one 64-bit key per element --
+//   [ordered fp16 value : 16 | 255 - bitrev8(i mod 256) : 16 | ~i : 32]
+// -- larger is better, 0 = not eligible, so any reduction order gives the
+// reference's answer.  Few long rows are split into chunks: kernel 1 writes
+// each chunk's best key, kernel 2 reduces a row's keys in one wave.
+#include "mi_device.h"
+#include "mi_host.h"
+
+namespace mi {
+namespace {
+
+// ---------------------------------------------------------------------------
+// Paged KV scatter
+// ---------------------------------------------------------------------------
+constexpr int kKvTokensPerWg = 4;  // one wave per token
+
+struct KvGeometry {
+    int64_t B, S;
+    int64_t layer, num_blocks, H_kv, D, block_size, max_blocks_per_seq;
+};
+
+template <int VEC>
+__global__ __launch_bounds__(256) void kv_scatter_kernel(const half_t* __restrict__ src0,
+                                                         half_t* __restrict__ cache0,
+                                                         const half_t* __restrict__ src1,
+                                                         half_t* __restrict__ cache1,
+                                                         const int* __restrict__ block_table,
+                                                         const int* __restrict__ seq_len,
+                                                         const int* __restrict__ start_pos,
+                                                         KvGeometry g) {
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    const int lane = threadIdx.x & (kWave - 1);
+    const int64_t tok = static_cast<int64_t>(blockIdx.x) * kKvTokensPerWg + wave;
+    if (tok >= g.B * g.S) return;  // wave-uniform; no cross-lane work follows
+    const int64_t b = tok / g.S;
+    const int64_t s = tok - b * g.S;
+    const int64_t pos = static_cast<int64_t>(start_pos[b]) + s;
+    if (pos >= seq_len[b] || pos < 0) return;
+    const int64_t blk = pos / g.block_size;
+    if (blk >= g.max_blocks_per_seq) return;
+    const int64_t phys = block_table[b * g.max_blocks_per_seq + blk];
+    if (phys < 0 || phys >= g.num_blocks) return;
+    const int64_t slot = pos - blk * g.block_size;
+
+    const int64_t row = g.H_kv * g.D;               // halves per token
+    const int64_t per_head = g.D / VEC;             // vectors per head
+    const int64_t nv = row / VEC;                   // vectors per token
+    const int64_t head_stride = g.block_size * g.D; // halves between heads in a block
+    const int64_t dst_base =
+        ((g.layer * g.num_blocks + phys) * g.H_kv) * head_stride + slot * g.D;
+    const half_t* s0 = src0 + tok * row;
+    const half_t* s1 = src1 ? src1 + tok * row : nullptr;
+    for (int64_t v = lane; v < nv; v += kWave) {
+        const int64_t h = v / per_head;
+        const int64_t d = (v - h * per_head) * VEC;
+        const int64_t dst = dst_base + h * head_stride + d;
+        if constexpr (VEC == 8) {
+            const h8 a = ld8_stream(s0 + v * 8);
+            h8 c;
+            if (s1) c = ld8_stream(s1 + v * 8);
+            st8_stream(cache0 + dst, a);
+            if (s1) st8_stream(cache1 + dst, c);
+        } else {
+            cache0[dst] = s0[v];
+            if (s1) cache1[dst] = s1[v];
+        }
+    }
+}
+
+int kv_scatter(const void* src0, void* cache0, const void* src1, void* cache1,
+               const int* block_table, const int* seq_len, const int* start_pos, int64_t B,
+               int64_t S, int64_t layer, int64_t num_blocks, int64_t H_kv, int64_t D,
+               int64_t block_size, int64_t max_blocks_per_seq, void* stream) {
+    if (B < 0 || S < 0 || layer < 0 || num_blocks < 0 || H_kv < 0 || D < 0 || block_size <= 0 ||
+        max_blocks_per_seq < 0)
+        return MI_ERR_INVALID_ARGUMENT;
+    if (B == 0 || S == 0 || H_kv == 0 || D == 0 || num_blocks == 0 || max_blocks_per_seq == 0)
+        return MI_OK;
+    if (!src0 || !cache0 || !block_table || !seq_len || !start_pos) return MI_ERR_INVALID_ARGUMENT;
+    if ((src1 == nullptr) != (cache1 == nullptr)) return MI_ERR_INVALID_ARGUMENT;
+    const int64_t tokens = B * S;
+    const int64_t grid = ceil_div(tokens, kKvTokensPerWg);
+    if (grid > kMaxGridX) return MI_ERR_UNSUPPORTED;
+    const int64_t src_bytes = tokens * H_kv * D * 2;
+    const int64_t cache_bytes = (layer + 1) * num_blocks * H_kv * block_size * D * 2;
+    if (overlaps(src0, src_bytes, cache0, cache_bytes)) return MI_ERR_ALIASING;
+    if (src1 && (overlaps(src1, src_bytes, cache1, cache_bytes) ||
+                 overlaps(cache0, cache_bytes, cache1, cache_bytes)))
+        return MI_ERR_ALIASING;
+    const KvGeometry g{B, S, layer, num_blocks, H_kv, D, block_size, max_blocks_per_seq};
+    const bool vec = D % 8 == 0 && aligned16(src0) && aligned16(cache0) &&
+                     (!src1 || (aligned16(src1) && aligned16(cache1)));
+    const hipStream_t st = as_stream(stream);
+    const auto* s0 = static_cast<const half_t*>(src0);
+    const auto* s1 = static_cast<const half_t*>(src1);
+    auto* c0 = static_cast<half_t*>(cache0);
+    auto* c1 = static_cast<half_t*>(cache1);
+    if (vec)
+        kv_scatter_kernel<8><<<dim3(static_cast<unsigned>(grid)), dim3(256), 0, st>>>(
+            s0, c0, s1, c1, block_table, seq_len, start_pos, g);
+    else
+        kv_scatter_kernel<1><<<dim3(static_cast<unsigned>(grid)), dim3(256), 0, st>>>(
+            s0, c0, s1, c1, block_table, seq_len, start_pos, g);
+    return launch_status();
+}
+
+// ---------------------------------------------------------------------------
+// Greedy argmax
+// ---------------------------------------------------------------------------
+typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
+
+constexpr int kArgmaxSplitMaxRows = 512;
+constexpr int kArgmaxMaxSplits = 64;
+
+// Order key of element i with fp16 bits h (see the file header); 0 when the
+// element can never be chosen (NaN or -inf).
+__device__ __forceinline__ uint64_t argmax_key(uint16_t h, int64_t i) {
+    if ((h & 0x7fffu) > 0x7c00u || h == 0xfc00u) return 0;  // NaN, -inf
+    if (h == 0x8000u) h = 0;                                 // -0 == +0
+    const uint32_t ord = (h & 0x8000u) ? (~h & 0xffffu) : (h | 0x8000u);
+    const uint32_t tie = 255u - (__builtin_bitreverse32(static_cast<uint32_t>(i & 255)) >> 24);
+    return (static_cast<uint64_t>(ord) << 48) | (static_cast<uint64_t>(tie) << 32) |
+           static_cast<uint64_t>(~static_cast<uint32_t>(i));
+}
+
+__device__ __forceinline__ uint64_t max_u64(uint64_t a, uint64_t b) { return a > b ? a : b; }
+
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        const uint32_t lo = __shfl_xor(static_cast<uint32_t>(v), off, kWave);
+        const uint32_t hi = __shfl_xor(static_cast<uint32_t>(v >> 32), off, kWave);
+        v = max_u64(v, (static_cast<uint64_t>(hi) << 32) | lo);
+    }
+    return v;
+}
+
+__device__ __forceinline__ int32_t key_index(uint64_t key) {
+    return key == 0 ? -1 : static_cast<int32_t>(~static_cast<uint32_t>(key));
+}
+
+// Best key of elements [begin, end) of a row, over the workgroup.
+template <int VEC>
+__device__ __forceinline__ uint64_t chunk_best(const half_t* xr, int64_t begin, int64_t end,
+                                               uint64_t* slots) {
+    uint64_t best = 0;
+    const int64_t step = static_cast<int64_t>(blockDim.x) * VEC;
+    for (int64_t i0 = begin + static_cast<int64_t>(threadIdx.x) * VEC; i0 < end; i0 += 2 * step) {
+        if constexpr (VEC == 8) {
+            // bit patterns of the whole vector at once (bit-casting single
+            // elements of an fp16 vector was miscompiled into reusing
+            // element 0's pattern for all eight)
+            const u16x8 a = __builtin_bit_cast(u16x8, ld8_stream(xr + i0));
+            u16x8 c = u16x8(0);
+            const bool second = i0 + step < end;
+            if (second) c = __builtin_bit_cast(u16x8, ld8_stream(xr + i0 + step));
+#pragma unroll
+            for (int k = 0; k < 8; ++k) best = max_u64(best, argmax_key(a[k], i0 + k));
+            if (second) {
+#pragma unroll
+                for (int k = 0; k < 8; ++k) best = max_u64(best, argmax_key(c[k], i0 + step + k));
+            }
+        } else {
+            best = max_u64(best, argmax_key(__builtin_bit_cast(uint16_t, xr[i0]), i0));
+            if (i0 + step < end)
+                best = max_u64(best,
+                               argmax_key(__builtin_bit_cast(uint16_t, xr[i0 + step]), i0 + step));
+        }
+    }
+    best = wave_max_u64(best);
+    const int wave = threadIdx.x / kWave;
+    if ((threadIdx.x & (kWave - 1)) == 0) slots[wave] = best;
+    __syncthreads();
+    uint64_t t = 0;
+    for (int w = 0; w < static_cast<int>(blockDim.x / kWave); ++w) t = max_u64(t, slots[w]);
+    return t;
+}
+
+// grid (splits, B).  With one split the index goes straight to `out`;
+// otherwise each chunk's key goes to ws[row * splits + split].
+template <int VEC>
+__global__ __launch_bounds__(256) void argmax_partial_kernel(const half_t* __restrict__ x,
+                                                             int64_t V, int64_t chunk,
+                                                             uint64_t* __restrict__ ws,
+                                                             int32_t* __restrict__ out) {
+    __shared__ uint64_t slots[256 / kWave];
+    const int split = blockIdx.x, splits = gridDim.x;
+    const int64_t row = blockIdx.y;
+    const int64_t b = split * chunk;
+    const int64_t e = b + chunk < V ? b + chunk : V;
+    const uint64_t best = chunk_best<VEC>(x + row * V, b, e, slots);
+    if (threadIdx.x == 0) {
+        if (splits == 1)
+            out[row] = key_index(best);
+        else
+            ws[row * splits + split] = best;
+    }
+}
+
+// One wave per row: lane j reads chunk j's key.
+__global__ __launch_bounds__(256) void argmax_final_kernel(const uint64_t* __restrict__ ws,
+                                                           int splits, int64_t B,
+                                                           int32_t* __restrict__ out) {
+    const int64_t row = static_cast<int64_t>(blockIdx.x) * (256 / kWave) + threadIdx.x / kWave;
+    const int lane = threadIdx.x & (kWave - 1);
+    if (row >= B) return;  // wave-uniform
+    uint64_t k = lane < splits ? ws[row * splits + lane] : 0;
+    k = wave_max_u64(k);
+    if (lane == 0) out[row] = key_index(k);
+}
+
+int64_t argmax_splits(int64_t B, int64_t V, int64_t& chunk) {
+    chunk = V;
+    if (B >= kArgmaxSplitMaxRows || V < 8192) return 1;
+    int64_t sp = ceil_div(2048, B);
+    if (sp > kArgmaxMaxSplits) sp = kArgmaxMaxSplits;
+    const int64_t max_by_len = V / 2048 > 1 ? V / 2048 : 1;
+    if (sp > max_by_len) sp = max_by_len;
+    chunk = ceil_div(ceil_div(V, sp), 16) * 16;  // two 8-element vectors per lane step
+    return ceil_div(V, chunk);
+}
+
+int64_t argmax_ws_bytes(int64_t B, int64_t V) {
+    int64_t chunk;
+    const int64_t sp = argmax_splits(B, V, chunk);
+    return sp > 1 ? B * sp * static_cast<int64_t>(sizeof(uint64_t)) : 0;
+}
+
+int argmax(const void* logits, int64_t B, int64_t V, int32_t* out, void* ws, int64_t ws_bytes,
+           void* stream) {
+    if (B < 0 || V < 0 || ws_bytes < 0) return MI_ERR_INVALID_ARGUMENT;
+    if (B == 0) return MI_OK;
+    if (!logits || !out) return MI_ERR_INVALID_ARGUMENT;
+    if (B > 65535) return MI_ERR_UNSUPPORTED;  // grid.y
+    if (V > 0x7fffffff) return MI_ERR_UNSUPPORTED;
+    int64_t chunk;
+    const int64_t splits = V == 0 ? 1 : argmax_splits(B, V, chunk);
+    if (V == 0) chunk = 0;
+    const int64_t need = splits > 1 ? B * splits * 8 : 0;
+    if (need > 0 && (!ws || ws_bytes < need)) return MI_ERR_INVALID_ARGUMENT;
+    const hipStream_t st = as_stream(stream);
+    const auto* x = static_cast<const half_t*>(logits);
+    auto* w = static_cast<uint64_t*>(ws);
+    const dim3 g(static_cast<unsigned>(splits), static_cast<unsigned>(B));
+    if (V % 16 == 0 && aligned16(logits))
+        argmax_partial_kernel<8><<<g, dim3(256), 0, st>>>(x, V, chunk, w, out);
+    else
+        argmax_partial_kernel<1><<<g, dim3(256), 0, st>>>(x, V, chunk, w, out);
+    if (splits > 1)
+        argmax_final_kernel<<<dim3(static_cast<unsigned>(ceil_div(B, 256 / kWave))), dim3(256), 0,
+                              st>>>(w, static_cast<int>(splits), B, out);
+    return launch_status();
+}
+
+}  // namespace
+}  // namespace mi
+
+extern "C" int mi_paged_kv_scatter_f16(const void* src, void* cache, const int* block_table,
+                                       const int* seq_len, const int* start_pos, int64_t B,
+                                       int64_t S, int64_t layer, int64_t num_blocks, int64_t H_kv,
+                                       int64_t D, int64_t block_size, int64_t max_blocks_per_seq,
+                                       void* stream) {
+    return mi::kv_scatter(src, cache, nullptr, nullptr, block_table, seq_len, start_pos, B, S,
+                          layer, num_blocks, H_kv, D, block_size, max_blocks_per_seq, stream);
+}
+
+extern "C" int mi_paged_kv_scatter_kv_f16(const void* k_src, const void* v_src, void* k_cache,
+                                          void* v_cache, const int* block_table,
+                                          const int* seq_len, const int* start_pos, int64_t B,
+                                          int64_t S, int64_t layer, int64_t num_blocks,
+                                          int64_t H_kv, int64_t D, int64_t block_size,
+                                          int64_t max_blocks_per_seq, void* stream) {
+    if (!v_src || !v_cache) return MI_ERR_INVALID_ARGUMENT;
+    return mi::kv_scatter(k_src, k_cache, v_src, v_cache, block_table, seq_len, start_pos, B, S,
+                          layer, num_blocks, H_kv, D, block_size, max_blocks_per_seq, stream);
+}
+
+extern "C" int64_t mi_greedy_argmax_workspace_bytes(int64_t B, int64_t V) {
+    if (B <= 0 || V <= 0) return 0;
+    return mi::argmax_ws_bytes(B, V);
+}
+
+extern "C" int mi_greedy_argmax_ws_f16(const void* logits, int64_t B, int64_t V, int32_t* out,
+                                       void* workspace, int64_t workspace_bytes, void* stream) {
+    return mi::argmax(logits, B, V, out, workspace, workspace_bytes, stream);
+}
+
+extern "C" int mi_greedy_argmax_f16(const void* logits, int64_t B, int64_t V, int32_t* out,
+                                    void* stream) {
+    const int64_t need = (B > 0 && V > 0) ? mi::argmax_ws_bytes(B, V) : 0;
+    if (need == 0) return mi::argmax(logits, B, V, out, nullptr, 0, stream);
+    if (!logits || !out) return MI_ERR_INVALID_ARGUMENT;
+    const hipStream_t s = mi::as_stream(stream);
+    void* ws = nullptr;
+    hipError_t e = hipMallocAsync(&ws, static_cast<size_t>(need), s);
+    if (e != hipSuccess) return static_cast<int>(e);
+    const int st = mi::argmax(logits, B, V, out, ws, need, stream);
+    e = hipFreeAsync(ws, s);
+    if (st != MI_OK) return st;
+    return e == hipSuccess ? MI_OK : static_cast<int>(e);
+}

@@ -12,6 +12,7 @@
 #include "kernels/model_utils_kernel.h"
 #include "kernels/rmsnorm_kernel.h"
 #include "kernels/rope_kernel.h"
+#include "kernels/sampling_kernel.h"
 #include "kernels/softmax_kernel.h"
 #include "kernels/swiglu_kernel.h"
 #include "mi_kernels.h"
@@ -127,6 +128,37 @@ void launch_scale_inplace(__half* y, float scale, int64_t n, hipStream_t stream)
 
 void launch_mul_inplace(__half* y, const __half* x, int64_t n, hipStream_t stream) {
     check(mi_mul_inplace_f16(y, x, n, sv(stream)), "launch_mul_inplace");
+}
+
+void launch_paged_kv_scatter(const __half* src, __half* cache, const int* block_table,
+                             const int* seq_len, const int* start_pos, int B, int S, int layer,
+                             int num_blocks, int H_kv, int D, int block_size,
+                             int max_blocks_per_seq, hipStream_t stream) {
+    check(mi_paged_kv_scatter_f16(src, cache, block_table, seq_len, start_pos, B, S, layer,
+                                  num_blocks, H_kv, D, block_size, max_blocks_per_seq, sv(stream)),
+          "launch_paged_kv_scatter");
+}
+
+void launch_paged_kv_scatter_kv(const __half* k_src, const __half* v_src, __half* k_cache,
+                                __half* v_cache, const int* block_table, const int* seq_len,
+                                const int* start_pos, int B, int S, int layer, int num_blocks,
+                                int H_kv, int D, int block_size, int max_blocks_per_seq,
+                                hipStream_t stream) {
+    check(mi_paged_kv_scatter_kv_f16(k_src, v_src, k_cache, v_cache, block_table, seq_len,
+                                     start_pos, B, S, layer, num_blocks, H_kv, D, block_size,
+                                     max_blocks_per_seq, sv(stream)),
+          "launch_paged_kv_scatter_kv");
+}
+
+void launch_greedy_sample(const __half* logits, int vocab, int* out, hipStream_t stream) {
+    check(mi_greedy_argmax_f16(logits, 1, vocab, out, sv(stream)), "launch_greedy_sample");
+}
+
+void launch_greedy_sample_batched(const __half* logits, int B, int vocab, int* out,
+                                  hipStream_t stream) {
+    if (B <= 0) return;
+    check(mi_greedy_argmax_f16(logits, B, vocab, out, sv(stream)),
+          "launch_greedy_sample_batched");
 }
 
 }  // namespace kernels

@@ -1,7 +1,7 @@
 // model_utils_kernel.h -- the model-chain utility launchers on the hot path,
-// with the reference's signatures (src/kernels/model_utils_kernel.cuh:12-29).
-// launch_add_bias and launch_paged_kv_scatter belong to the attention path
-// and are not part of this library.
+// with the reference's signatures (src/kernels/model_utils_kernel.cuh:12-67).
+// launch_add_bias belongs to the QKV projection and is not part of this
+// library.
 #pragma once
 
 #include <cstdint>
@@ -26,6 +26,22 @@ void launch_scale_inplace(__half* y, float scale, int64_t n, hipStream_t stream)
 
 // y[i] = half(y[i] * x[i])
 void launch_mul_inplace(__half* y, const __half* x, int64_t n, hipStream_t stream);
+
+// Scatter src [B, S, H_kv, D] into the paged cache [L, num_blocks, H_kv,
+// block_size, D] of `layer`: token (b, s) at p = start_pos[b] + s goes to
+// block block_table[b, p / block_size], slot p % block_size, when
+// p < seq_len[b].  block_table / seq_len / start_pos are int32 on the GPU.
+void launch_paged_kv_scatter(const __half* src, __half* cache, const int* block_table,
+                             const int* seq_len, const int* start_pos, int B, int S, int layer,
+                             int num_blocks, int H_kv, int D, int block_size,
+                             int max_blocks_per_seq, hipStream_t stream);
+
+// K and V together in one launch (same block table).
+void launch_paged_kv_scatter_kv(const __half* k_src, const __half* v_src, __half* k_cache,
+                                __half* v_cache, const int* block_table, const int* seq_len,
+                                const int* start_pos, int B, int S, int layer, int num_blocks,
+                                int H_kv, int D, int block_size, int max_blocks_per_seq,
+                                hipStream_t stream);
 
 }  // namespace kernels
 }  // namespace mini_infer

@@ -46,6 +46,10 @@ SIGNATURES = {
     "mi_softmax_f16": [_c_void_p, _c_void_p, _i64, _i64, _c_void_p],
     "mi_embedding_gather_f16": [_c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64, _c_void_p],
     "mi_softmax_ws_f16": [_c_void_p, _c_void_p, _i64, _i64, _c_void_p, _i64, _c_void_p],
+    "mi_paged_kv_scatter_f16": [_c_void_p] * 5 + [_i64] * 8 + [_c_void_p],
+    "mi_paged_kv_scatter_kv_f16": [_c_void_p] * 7 + [_i64] * 8 + [_c_void_p],
+    "mi_greedy_argmax_f16": [_c_void_p, _i64, _i64, _c_void_p, _c_void_p],
+    "mi_greedy_argmax_ws_f16": [_c_void_p, _i64, _i64, _c_void_p, _c_void_p, _i64, _c_void_p],
     "mi_abi_version": [],
 }
 
@@ -66,6 +70,8 @@ def load_library(path: os.PathLike | str | None = None) -> ctypes.CDLL:
         fn = getattr(lib, name)
         fn.argtypes = argtypes
         fn.restype = _int
+    lib.mi_greedy_argmax_workspace_bytes.argtypes = [_i64, _i64]
+    lib.mi_greedy_argmax_workspace_bytes.restype = _i64
     lib.mi_softmax_workspace_bytes.argtypes = [_i64, _i64]
     lib.mi_softmax_workspace_bytes.restype = _i64
     lib.mi_status_string.argtypes = [_int]
@@ -385,4 +391,72 @@ def embedding_gather(ids, table, out=None, check_range: bool = True, stream=None
     vocab = V if check_range else 0
     _check(load_library().mi_embedding_gather_f16(_ptr(ids), _ptr(table), _ptr(out), T, H, vocab,
                                                   _stream(stream)), "mi_embedding_gather_f16")
+    return out
+
+
+# ---------------------------------------------------------------------------
+# Paged KV scatter (reference: launch_paged_kv_scatter, model_utils_kernel.cuh:55)
+# ---------------------------------------------------------------------------
+
+def paged_kv_scatter(src, cache, block_table, seq_len, start_pos, layer: int, block_size: int,
+                     v_src=None, v_cache=None, stream=None):
+    """Scatter src [B, S, H_kv, D] into cache [L, num_blocks, H_kv, bs, D] (and
+    v_src into v_cache in the same launch when given)."""
+    torch = _torch()
+    _need(src, _f16(), "src"); _need(cache, _f16(), "cache")
+    for t, n in ((block_table, "block_table"), (seq_len, "seq_len"), (start_pos, "start_pos")):
+        _need(t, torch.int32, n)
+    if src.dim() != 4 or cache.dim() != 5:
+        raise ValueError("src must be [B, S, H_kv, D] and cache [L, num_blocks, H_kv, bs, D]")
+    B, S, H, D = src.shape
+    L, NB, Hc, bs, Dc = cache.shape
+    if Hc != H or Dc != D or bs != block_size or not 0 <= layer < L:
+        raise ValueError("cache shape does not match src / block_size / layer")
+    if block_table.dim() != 2 or block_table.shape[0] != B or seq_len.numel() != B or \
+            start_pos.numel() != B:
+        raise ValueError("block_table must be [B, max_blocks]; seq_len, start_pos [B]")
+    mb = block_table.shape[1]
+    lib = load_library()
+    if v_src is None:
+        _check(lib.mi_paged_kv_scatter_f16(_ptr(src), _ptr(cache), _ptr(block_table), _ptr(seq_len),
+                                           _ptr(start_pos), B, S, layer, NB, H, D, block_size, mb,
+                                           _stream(stream)), "mi_paged_kv_scatter_f16")
+    else:
+        _need(v_src, _f16(), "v_src"); _need(v_cache, _f16(), "v_cache")
+        if v_src.shape != src.shape or v_cache.shape != cache.shape:
+            raise ValueError("v_src / v_cache must match src / cache")
+        _check(lib.mi_paged_kv_scatter_kv_f16(_ptr(src), _ptr(v_src), _ptr(cache), _ptr(v_cache),
+                                              _ptr(block_table), _ptr(seq_len), _ptr(start_pos),
+                                              B, S, layer, NB, H, D, block_size, mb,
+                                              _stream(stream)), "mi_paged_kv_scatter_kv_f16")
+    return cache
+
+
+# ---------------------------------------------------------------------------
+# Greedy sampling (reference: launch_greedy_sample[_batched], sampling_kernel.cuh:17-30)
+# ---------------------------------------------------------------------------
+
+def greedy_argmax_workspace_bytes(B: int, V: int) -> int:
+    return int(load_library().mi_greedy_argmax_workspace_bytes(B, V))
+
+
+def greedy_argmax(logits, out=None, workspace=None, stream=None):
+    """int32 [B] argmax of logits [B, V] (or [V]) with the reference's tie rule."""
+    torch = _torch()
+    _need(logits, _f16(), "logits")
+    x = logits if logits.dim() == 2 else logits.view(1, -1)
+    B, V = x.shape
+    if out is None:
+        out = torch.empty(B, dtype=torch.int32, device=logits.device)
+    _need(out, torch.int32, "out")
+    if out.numel() != B:
+        raise ValueError("out must hold B entries")
+    lib = load_library()
+    if workspace is None:
+        _check(lib.mi_greedy_argmax_f16(_ptr(x), B, V, _ptr(out), _stream(stream)),
+               "mi_greedy_argmax_f16")
+    else:
+        nbytes = workspace.numel() * workspace.element_size()
+        _check(lib.mi_greedy_argmax_ws_f16(_ptr(x), B, V, _ptr(out), _ptr(workspace), nbytes,
+                                           _stream(stream)), "mi_greedy_argmax_ws_f16")
     return out

@@ -416,3 +416,60 @@ void mio_embedding_gather(const int64_t* ids, const uint16_t* table,
     gather_ctx c = {ids, table, out, H, vocab};
     parallel_for(gather_rows, &c, T, nthreads);
 }
+
+/* ------------------------------------------------------------------------ */
+/* Paged KV scatter and greedy argmax                                        */
+/* ------------------------------------------------------------------------ */
+
+void mio_paged_kv_scatter(const uint16_t* src, uint16_t* cache, const int32_t* block_table,
+                          const int32_t* seq_len, const int32_t* start_pos, int64_t B,
+                          int64_t S, int64_t layer, int64_t num_blocks, int64_t H_kv, int64_t D,
+                          int64_t block_size, int64_t max_blocks_per_seq) {
+    for (int64_t b = 0; b < B; ++b) {
+        for (int64_t s = 0; s < S; ++s) {
+            const int64_t pos = (int64_t)start_pos[b] + s;
+            if (pos < 0 || pos >= seq_len[b]) continue;
+            const int64_t blk = pos / block_size;
+            if (blk >= max_blocks_per_seq) continue;
+            const int64_t phys = block_table[b * max_blocks_per_seq + blk];
+            if (phys < 0 || phys >= num_blocks) continue;
+            const int64_t slot = pos % block_size;
+            for (int64_t h = 0; h < H_kv; ++h) {
+                const uint16_t* from = src + ((b * S + s) * H_kv + h) * D;
+                uint16_t* to = cache + ((layer * num_blocks + phys) * H_kv + h) * block_size * D
+                               + slot * D;
+                memcpy(to, from, (size_t)D * 2u);
+            }
+        }
+    }
+}
+
+void mio_greedy_argmax(const uint16_t* logits, int64_t B, int64_t V, int32_t* out) {
+    enum { BLOCK = 256 };
+    float best_v[BLOCK];
+    int32_t best_i[BLOCK];
+    for (int64_t r = 0; r < B; ++r) {
+        const uint16_t* row = logits + r * V;
+        /* each "thread" keeps its first strict maximum over a stride-256 scan */
+        for (int t = 0; t < BLOCK; ++t) {
+            float m = -INFINITY;
+            int32_t idx = -1;
+            for (int64_t i = t; i < V; i += BLOCK) {
+                const float v = mio_f16_to_f32(row[i]);
+                if (v > m) { m = v; idx = (int32_t)i; }
+            }
+            best_v[t] = m;
+            best_i[t] = idx;
+        }
+        /* tree reduction: the partner's value replaces only when strictly larger */
+        for (int off = BLOCK / 2; off > 0; off >>= 1) {
+            for (int t = 0; t < off; ++t) {
+                if (best_v[t + off] > best_v[t]) {
+                    best_v[t] = best_v[t + off];
+                    best_i[t] = best_i[t + off];
+                }
+            }
+        }
+        out[r] = best_i[0];
+    }
+}

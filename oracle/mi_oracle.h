@@ -116,6 +116,21 @@ void mio_embedding_gather(const int64_t* ids, const uint16_t* table,
                           uint16_t* out, int64_t T, int64_t H, int64_t vocab,
                           int nthreads);
 
+/* Paged KV scatter (src/kernels/model_utils_kernel.cu:108-145): token (b, s)
+ * of src [B, S, H_kv, D] at position p = start_pos[b] + s goes, when
+ * p < seq_len[b], to block block_table[b * max_blocks + p / bs], slot p % bs,
+ * of `layer` in cache [L, num_blocks, H_kv, bs, D].  Entries outside the cache
+ * are skipped (the reference writes out of bounds there). */
+void mio_paged_kv_scatter(const uint16_t* src, uint16_t* cache, const int32_t* block_table,
+                          const int32_t* seq_len, const int32_t* start_pos, int64_t B,
+                          int64_t S, int64_t layer, int64_t num_blocks, int64_t H_kv, int64_t D,
+                          int64_t block_size, int64_t max_blocks_per_seq);
+
+/* Greedy argmax per row, simulating the reference kernel's 256-thread
+ * strided scan and shared-memory tree reduction literally
+ * (src/kernels/sampling_kernel.cu:52-76). */
+void mio_greedy_argmax(const uint16_t* logits, int64_t B, int64_t V, int32_t* out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -58,6 +58,8 @@ def lib() -> ctypes.CDLL:
             "mio_scale_inplace": ([P, F, I64], None),
             "mio_softmax": ([P, P, I64, I64, I], None),
             "mio_embedding_gather": ([P, P, P, I64, I64, I64, I], None),
+            "mio_paged_kv_scatter": ([P, P, P, P, P] + [I64] * 8, None),
+            "mio_greedy_argmax": ([P, I64, I64, P], None),
         }
         for name, (args, res) in sig.items():
             fn = getattr(L, name)
@@ -226,4 +228,29 @@ def embedding_gather(ids, table, vocab=None, nthreads=1) -> np.ndarray:
     out = np.empty((*ids.shape, H), dtype=np.float16)
     lib().mio_embedding_gather(_p(ids), _p(table), _p(out), ids.size, H,
                                V if vocab is None else vocab, nthreads)
+    return out
+
+
+def paged_kv_scatter(src, cache, block_table, seq_len, start_pos, layer, block_size):
+    """src [B, S, H_kv, D] fp16; cache [L, num_blocks, H_kv, bs, D] fp16 (copied
+    and returned); block_table int32 [B, max_blocks]; seq_len, start_pos int32 [B]."""
+    src = _h(src); out = _h(cache).copy()
+    bt = np.ascontiguousarray(np.asarray(block_table, dtype=np.int32))
+    sl = np.ascontiguousarray(np.asarray(seq_len, dtype=np.int32))
+    sp = np.ascontiguousarray(np.asarray(start_pos, dtype=np.int32))
+    B, S, H, D = src.shape
+    L, NB = out.shape[0], out.shape[1]
+    assert out.shape == (L, NB, H, block_size, D)
+    lib().mio_paged_kv_scatter(_p(src), _p(out), _p(bt), _p(sl), _p(sp), B, S, layer, NB, H, D,
+                               block_size, bt.shape[1])
+    return out
+
+
+def greedy_argmax(logits) -> np.ndarray:
+    x = _h(logits)
+    if x.ndim == 1:
+        x = x.reshape(1, -1)
+    B, V = x.shape
+    out = np.empty(B, dtype=np.int32)
+    lib().mio_greedy_argmax(_p(x), B, V, _p(out))
     return out

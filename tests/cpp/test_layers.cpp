@@ -22,6 +22,7 @@
 #include "kernels/model_utils_kernel.h"
 #include "kernels/rmsnorm_kernel.h"
 #include "kernels/rope_kernel.h"
+#include "kernels/sampling_kernel.h"
 #include "kernels/softmax_kernel.h"
 #include "kernels/swiglu_kernel.h"
 #include "layers/mlp_activation.h"
@@ -281,6 +282,47 @@ void gpu_checks() {
                                                        D, 1e-6f, 0, 0);
                }),
                "launcher rejects a null weight");
+    }
+    // --- paged KV scatter and greedy sampling ------------------------------
+    std::printf("[gpu] KV scatter, greedy sampling\n");
+    {
+        const int B = 2, S = 20, Hk = 4, D = 128, BS = 16, L = 2, NB = 8, MB = 3;
+        Tensor src = reftest_f16({B, S, Hk, D}, 1.0f, 41);
+        Tensor cache = reftest_f16({L, NB, Hk, BS, D}, 1.0f, 42);
+        std::vector<int32_t> bt = {5, 2, 7, 0, 6, 3}, sl = {20, 30}, sp = {0, 9};
+        std::vector<uint16_t> ref(bits(cache), bits(cache) + cache.numel());
+        mio_paged_kv_scatter(bits(src), ref.data(), bt.data(), sl.data(), sp.data(), B, S, 1, NB,
+                             Hk, D, BS, MB);
+        auto i32 = [](const std::vector<int32_t>& v) {
+            Tensor t(std::vector<int64_t>{static_cast<int64_t>(v.size())}, DType::INT32,
+                     Device::cpu());
+            std::memcpy(t.data(), v.data(), v.size() * 4);
+            return t.to(Device::cuda(0));
+        };
+        Tensor btd = i32(bt), sld = i32(sl), spd = i32(sp);
+        Tensor cd = cache.to(Device::cuda(0)), sd = src.to(Device::cuda(0));
+        mini_infer::kernels::launch_paged_kv_scatter(
+            static_cast<const __half*>(sd.data()), static_cast<__half*>(cd.data()),
+            static_cast<const int*>(btd.data()), static_cast<const int*>(sld.data()),
+            static_cast<const int*>(spd.data()), B, S, 1, NB, Hk, D, BS, MB, 0);
+        EXPECT(bit_equal(cd, ref.data(), "launch_paged_kv_scatter"), "kv scatter");
+
+        const int R = 3, V = 152064;
+        Tensor lg = reftest_f16({R, V}, 8.0f, 43);
+        std::vector<int32_t> want(R);
+        mio_greedy_argmax(bits(lg), R, V, want.data());
+        Tensor lgd = lg.to(Device::cuda(0));
+        Tensor od = Tensor::empty({R}, DType::INT32, Device::cuda(0));
+        mini_infer::kernels::launch_greedy_sample_batched(static_cast<const __half*>(lgd.data()), R,
+                                                          V, static_cast<int*>(od.data()), 0);
+        Tensor oh = od.to(Device::cpu());
+        const bool ok = std::memcmp(oh.data(), want.data(), R * 4) == 0;
+        std::printf("  %-40s %s\n", "launch_greedy_sample_batched [3,152064]", ok ? "OK" : "FAIL");
+        EXPECT(ok, "greedy batched");
+        mini_infer::kernels::launch_greedy_sample(static_cast<const __half*>(lgd.data()), V,
+                                                  static_cast<int*>(od.data()), 0);
+        oh = od.to(Device::cpu());
+        EXPECT(static_cast<const int32_t*>(oh.data())[0] == want[0], "greedy single row");
     }
     // --- device Tensor round trip --------------------------------------------
     {

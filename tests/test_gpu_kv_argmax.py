@@ -1,0 +1,141 @@
+"""GPU parity: paged KV-cache scatter and greedy argmax sampling (bit-exact:
+both are selections, with no arithmetic to round)."""
+import numpy as np
+import pytest
+
+from helpers import assert_bits_equal, normal_f16, to_dev, to_host
+
+pytestmark = pytest.mark.gpu
+
+
+def _case(msg):
+    print(f"[case] {msg}", flush=True)
+
+
+def _paged_setup(rng, B, S, H, D, bs, L, NB, starts, seqs):
+    mb = max(1, -(-int(max(seqs)) // bs))
+    src = normal_f16(rng, (B, S, H, D))
+    cache = normal_f16(rng, (L, NB, H, bs, D))
+    bt = rng.permutation(NB)[:B * mb].reshape(B, mb).astype(np.int32)
+    return src, cache, bt, np.asarray(seqs, np.int32), np.asarray(starts, np.int32)
+
+
+@pytest.mark.parametrize("B,S,starts,seqs", [
+    (1, 3000, [0], [3000]),                      # a prefill
+    (64, 1, list(range(100, 6500, 100)), [p + 1 for p in range(100, 6500, 100)]),  # decode batch
+    (3, 17, [0, 5, 40], [17, 20, 57]),           # ragged: b=1 stops at s = 15
+])
+def test_kv_scatter_vs_oracle(mk, orc, dev, B, S, starts, seqs):
+    _case(f"kv scatter B={B} S={S}")
+    rng = np.random.default_rng(B * 1000 + S)
+    H, D, bs, L = 4, 128, 16, 2
+    NB = B * (max(seqs) // bs + 2) + 3
+    src, cache, bt, sl, sp = _paged_setup(rng, B, S, H, D, bs, L, NB, starts, seqs)
+    cd = to_dev(cache, dev)
+    mk.paged_kv_scatter(to_dev(src, dev), cd, to_dev(bt, dev), to_dev(sl, dev), to_dev(sp, dev),
+                        layer=1, block_size=bs)
+    ref = orc.paged_kv_scatter(src, cache, bt, sl, sp, layer=1, block_size=bs)
+    assert_bits_equal(to_host(cd), ref, what="cache")
+
+
+def test_kv_scatter_pair_and_bad_blocks(mk, orc, dev):
+    """K and V in one launch; a -1 / out-of-range block entry is skipped."""
+    _case("kv scatter K+V, bad blocks")
+    rng = np.random.default_rng(7)
+    B, S, H, D, bs, L = 4, 40, 4, 128, 16, 3
+    NB = 30
+    starts, seqs = [0, 10, 0, 7], [40, 50, 33, 47]
+    k, kc, bt, sl, sp = _paged_setup(rng, B, S, H, D, bs, L, NB, starts, seqs)
+    v = normal_f16(rng, k.shape)
+    vc = normal_f16(rng, kc.shape)
+    bt[1, 1] = -1
+    bt[3, 2] = NB + 5
+    kcd, vcd = to_dev(kc, dev), to_dev(vc, dev)
+    args = (to_dev(bt, dev), to_dev(sl, dev), to_dev(sp, dev))
+    mk.paged_kv_scatter(to_dev(k, dev), kcd, *args, layer=2, block_size=bs, v_src=to_dev(v, dev),
+                        v_cache=vcd)
+    assert_bits_equal(to_host(kcd), orc.paged_kv_scatter(k, kc, bt, sl, sp, 2, bs), what="k")
+    assert_bits_equal(to_host(vcd), orc.paged_kv_scatter(v, vc, bt, sl, sp, 2, bs), what="v")
+
+
+def test_kv_scatter_odd_head_dim(mk, orc, dev):
+    _case("kv scatter D=6 (scalar path)")
+    rng = np.random.default_rng(8)
+    src, cache, bt, sl, sp = _paged_setup(rng, 2, 5, 3, 6, 4, 1, 10, [0, 3], [5, 8])
+    cd = to_dev(cache, dev)
+    mk.paged_kv_scatter(to_dev(src, dev), cd, to_dev(bt, dev), to_dev(sl, dev), to_dev(sp, dev),
+                        layer=0, block_size=4)
+    assert_bits_equal(to_host(cd), orc.paged_kv_scatter(src, cache, bt, sl, sp, 0, 4), what="cache")
+
+
+@pytest.mark.parametrize("B,V,levels", [(64, 152064, None), (64, 152064, 7), (1, 152064, None),
+                                        (600, 4096, 5), (3, 1000, 3), (5, 100003, 9),
+                                        (2, 17, None), (512, 152064, None)])
+def test_greedy_argmax_vs_oracle(mk, orc, dev, B, V, levels):
+    """levels: values drawn from a few integers, so maxima tie often and the
+    reference's tie order decides."""
+    _case(f"argmax [{B},{V}] levels={levels}")
+    rng = np.random.default_rng(B + V)
+    if levels is None:
+        x = normal_f16(rng, (B, V), 0, 4)
+    else:
+        x = rng.integers(-levels, levels + 1, (B, V)).astype(np.float16)
+    got = to_host(mk.greedy_argmax(to_dev(x, dev)))
+    ref = orc.greedy_argmax(x)
+    assert (got == ref).all(), f"{int((got != ref).sum())} rows differ"
+
+
+def test_greedy_argmax_specials(mk, orc, dev):
+    _case("argmax NaN / -inf / -0")
+    x = np.zeros((4, 9000), dtype=np.float16)
+    x[0, :] = -np.inf                   # nothing eligible -> -1
+    x[1, ::2] = np.nan
+    x[1, 5] = 3.0                       # NaN never chosen
+    x[2, :] = -0.0
+    x[2, 4000] = 0.0                    # -0 ties +0
+    x[3, 17] = np.inf
+    got = to_host(mk.greedy_argmax(to_dev(x, dev)))
+    assert (got == orc.greedy_argmax(x)).all()
+    assert got[0] == -1 and got[1] == 5 and got[3] == 17
+
+
+def test_greedy_argmax_workspace_graph(mk, orc, dev):
+    _case("argmax with workspace in a graph")
+    import torch
+    rng = np.random.default_rng(9)
+    x = normal_f16(rng, (64, 152064), 0, 4)
+    xd = to_dev(x, dev)
+    ws = torch.empty(max(1, mk.greedy_argmax_workspace_bytes(64, 152064)), dtype=torch.uint8,
+                     device=dev)
+    out = torch.empty(64, dtype=torch.int32, device=dev)
+    mk.greedy_argmax(xd, out=out, workspace=ws)
+    ref = orc.greedy_argmax(x)
+    assert (to_host(out) == ref).all()
+    g = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    torch.cuda.current_stream().wait_stream(side)
+    with torch.cuda.graph(g):
+        mk.greedy_argmax(xd, out=out, workspace=ws)
+    for _ in range(3):
+        out.fill_(-7)
+        torch.cuda.synchronize()
+        g.replay()
+        assert (to_host(out) == ref).all()
+
+
+def test_greedy_argmax_max_at_every_vector_position(mk, orc, dev):
+    """Regression: one unique maximum per row at offsets 0..15 inside a
+    16-element pair of vectors, at the start, middle and end of long rows."""
+    _case("argmax max at every vector lane")
+    V = 152064
+    rows = []
+    for base in (0, 74000 - 74000 % 16, V - 16):
+        for k in range(16):
+            r = np.zeros(V, dtype=np.float16)
+            r[base + k] = 1.0
+            rows.append(r)
+    x = np.stack(rows)
+    got = to_host(mk.greedy_argmax(to_dev(x, dev)))
+    want = np.array([int(np.argmax(r)) for r in rows], dtype=np.int32)
+    assert (got == want).all() and (orc.greedy_argmax(x) == want).all()

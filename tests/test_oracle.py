@@ -295,3 +295,76 @@ def test_threaded_matches_single_thread():
     w = normal_f16(rng, (512,), 1.0, 0.1)
     assert (O.rmsnorm(x, w, nthreads=1) == O.rmsnorm(x, w, nthreads=8)).all()
     assert (O.softmax(x, nthreads=1) == O.softmax(x, nthreads=8)).all()
+
+
+# ---------------------------------------------------------------------------
+# Paged KV scatter and greedy argmax (the steps either side of the chain)
+# ---------------------------------------------------------------------------
+
+def _bitrev8(u):
+    return int(f"{u:08b}"[::-1], 2)
+
+
+def _argmax_rule(row):
+    """The reference kernel's result stated as a rule: among entries equal to
+    the maximum (NaN ignored, -0 == +0, only values above -inf), the one whose
+    thread u = i mod 256 has the smallest 8-bit bit reversal (the tree keeps
+    the lower slot, so u's low bits decide first), then the smallest i; -1 if
+    none."""
+    v = row.astype(np.float32)
+    ok = ~np.isnan(v) & (v > -np.inf)
+    if not ok.any():
+        return -1
+    m = v[ok].max()
+    idx = np.nonzero(ok & (v == m))[0]
+    return int(min(idx, key=lambda i: (_bitrev8(i % 256), i)))
+
+
+def test_greedy_argmax_simulation_matches_rule_and_numpy():
+    rng = np.random.default_rng(11)
+    # distinct maxima: plain argmax
+    x = normal_f16(rng, (6, 5000), 0, 4)
+    x[np.arange(6), rng.integers(0, 5000, 6)] = 60.0
+    assert (O.greedy_argmax(x) == np.argmax(x.astype(np.float32), axis=1)).all()
+    # heavy ties: values on a coarse grid
+    t = (rng.integers(-3, 4, (20, 3000))).astype(np.float16)
+    got = O.greedy_argmax(t)
+    assert [int(g) for g in got] == [_argmax_rule(r) for r in t]
+    # ties where the smaller index is not the answer: thread 128 (reversed 1)
+    # beats thread 1 (reversed 128); i = 300 (thread 44 = 0b00101100,
+    # reversed 52) beats i = 100 (thread 100 = 0b01100100, reversed 38)? no:
+    # 38 < 52, so 100 wins there
+    r = np.zeros(1500, dtype=np.float16)
+    r[1281] = 5; r[128] = 5
+    assert O.greedy_argmax(r)[0] == 128 == _argmax_rule(r)
+    r = np.zeros(1000, dtype=np.float16)
+    r[100] = 5; r[300] = 5
+    assert O.greedy_argmax(r)[0] == 100 == _argmax_rule(r)
+    r = np.zeros(1000, dtype=np.float16)
+    r[2] = 5; r[257] = 5  # thread 2 (reversed 64) vs thread 1 (reversed 128)
+    assert O.greedy_argmax(r)[0] == 2 == _argmax_rule(r)
+    # NaN never chosen, -0 == +0, all -inf -> -1
+    r = np.array([np.nan, -0.0, 0.0, -1.0], dtype=np.float16)
+    assert O.greedy_argmax(r)[0] == 2 == _argmax_rule(r)  # -0 ties +0; thread 2 beats 1
+    assert O.greedy_argmax(np.full(10, -np.inf, dtype=np.float16))[0] == -1
+
+
+def test_paged_kv_scatter_brute_force():
+    rng = np.random.default_rng(12)
+    B, S, H, D, bs, L, NB, MB = 3, 9, 2, 16, 4, 2, 20, 5
+    src = normal_f16(rng, (B, S, H, D))
+    cache = normal_f16(rng, (L, NB, H, bs, D))
+    bt = rng.permutation(NB)[:B * MB].reshape(B, MB).astype(np.int32)
+    bt[2, 3] = -1                     # an unallocated block: skipped
+    start = np.array([0, 5, 8], dtype=np.int32)
+    seq = np.array([9, 12, 20], dtype=np.int32)  # b=1 keeps s < 7
+    out = O.paged_kv_scatter(src, cache, bt, seq, start, layer=1, block_size=bs)
+    ref = cache.copy()
+    for b in range(B):
+        for s in range(S):
+            p = start[b] + s
+            if p >= seq[b] or p // bs >= MB or bt[b, p // bs] < 0:
+                continue
+            ref[1, bt[b, p // bs], :, p % bs, :] = src[b, s]
+    assert (out.view(np.uint16) == ref.view(np.uint16)).all()
+    assert (out[0].view(np.uint16) == cache[0].view(np.uint16)).all()  # other layer untouched
