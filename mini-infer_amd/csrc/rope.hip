@@ -12,11 +12,11 @@
 // is then rounded to fp16 -- the same two roundings the reference performs, so
 // outputs match it bit for bit given equal tables.
 //
-// cos/sin: the fp32 sincosf result (a few ulp) is rounded to fp16; when the
-// value lies within 2^-20 (relative) of an fp16 rounding boundary the angle is
-// re-evaluated in fp64, so the fp16 value always equals half(RN32(cos(angle)))
-// computed from the exact cosine.  This makes the tables independent of the
-// fp32 sincos implementation.
+// cos/sin: a compact fp32 sin/cos (rope_sincos.h: Cody-Waite reduction,
+// Taylor polynomials; a few ulp) is rounded to fp16; when the value lies
+// within 2^-20 (relative, 2^-29 absolute floor) of an fp16 rounding boundary
+// the angle is re-evaluated in fp64, so the fp16 value always equals
+// half(RN32(cos(angle))) computed from the exact cosine.
 //
 // Design (HBM-bound: 8 bytes/element in place, + 8 bytes/token of positions):
 //   a 256-lane workgroup takes 1-8 tokens.  Every lane first issues
@@ -29,6 +29,7 @@
 
 #include "mi_device.h"
 #include "mi_host.h"
+#include "rope_sincos.h"
 
 namespace mi {
 namespace {
@@ -40,21 +41,22 @@ struct InvFreq {
     float v[kMaxHalf];
 };
 
-#ifndef MI_ROPE_GUARD
-#define MI_ROPE_GUARD 9.5367431640625e-07f  // 2^-20
-#endif
+// fp16 cos/sin of an fp32 angle, equal to half(RN32(exact)) (see file header).
+// |ang| <= 2^20: the fp32 Cody-Waite form, re-evaluated in fp64 when a value
+// lies within rope_guard_width of an fp16 rounding boundary; larger angles
+// (positions beyond 2^20 / inv_freq) go straight to the fp64 form, which holds
+// to |ang| <= 2^30.
 __device__ __forceinline__ bool near_half_boundary(float v) {
-    const float d = v * MI_ROPE_GUARD;  // relative half-width of the guard window
+    const float d = rope_guard_width(v);
     return to_half(v - d) != to_half(v + d);
 }
 
-// fp16 cos/sin of an fp32 angle, equal to half(RN32(exact)) (see file header).
 __device__ __forceinline__ void cos_sin_half(float ang, half_t& hc, half_t& hs) {
     float s, c;
-    sincosf(ang, &s, &c);
-    if (near_half_boundary(c) || near_half_boundary(s)) {
+    rope_sincos_f32(ang, &s, &c);
+    if (!rope_sincos_f32_ok(ang) || near_half_boundary(c) || near_half_boundary(s)) {
         double sd, cd;
-        sincos(static_cast<double>(ang), &sd, &cd);
+        rope_sincos_f64(static_cast<double>(ang), &sd, &cd);
         c = static_cast<float>(cd);
         s = static_cast<float>(sd);
     }
@@ -319,6 +321,166 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(half_t* q, int Hq, ha
     }
 }
 
+// Persistent, software-pipelined form of qk_norm_rope_kernel: a grid of
+// about the resident capacity walks groups of G tokens (G * units-per-token
+// <= 256 * P, G * head_dim/2 <= 256), and while it normalises and rotates
+// group g it already holds the loads of the next group in flight and builds
+// that group's cos/sin rows in the other half of a double-buffered LDS table.
+// HBM reads of the next group overlap the writes of the current one, which a
+// single round of load-everything / barrier / store-everything workgroups
+// cannot do.
+//
+// The vector-memory counter retires loads and stores in issue order, so the
+// loop is arranged so that no wait drains more than it needs to:
+//   * each step begins with one full drain -- the current group's data and
+//     the next group's positions, both issued a step earlier, and the last
+//     step's stores -- and only then issues its prefetch, so nothing inside
+//     the step waits for the loads just issued (with loads and stores both
+//     outstanding, the compiler can only wait for a load with a full drain);
+//   * the two register buffers are used ping-pong (no loop-carried copies);
+//   * each lane's table entry (token-in-group, frequency index) is the same in
+//     every group, so its inv_freq is read once.
+// One barrier per group: the table half written in a step was last read in
+// the step before, ahead of this step's barrier.
+//
+// s_waitcnt immediate for gfx9-family: vmcnt = 0 (bits 3:0 and 15:14),
+// expcnt = 7 (bits 6:4) and lgkmcnt = 15 (bits 11:8) left unconstrained.
+constexpr int kDrainVmem = 0x0F70;
+template <int CPH, int P>
+__global__ __launch_bounds__(256) void qk_norm_rope_pipe_kernel(
+    half_t* q, int Hq, half_t* k, int Hkv, const half_t* __restrict__ wq,
+    const half_t* __restrict__ wk, const int64_t* __restrict__ positions, int64_t T, int G,
+    float eps, float w_bias, InvFreq inv) {
+    constexpr int HALF = CPH * 8;
+    constexpr int HD = 2 * HALF;
+    constexpr int kTab = 256;  // cos (or sin) entries per table half: G * HALF <= kTab
+    __shared__ float cs[2][2 * kTab];
+    // (w + bias) in fp32 for Q heads (row 0) and K heads (row 1), read from
+    // LDS per unit rather than held in 32 registers across the loop; the
+    // loop's first barrier orders these writes before any read.
+    __shared__ float wt[2][HD];
+    for (int i = threadIdx.x; i < 2 * HD; i += 256) {
+        const int r = i / HD, j = i - r * HD;
+        wt[r][j] = (r == 0 || Hkv > 0) ? (float)(r == 0 ? wq : wk)[j] + w_bias : 0.0f;
+    }
+    const int upt = (Hq + Hkv) * CPH;
+    const int c = threadIdx.x & (CPH - 1);
+    const int64_t ngroups = (T + G - 1) / G;
+    const int64_t stride = gridDim.x;
+
+    // A lane's slots are the same (token-in-group, head) pairs in every
+    // group; only the group's first token moves.
+    int slot_t[P];
+    int64_t slot_off[P];  // element offset of the head at token 0 of the group
+    bool slot_k[P], slot_on[P];
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+        const int u = threadIdx.x + p * 256;
+        const int t = u / upt;
+        const int h = (u - t * upt) / CPH;
+        slot_t[p] = t;
+        slot_on[p] = t < G;
+        slot_k[p] = h >= Hq;
+        slot_off[p] = slot_k[p] ? (static_cast<int64_t>(t) * Hkv + (h - Hq)) * HD + c * 8
+                                : (static_cast<int64_t>(t) * Hq + h) * HD + c * 8;
+    }
+    // This lane's table entry.
+    const bool tab_on = static_cast<int>(threadIdx.x) < G * HALF;
+    const int tab_t = threadIdx.x / HALF;
+    const float tab_f = inv.v[threadIdx.x % HALF];
+
+    auto slot_ptr = [&](int p, int64_t tok0) -> half_t* {
+        return slot_k[p] ? k + tok0 * Hkv * HD + slot_off[p] : q + tok0 * Hq * HD + slot_off[p];
+    };
+    auto load_position = [&](int64_t g) -> int64_t {
+        const int64_t tok = g * G + tab_t;
+        return (g < ngroups && tab_on && tok < T) ? positions[tok] : 0;
+    };
+    auto load_group = [&](int64_t g, h8* a1, h8* a2) {
+        const int64_t tok0 = g * G;
+#pragma unroll
+        for (int p = 0; p < P; ++p) {
+            a1[p] = h8(0);
+            a2[p] = h8(0);
+            if (slot_on[p] && tok0 + slot_t[p] < T) {
+                const half_t* hp = slot_ptr(p, tok0);
+                a1[p] = ld8_stream(hp);
+                a2[p] = ld8_stream(hp + HALF);
+            }
+        }
+    };
+    auto build_table = [&](int64_t pos, float* tab) {
+        if (tab_on) {
+            half_t hc, hs;
+            cos_sin_half(static_cast<float>(pos) * tab_f, hc, hs);
+            tab[threadIdx.x] = (float)hc;
+            tab[kTab + threadIdx.x] = (float)hs;
+        }
+    };
+    auto process = [&](int64_t g, const float* tab, const h8* a1, const h8* a2) {
+        const int64_t tok0 = g * G;
+#pragma unroll
+        for (int p = 0; p < P; ++p) {
+            float ss = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float f1 = (float)a1[p][e], f2 = (float)a2[p][e];
+                ss = fmaf(f1, f1, ss);
+                ss = fmaf(f2, f2, ss);
+            }
+            ss = group_sum<CPH>(ss);
+            if (!slot_on[p] || tok0 + slot_t[p] >= T) continue;
+            const float rrms = rsqrtf(ss / static_cast<float>(HD) + eps);
+            const float* w = &wt[slot_k[p] ? 1 : 0][c * 8];
+            const float* cst = tab + slot_t[p] * HALF + c * 8;
+            h8 y1, y2;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float v1 = (float)to_half((float)a1[p][e] * rrms * w[e]);
+                const float v2 = (float)to_half((float)a2[p][e] * rrms * w[HALF + e]);
+                const float cv = cst[e], sv = cst[kTab + e];
+                y1[e] = to_half(fp32_rounded(v1 * cv - v2 * sv));
+                y2[e] = to_half(fp32_rounded(v2 * cv + v1 * sv));
+            }
+            half_t* hp = slot_ptr(p, tok0);
+            st8_stream(hp, y1);
+            st8_stream(hp + HALF, y2);
+        }
+    };
+
+    int64_t g = blockIdx.x;
+    if (g >= ngroups) return;  // whole workgroup: no barrier is skipped by part of it
+    h8 a1[P], a2[P], b1[P], b2[P];
+    int64_t pos = load_position(g);
+    load_group(g, a1, a2);
+    int64_t pos_next = load_position(g + stride);
+    build_table(pos, cs[0]);
+    // One step: prefetch group g + stride into (n1, n2) and its table into
+    // cs[nb], prefetch the positions of g + 2 * stride, then process g.
+    auto step = [&](int cb, const h8* c1, const h8* c2, h8* n1, h8* n2) -> bool {
+        // Drain here, before the next loads are issued: with stores in
+        // flight every wait on a load is a full drain, so the only wait of a
+        // step must come before its prefetch, not after it.
+        __builtin_amdgcn_s_waitcnt(kDrainVmem);
+        const int64_t gn = g + stride;
+        const bool more = gn < ngroups;
+        if (more) {
+            const int64_t pn = pos_next;
+            pos_next = load_position(gn + stride);
+            load_group(gn, n1, n2);
+            build_table(pn, cs[cb ^ 1]);
+        }
+        __syncthreads();
+        process(g, cs[cb], c1, c2);
+        g = gn;
+        return more;
+    };
+    for (;;) {
+        if (!step(0, a1, a2, b1, b2)) break;
+        if (!step(1, b1, b2, a1, a2)) break;
+    }
+}
+
 __global__ __launch_bounds__(256) void rope_table_kernel(const int64_t* __restrict__ positions,
                                                          half_t* __restrict__ cos_t,
                                                          half_t* __restrict__ sin_t, int64_t N,
@@ -412,10 +574,53 @@ int launch_rope(const half_t* q_in, half_t* q_out, int64_t Hq, const half_t* k_i
                                    inv, s);
 }
 
+// MI_QKN_PIPE=0 selects the one-round kernel for every shape (measurement).
+#ifndef MI_QKN_PIPE
+#define MI_QKN_PIPE 1
+#endif
+
+// Pipelined launch: P register slots per lane (the fewest that hold one
+// token's units), G tokens per group (as many as the slots and the table
+// hold), and a grid of the resident capacity, so every workgroup stays
+// resident and walks ngroups / grid groups.  Measured at T = 6064, Qwen2.5
+// heads: 63% of HBM peak against 56% for the one-round kernel; two tokens
+// per step (P = 2) and a grid of twice the capacity both measured lower.
+template <int CPH, int P>
+int launch_qk_norm_rope_pipe(half_t* q, int hq, half_t* k, int hk, const half_t* wq,
+                             const half_t* wk, const int64_t* positions, int64_t T, float eps,
+                             float w_bias, const InvFreq& inv, hipStream_t s) {
+    constexpr int HALF = CPH * 8;
+    const int upt = (hq + hk) * CPH;
+    int G = (256 * P) / upt;
+    if (G > 256 / HALF) G = 256 / HALF;
+    const int64_t ngroups = ceil_div(T, G);
+    const int64_t cap =
+        resident_workgroups(reinterpret_cast<const void*>(qk_norm_rope_pipe_kernel<CPH, P>), 256);
+    int64_t grid = cap > 0 ? cap : ngroups;
+    if (grid > ngroups) grid = ngroups;
+    if (grid > kMaxGridX) grid = kMaxGridX;
+    qk_norm_rope_pipe_kernel<CPH, P><<<dim3(static_cast<unsigned>(grid)), dim3(256), 0, s>>>(
+        q, hq, k, hk, wq, wk, positions, T, G, eps, w_bias, inv);
+    return launch_status();
+}
+
 template <int CPH>
 int launch_qk_norm_rope_t(half_t* q, int hq, half_t* k, int hk, const half_t* wq,
                           const half_t* wk, const int64_t* positions, int64_t T, float eps,
                           float w_bias, const InvFreq& inv, hipStream_t s) {
+    if (MI_QKN_PIPE) {
+        const int upt = (hq + hk) * CPH;
+        if (upt <= 256)
+            return launch_qk_norm_rope_pipe<CPH, 1>(q, hq, k, hk, wq, wk, positions, T, eps,
+                                                    w_bias, inv, s);
+        if (upt <= 512)
+            return launch_qk_norm_rope_pipe<CPH, 2>(q, hq, k, hk, wq, wk, positions, T, eps,
+                                                    w_bias, inv, s);
+        if (upt <= 1024)
+            return launch_qk_norm_rope_pipe<CPH, 4>(q, hq, k, hk, wq, wk, positions, T, eps,
+                                                    w_bias, inv, s);
+        // more than 1024 units per token: the one-round kernel below
+    }
     const int tpw = pick_tokens_per_wg(T, qk_norm_rope_kernel<CPH, 1>, qk_norm_rope_kernel<CPH, 2>,
                                        qk_norm_rope_kernel<CPH, 4>, qk_norm_rope_kernel<CPH, 8>);
     const int64_t grid = ceil_div(T, tpw);

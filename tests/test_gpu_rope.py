@@ -13,7 +13,7 @@ from pathlib import Path
 import numpy as np
 import pytest
 
-from helpers import assert_bits_equal, assert_close, normal_f16, to_dev, to_host
+from helpers import ATOL, RTOL, assert_bits_equal, assert_close, normal_f16, to_dev, to_host
 
 pytestmark = pytest.mark.gpu
 GOLD = np.load(Path(__file__).resolve().parent / "golden" / "ref_cases.npz")
@@ -59,6 +59,21 @@ def test_tables_large_positions(mk, orc, dev):
     c_ref, s_ref = orc.rope_tables(inv, pos)
     assert_bits_equal(to_host(c), c_ref, what="cos")
     assert_bits_equal(to_host(s), s_ref, what="sin")
+
+
+@pytest.mark.parametrize("lo,hi", [(1 << 20, 1 << 22), (1 << 22, 1 << 24)])
+def test_tables_huge_positions(mk, orc, dev, lo, hi):
+    """Positions past 2^20 (angles beyond the fp32 sin/cos range, evaluated in
+    fp64 directly), theta 1e4 and 1e6: still bit-exact."""
+    _case(f"rope tables positions in [{lo}, {hi})")
+    rng = np.random.default_rng(lo)
+    pos = rng.integers(lo, hi, 4096).astype(np.int64)
+    for theta in (1e4, 1e6):
+        inv = orc.rope_inv_freq(128, theta)
+        c, s = mk.rope_tables(inv, to_dev(pos, dev))
+        c_ref, s_ref = orc.rope_tables(inv, pos)
+        assert_bits_equal(to_host(c), c_ref, what=f"cos theta={theta}")
+        assert_bits_equal(to_host(s), s_ref, what=f"sin theta={theta}")
 
 
 def test_config3_fused_qk(mk, orc, dev):
@@ -144,12 +159,47 @@ def _qk_norm_rope_ref(orc, x, w, pos, inv, eps=1e-6, add_one=False):
     return orc.rope_neox(n16, c, s, nthreads=8), n16
 
 
+def _ulp16(v):
+    return np.spacing(np.abs(np.asarray(v, np.float32)).astype(np.float16)).astype(np.float32)
+
+
+def _assert_norm_rope_close(ours, ref, n16, what):
+    """rtol = atol = 1e-3, except at elements whose fp16 normalised input sits
+    on a rounding boundary.  The oracle's statistics are exact (double sum of
+    squares, double 1/sqrt); a GPU kernel -- the reference's included --
+    sums in an fp32 tree and uses an fp32 reciprocal square root, so the fp16
+    value it hands to the rotation can be one ulp away there.  RoPE then
+    carries that ulp into an output that may be much smaller (x1 c - x2 s
+    cancels).  Such elements must be rare (< 1e-5 of the tensor) and within
+    one ulp of each rotated operand plus one output ulp."""
+    ours = np.asarray(ours).astype(np.float32)
+    ref = np.asarray(ref, np.float32)
+    diff = np.abs(ours - ref)
+    out = diff > ATOL + RTOL * np.abs(ref)
+    if not out.any():
+        return
+    half = n16.shape[-1] // 2
+    partner = np.concatenate([n16[..., half:], n16[..., :half]], axis=-1)
+    bound = _ulp16(n16) + _ulp16(partner) + _ulp16(ref)
+    worst = np.unravel_index(np.argmax(diff - bound), diff.shape)
+    assert (diff[out] <= bound[out]).all(), (
+        f"{what}: error beyond one ulp of the normalised operands at {worst}: "
+        f"ours={ours[worst]} ref={ref[worst]} bound={bound[worst]}")
+    assert out.mean() < 1e-5, f"{what}: {int(out.sum())} of {out.size} outside tolerance"
+
+
 @pytest.mark.parametrize("T,Hq,Hkv,hd", [(6064, 28, 4, 128), (37, 8, 2, 64), (5, 3, 1, 256),
                                          (9, 2, 2, 16), (3, 4, 0, 128), (4, 0, 2, 128),
-                                         (2, 2, 1, 512), (11, 5, 3, 32)])
+                                         (2, 2, 1, 512), (11, 5, 3, 32), (20000, 8, 2, 64),
+                                         (3001, 40, 8, 128), (500, 64, 32, 128),
+                                         (50, 128, 16, 128)])
 def test_qk_norm_rope(mk, orc, dev, T, Hq, Hkv, hd):
     """Fused Q/K RMSNorm + RoPE == the reference's norm-then-rope composition
-    (src/layers/attention.cpp:754-780), within rtol = atol = 1e-3."""
+    (src/layers/attention.cpp:754-780), within rtol = atol = 1e-3.  Shapes
+    cover both launch forms: token groups of 1 to 32 tokens with a ragged
+    last group, groups walked several times per workgroup (T = 20000, 6064),
+    2 and 4 register slots per lane (48 and 96 heads of 128), and the
+    one-round kernel (144 heads of 128: more than 1024 lanes per token)."""
     _case(f"qk_norm_rope T={T} Hq={Hq} Hkv={Hkv} hd={hd}")
     rng = np.random.default_rng(T * 7 + hd)
     q = normal_f16(rng, (T, Hq, hd))
@@ -161,11 +211,26 @@ def test_qk_norm_rope(mk, orc, dev, T, Hq, Hkv, hd):
     qd, kd = to_dev(q, dev), to_dev(k, dev)
     mk.qk_norm_rope(qd, kd if Hkv else None, to_dev(wq, dev), to_dev(wk, dev), to_dev(pos, dev), inv)
     if Hq:
-        ref, _ = _qk_norm_rope_ref(orc, q, wq, pos, inv)
-        assert_close(to_host(qd), ref, what="q")
+        ref, n16 = _qk_norm_rope_ref(orc, q, wq, pos, inv)
+        _assert_norm_rope_close(to_host(qd), ref, n16, what="q")
     if Hkv:
-        ref, _ = _qk_norm_rope_ref(orc, k, wk, pos, inv)
-        assert_close(to_host(kd), ref, what="k")
+        ref, n16 = _qk_norm_rope_ref(orc, k, wk, pos, inv)
+        _assert_norm_rope_close(to_host(kd), ref, n16, what="k")
+
+
+def test_qk_norm_rope_huge_positions(mk, orc, dev):
+    """Positions up to 2^23: the in-kernel table takes the fp64 path."""
+    _case("qk_norm_rope positions up to 2^23")
+    rng = np.random.default_rng(23)
+    T, Hq, Hkv, hd = 300, 28, 4, 128
+    q = normal_f16(rng, (T, Hq, hd)); k = normal_f16(rng, (T, Hkv, hd))
+    wq = normal_f16(rng, (hd,), 1.0, 0.1); wk = normal_f16(rng, (hd,), 1.0, 0.1)
+    pos = rng.integers(0, 1 << 23, T).astype(np.int64)
+    inv = orc.rope_inv_freq(hd, 1e4)
+    qd, kd = to_dev(q, dev), to_dev(k, dev)
+    mk.qk_norm_rope(qd, kd, to_dev(wq, dev), to_dev(wk, dev), to_dev(pos, dev), inv)
+    _assert_norm_rope_close(to_host(qd), *_qk_norm_rope_ref(orc, q, wq, pos, inv), what="q")
+    _assert_norm_rope_close(to_host(kd), *_qk_norm_rope_ref(orc, k, wk, pos, inv), what="k")
 
 
 def test_qk_norm_rope_vs_two_launches(mk, orc, dev):
