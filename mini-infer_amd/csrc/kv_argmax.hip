@@ -132,7 +132,7 @@ int kv_scatter(const void* src0, void* cache0, const void* src1, void* cache1,
 typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
 
 constexpr int kArgmaxSplitMaxRows = 512;
-constexpr int kArgmaxMaxSplits = 64;
+constexpr int kArgmaxMaxSplits = 1024;
 
 // Order key of element i with fp16 bits h (see the file header); 0 when the
 // element can never be chosen (NaN or -inf).
@@ -161,32 +161,61 @@ __device__ __forceinline__ int32_t key_index(uint64_t key) {
     return key == 0 ? -1 : static_cast<int32_t>(~static_cast<uint32_t>(key));
 }
 
-// Best key of elements [begin, end) of a row, over the workgroup.
-template <int VEC>
+// Best key of elements [begin, end) of a row, over the workgroup.  The range
+// is walked in tiles of 256 * VEC * U elements; every load of a tile is
+// issued before any arithmetic, so a workgroup whose chunk is one tile waits
+// for HBM once.  With VEC = 8, begin is a multiple of 2048 and end - begin a
+// multiple of 16.
+template <int VEC, int U>
 __device__ __forceinline__ uint64_t chunk_best(const half_t* xr, int64_t begin, int64_t end,
                                                uint64_t* slots) {
     uint64_t best = 0;
-    const int64_t step = static_cast<int64_t>(blockDim.x) * VEC;
-    for (int64_t i0 = begin + static_cast<int64_t>(threadIdx.x) * VEC; i0 < end; i0 += 2 * step) {
+    constexpr int64_t kTile = 256 * VEC * U;
+    for (int64_t t0 = begin; t0 < end; t0 += kTile) {
         if constexpr (VEC == 8) {
-            // bit patterns of the whole vector at once (bit-casting single
-            // elements of an fp16 vector was miscompiled into reusing
-            // element 0's pattern for all eight)
-            const u16x8 a = __builtin_bit_cast(u16x8, ld8_stream(xr + i0));
-            u16x8 c = u16x8(0);
-            const bool second = i0 + step < end;
-            if (second) c = __builtin_bit_cast(u16x8, ld8_stream(xr + i0 + step));
+            // Lane maximum first (packed fp16 max, which passes over NaN),
+            // then the element equal to it that the tie order prefers: for
+            // i = t0 + (lane + 256 j) * 8 + k with t0 = 0 mod 256,
+            // bitrev8(i mod 256) = bitrev3(k) << 5 | bitrev5(lane mod 32), so
+            // within a lane a smaller bitrev3(k) wins, then a smaller j.  Only
+            // that one element's 64-bit key is formed.
+            h8 a[U];
 #pragma unroll
-            for (int k = 0; k < 8; ++k) best = max_u64(best, argmax_key(a[k], i0 + k));
-            if (second) {
+            for (int j = 0; j < U; ++j) {
+                const int64_t i = t0 + (threadIdx.x + j * 256) * 8;
+                a[j] = i < end ? ld8_stream(xr + i) : h8(-__builtin_huge_valf16());
+            }
+            h2 m2 = h2(-__builtin_huge_valf16());
 #pragma unroll
-                for (int k = 0; k < 8; ++k) best = max_u64(best, argmax_key(c[k], i0 + step + k));
+            for (int j = 0; j < U; ++j) {
+#pragma unroll
+                for (int k = 0; k < 8; k += 2) m2 = __builtin_elementwise_max(m2, h2{a[j][k], a[j][k + 1]});
+            }
+            const half_t M = __builtin_elementwise_max(m2.x, m2.y);
+            if (M > -__builtin_huge_valf16()) {  // false for NaN and -inf: nothing eligible
+                constexpr int kLowToHigh[8] = {7, 3, 5, 1, 6, 2, 4, 0};  // k by falling bitrev3
+                int code = 0;
+#pragma unroll
+                for (int q = 0; q < 8; ++q) {
+#pragma unroll
+                    for (int j = U - 1; j >= 0; --j)
+                        if (a[j][kLowToHigh[q]] == M) code = j * 8 + kLowToHigh[q];
+                }
+                const int64_t i = t0 + (threadIdx.x + (code >> 3) * 256) * 8 + (code & 7);
+                best = max_u64(best, argmax_key(__builtin_bit_cast(uint16_t, M), i));
             }
         } else {
-            best = max_u64(best, argmax_key(__builtin_bit_cast(uint16_t, xr[i0]), i0));
-            if (i0 + step < end)
-                best = max_u64(best,
-                               argmax_key(__builtin_bit_cast(uint16_t, xr[i0 + step]), i0 + step));
+            uint16_t a[U];
+#pragma unroll
+            for (int j = 0; j < U; ++j) {
+                const int64_t i = t0 + threadIdx.x + j * 256;
+                a[j] = i < end ? __builtin_bit_cast(uint16_t, xr[i]) : uint16_t(0);
+            }
+#pragma unroll
+            for (int j = 0; j < U; ++j) {
+                const int64_t i = t0 + threadIdx.x + j * 256;
+                if (i < end) best = max_u64(best, argmax_key(a[j], i));
+            }
         }
     }
     best = wave_max_u64(best);
@@ -200,7 +229,7 @@ __device__ __forceinline__ uint64_t chunk_best(const half_t* xr, int64_t begin, 
 
 // grid (splits, B).  With one split the index goes straight to `out`;
 // otherwise each chunk's key goes to ws[row * splits + split].
-template <int VEC>
+template <int VEC, int U>
 __global__ __launch_bounds__(256) void argmax_partial_kernel(const half_t* __restrict__ x,
                                                              int64_t V, int64_t chunk,
                                                              uint64_t* __restrict__ ws,
@@ -210,7 +239,7 @@ __global__ __launch_bounds__(256) void argmax_partial_kernel(const half_t* __res
     const int64_t row = blockIdx.y;
     const int64_t b = split * chunk;
     const int64_t e = b + chunk < V ? b + chunk : V;
-    const uint64_t best = chunk_best<VEC>(x + row * V, b, e, slots);
+    const uint64_t best = chunk_best<VEC, U>(x + row * V, b, e, slots);
     if (threadIdx.x == 0) {
         if (splits == 1)
             out[row] = key_index(best);
@@ -219,26 +248,37 @@ __global__ __launch_bounds__(256) void argmax_partial_kernel(const half_t* __res
     }
 }
 
-// One wave per row: lane j reads chunk j's key.
+// One wave per row: lane j folds chunks j, j + 64, ...
 __global__ __launch_bounds__(256) void argmax_final_kernel(const uint64_t* __restrict__ ws,
                                                            int splits, int64_t B,
                                                            int32_t* __restrict__ out) {
     const int64_t row = static_cast<int64_t>(blockIdx.x) * (256 / kWave) + threadIdx.x / kWave;
     const int lane = threadIdx.x & (kWave - 1);
     if (row >= B) return;  // wave-uniform
-    uint64_t k = lane < splits ? ws[row * splits + lane] : 0;
+    uint64_t k = 0;
+    for (int j = lane; j < splits; j += kWave) k = max_u64(k, ws[row * splits + j]);
     k = wave_max_u64(k);
     if (lane == 0) out[row] = key_index(k);
+}
+
+// Few long rows are cut into chunks of whole tiles: aim at ~2048 workgroups
+// (a 19.5 MB read-and-reduce measured flat at 5.0-5.5 us for 1216 to 4800
+// workgroups and slower below), chunk = the nearest whole number of tiles.
+// Tiles of 4096 elements (two vectors per lane) when that still gives >= 1024
+// workgroups, else 2048.
+int argmax_tile(int64_t B, int64_t V) {
+    return B * ceil_div(V, 4096) >= 1024 ? 4096 : 2048;
 }
 
 int64_t argmax_splits(int64_t B, int64_t V, int64_t& chunk) {
     chunk = V;
     if (B >= kArgmaxSplitMaxRows || V < 8192) return 1;
+    const int64_t tile = argmax_tile(B, V);
     int64_t sp = ceil_div(2048, B);
     if (sp > kArgmaxMaxSplits) sp = kArgmaxMaxSplits;
-    const int64_t max_by_len = V / 2048 > 1 ? V / 2048 : 1;
-    if (sp > max_by_len) sp = max_by_len;
-    chunk = ceil_div(ceil_div(V, sp), 16) * 16;  // two 8-element vectors per lane step
+    int64_t tiles = (ceil_div(V, sp) + tile / 2) / tile;  // nearest whole number of tiles
+    if (tiles < 1) tiles = 1;
+    chunk = tiles * tile;
     return ceil_div(V, chunk);
 }
 
@@ -264,10 +304,15 @@ int argmax(const void* logits, int64_t B, int64_t V, int32_t* out, void* ws, int
     const auto* x = static_cast<const half_t*>(logits);
     auto* w = static_cast<uint64_t*>(ws);
     const dim3 g(static_cast<unsigned>(splits), static_cast<unsigned>(B));
-    if (V % 16 == 0 && aligned16(logits))
-        argmax_partial_kernel<8><<<g, dim3(256), 0, st>>>(x, V, chunk, w, out);
-    else
-        argmax_partial_kernel<1><<<g, dim3(256), 0, st>>>(x, V, chunk, w, out);
+    const bool two = splits == 1 || argmax_tile(B, V) == 4096;
+    if (V % 16 == 0 && aligned16(logits)) {
+        if (two)
+            argmax_partial_kernel<8, 2><<<g, dim3(256), 0, st>>>(x, V, chunk, w, out);
+        else
+            argmax_partial_kernel<8, 1><<<g, dim3(256), 0, st>>>(x, V, chunk, w, out);
+    } else {
+        argmax_partial_kernel<1, 8><<<g, dim3(256), 0, st>>>(x, V, chunk, w, out);
+    }
     if (splits > 1)
         argmax_final_kernel<<<dim3(static_cast<unsigned>(ceil_div(B, 256 / kWave))), dim3(256), 0,
                               st>>>(w, static_cast<int>(splits), B, out);

@@ -12,9 +12,12 @@
 //   * Few long rows (the LM-head case, 64 x 152064): one workgroup per row
 //     would light up 64 of 256 CUs, so each row is cut into `splits` chunks.
 //     Kernel 1 writes a (max, sum) pair per chunk to a small stream-ordered
-//     workspace (8 bytes per chunk);
-//     kernel 2, on the same grid, merges the row's pairs (one lane per
-//     chunk, wave reductions, no barrier) and writes its chunk.  Both grids
+//     workspace (8 bytes per chunk), from tiles whose loads are all issued
+//     first (one HBM wait per tile), a packed fp16 lane maximum and one exp
+//     per element;
+//     kernel 2, on the same grid, merges the row's pairs (each lane folds
+//     every 64th chunk, then wave reductions, no barrier) and writes its
+//     chunk.  Both grids
 //     map block (split, row) to the same XCD, so kernel 2's re-read of the
 //     chunk hits the L2 / Infinity Cache that kernel 1 filled.
 #include "mi_device.h"
@@ -24,15 +27,11 @@ namespace mi {
 namespace {
 
 constexpr int kSplitMaxRows = 512;  // below this many rows, split each row
-constexpr int kMaxSplits = 64;      // chunk pairs of a row fit one wave
+constexpr int kMaxSplits = 1024;    // chunk pairs of a row, folded by one wave
 #ifndef MI_SOFTMAX_TARGET_WGS
 #define MI_SOFTMAX_TARGET_WGS 2048
 #endif
-#ifndef MI_SOFTMAX_MIN_CHUNK
-#define MI_SOFTMAX_MIN_CHUNK 2048
-#endif
 constexpr int64_t kSplitTargetWgs = MI_SOFTMAX_TARGET_WGS;
-constexpr int64_t kMinChunk = MI_SOFTMAX_MIN_CHUNK;
 
 // Fold one loaded value group into the lane's online (m, s).
 template <int VEC>
@@ -77,6 +76,43 @@ __device__ __forceinline__ void lane_stats(const half_t* xr, int64_t begin, int6
         }
 #pragma unroll
         for (int j = 0; j < kStatUnroll; ++j) fold<VEC>(v[j], m, s);
+    }
+}
+
+// Vector form for split rows: [begin, end) is walked in tiles of 2048 * U
+// elements (U vectors per lane), all loads of a tile issued first.  The
+// tile's lane maximum comes from packed fp16 max (which passes over NaN, as
+// fmaxf does), then one exp per element against it, and one online merge
+// per tile -- not a rescale per vector.  Out-of-range slots hold -inf, whose
+// exp is 0.
+template <int U>
+__device__ __forceinline__ void tile_stats(const half_t* xr, int64_t begin, int64_t end, float& m,
+                                           float& s) {
+    constexpr int64_t kTile = 256 * 8 * U;
+    for (int64_t t0 = begin; t0 < end; t0 += kTile) {
+        h8 a[U];
+#pragma unroll
+        for (int j = 0; j < U; ++j) {
+            const int64_t i = t0 + (threadIdx.x + j * 256) * 8;
+            a[j] = i < end ? ld8(xr + i) : h8(-__builtin_huge_valf16());
+        }
+        h2 m2 = h2(-__builtin_huge_valf16());
+#pragma unroll
+        for (int j = 0; j < U; ++j) {
+#pragma unroll
+            for (int k = 0; k < 8; k += 2) m2 = __builtin_elementwise_max(m2, h2{a[j][k], a[j][k + 1]});
+        }
+        const float mt = (float)__builtin_elementwise_max(m2.x, m2.y);
+        if (!(mt > -INFINITY)) continue;  // nothing but -inf (or NaN) in this lane's tile
+        float st = 0.0f;
+#pragma unroll
+        for (int j = 0; j < U; ++j) {
+#pragma unroll
+            for (int k = 0; k < 8; ++k) st += fast_exp((float)a[j][k] - mt);
+        }
+        const float mn = fmaxf(m, mt);
+        s = s * fast_exp(m - mn) + st * fast_exp(mt - mn);
+        m = mn;
     }
 }
 
@@ -136,7 +172,8 @@ __global__ __launch_bounds__(1024) void softmax_row_kernel(const half_t* x, half
     write_range<VEC>(xr, yr, 0, D, m, 1.0f / s);
 }
 
-template <int VEC>
+// VEC = 8: U vectors per lane per tile (tile_stats); VEC = 1: lane_stats.
+template <int VEC, int U>
 __global__ __launch_bounds__(256) void softmax_partial_kernel(const half_t* x, float* ws,
                                                               int64_t D, int64_t chunk) {
     __shared__ float slots[256 / kWave];
@@ -145,7 +182,10 @@ __global__ __launch_bounds__(256) void softmax_partial_kernel(const half_t* x, f
     const int64_t b = split * chunk;
     const int64_t e = b + chunk < D ? b + chunk : D;
     float m = -INFINITY, s = 0.0f;
-    lane_stats<VEC>(x + row * D, b, e, m, s);
+    if constexpr (VEC == 8)
+        tile_stats<U>(x + row * D, b, e, m, s);
+    else
+        lane_stats<VEC>(x + row * D, b, e, m, s);
     block_merge(m, s, slots);
     if (threadIdx.x == 0) {
         float* p = ws + (row * splits + split) * 2;
@@ -161,12 +201,15 @@ __global__ __launch_bounds__(256) void softmax_finish_kernel(const half_t* x, ha
     const int split = blockIdx.x, splits = gridDim.x;
     const int64_t row = blockIdx.y;
     const int lane = threadIdx.x & (kWave - 1);
-    // Every wave merges the row's pairs itself: lane j holds chunk j.
+    // Every wave merges the row's pairs itself: lane j folds chunks j, j + 64, ...
     float m = -INFINITY, s = 0.0f;
-    if (lane < splits) {
-        const float* p = ws + (row * splits + lane) * 2;
-        m = p[0];
-        s = p[1];
+    for (int j = lane; j < splits; j += kWave) {
+        const float* p = ws + (row * splits + j) * 2;
+        const float mj = p[0], sj = p[1];
+        if (mj == -INFINITY) continue;
+        const float mn = fmaxf(m, mj);
+        s = s * fast_exp(m - mn) + sj * fast_exp(mj - mn);
+        m = mn;
     }
     const float M = group_max<kWave>(m);
     const float S = group_sum<kWave>(m == -INFINITY ? 0.0f : s * fast_exp(m - M));
@@ -177,20 +220,25 @@ __global__ __launch_bounds__(256) void softmax_finish_kernel(const half_t* x, ha
 
 enum class Plan { kRow, kTwoPass };
 
-// Few long rows are split into chunks: aim for >= 2048 workgroups and chunks
-// of >= 2048 elements, chunk a multiple of 8 so vector accesses stay aligned.
-// (Keeping a whole row in one workgroup's registers instead measured 2x
-// slower at [64, 152064]: a single CU sustains only ~12 GB/s, so 64 busy CUs
-// cannot feed HBM.)
+// Few long rows are split into chunks: aim at ~2048 workgroups (a 19.5 MB
+// read-and-reduce measured flat at 5.0-5.5 us from 1216 to 4800 workgroups)
+// with chunks of a whole number of tiles -- 4096 elements (two vectors per
+// lane) when that still gives >= 1024 workgroups, else 2048.  (Keeping a
+// whole row in one workgroup's registers instead measured 2x slower at
+// [64, 152064]: a single CU sustains only ~12 GB/s, so 64 busy CUs cannot
+// feed HBM.)
+int64_t split_tile(int64_t N, int64_t D) { return N * ceil_div(D, 4096) >= 1024 ? 4096 : 2048; }
+
 Plan plan(int64_t N, int64_t D, int64_t& splits, int64_t& chunk) {
     splits = 1;
     chunk = D;
     if (N >= kSplitMaxRows || D < 8192) return Plan::kRow;
+    const int64_t tile = split_tile(N, D);
     int64_t sp = ceil_div(kSplitTargetWgs, N);
     if (sp > kMaxSplits) sp = kMaxSplits;
-    const int64_t max_by_len = D / kMinChunk > 1 ? D / kMinChunk : 1;
-    if (sp > max_by_len) sp = max_by_len;
-    chunk = ceil_div(ceil_div(D, sp), 8) * 8;
+    int64_t tiles = (ceil_div(D, sp) + tile / 2) / tile;  // nearest whole number of tiles
+    if (tiles < 1) tiles = 1;
+    chunk = tiles * tile;
     splits = ceil_div(D, chunk);
     return Plan::kTwoPass;
 }
@@ -234,10 +282,13 @@ int softmax_checked(const void* x, void* y, int64_t N, int64_t D, void* ws, int6
         case Plan::kTwoPass: {
             const dim3 g(static_cast<unsigned>(splits), static_cast<unsigned>(N));
             if (vec) {
-                softmax_partial_kernel<8><<<g, dim3(256), 0, s>>>(xh, part, D, chunk);
+                if (split_tile(N, D) == 4096)
+                    softmax_partial_kernel<8, 2><<<g, dim3(256), 0, s>>>(xh, part, D, chunk);
+                else
+                    softmax_partial_kernel<8, 1><<<g, dim3(256), 0, s>>>(xh, part, D, chunk);
                 softmax_finish_kernel<8><<<g, dim3(256), 0, s>>>(xh, yh, part, D, chunk);
             } else {
-                softmax_partial_kernel<1><<<g, dim3(256), 0, s>>>(xh, part, D, chunk);
+                softmax_partial_kernel<1, 1><<<g, dim3(256), 0, s>>>(xh, part, D, chunk);
                 softmax_finish_kernel<1><<<g, dim3(256), 0, s>>>(xh, yh, part, D, chunk);
             }
             break;
