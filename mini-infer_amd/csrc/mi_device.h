@@ -17,6 +17,11 @@ typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 
 constexpr int kWave = 64;
 
+// s_waitcnt immediate (gfx9 family) that waits for every outstanding vector
+// memory operation: vmcnt = 0 (bits 3:0 and 15:14), expcnt = 7 (bits 6:4)
+// and lgkmcnt = 15 (bits 11:8) left unconstrained.
+constexpr int kDrainVmem = 0x0F70;  // __builtin_amdgcn_s_waitcnt(kDrainVmem)
+
 __device__ __forceinline__ h8 ld8(const half_t* p) {
     return *reinterpret_cast<const h8*>(p);
 }

@@ -342,10 +342,7 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(half_t* q, int Hq, ha
 //     every group, so its inv_freq is read once.
 // One barrier per group: the table half written in a step was last read in
 // the step before, ahead of this step's barrier.
-//
-// s_waitcnt immediate for gfx9-family: vmcnt = 0 (bits 3:0 and 15:14),
-// expcnt = 7 (bits 6:4) and lgkmcnt = 15 (bits 11:8) left unconstrained.
-constexpr int kDrainVmem = 0x0F70;
+
 template <int CPH, int P>
 __global__ __launch_bounds__(256) void qk_norm_rope_pipe_kernel(
     half_t* q, int Hq, half_t* k, int Hkv, const half_t* __restrict__ wq,

@@ -105,7 +105,7 @@ def test_greedy_argmax_workspace_graph(mk, orc, dev):
     rng = np.random.default_rng(9)
     x = normal_f16(rng, (64, 152064), 0, 4)
     xd = to_dev(x, dev)
-    ws = torch.empty(max(1, mk.greedy_argmax_workspace_bytes(64, 152064)), dtype=torch.uint8,
+    ws = torch.zeros(max(1, mk.greedy_argmax_workspace_bytes(64, 152064)), dtype=torch.uint8,
                      device=dev)
     out = torch.empty(64, dtype=torch.int32, device=dev)
     mk.greedy_argmax(xd, out=out, workspace=ws)
@@ -139,3 +139,19 @@ def test_greedy_argmax_max_at_every_vector_position(mk, orc, dev):
     got = to_host(mk.greedy_argmax(to_dev(x, dev)))
     want = np.array([int(np.argmax(r)) for r in rows], dtype=np.int32)
     assert (got == want).all() and (orc.greedy_argmax(x) == want).all()
+
+
+def test_greedy_argmax_workspace_reuse(mk, orc, dev):
+    """One workspace serves calls of different shapes in turn (each call
+    writes every chunk key it reads back)."""
+    _case("argmax workspace reuse across shapes")
+    import torch
+    ws = torch.full((max(1, mk.greedy_argmax_workspace_bytes(64, 152064)),), 0xAB,
+                    dtype=torch.uint8, device=dev)  # stale contents must not matter
+    rng = np.random.default_rng(12)
+    for B, V, levels in ((64, 152064, None), (3, 152064, 2), (64, 100000, None), (1, 32768, 1)):
+        assert mk.greedy_argmax_workspace_bytes(B, V) <= ws.numel()
+        x = (normal_f16(rng, (B, V), 0, 4) if levels is None
+             else rng.integers(-levels, levels + 1, (B, V)).astype(np.float16))
+        got = to_host(mk.greedy_argmax(to_dev(x, dev), workspace=ws))
+        assert (got == orc.greedy_argmax(x)).all(), f"[{B},{V}]"
