@@ -12,10 +12,14 @@
 //     it twice) and, fused, residual is read and written once;
 //   * 16-byte vector accesses (8 halves per lane per access), non-temporal
 //     for the streamed rows, cached for the weight every workgroup re-reads;
-//   * long rows (hidden 3584): a workgroup of ceil(D/8) lanes (448 for 3584)
-//     takes kRowsPerWg rows (1 by default: measured fastest at [8192, 3584];
-//     with more, every row's loads are issued before the first reduction),
-//     one wave64 DPP reduction per row and ONE barrier for all of them;
+//   * long rows (hidden 3584): a workgroup of up to 256 lanes, each holding
+//     VPT = ceil(D / 2048) vectors of the row (3584: 2 vectors, 224 busy
+//     lanes; rows past 8 vectors per lane widen to 1024 lanes), takes
+//     kRowsPerWg rows (1 by default; with more, every row's loads are issued
+//     before the first reduction), one wave64 DPP reduction per row and ONE
+//     barrier for all of them.  Measured at [8192, 3584]: 256 lanes x 2
+//     vectors reach 75% of HBM peak fused and 71% plain, against 72-74% and
+//     60-62% for 448 lanes x 1 vector and 74% / 70% for 192 x 3;
 //   * short rows (Q/K-norm, head_dim 128): a G-lane slice of a wave owns a
 //     row (G = 16 for 128), each slice takes kRowsPerGroup rows, and the
 //     reduction is DPP-only: no LDS, no barrier;
@@ -31,7 +35,7 @@
 #define MI_RMS_ROWS_PER_GROUP 1
 #endif
 #ifndef MI_RMS_MAX_THREADS
-#define MI_RMS_MAX_THREADS 512
+#define MI_RMS_MAX_THREADS 256
 #endif
 
 namespace mi {
@@ -228,11 +232,19 @@ int launch_small(const half_t* x, half_t* r, const half_t* w, half_t* y, int64_t
     return launch_status();
 }
 
+// Vectors per lane for a row of `chunks` 16-byte vectors: kMaxThreads lanes
+// while that needs at most 8 per lane, else 1024 lanes (rows <= 65536).
+int row_vpt(int64_t chunks) {
+    int64_t v = ceil_div(chunks, kMaxThreads);
+    if (v > 8) v = ceil_div(chunks, 1024);
+    return static_cast<int>(v);
+}
+
 template <int RPW, bool FUSED>
 int launch_row_rpw(const half_t* x, half_t* r, const half_t* w, half_t* y, int64_t N, int64_t D,
                    float eps, float bias, hipStream_t s) {
     const int64_t chunks = D >> 3;
-    const int vpt = static_cast<int>(ceil_div(chunks, kMaxThreads));
+    const int vpt = row_vpt(chunks);
     const int threads = static_cast<int>(ceil_div(ceil_div(chunks, vpt), kWave) * kWave);
     const int64_t grid = ceil_div(N, RPW);
     if (grid > kMaxGridX) return MI_ERR_UNSUPPORTED;
@@ -259,7 +271,7 @@ int launch_row(const half_t* x, half_t* r, const half_t* w, half_t* y, int64_t N
                float eps, float bias, hipStream_t s) {
     // Several rows per workgroup only pay off with enough rows to fill the
     // GPU; large-VPT rows already keep many bytes in flight per lane.
-    const int vpt = static_cast<int>(ceil_div(D >> 3, kMaxThreads));
+    const int vpt = row_vpt(D >> 3);
     if (kRowsPerWg > 1 && vpt <= 2 && N >= 2048)
         return launch_row_rpw<kRowsPerWg, FUSED>(x, r, w, y, N, D, eps, bias, s);
     return launch_row_rpw<1, FUSED>(x, r, w, y, N, D, eps, bias, s);
@@ -287,7 +299,7 @@ int rmsnorm_dispatch(const void* xv, void* rv, const void* wv, void* yv, int64_t
     const bool vec = (D % 8 == 0) && aligned16(x) && aligned16(w) && aligned16(y) &&
                      (!FUSED || aligned16(r));
     if (vec && D <= 512) return launch_small<FUSED>(x, r, w, y, N, static_cast<int>(D), eps, bias, s);
-    if (vec && D <= int64_t{8} * kMaxThreads * 8)
+    if (vec && D <= int64_t{8} * 1024 * 8)
         return launch_row<FUSED>(x, r, w, y, N, D, eps, bias, s);
     rms_scalar_kernel<FUSED><<<dim3(static_cast<unsigned>(N)), dim3(256), 0, s>>>(x, r, w, y, D, eps,
                                                                                   bias);

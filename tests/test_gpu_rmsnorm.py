@@ -46,7 +46,8 @@ def test_config1_16x3584(mk, orc, dev):
 
 @pytest.mark.parametrize("N,D", [(5, 8), (33, 16), (17, 64), (100, 128), (9, 136), (31, 320),
                                  (8, 512), (8, 520), (3, 1000), (7, 4096), (4, 8192),
-                                 (2, 40000), (2, 70000), (3, 3583), (6, 7)])
+                                 (2, 16384), (2, 16392), (2, 40000), (2, 70000), (3, 3583),
+                                 (6, 7)])
 @pytest.mark.parametrize("add_one", [False, True])
 def test_shapes(mk, orc, dev, N, D, add_one):
     _case(f"rmsnorm [{N},{D}] add_one={add_one}")
