@@ -307,6 +307,25 @@ void gpu_checks() {
             static_cast<const int*>(spd.data()), B, S, 1, NB, Hk, D, BS, MB, 0);
         EXPECT(bit_equal(cd, ref.data(), "launch_paged_kv_scatter"), "kv scatter");
 
+        // K and V in one launch (layer 0 this time); V gets its own source and cache
+        Tensor vsrc = reftest_f16({B, S, Hk, D}, 1.0f, 44);
+        Tensor vcache = reftest_f16({L, NB, Hk, BS, D}, 1.0f, 45);
+        std::vector<uint16_t> kref(bits(cache), bits(cache) + cache.numel());
+        std::vector<uint16_t> vref(bits(vcache), bits(vcache) + vcache.numel());
+        mio_paged_kv_scatter(bits(src), kref.data(), bt.data(), sl.data(), sp.data(), B, S, 0, NB,
+                             Hk, D, BS, MB);
+        mio_paged_kv_scatter(bits(vsrc), vref.data(), bt.data(), sl.data(), sp.data(), B, S, 0,
+                             NB, Hk, D, BS, MB);
+        Tensor kcd = cache.to(Device::cuda(0)), vcd = vcache.to(Device::cuda(0));
+        Tensor vsd = vsrc.to(Device::cuda(0));
+        mini_infer::kernels::launch_paged_kv_scatter_kv(
+            static_cast<const __half*>(sd.data()), static_cast<const __half*>(vsd.data()),
+            static_cast<__half*>(kcd.data()), static_cast<__half*>(vcd.data()),
+            static_cast<const int*>(btd.data()), static_cast<const int*>(sld.data()),
+            static_cast<const int*>(spd.data()), B, S, 0, NB, Hk, D, BS, MB, 0);
+        EXPECT(bit_equal(kcd, kref.data(), "launch_paged_kv_scatter_kv (K)"), "kv scatter K");
+        EXPECT(bit_equal(vcd, vref.data(), "launch_paged_kv_scatter_kv (V)"), "kv scatter V");
+
         const int R = 3, V = 152064;
         Tensor lg = reftest_f16({R, V}, 8.0f, 43);
         std::vector<int32_t> want(R);
