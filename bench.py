@@ -380,6 +380,99 @@ def cpu_baseline(budget_s=10.0):
     }
 
 
+def cpu_kernel_table(budget_s=1.0):
+    """The CPU oracle timed at every config of the kernel table (the
+    cpu_baseline leg, per config): the same workload shapes, seeded host
+    inputs, `budget_s` of repeated passes each (at least one), threads over
+    rows.  Reported beside the GPU rows, not as a target."""
+    import numpy as np
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import oracle  # the checker, timed here as the CPU reference implementation
+    cores = max(1, min(16, os.cpu_count() or 1))
+    rng = np.random.default_rng(2)
+
+    def h(shape, mean=0.0, std=1.0):
+        return (rng.standard_normal(shape, dtype=np.float32) * std + mean).astype(np.float16)
+
+    def timed(fn):
+        fn()
+        n, t0 = 0, time.perf_counter()
+        while True:
+            fn()
+            n += 1
+            el = time.perf_counter() - t0
+            if el >= budget_s:
+                return el / n
+
+    rows = []
+
+    def add(kernel, cfg, nbytes, tokens, fn, note=""):
+        sec = timed(fn)
+        rows.append({"kernel": kernel, "config": cfg, "cpu_us": round(sec * 1e6, 1),
+                     "cpu_GBps": round(nbytes / sec / 1e9, 3),
+                     "cpu_tokens_per_s": round(tokens / sec, 1), "cpu_note": note})
+
+    D, I, V = 3584, 18944, 152064
+    x, w = h((16, D)), h((D,), 1.0, 0.1)
+    add("rmsnorm", "[16,3584]", 2 * 16 * D * 2 + D * 2, 16,
+        lambda: oracle.rmsnorm(x, w, nthreads=cores))
+    for T, cfg in ((8192, "[8192,3584]"), (6064, "chain [6064,3584]")):
+        x, r = h((T, D)), h((T, D))
+        add("fused_add_rmsnorm", cfg, 4 * T * D * 2 + D * 2, T,
+            lambda: oracle.fused_add_rmsnorm(x, r, w, nthreads=cores))
+    inv = oracle.rope_inv_freq(128, 1e6)
+    for T, pos, cfg in ((4096, config3_positions(rng, 4096, 8, 28000), "Q[4096,28,128]+K[4096,4,128]"),
+                        (6064, chain_positions(rng), "chain Q[6064,28,128]+K[6064,4,128]")):
+        q, k = h((T, 28, 128)), h((T, 4, 128))
+
+        def rope_qk():
+            c, sn = oracle.rope_tables(inv, pos)
+            oracle.rope_neox(q, c, sn, nthreads=cores)
+            oracle.rope_neox(k, c, sn, nthreads=cores)
+        add("rope_neox_qk", cfg, 2 * T * 32 * 128 * 2 + T * 8, T, rope_qk,
+            "tables from positions, then Q and K rotated")
+        if T == 6064:
+            wq, wk = h((128,), 1.0, 0.1), h((128,), 1.0, 0.1)
+            add("qk_rmsnorm", "chain Q[6064*28,128]+K[6064*4,128]", 2 * T * 32 * 128 * 2 + 512, T,
+                lambda: (oracle.rmsnorm(q.reshape(-1, 128), wq, nthreads=cores),
+                         oracle.rmsnorm(k.reshape(-1, 128), wk, nthreads=cores)))
+
+            def qk_norm_rope():
+                c, sn = oracle.rope_tables(inv, pos)
+                for t, wt in ((q, wq), (k, wk)):
+                    n16 = oracle.f32_to_f16(oracle.rmsnorm(t.reshape(-1, 128), wt, nthreads=cores))
+                    oracle.rope_neox(n16.reshape(t.shape), c, sn, nthreads=cores)
+            add("qk_norm_rope", cfg, 2 * T * 32 * 128 * 2 + T * 8 + 512, T, qk_norm_rope,
+                "norm, fp16 rounding, then rotation (the reference's composition)")
+    for name, fn, T, I_, cfg in (("swiglu", oracle.swiglu, 4096, I, "[4096,18944]"),
+                                 ("geglu", oracle.geglu, 4096, 14336, "[4096,14336]"),
+                                 ("swiglu", oracle.swiglu, 6064, I, "chain [6064,18944]")):
+        g, u = h((T, I_)), h((T, I_))
+        add(name, cfg, 3 * T * I_ * 2, T, lambda: fn(g, u, nthreads=cores))
+        del g, u
+    T, VR = 6064, 32768
+    table = h((VR, D), 0.0, 0.02)
+    ids = rng.integers(0, VR, T).astype(np.int64)
+    add("embedding_gather", "T=6064 from [152064,3584]", T * 8 + 2 * T * D * 2, T,
+        lambda: oracle.embedding_gather(ids, table, nthreads=cores),
+        "from a 32768-row table (235 MB, past the host caches like the 1.09 GB one)")
+    del table
+    lg = h((64, V), 0.0, 4.0)
+    add("softmax", "[64,152064]", 2 * 64 * V * 2, 64, lambda: oracle.softmax(lg, nthreads=cores))
+    add("greedy_argmax", "[64,152064]", 64 * V * 2 + 64 * 4, 64, lambda: oracle.greedy_argmax(lg),
+        "single thread: the oracle replays the reference's 256-thread scan and tree")
+    H, hd, bs = 4, 128, 16
+    mb = -(-T // bs)
+    bt = rng.permutation(mb).astype(np.int32).reshape(1, mb)
+    ksrc, kc = h((1, T, H, hd)), h((1, mb, H, bs, hd))
+    sl, sp = np.array([T], np.int32), np.array([0], np.int32)
+    add("paged_kv_scatter_kv", "chain K+V [6064,4,128] bs=16", 2 * 2 * T * H * hd * 2 + (mb + 2) * 4,
+        T, lambda: (oracle.paged_kv_scatter(ksrc, kc, bt, sl, sp, 0, bs),
+                    oracle.paged_kv_scatter(ksrc, kc, bt, sl, sp, 0, bs)),
+        "single thread; K and V as two scatters")
+    return cores, rows
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawTextHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -388,6 +481,8 @@ def main():
     ap.add_argument("--no-kernels", action="store_true", help="skip the per-config table")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--cpu-seconds-per-config", type=float, default=1.0,
+                    help="CPU oracle time per kernel-table config")
     ap.add_argument("--eager", action="store_true",
                     help="launch eagerly instead of replaying a HIP graph (profiler counter runs)")
     args = ap.parse_args()
@@ -429,6 +524,18 @@ def main():
     if not args.no_cpu:
         log("[bench] CPU baseline (oracle on host cores)")
         cpu = cpu_baseline(args.cpu_seconds)
+        if kernels is not None:
+            cores, cpu_rows = cpu_kernel_table(args.cpu_seconds_per_config)
+            by_key = {(r["kernel"], r["config"]): r for r in cpu_rows}
+            for k in kernels:
+                c = by_key.get((k["kernel"], k["config"]))
+                if c is None:
+                    continue
+                k.update({kk: v for kk, v in c.items() if kk not in ("kernel", "config")})
+                k["cpu_cores"] = cores
+                k["gpu_over_cpu"] = round(c["cpu_us"] / k["us"], 1)
+                log(f"[bench]   cpu {k['kernel']:<18} {k['config']:<38} {c['cpu_us']:>11.1f} us "
+                    f"{c['cpu_GBps']:>8.2f} GB/s  ({cores} threads)")
 
     traffic = None
     tf = ROOT / "profiles" / "fused_add_rmsnorm_8192x3584_traffic.json"
