@@ -491,8 +491,8 @@ def main():
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: these layer kernels are row-independent and run "
-              "without communication; multi-GPU sharding is described in DESIGN.md, not "
-              "benchmarked.", file=sys.stderr)
+              "without communication, so a multi-GPU run would only repeat the one-GPU figure "
+              "per rank; --gpus N > 1 is not benchmarked.", file=sys.stderr)
         sys.exit(2)
 
     import torch

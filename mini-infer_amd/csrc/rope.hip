@@ -502,9 +502,11 @@ bool load_inv_freq(const float* host, int64_t half, InvFreq& out) {
 // Tokens per workgroup: the candidate whose grid leaves the least idle tail
 // in the GPU's last round of resident workgroups, with a small charge per
 // extra round (each round repeats the load-latency / table / barrier ramp).
-// Measured on MI355X: T = 4096 -> 4 tokens (1024 workgroups, one round);
-// T = 6064 -> 8 (758 workgroups, one round) instead of 4 (1516, a second
-// round 18% full: 58% -> 68% of HBM peak).
+// With residencies of 2048/1792/1280/1024 workgroups for 1/2/4/8 tokens this
+// picks 1 token at T = 4096 (two full rounds) and at T = 6064 (three rounds,
+// 99% full).  The charge matters when residency is lower: with 1280 at
+// 4 tokens, T = 6064 in 1516 workgroups leaves a second round 18% full, and
+// taking 8 tokens in one round instead measured 58% -> 68% of HBM peak.
 template <typename K1, typename K2, typename K4, typename K8>
 int pick_tokens_per_wg(int64_t T, K1 k1, K2 k2, K4 k4, K8 k8) {
     const void* ks[4] = {reinterpret_cast<const void*>(k1), reinterpret_cast<const void*>(k2),
