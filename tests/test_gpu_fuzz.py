@@ -1,0 +1,208 @@
+"""GPU parity over seeded random shapes: every kernel, many small cases.
+
+Each case draws its shape and options from a fixed-seed generator, so a
+failure names a reproducible case.  The draws reach the paths the fixed-shape
+tests pin one at a time:
+* vector (16-byte) and scalar paths: sizes not a multiple of 8, and buffers
+  misaligned by one fp16 element (a contiguous view at storage offset 1);
+* in-place and out-of-place calls;
+* split and whole rows for softmax / argmax;
+* invalid ids and KV blocks;
+* ties, NaN and -inf in argmax rows.
+The bar is the same as everywhere: bit-exact for copies, RoPE and argmax;
+rtol = atol = 1e-3 for the fp32-math outputs (norm-then-rope with its
+documented one-ulp intermediate allowance).
+"""
+import numpy as np
+import pytest
+
+from helpers import assert_bits_equal, assert_close, normal_f16, to_host
+
+pytestmark = pytest.mark.gpu
+CASES = 32
+
+
+def _case(msg):
+    print(f"[case] {msg}", flush=True)
+
+
+def _dev_array(a, dev, misalign=False):
+    """`a` on the device, optionally at a 2-byte-misaligned address."""
+    import torch
+    t = torch.from_numpy(np.ascontiguousarray(a))
+    if not misalign:
+        return t.to(dev)
+    flat = torch.empty(t.numel() + 1, dtype=t.dtype, device=dev)
+    view = flat[1:].view(t.shape)
+    view.copy_(t.to(dev))
+    return view
+
+
+@pytest.mark.parametrize("seed", range(CASES))
+def test_fuzz_rmsnorm(mk, orc, dev, seed):
+    rng = np.random.default_rng(1000 + seed)
+    N = int(rng.integers(1, 200))
+    D = int(rng.choice([int(rng.integers(1, 600)), 8 * int(rng.integers(1, 1200)),
+                        int(rng.integers(600, 9000))]))
+    add_one = bool(rng.integers(0, 2))
+    mis = bool(rng.integers(0, 4) == 0)
+    inplace = bool(rng.integers(0, 2))
+    _case(f"rmsnorm seed={seed} N={N} D={D} add_one={add_one} misaligned={mis} inplace={inplace}")
+    x, w = normal_f16(rng, (N, D)), normal_f16(rng, (D,), 1.0, 0.1)
+    xd = _dev_array(x, dev, mis)
+    y = mk.rmsnorm(xd, _dev_array(w, dev), y=xd if inplace else None, add_one=add_one)
+    assert_close(to_host(y), orc.rmsnorm(x, w, add_one=add_one), what="rmsnorm")
+
+
+@pytest.mark.parametrize("seed", range(CASES))
+def test_fuzz_fused_add_rmsnorm(mk, orc, dev, seed):
+    rng = np.random.default_rng(2000 + seed)
+    N = int(rng.integers(1, 200))
+    D = int(rng.choice([int(rng.integers(1, 600)), 8 * int(rng.integers(1, 1200))]))
+    add_one = bool(rng.integers(0, 2))
+    mis = bool(rng.integers(0, 4) == 0)
+    _case(f"fused_add_rmsnorm seed={seed} N={N} D={D} add_one={add_one} misaligned={mis}")
+    x, r = normal_f16(rng, (N, D)), normal_f16(rng, (N, D))
+    w = normal_f16(rng, (D,), 1.0, 0.1)
+    rd = _dev_array(r, dev, mis)
+    y = mk.fused_add_rmsnorm(_dev_array(x, dev, mis), rd, _dev_array(w, dev), add_one=add_one)
+    r_ref, y_ref = orc.fused_add_rmsnorm(x, r, w, add_one=add_one)
+    assert_bits_equal(to_host(rd), r_ref, what="residual")
+    assert_close(to_host(y), y_ref, what="y")
+
+
+@pytest.mark.parametrize("seed", range(CASES))
+def test_fuzz_rope_qk(mk, orc, dev, seed):
+    rng = np.random.default_rng(3000 + seed)
+    T = int(rng.integers(1, 300))
+    hd = int(rng.choice([2, 6, 16, 32, 64, 96, 128, 256, 512]))
+    Hq, Hkv = int(rng.integers(0, 40)), int(rng.integers(0, 9))
+    if Hq + Hkv == 0:
+        Hq = 1
+    theta = float(rng.choice([1e4, 1e6]))
+    _case(f"rope_neox_qk seed={seed} T={T} Hq={Hq} Hkv={Hkv} hd={hd} theta={theta}")
+    q, k = normal_f16(rng, (T, Hq, hd)), normal_f16(rng, (T, Hkv, hd))
+    pos = rng.integers(0, 1 << int(rng.integers(4, 22)), T).astype(np.int64)
+    inv = orc.rope_inv_freq(hd, theta)
+    qd, kd = _dev_array(q, dev), _dev_array(k, dev)
+    mk.rope_neox_qk(qd, kd if Hkv else None, _dev_array(pos, dev), inv)
+    c, s = orc.rope_tables(inv, pos)
+    if Hq:
+        assert_bits_equal(to_host(qd), orc.rope_neox(q, c, s).astype(np.float16), what="q")
+    if Hkv:
+        assert_bits_equal(to_host(kd), orc.rope_neox(k, c, s).astype(np.float16), what="k")
+
+
+@pytest.mark.parametrize("seed", range(CASES))
+def test_fuzz_qk_norm_rope(mk, orc, dev, seed):
+    from test_gpu_rope import _assert_norm_rope_close, _qk_norm_rope_ref
+    rng = np.random.default_rng(4000 + seed)
+    T = int(rng.integers(1, 400))
+    hd = int(rng.choice([16, 32, 64, 128, 256, 512]))
+    Hq, Hkv = int(rng.integers(0, 50)), int(rng.integers(0, 9))
+    if Hq + Hkv == 0:
+        Hkv = 1
+    _case(f"qk_norm_rope seed={seed} T={T} Hq={Hq} Hkv={Hkv} hd={hd}")
+    q, k = normal_f16(rng, (T, Hq, hd)), normal_f16(rng, (T, Hkv, hd))
+    wq, wk = normal_f16(rng, (hd,), 1.0, 0.1), normal_f16(rng, (hd,), 1.0, 0.1)
+    pos = rng.integers(0, 40000, T).astype(np.int64)
+    inv = orc.rope_inv_freq(hd, 1e6)
+    qd, kd = _dev_array(q, dev), _dev_array(k, dev)
+    mk.qk_norm_rope(qd, kd if Hkv else None, _dev_array(wq, dev), _dev_array(wk, dev),
+                    _dev_array(pos, dev), inv)
+    if Hq:
+        _assert_norm_rope_close(to_host(qd), *_qk_norm_rope_ref(orc, q, wq, pos, inv), what="q")
+    if Hkv:
+        _assert_norm_rope_close(to_host(kd), *_qk_norm_rope_ref(orc, k, wk, pos, inv), what="k")
+
+
+@pytest.mark.parametrize("seed", range(CASES))
+def test_fuzz_activations(mk, orc, dev, seed):
+    rng = np.random.default_rng(5000 + seed)
+    n = int(rng.choice([int(rng.integers(1, 100)), int(rng.integers(100, 200000)),
+                        8 * int(rng.integers(1, 100000))]))
+    mis = bool(rng.integers(0, 4) == 0)
+    _case(f"activations seed={seed} n={n} misaligned={mis}")
+    g, u = normal_f16(rng, (n,), 0.0, 3.0), normal_f16(rng, (n,))
+    gd, ud = _dev_array(g, dev, mis), _dev_array(u, dev, mis)
+    assert_close(to_host(mk.swiglu(gd, ud)), orc.swiglu(g, u), what="swiglu")
+    assert_close(to_host(mk.geglu(gd, ud)), orc.geglu(g, u), what="geglu")
+    assert_close(to_host(mk.gelu_tanh(gd)), orc.gelu_tanh(g), what="gelu_tanh")
+
+
+@pytest.mark.parametrize("seed", range(CASES))
+def test_fuzz_softmax(mk, orc, dev, seed):
+    rng = np.random.default_rng(6000 + seed)
+    split = bool(rng.integers(0, 2))
+    N = int(rng.integers(1, 64)) if split else int(rng.integers(1, 700))
+    D = (int(rng.integers(8192, 300000)) if split
+         else int(rng.choice([int(rng.integers(1, 64)), int(rng.integers(64, 8192))])))
+    mis = bool(rng.integers(0, 4) == 0)
+    _case(f"softmax seed={seed} N={N} D={D} misaligned={mis}")
+    x = normal_f16(rng, (N, D), 0.0, 4.0)
+    y = mk.softmax(_dev_array(x, dev, mis))
+    assert_close(to_host(y), orc.softmax(x), what="softmax")
+
+
+@pytest.mark.parametrize("seed", range(CASES))
+def test_fuzz_gather(mk, orc, dev, seed):
+    rng = np.random.default_rng(7000 + seed)
+    T = int(rng.integers(1, 500))
+    H = int(rng.choice([int(rng.integers(1, 300)), 8 * int(rng.integers(1, 600))]))
+    V = int(rng.integers(1, 3000))
+    mis = bool(rng.integers(0, 4) == 0)
+    _case(f"gather seed={seed} T={T} H={H} V={V} misaligned={mis}")
+    table = normal_f16(rng, (V, H), 0.0, 0.02)
+    ids = rng.integers(-3, V + 3, T).astype(np.int64)
+    out = mk.embedding_gather(_dev_array(ids, dev), _dev_array(table, dev, mis))
+    assert_bits_equal(to_host(out), orc.embedding_gather(ids, table), what="gather")
+
+
+@pytest.mark.parametrize("seed", range(CASES))
+def test_fuzz_argmax(mk, orc, dev, seed):
+    rng = np.random.default_rng(8000 + seed)
+    split = bool(rng.integers(0, 2))
+    B = int(rng.integers(1, 64)) if split else int(rng.integers(1, 700))
+    V = int(rng.integers(8192, 200000)) if split else int(rng.integers(1, 8192))
+    levels = int(rng.choice([0, 1, 3, 50]))
+    _case(f"argmax seed={seed} B={B} V={V} levels={levels}")
+    if levels:
+        x = rng.integers(-levels, levels + 1, (B, V)).astype(np.float16)
+    else:
+        x = normal_f16(rng, (B, V), 0.0, 4.0)
+    special = rng.random((B, V))
+    x[special < 0.001] = np.nan
+    x[(special >= 0.001) & (special < 0.002)] = -np.inf
+    got = to_host(mk.greedy_argmax(_dev_array(x, dev)))
+    ref = orc.greedy_argmax(x)
+    assert (got == ref).all(), f"{int((got != ref).sum())} rows differ"
+
+
+@pytest.mark.parametrize("seed", range(CASES))
+def test_fuzz_kv_scatter(mk, orc, dev, seed):
+    rng = np.random.default_rng(9000 + seed)
+    B = int(rng.integers(1, 9))
+    S = int(rng.integers(1, 70))
+    H = int(rng.integers(1, 9))
+    D = int(rng.choice([6, 8, 64, 128, 136]))
+    bs = int(rng.choice([1, 4, 16, 32]))
+    L = int(rng.integers(1, 4))
+    starts = rng.integers(0, 200, B)
+    seqs = starts + rng.integers(0, S + 20, B)
+    mb = max(1, -(-int(seqs.max() + 1) // bs))
+    NB = B * mb + 2
+    _case(f"kv scatter seed={seed} B={B} S={S} H={H} D={D} bs={bs} L={L}")
+    src = normal_f16(rng, (B, S, H, D))
+    cache = normal_f16(rng, (L, NB, H, bs, D))
+    # distinct physical blocks (two tokens on one cache slot would race, in the
+    # reference too), ~10% of entries invalid: -1 or past num_blocks
+    bt = rng.permutation(NB)[:B * mb].reshape(B, mb).astype(np.int32)
+    bad = rng.random((B, mb)) < 0.1
+    bt[bad] = rng.choice([-1, NB, NB + 7], int(bad.sum())).astype(np.int32)
+    sl, sp = seqs.astype(np.int32), starts.astype(np.int32)
+    layer = int(rng.integers(0, L))
+    cd = _dev_array(cache, dev)
+    mk.paged_kv_scatter(_dev_array(src, dev), cd, _dev_array(bt, dev), _dev_array(sl, dev),
+                        _dev_array(sp, dev), layer=layer, block_size=bs)
+    assert_bits_equal(to_host(cd), orc.paged_kv_scatter(src, cache, bt, sl, sp, layer, bs),
+                      what="cache")
