@@ -17,9 +17,10 @@
 //     per element;
 //     kernel 2, on the same grid, merges the row's pairs (each lane folds
 //     every 64th chunk, then wave reductions, no barrier) and writes its
-//     chunk.  Both grids
-//     map block (split, row) to the same XCD, so kernel 2's re-read of the
-//     chunk hits the L2 / Infinity Cache that kernel 1 filled.
+//     chunk.  Its re-read of the chunk misses L2, which does not carry
+//     data across kernel launches on this multi-XCD GPU (FETCH_SIZE counts
+//     the full 2 bytes/element again); it is served from the 256 MB
+//     Infinity Cache when the logits are still resident there, else HBM.
 #include "mi_device.h"
 #include "mi_host.h"
 
