@@ -139,16 +139,28 @@ int mi_scale_inplace_f16(void* y, float scale, int64_t n, void* stream);
 int mi_softmax_f16(const void* x, void* y, int64_t N, int64_t D, void* stream);
 
 /* Bytes of device workspace mi_softmax_ws_f16 needs for [N, D]: 0 when rows
- * are processed one workgroup each (N >= 512 or D < 8192), else one fp32
- * (max, sum) pair per row chunk, at most 64 chunks per row (<= 256 KiB). */
+ * are processed one workgroup each (N >= 512 or D < 8192), else 532,480 bytes
+ * of one-pass row records (fixed: 512 rows x 1040 B) plus one fp32 (max, sum)
+ * pair per row chunk for the two-pass form. */
 int64_t mi_softmax_workspace_bytes(int64_t N, int64_t D);
 
 /* mi_softmax_f16 with a caller-provided device workspace of at least
- * mi_softmax_workspace_bytes(N, D) bytes (may be NULL when that is 0), so the
- * call allocates nothing and can be captured into a HIP graph.  Calls that
- * share one workspace must not overlap in time. */
+ * mi_softmax_workspace_bytes(N, D) bytes (may be NULL when that is 0;
+ * 16-byte aligned), so the call allocates nothing and can be captured into a
+ * HIP graph.  The workspace must hold zeros before its first use and then be
+ * used only by this function (any shapes); each call leaves it valid for the
+ * next.  With y != x and aligned rows of <= 64 x 8192 elements, split rows
+ * run in ONE launch: chunks exchange (max, sum) through tagged per-row
+ * records, with no atomics on a shared address; in place, or otherwise, the
+ * two-launch form runs.  Calls that share one workspace must not overlap in
+ * time. */
 int mi_softmax_ws_f16(const void* x, void* y, int64_t N, int64_t D, void* workspace,
                       int64_t workspace_bytes, void* stream);
+
+/* Test hook (no counterpart in the reference): bound on the polls a one-pass
+ * softmax chunk makes before computing its row's statistics from x itself;
+ * 0 forces that fallback everywhere.  Returns the previous bound. */
+int mi_softmax_test_poll_limit(int limit);
 
 /* out[t, :] = table[ids[t], :] for t < T; table: [vocab, H], ids: int64 [T].
  * Bit-exact copy.  When vocab > 0, an id outside [0, vocab) yields a zero

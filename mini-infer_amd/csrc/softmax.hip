@@ -10,7 +10,10 @@
 //   * Many rows (N >= 512): one workgroup per row; the write pass re-reads the
 //     row, which the workgroup has just streamed through L2.
 //   * Few long rows (the LM-head case, 64 x 152064): one workgroup per row
-//     would light up 64 of 256 CUs, so each row is cut into `splits` chunks.
+//     would light up 64 of 256 CUs, so each row is cut into chunks.  With a
+//     caller workspace and y != x, one launch (softmax_onepass_kernel, below):
+//     chunks stay in registers and exchange their (max, sum) through tagged
+//     per-row records.  Otherwise two launches, with `splits` chunks:
 //     Kernel 1 writes a (max, sum) pair per chunk to a small stream-ordered
 //     workspace (8 bytes per chunk), from tiles whose loads are all issued
 //     first (one HBM wait per tile), a packed fp16 lane maximum and one exp
@@ -21,6 +24,8 @@
 //     data across kernel launches on this multi-XCD GPU (FETCH_SIZE counts
 //     the full 2 bytes/element again); it is served from the 256 MB
 //     Infinity Cache when the logits are still resident there, else HBM.
+#include <atomic>
+
 #include "mi_device.h"
 #include "mi_host.h"
 
@@ -219,6 +224,154 @@ __global__ __launch_bounds__(256) void softmax_finish_kernel(const half_t* x, ha
     write_range<VEC>(x + row * D, y + row * D, b, e, M, 1.0f / S);
 }
 
+// ---------------------------------------------------------------------------
+// One-pass split rows (mi_softmax_ws_f16 with x != y): each workgroup holds
+// its 8192-element chunk in registers, publishes the chunk's (max, sum), and
+// reads every chunk's pair of its row to finish -- one launch, one read of x,
+// no atomics on a contended address.
+//
+// Workspace (zero before first use; every call leaves it valid for the
+// next): row r owns a fixed record at r * kRowRecordBytes -- an epoch word,
+// then kOnePassMaxSplits slots of two 64-bit words {tag << 32 | bits(max)},
+// {tag << 32 | bits(sum)}.  A call reads the row's epoch E; every chunk
+// publishes its pair tagged E + 1 and polls the row's slots until all carry
+// E + 1.  Because slots are fixed per (row, chunk) whatever the call's shape,
+// and a row's epoch only grows, a slot left by an earlier call never carries
+// the tag a later call waits for:
+//   * the chunk-0 workgroup raises the epoch to E + 1 (atomic max, one per
+//     row) after it has seen every slot tagged E + 1 -- so every workgroup of
+//     the row has already read E;
+//   * a workgroup whose polling runs out (kPollLimit; not expected when the
+//     grid fits the GPU) computes the row's statistics itself from x and
+//     raises the epoch to E + 2, so no tag written in this call can pass for
+//     fresh later.  Polling is bounded: no workgroup can wait forever.
+// Each 64-bit word is stored and loaded whole at device scope (write-through
+// stores, L2-bypassing loads), so a tag always travels with its value.
+// ---------------------------------------------------------------------------
+constexpr int kOnePassMaxSplits = 64;
+constexpr int64_t kOnePassChunk = 8192;  // 4 vectors per lane
+constexpr int64_t kRowRecordBytes = 16 + kOnePassMaxSplits * 16;
+constexpr int kPollLimit = 1 << 16;
+std::atomic<int> g_poll_limit{kPollLimit};  // mi_softmax_test_poll_limit
+
+__device__ __forceinline__ uint64_t tagged(uint32_t tag, float v) {
+    return (static_cast<uint64_t>(tag) << 32) | __builtin_bit_cast(uint32_t, v);
+}
+
+__global__ __launch_bounds__(256) void softmax_onepass_kernel(const half_t* x, half_t* y,
+                                                              unsigned char* ws, int64_t D,
+                                                              int poll_limit) {
+    constexpr int U = 4;
+    __shared__ float slots[256 / kWave];
+    __shared__ float row_stats[3];  // M, S, fallback flag
+    __shared__ uint32_t epoch_sh;
+    const int split = blockIdx.x, splits = gridDim.x;
+    const int64_t row = blockIdx.y;
+    unsigned char* rec = ws + row * kRowRecordBytes;
+    uint32_t* epoch = reinterpret_cast<uint32_t*>(rec);
+    uint64_t* slot = reinterpret_cast<uint64_t*>(rec + 16);
+    const half_t* xr = x + row * D;
+    const int64_t b = split * kOnePassChunk;
+    const int64_t e = b + kOnePassChunk < D ? b + kOnePassChunk : D;
+
+    if (threadIdx.x == 0)
+        epoch_sh = __hip_atomic_load(epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // the chunk, all loads first (-inf past the end of the row)
+    h8 a[U];
+#pragma unroll
+    for (int j = 0; j < U; ++j) {
+        const int64_t i = b + (threadIdx.x + j * 256) * 8;
+        a[j] = i < e ? ld8(xr + i) : h8(-__builtin_huge_valf16());
+    }
+    h2 m2 = h2(-__builtin_huge_valf16());
+#pragma unroll
+    for (int j = 0; j < U; ++j) {
+#pragma unroll
+        for (int k = 0; k < 8; k += 2) m2 = __builtin_elementwise_max(m2, h2{a[j][k], a[j][k + 1]});
+    }
+    float m = (float)__builtin_elementwise_max(m2.x, m2.y), s = 0.0f;
+    if (m > -INFINITY) {
+#pragma unroll
+        for (int j = 0; j < U; ++j) {
+#pragma unroll
+            for (int k = 0; k < 8; ++k) s += fast_exp((float)a[j][k] - m);
+        }
+    } else {
+        m = -INFINITY;  // NaN-free lane maximum of an all -inf (or NaN) lane
+    }
+    block_merge(m, s, slots);  // barriers: epoch_sh is visible after this
+    const uint32_t E = epoch_sh;
+    if (threadIdx.x == 0) {
+        __hip_atomic_store(&slot[2 * split], tagged(E + 1, m), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(&slot[2 * split + 1], tagged(E + 1, s), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if (threadIdx.x < kWave) {
+        // wave 0 polls the row's slots: lane j reads chunk j
+        const int lane = threadIdx.x;
+        float mj = -INFINITY, sj = 0.0f;
+        bool all = false;
+        for (int it = 0; it < poll_limit && !all; ++it) {
+            bool mine = true;
+            if (lane < splits) {
+                const uint64_t w0 = __hip_atomic_load(&slot[2 * lane], __ATOMIC_RELAXED,
+                                                      __HIP_MEMORY_SCOPE_AGENT);
+                const uint64_t w1 = __hip_atomic_load(&slot[2 * lane + 1], __ATOMIC_RELAXED,
+                                                      __HIP_MEMORY_SCOPE_AGENT);
+                mine = static_cast<uint32_t>(w0 >> 32) == E + 1 &&
+                       static_cast<uint32_t>(w1 >> 32) == E + 1;
+                mj = __builtin_bit_cast(float, static_cast<uint32_t>(w0));
+                sj = __builtin_bit_cast(float, static_cast<uint32_t>(w1));
+            }
+            all = __all(mine);
+            if (!all) __builtin_amdgcn_s_sleep(2);
+        }
+        if (all) {
+            if (lane >= splits) {
+                mj = -INFINITY;
+                sj = 0.0f;
+            }
+            const float M = group_max<kWave>(mj);
+            const float S = group_sum<kWave>(mj == -INFINITY ? 0.0f : sj * fast_exp(mj - M));
+            if (lane == 0) {
+                row_stats[0] = M;
+                row_stats[1] = S;
+                row_stats[2] = 0.0f;
+            }
+        } else if (lane == 0) {
+            row_stats[2] = 1.0f;
+        }
+    }
+    __syncthreads();
+    float M = row_stats[0], S = row_stats[1];
+    const bool fallback = row_stats[2] != 0.0f;
+    if (fallback) {
+        // the row's statistics from x itself (x is not written: y != x)
+        float fm = -INFINITY, fs = 0.0f;
+        tile_stats<2>(xr, 0, D, fm, fs);
+        __syncthreads();  // slots reused
+        block_merge(fm, fs, slots);
+        M = fm;
+        S = fs;
+    }
+    if (threadIdx.x == 0 && (split == 0 || fallback))
+        __hip_atomic_fetch_max(epoch, fallback ? E + 2 : E + 1, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+    const float inv = 1.0f / S;
+    half_t* yr = y + row * D;
+#pragma unroll
+    for (int j = 0; j < U; ++j) {
+        const int64_t i = b + (threadIdx.x + j * 256) * 8;
+        if (i < e) {
+            h8 o;
+#pragma unroll
+            for (int k = 0; k < 8; ++k) o[k] = to_half(fast_exp((float)a[j][k] - M) * inv);
+            st8_stream(yr + i, o);
+        }
+    }
+}
+
 enum class Plan { kRow, kTwoPass };
 
 // Few long rows are split into chunks: aim at ~2048 workgroups (a 19.5 MB
@@ -244,29 +397,46 @@ Plan plan(int64_t N, int64_t D, int64_t& splits, int64_t& chunk) {
     return Plan::kTwoPass;
 }
 
-// Workspace of a split plan: one (max, sum) pair per chunk.
-int64_t workspace_bytes(int64_t N, int64_t D) {
+// Workspace of the two-pass split plan: one (max, sum) pair per chunk.
+int64_t twopass_bytes(int64_t N, int64_t D) {
     int64_t splits, chunk;
     if (plan(N, D, splits, chunk) == Plan::kRow) return 0;
     return N * splits * 2 * static_cast<int64_t>(sizeof(float));
 }
 
+// mi_softmax_ws_f16's workspace for split rows: the one-pass records of
+// every possible row (fixed, so any call shape finds its rows' records in the
+// same place), then the two-pass pairs (in-place or unaligned calls).
+constexpr int64_t kOnePassRegion = kSplitMaxRows * kRowRecordBytes;
+int64_t workspace_bytes(int64_t N, int64_t D) {
+    const int64_t two = twopass_bytes(N, D);
+    return two > 0 ? kOnePassRegion + two : 0;
+}
+
+#ifndef MI_SOFTMAX_ONEPASS
+#define MI_SOFTMAX_ONEPASS 1
+#endif
+
+// onepass_ws: a workspace laid out as workspace_bytes() describes (zero
+// before first use), else nullptr and `ws` holds only the two-pass pairs.
 int softmax_checked(const void* x, void* y, int64_t N, int64_t D, void* ws, int64_t ws_bytes,
-                    void* stream) {
+                    bool onepass_ws, void* stream) {
     if (N < 0 || D < 0 || ws_bytes < 0) return MI_ERR_INVALID_ARGUMENT;
     if (N == 0 || D == 0) return MI_OK;
     if (!x || !y) return MI_ERR_INVALID_ARGUMENT;
     if (N > kMaxGridX) return MI_ERR_UNSUPPORTED;
     const int64_t bytes = N * D * 2;
     if (x != y && overlaps(x, bytes, y, bytes)) return MI_ERR_ALIASING;
-    const int64_t need = workspace_bytes(N, D);
+    const int64_t need = onepass_ws ? workspace_bytes(N, D) : twopass_bytes(N, D);
     if (need > 0) {
         if (!ws || ws_bytes < need) return MI_ERR_INVALID_ARGUMENT;
         if (overlaps(ws, need, x, bytes) || overlaps(ws, need, y, bytes)) return MI_ERR_ALIASING;
+        if (onepass_ws && reinterpret_cast<uintptr_t>(ws) % 16 != 0) return MI_ERR_INVALID_ARGUMENT;
     }
     const auto* xh = static_cast<const half_t*>(x);
     auto* yh = static_cast<half_t*>(y);
-    auto* part = static_cast<float*>(ws);
+    auto* part = reinterpret_cast<float*>(static_cast<unsigned char*>(ws) +
+                                          (onepass_ws && need > 0 ? kOnePassRegion : 0));
     const hipStream_t s = as_stream(stream);
     const bool vec = D % 8 == 0 && aligned16(x) && aligned16(y);
     int64_t splits, chunk;
@@ -281,6 +451,19 @@ int softmax_checked(const void* x, void* y, int64_t N, int64_t D, void* ws, int6
             break;
         }
         case Plan::kTwoPass: {
+            const int64_t sp1 = ceil_div(D, kOnePassChunk);
+            // one launch when every chunk workgroup of the grid can be
+            // resident at once (no chunk polls for a row-mate still queued)
+            if (MI_SOFTMAX_ONEPASS && onepass_ws && vec && x != y && sp1 <= kOnePassMaxSplits &&
+                N <= 65535 &&
+                sp1 * N <= resident_workgroups(
+                               reinterpret_cast<const void*>(softmax_onepass_kernel), 256)) {
+                softmax_onepass_kernel<<<dim3(static_cast<unsigned>(sp1), static_cast<unsigned>(N)),
+                                         dim3(256), 0, s>>>(xh, yh,
+                                                            static_cast<unsigned char*>(ws), D,
+                                                            g_poll_limit.load());
+                break;
+            }
             const dim3 g(static_cast<unsigned>(splits), static_cast<unsigned>(N));
             if (vec) {
                 if (split_tile(N, D) == 4096)
@@ -308,12 +491,14 @@ extern "C" int64_t mi_softmax_workspace_bytes(int64_t N, int64_t D) {
 
 extern "C" int mi_softmax_ws_f16(const void* x, void* y, int64_t N, int64_t D, void* workspace,
                                  int64_t workspace_bytes, void* stream) {
-    return mi::softmax_checked(x, y, N, D, workspace, workspace_bytes, stream);
+    return mi::softmax_checked(x, y, N, D, workspace, workspace_bytes, true, stream);
 }
 
 extern "C" int mi_softmax_f16(const void* x, void* y, int64_t N, int64_t D, void* stream) {
-    const int64_t need = (N > 0 && D > 0) ? mi::workspace_bytes(N, D) : 0;
-    if (need == 0) return mi::softmax_checked(x, y, N, D, nullptr, 0, stream);
+    // a fresh pool allocation is not zeroed: the two-pass form, which needs
+    // no state between calls
+    const int64_t need = (N > 0 && D > 0) ? mi::twopass_bytes(N, D) : 0;
+    if (need == 0) return mi::softmax_checked(x, y, N, D, nullptr, 0, false, stream);
     // Few long rows: a stream-ordered workspace from the device's default
     // pool (concurrent calls on other streams get their own).
     if (!x || !y) return MI_ERR_INVALID_ARGUMENT;
@@ -321,8 +506,13 @@ extern "C" int mi_softmax_f16(const void* x, void* y, int64_t N, int64_t D, void
     void* ws = nullptr;
     hipError_t e = hipMallocAsync(&ws, static_cast<size_t>(need), s);
     if (e != hipSuccess) return static_cast<int>(e);
-    const int st = mi::softmax_checked(x, y, N, D, ws, need, stream);
+    const int st = mi::softmax_checked(x, y, N, D, ws, need, false, stream);
     e = hipFreeAsync(ws, s);
     if (st != MI_OK) return st;
     return e == hipSuccess ? MI_OK : static_cast<int>(e);
+}
+
+extern "C" int mi_softmax_test_poll_limit(int limit) {
+    if (limit < 0) return MI_ERR_INVALID_ARGUMENT;
+    return mi::g_poll_limit.exchange(limit);
 }

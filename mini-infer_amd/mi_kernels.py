@@ -50,6 +50,7 @@ SIGNATURES = {
     "mi_paged_kv_scatter_kv_f16": [_c_void_p] * 7 + [_i64] * 8 + [_c_void_p],
     "mi_greedy_argmax_f16": [_c_void_p, _i64, _i64, _c_void_p, _c_void_p],
     "mi_greedy_argmax_ws_f16": [_c_void_p, _i64, _i64, _c_void_p, _c_void_p, _i64, _c_void_p],
+    "mi_softmax_test_poll_limit": [_int],
     "mi_abi_version": [],
 }
 
@@ -349,7 +350,9 @@ def softmax_workspace_bytes(N: int, D: int) -> int:
 
 def softmax(x, y=None, workspace=None, stream=None):
     """Row softmax of x [N, D].  With `workspace` (a device tensor of at least
-    softmax_workspace_bytes(N, D) bytes) nothing is allocated per call."""
+    softmax_workspace_bytes(N, D) bytes, zero before its first use and kept
+    for softmax calls only) nothing is allocated per call, and out-of-place
+    split rows run in one launch."""
     _need(x, _f16(), "x")
     if x.dim() != 2:
         raise ValueError("x must be 2-D [N, D]")
@@ -369,6 +372,15 @@ def softmax(x, y=None, workspace=None, stream=None):
                                             _ptr(workspace), nbytes, _stream(stream)),
            "mi_softmax_ws_f16")
     return y
+
+
+def softmax_test_poll_limit(limit: int) -> int:
+    """Test hook: bound on one-pass softmax polling (0 forces the fallback that
+    computes each row's statistics from x); returns the previous bound."""
+    prev = int(load_library().mi_softmax_test_poll_limit(int(limit)))
+    if prev < 0:
+        raise ValueError("limit must be >= 0")
+    return prev
 
 
 # ---------------------------------------------------------------------------

@@ -97,14 +97,58 @@ def test_softmax_workspace_variant(mk, orc, dev):
     xd = to_dev(x, dev)
     nb = mk.softmax_workspace_bytes(64, 152064)
     assert nb > 0
-    ws = torch.empty(nb, dtype=torch.uint8, device=dev)
-    y1 = to_host(mk.softmax(xd, workspace=ws))
-    y2 = to_host(mk.softmax(xd))
-    assert_bits_equal(y1, y2, what="ws vs pool")
+    ws = torch.zeros(nb, dtype=torch.uint8, device=dev)
+    y1 = to_host(mk.softmax(xd, workspace=ws))  # one launch (out of place)
+    y2 = to_host(mk.softmax(xd))                # two launches (pool workspace)
+    ref = orc.softmax(x, nthreads=8)
+    assert_close(y1, ref, what="one-pass vs oracle")
+    assert_close(y2, ref, what="two-pass vs oracle")
     for _ in range(3):
         assert_bits_equal(to_host(mk.softmax(xd, workspace=ws)), y1, what="repeat")
     with pytest.raises(RuntimeError, match="status -1"):
         mk.softmax(xd, workspace=ws[: nb - 8])
+
+
+def test_softmax_onepass_workspace_across_shapes(mk, orc, dev):
+    """One zeroed workspace through calls of different shapes, an in-place
+    call (two-launch form) in between, and calls repeated: every result
+    matches the oracle, so no record left by an earlier call passes for
+    fresh."""
+    _case("softmax one-pass workspace across shapes")
+    import torch
+    rng = np.random.default_rng(56)
+    ws = torch.zeros(mk.softmax_workspace_bytes(511, 524288), dtype=torch.uint8, device=dev)
+    for N, D, inplace in ((64, 152064, False), (3, 100000, False), (64, 152064, False),
+                          (17, 8192, True), (64, 152064, False), (200, 524288, False),
+                          (5, 600000, False), (3, 100000, False)):
+        x = normal_f16(rng, (N, D), 0, 4)
+        xd = to_dev(x, dev)
+        y = mk.softmax(xd, y=xd if inplace else None, workspace=ws)
+        assert_close(to_host(y), orc.softmax(x, nthreads=8), what=f"[{N},{D}] inplace={inplace}")
+
+
+def test_softmax_onepass_forced_fallback(mk, orc, dev):
+    """The bounded-poll fallback, forced from the host (poll bound 0): every
+    chunk computes its row's statistics from x; the results still match, and
+    normal one-pass calls afterwards are still right (the fallback's epoch
+    step keeps its tags from passing for fresh)."""
+    _case("softmax one-pass forced fallback")
+    import torch
+    rng = np.random.default_rng(57)
+    ws = torch.zeros(mk.softmax_workspace_bytes(64, 152064), dtype=torch.uint8, device=dev)
+    x = normal_f16(rng, (64, 152064), 0, 4)
+    xd = to_dev(x, dev)
+    ref = orc.softmax(x, nthreads=8)
+    prev = mk.softmax_test_poll_limit(0)
+    try:
+        assert_close(to_host(mk.softmax(xd, workspace=ws)), ref, what="forced fallback")
+    finally:
+        mk.softmax_test_poll_limit(prev)
+    x2 = normal_f16(rng, (64, 152064), 0, 4)
+    ref2 = orc.softmax(x2, nthreads=8)
+    for i in range(3):
+        assert_close(to_host(mk.softmax(to_dev(x2, dev), workspace=ws)), ref2,
+                     what=f"after fallback, call {i}")
 
 
 def test_softmax_graph_replay(mk, orc, dev):
