@@ -313,7 +313,7 @@ def all_kernels(mk, dev, iters, warmup):
     out.append(report("softmax", "[64,152064]", nb, sec, N))
     # 5g. greedy argmax over the same logits (the step after the LM head)
     nb = N * V * 2 + N * 4
-    wsa = torch.empty(max(1, mk.greedy_argmax_workspace_bytes(N, V)), dtype=torch.uint8, device=dev)
+    wsa = torch.zeros(max(1, mk.greedy_argmax_workspace_bytes(N, V)), dtype=torch.uint8, device=dev)
     outi = torch.empty(N, dtype=torch.int32, device=dev)
     sec = time_launches(lambda i: mk.greedy_argmax(sets[i][0], out=outi, workspace=wsa), ns, iters,
                         warmup)

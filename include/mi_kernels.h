@@ -203,13 +203,25 @@ int mi_paged_kv_scatter_kv_f16(const void* k_src, const void* v_src, void* k_cac
  * workspace for the call, as mi_softmax_f16 does. */
 int mi_greedy_argmax_f16(const void* logits, int64_t B, int64_t V, int32_t* out, void* stream);
 
-/* Workspace bytes mi_greedy_argmax_ws_f16 needs (0 when rows are not split). */
+/* Workspace bytes mi_greedy_argmax_ws_f16 needs: 0 when rows are not split,
+ * else 532,480 bytes of one-launch row records (512 rows x 1040 B) plus one
+ * 64-bit key per row chunk for the two-launch form. */
 int64_t mi_greedy_argmax_workspace_bytes(int64_t B, int64_t V);
 
 /* mi_greedy_argmax_f16 with a caller-provided device workspace (allocates
- * nothing; graph-capturable).  Calls sharing a workspace must not overlap. */
+ * nothing; graph-capturable; 16-byte aligned).  The workspace must hold zeros
+ * before its first use and then be used only by this function (any shapes);
+ * each call leaves it valid for the next.  Split rows with V % 16 == 0 and
+ * V <= 64 x 8192 run in ONE launch: every chunk publishes its best key to a
+ * tagged per-row record and only chunk 0 of each row waits to combine them.
+ * Calls sharing a workspace must not overlap. */
 int mi_greedy_argmax_ws_f16(const void* logits, int64_t B, int64_t V, int32_t* out,
                             void* workspace, int64_t workspace_bytes, void* stream);
+
+/* Test hook (no counterpart in the reference): bound on the polls chunk 0 of
+ * a one-launch argmax row makes before scanning the row itself; 0 forces
+ * that fallback everywhere.  Returns the previous bound. */
+int mi_greedy_argmax_test_poll_limit(int limit);
 
 #ifdef __cplusplus
 }

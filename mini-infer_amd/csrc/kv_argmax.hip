@@ -25,6 +25,8 @@
 // -- larger is better, 0 = not eligible, so any reduction order gives the
 // reference's answer.  Few long rows are split into chunks: kernel 1 writes
 // each chunk's best key, kernel 2 reduces a row's keys in one wave.
+#include <atomic>
+
 #include "mi_device.h"
 #include "mi_host.h"
 
@@ -282,14 +284,109 @@ int64_t argmax_splits(int64_t B, int64_t V, int64_t& chunk) {
     return ceil_div(V, chunk);
 }
 
-int64_t argmax_ws_bytes(int64_t B, int64_t V) {
+// ---------------------------------------------------------------------------
+// One-launch split rows (mi_greedy_argmax_ws_f16): every chunk workgroup
+// publishes its best key to a fixed per-row record and exits; only chunk 0
+// of each row waits, polls the row's records, and writes the index.  The
+// record scheme is the one-pass softmax's (epoch word, slots tagged epoch + 1,
+// chunk 0 raises the epoch once it has seen every slot; a poll that runs out
+// makes chunk 0 scan the whole row itself and raise the epoch by 2).  A key
+// travels as two 64-bit words {tag << 32 | key >> 32}, {tag << 32 | key
+// & 0xffffffff}, each stored and loaded whole at device scope.  The workspace
+// must be zero before its first use.
+// ---------------------------------------------------------------------------
+constexpr int kArgmaxOnePassMaxSplits = 64;
+constexpr int64_t kArgmaxOnePassChunk = 8192;  // 4 vectors per lane
+constexpr int64_t kArgmaxRecordBytes = 16 + kArgmaxOnePassMaxSplits * 16;
+constexpr int64_t kArgmaxRecordRegion = kArgmaxSplitMaxRows * kArgmaxRecordBytes;
+constexpr int kArgmaxPollLimit = 1 << 16;
+std::atomic<int> g_argmax_poll_limit{kArgmaxPollLimit};  // mi_greedy_argmax_test_poll_limit
+
+__global__ __launch_bounds__(256) void argmax_onepass_kernel(const half_t* __restrict__ x,
+                                                             int64_t V, unsigned char* ws,
+                                                             int32_t* __restrict__ out,
+                                                             int poll_limit) {
+    __shared__ uint64_t slots[256 / kWave];
+    __shared__ uint32_t epoch_sh;
+    __shared__ int fallback_sh;
+    const int split = blockIdx.x, splits = gridDim.x;
+    const int64_t row = blockIdx.y;
+    unsigned char* rec = ws + row * kArgmaxRecordBytes;
+    uint32_t* epoch = reinterpret_cast<uint32_t*>(rec);
+    uint64_t* slot = reinterpret_cast<uint64_t*>(rec + 16);
+    const half_t* xr = x + row * V;
+    const int64_t b = split * kArgmaxOnePassChunk;
+    const int64_t e = b + kArgmaxOnePassChunk < V ? b + kArgmaxOnePassChunk : V;
+    if (threadIdx.x == 0)
+        epoch_sh = __hip_atomic_load(epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const uint64_t best = chunk_best<8, 4>(xr, b, e, slots);  // barrier inside
+    const uint32_t tag = epoch_sh + 1;
+    if (threadIdx.x == 0) {
+        __hip_atomic_store(&slot[2 * split], (static_cast<uint64_t>(tag) << 32) | (best >> 32),
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(&slot[2 * split + 1],
+                           (static_cast<uint64_t>(tag) << 32) | (best & 0xffffffffu),
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if (split != 0) return;  // whole workgroup
+    if (threadIdx.x < kWave) {
+        const int lane = threadIdx.x;
+        uint64_t k = 0;
+        bool all = false;
+        for (int it = 0; it < poll_limit && !all; ++it) {
+            bool mine = true;
+            k = 0;
+            if (lane < splits) {
+                const uint64_t w0 = __hip_atomic_load(&slot[2 * lane], __ATOMIC_RELAXED,
+                                                      __HIP_MEMORY_SCOPE_AGENT);
+                const uint64_t w1 = __hip_atomic_load(&slot[2 * lane + 1], __ATOMIC_RELAXED,
+                                                      __HIP_MEMORY_SCOPE_AGENT);
+                mine = static_cast<uint32_t>(w0 >> 32) == tag &&
+                       static_cast<uint32_t>(w1 >> 32) == tag;
+                k = (w0 << 32) | (w1 & 0xffffffffu);
+            }
+            all = __all(mine);
+            if (!all) __builtin_amdgcn_s_sleep(2);
+        }
+        if (all) {
+            k = wave_max_u64(k);
+            if (lane == 0) out[row] = key_index(k);
+        }
+        if (lane == 0) fallback_sh = all ? 0 : 1;
+    }
+    __syncthreads();
+    const bool fallback = fallback_sh != 0;
+    if (fallback) {
+        // the whole row from x (slots reused after the barrier above)
+        const uint64_t k = chunk_best<8, 4>(xr, 0, V, slots);
+        if (threadIdx.x == 0) out[row] = key_index(k);
+    }
+    if (threadIdx.x == 0)
+        __hip_atomic_fetch_max(epoch, fallback ? tag + 1 : tag, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Two-launch split rows: one key per chunk.
+int64_t argmax_keys_bytes(int64_t B, int64_t V) {
     int64_t chunk;
     const int64_t sp = argmax_splits(B, V, chunk);
     return sp > 1 ? B * sp * static_cast<int64_t>(sizeof(uint64_t)) : 0;
 }
 
+// mi_greedy_argmax_ws_f16's workspace for split rows: the one-launch records
+// of every possible row (fixed place whatever the call's shape), then the
+// two-launch keys.
+int64_t argmax_ws_bytes(int64_t B, int64_t V) {
+    const int64_t keys = argmax_keys_bytes(B, V);
+    return keys > 0 ? kArgmaxRecordRegion + keys : 0;
+}
+
+#ifndef MI_ARGMAX_ONEPASS
+#define MI_ARGMAX_ONEPASS 1
+#endif
+
 int argmax(const void* logits, int64_t B, int64_t V, int32_t* out, void* ws, int64_t ws_bytes,
-           void* stream) {
+           bool onepass_ws, void* stream) {
     if (B < 0 || V < 0 || ws_bytes < 0) return MI_ERR_INVALID_ARGUMENT;
     if (B == 0) return MI_OK;
     if (!logits || !out) return MI_ERR_INVALID_ARGUMENT;
@@ -298,14 +395,29 @@ int argmax(const void* logits, int64_t B, int64_t V, int32_t* out, void* ws, int
     int64_t chunk;
     const int64_t splits = V == 0 ? 1 : argmax_splits(B, V, chunk);
     if (V == 0) chunk = 0;
-    const int64_t need = splits > 1 ? B * splits * 8 : 0;
-    if (need > 0 && (!ws || ws_bytes < need)) return MI_ERR_INVALID_ARGUMENT;
+    const int64_t keys = splits > 1 ? B * splits * 8 : 0;
+    const int64_t need = keys > 0 && onepass_ws ? kArgmaxRecordRegion + keys : keys;
+    if (need > 0) {
+        if (!ws || ws_bytes < need) return MI_ERR_INVALID_ARGUMENT;
+        if (reinterpret_cast<uintptr_t>(ws) % 16 != 0) return MI_ERR_INVALID_ARGUMENT;
+        if (overlaps(ws, need, logits, B * V * 2) || overlaps(ws, need, out, B * 4))
+            return MI_ERR_ALIASING;
+    }
     const hipStream_t st = as_stream(stream);
     const auto* x = static_cast<const half_t*>(logits);
-    auto* w = static_cast<uint64_t*>(ws);
+    const bool vec = V % 16 == 0 && aligned16(logits);
+    const int64_t sp1 = ceil_div(V, kArgmaxOnePassChunk);
+    if (MI_ARGMAX_ONEPASS && onepass_ws && splits > 1 && vec && sp1 <= kArgmaxOnePassMaxSplits) {
+        argmax_onepass_kernel<<<dim3(static_cast<unsigned>(sp1), static_cast<unsigned>(B)),
+                                dim3(256), 0, st>>>(x, V, static_cast<unsigned char*>(ws), out,
+                                                    g_argmax_poll_limit.load());
+        return launch_status();
+    }
+    auto* w = reinterpret_cast<uint64_t*>(static_cast<unsigned char*>(ws) +
+                                          (onepass_ws && keys > 0 ? kArgmaxRecordRegion : 0));
     const dim3 g(static_cast<unsigned>(splits), static_cast<unsigned>(B));
     const bool two = splits == 1 || argmax_tile(B, V) == 4096;
-    if (V % 16 == 0 && aligned16(logits)) {
+    if (vec) {
         if (two)
             argmax_partial_kernel<8, 2><<<g, dim3(256), 0, st>>>(x, V, chunk, w, out);
         else
@@ -349,19 +461,25 @@ extern "C" int64_t mi_greedy_argmax_workspace_bytes(int64_t B, int64_t V) {
 
 extern "C" int mi_greedy_argmax_ws_f16(const void* logits, int64_t B, int64_t V, int32_t* out,
                                        void* workspace, int64_t workspace_bytes, void* stream) {
-    return mi::argmax(logits, B, V, out, workspace, workspace_bytes, stream);
+    return mi::argmax(logits, B, V, out, workspace, workspace_bytes, true, stream);
+}
+
+extern "C" int mi_greedy_argmax_test_poll_limit(int limit) {
+    if (limit < 0) return MI_ERR_INVALID_ARGUMENT;
+    return mi::g_argmax_poll_limit.exchange(limit);
 }
 
 extern "C" int mi_greedy_argmax_f16(const void* logits, int64_t B, int64_t V, int32_t* out,
                                     void* stream) {
-    const int64_t need = (B > 0 && V > 0) ? mi::argmax_ws_bytes(B, V) : 0;
-    if (need == 0) return mi::argmax(logits, B, V, out, nullptr, 0, stream);
+    // a fresh pool allocation is not zeroed: the two-launch form
+    const int64_t need = (B > 0 && V > 0) ? mi::argmax_keys_bytes(B, V) : 0;
+    if (need == 0) return mi::argmax(logits, B, V, out, nullptr, 0, false, stream);
     if (!logits || !out) return MI_ERR_INVALID_ARGUMENT;
     const hipStream_t s = mi::as_stream(stream);
     void* ws = nullptr;
     hipError_t e = hipMallocAsync(&ws, static_cast<size_t>(need), s);
     if (e != hipSuccess) return static_cast<int>(e);
-    const int st = mi::argmax(logits, B, V, out, ws, need, stream);
+    const int st = mi::argmax(logits, B, V, out, ws, need, false, stream);
     e = hipFreeAsync(ws, s);
     if (st != MI_OK) return st;
     return e == hipSuccess ? MI_OK : static_cast<int>(e);

@@ -51,6 +51,7 @@ SIGNATURES = {
     "mi_greedy_argmax_f16": [_c_void_p, _i64, _i64, _c_void_p, _c_void_p],
     "mi_greedy_argmax_ws_f16": [_c_void_p, _i64, _i64, _c_void_p, _c_void_p, _i64, _c_void_p],
     "mi_softmax_test_poll_limit": [_int],
+    "mi_greedy_argmax_test_poll_limit": [_int],
     "mi_abi_version": [],
 }
 
@@ -452,8 +453,20 @@ def greedy_argmax_workspace_bytes(B: int, V: int) -> int:
     return int(load_library().mi_greedy_argmax_workspace_bytes(B, V))
 
 
+def greedy_argmax_test_poll_limit(limit: int) -> int:
+    """Test hook: bound on one-launch argmax polling (0 forces chunk 0 to scan
+    its whole row); returns the previous bound."""
+    prev = int(load_library().mi_greedy_argmax_test_poll_limit(int(limit)))
+    if prev < 0:
+        raise ValueError("limit must be >= 0")
+    return prev
+
+
 def greedy_argmax(logits, out=None, workspace=None, stream=None):
-    """int32 [B] argmax of logits [B, V] (or [V]) with the reference's tie rule."""
+    """int32 [B] argmax of logits [B, V] (or [V]) with the reference's tie rule.
+    `workspace` (greedy_argmax_workspace_bytes bytes) must be zero before its
+    first use and kept for argmax calls only; split rows then run in one
+    launch."""
     torch = _torch()
     _need(logits, _f16(), "logits")
     x = logits if logits.dim() == 2 else logits.view(1, -1)

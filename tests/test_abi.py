@@ -121,8 +121,10 @@ def test_softmax_workspace_sizes(lib):
 def test_argmax_workspace_sizes(lib):
     lib.mi_greedy_argmax_workspace_bytes.argtypes = [ctypes.c_int64, ctypes.c_int64]
     lib.mi_greedy_argmax_workspace_bytes.restype = ctypes.c_int64
-    assert lib.mi_greedy_argmax_workspace_bytes(64, 152064) == 64 * 38 * 8  # one key per chunk
-    assert lib.mi_greedy_argmax_workspace_bytes(1, 152064) == 75 * 8        # 2048-element chunks
+    # split rows: the one-launch records (512 rows x 1040 B), then one key per
+    # chunk for the two-launch form (4096- or 2048-element chunks)
+    assert lib.mi_greedy_argmax_workspace_bytes(64, 152064) == 512 * 1040 + 64 * 38 * 8
+    assert lib.mi_greedy_argmax_workspace_bytes(1, 152064) == 512 * 1040 + 75 * 8
     assert lib.mi_greedy_argmax_workspace_bytes(512, 152064) == 0           # one workgroup per row
     assert lib.mi_greedy_argmax_workspace_bytes(64, 4096) == 0
-    assert 0 < lib.mi_greedy_argmax_workspace_bytes(511, 10**6) <= 256 * 1024
+    assert 0 < lib.mi_greedy_argmax_workspace_bytes(511, 10**6) <= 512 * 1040 + 256 * 1024

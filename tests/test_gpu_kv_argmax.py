@@ -142,16 +142,40 @@ def test_greedy_argmax_max_at_every_vector_position(mk, orc, dev):
 
 
 def test_greedy_argmax_workspace_reuse(mk, orc, dev):
-    """One workspace serves calls of different shapes in turn (each call
-    writes every chunk key it reads back)."""
+    """One zeroed workspace serves calls of different shapes in turn, one-
+    launch (V % 16 == 0) and two-launch (V % 16 != 0) alike: no record left by
+    an earlier call passes for fresh."""
     _case("argmax workspace reuse across shapes")
     import torch
-    ws = torch.full((max(1, mk.greedy_argmax_workspace_bytes(64, 152064)),), 0xAB,
-                    dtype=torch.uint8, device=dev)  # stale contents must not matter
+    ws = torch.zeros(max(1, mk.greedy_argmax_workspace_bytes(511, 600000)), dtype=torch.uint8,
+                     device=dev)
     rng = np.random.default_rng(12)
-    for B, V, levels in ((64, 152064, None), (3, 152064, 2), (64, 100000, None), (1, 32768, 1)):
+    for B, V, levels in ((64, 152064, None), (3, 152064, 2), (64, 100000, None), (1, 32768, 1),
+                         (64, 152064, 3), (5, 100003, None), (300, 600000, None),
+                         (3, 152064, 2)):
         assert mk.greedy_argmax_workspace_bytes(B, V) <= ws.numel()
         x = (normal_f16(rng, (B, V), 0, 4) if levels is None
              else rng.integers(-levels, levels + 1, (B, V)).astype(np.float16))
         got = to_host(mk.greedy_argmax(to_dev(x, dev), workspace=ws))
         assert (got == orc.greedy_argmax(x)).all(), f"[{B},{V}]"
+
+
+def test_greedy_argmax_onepass_forced_fallback(mk, orc, dev):
+    """Chunk 0's bounded poll, forced to run out from the host (bound 0): it
+    scans its whole row itself; results match, and later one-launch calls on
+    the same workspace are still right."""
+    _case("argmax one-launch forced fallback")
+    import torch
+    rng = np.random.default_rng(13)
+    ws = torch.zeros(mk.greedy_argmax_workspace_bytes(64, 152064), dtype=torch.uint8, device=dev)
+    x = rng.integers(-3, 4, (64, 152064)).astype(np.float16)
+    prev = mk.greedy_argmax_test_poll_limit(0)
+    try:
+        got = to_host(mk.greedy_argmax(to_dev(x, dev), workspace=ws))
+    finally:
+        mk.greedy_argmax_test_poll_limit(prev)
+    assert (got == orc.greedy_argmax(x)).all()
+    for i in range(3):
+        x2 = normal_f16(rng, (64, 152064), 0, 4)
+        got = to_host(mk.greedy_argmax(to_dev(x2, dev), workspace=ws))
+        assert (got == orc.greedy_argmax(x2)).all(), f"call {i} after the fallback"
