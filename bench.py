@@ -473,6 +473,106 @@ def cpu_kernel_table(budget_s=1.0):
     return cores, rows
 
 
+def decoder_chain(mk, dev, iters, warmup):
+    """BASELINE config 5 as one step: the non-GEMM launches of a decoder layer
+    at T = 6064 (64 decode tokens + two 3000-token prefills), then the LM-head
+    side, all captured back to back:
+      gather -> residual-add + RMSNorm -> Q/K-norm + RoPE -> paged K+V scatter
+      -> SwiGLU [6064,18944] -> softmax [64,152064] -> greedy argmax.
+    Timed twice: with this library's fused entry points, and as the
+    reference's caller composes the same steps from its unfused launchers
+    (src/model/transformer_model.cpp:414-424, :448; src/layers/attention.cpp:
+    754-780): add in place, a device copy, RMSNorm; Q-norm and K-norm; cos/sin
+    tables, then RoPE of Q and of K from the tables; one scatter for K and one
+    for V.  Both run this library's kernels, so the difference is the fusion
+    alone.  Bytes are the fused step's algorithmic bytes."""
+    import numpy as np
+    import torch
+    gen = torch.Generator(device=dev).manual_seed(5)
+    rng = np.random.default_rng(5)
+    f16 = torch.float16
+    T, D, I, V, N = 6064, 3584, 18944, 152064, 64
+    Hq, Hkv, hd, bs = 28, 4, 128, 16
+    table = randn16((V, D), gen, dev, 0.0, 0.02)
+    w1 = randn16((D,), gen, dev, 1.0, 0.1)
+    wq, wk = randn16((hd,), gen, dev, 1.0, 0.1), randn16((hd,), gen, dev, 1.0, 0.1)
+    inv = mk.rope_inv_freq(hd)
+    pos = torch.from_numpy(chain_positions(rng)).to(dev)
+    mb = -(-T // bs)
+    bt = torch.from_numpy(rng.permutation(mb).astype(np.int32)).to(dev).view(1, mb)
+    sl = torch.tensor([T], dtype=torch.int32, device=dev)
+    sp = torch.tensor([0], dtype=torch.int32, device=dev)
+    cos_t = torch.empty((T, hd // 2), dtype=f16, device=dev)
+    sin_t = torch.empty_like(cos_t)
+    wss = torch.zeros(max(1, mk.softmax_workspace_bytes(N, V)), dtype=torch.uint8, device=dev)
+    wsa = torch.zeros(max(1, mk.greedy_argmax_workspace_bytes(N, V)), dtype=torch.uint8,
+                      device=dev)
+    am = torch.empty(N, dtype=torch.int32, device=dev)
+
+    def make_set():
+        return {
+            "ids": torch.from_numpy(rng.integers(0, V, T).astype(np.int64)).to(dev),
+            "hidden": torch.empty((T, D), dtype=f16, device=dev),
+            "attn": randn16((T, D), gen, dev),
+            "hid2d": torch.empty((T, D), dtype=f16, device=dev),
+            "normed": torch.empty((T, D), dtype=f16, device=dev),
+            "q": randn16((T, Hq, hd), gen, dev), "k": randn16((T, Hkv, hd), gen, dev),
+            "v": randn16((T, Hkv, hd), gen, dev),
+            "kc": torch.empty((1, mb, Hkv, bs, hd), dtype=f16, device=dev),
+            "vc": torch.empty((1, mb, Hkv, bs, hd), dtype=f16, device=dev),
+            "g": randn16((T, I), gen, dev), "u": randn16((T, I), gen, dev),
+            "act": torch.empty((T, I), dtype=f16, device=dev),
+            "logits": randn16((N, V), gen, dev, 0.0, 4.0),
+            "probs": torch.empty((N, V), dtype=f16, device=dev),
+        }
+    sets = [make_set() for _ in range(2)]  # ~1.1 GB of streamed data per step
+
+    def tail(b):
+        mk.swiglu(b["g"], b["u"], out=b["act"])
+        mk.softmax(b["logits"], y=b["probs"], workspace=wss)
+        mk.greedy_argmax(b["logits"], out=am, workspace=wsa)
+
+    def fused(i):
+        b = sets[i]
+        mk.embedding_gather(b["ids"], table, out=b["hidden"])
+        mk.fused_add_rmsnorm(b["attn"], b["hidden"], w1, y=b["normed"])
+        mk.qk_norm_rope(b["q"], b["k"], wq, wk, pos, inv)
+        mk.paged_kv_scatter(b["k"].view(1, T, Hkv, hd), b["kc"], bt, sl, sp, 0, bs,
+                            v_src=b["v"].view(1, T, Hkv, hd), v_cache=b["vc"])
+        tail(b)
+
+    def unfused(i):
+        b = sets[i]
+        mk.embedding_gather(b["ids"], table, out=b["hidden"])
+        mk.add_inplace(b["hidden"], b["attn"])
+        b["hid2d"].copy_(b["hidden"])
+        mk.rmsnorm(b["hid2d"], w1, y=b["normed"])
+        q2, k2 = b["q"].view(T * Hq, hd), b["k"].view(T * Hkv, hd)
+        mk.rmsnorm(q2, wq, y=q2)
+        mk.rmsnorm(k2, wk, y=k2)
+        mk.rope_tables(inv, pos, cos_t=cos_t, sin_t=sin_t)
+        q4, k4 = b["q"].view(1, T, Hq, hd), b["k"].view(1, T, Hkv, hd)
+        mk.rope_neox(q4, cos_t, sin_t, y=q4)
+        mk.rope_neox(k4, cos_t, sin_t, y=k4)
+        mk.paged_kv_scatter(k4, b["kc"], bt, sl, sp, 0, bs)
+        mk.paged_kv_scatter(b["v"].view(1, T, Hkv, hd), b["vc"], bt, sl, sp, 0, bs)
+        tail(b)
+
+    nb = ((T * 8 + 2 * T * D * 2) + (4 * T * D * 2 + D * 2)
+          + (2 * T * (Hq + Hkv) * hd * 2 + T * 8 + 2 * hd * 2)
+          + (2 * 2 * T * Hkv * hd * 2 + (mb + 2) * 4) + 3 * T * I * 2
+          + 2 * N * V * 2 + (N * V * 2 + N * 4))
+    cfg = "gather+add&norm+qk-norm&rope+kv+swiglu+softmax+argmax T=6064"
+    rows = []
+    for name, fn in (("decoder_chain_fused", fused), ("decoder_chain_unfused", unfused)):
+        sec = time_launches(fn, len(sets), iters, warmup)
+        rows.append(report(name, cfg, nb, sec, T))
+    rows[0]["speedup_over_unfused"] = round(rows[1]["us"] / rows[0]["us"], 3)
+    del sets, table
+    torch.cuda.synchronize()
+    return rows
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawTextHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -514,6 +614,7 @@ def main():
     if not args.no_kernels:
         log("[bench] per-config kernel table")
         kernels = all_kernels(mk, dev, max(20, args.steps // 2), max(5, args.warmup // 2))
+        kernels += decoder_chain(mk, dev, max(10, args.steps // 8), max(3, args.warmup // 4))
         for k in kernels:
             floor = (f"  copy floor {k['copy_floor_us']:7.2f} us ({100 * k['frac_of_copy_floor']:5.1f}%)"
                      if "copy_floor_us" in k else "")
