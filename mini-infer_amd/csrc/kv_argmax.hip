@@ -30,6 +30,9 @@
 #include "mi_device.h"
 #include "mi_host.h"
 
+#ifndef MI_WT_KV
+#define MI_WT_KV 1
+#endif
 namespace mi {
 namespace {
 
@@ -82,8 +85,8 @@ __global__ __launch_bounds__(256) void kv_scatter_kernel(const half_t* __restric
             const h8 a = ld8_stream(s0 + v * 8);
             h8 c;
             if (s1) c = ld8_stream(s1 + v * 8);
-            st8_stream(cache0 + dst, a);
-            if (s1) st8_stream(cache1 + dst, c);
+            st8_out<MI_WT_KV>(cache0 + dst, a);
+            if (s1) st8_out<MI_WT_KV>(cache1 + dst, c);
         } else {
             cache0[dst] = s0[v];
             if (s1) cache1[dst] = s1[v];

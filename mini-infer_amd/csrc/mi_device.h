@@ -52,6 +52,24 @@ __device__ __forceinline__ void st8_stream(half_t* p, h8 v) {
     st8(p, v);
 #endif
 }
+// Streaming store at device scope ("nt sc1"): written through the XCD's L2
+// instead of left there dirty.  Faster where a kernel's writes are scattered
+// or its launch is short (paged KV scatter, in-place Q/K passes); slower for
+// the long dense streams, which keep st8_stream.
+// A VALU write to the data registers of a store wider than 8 bytes needs a
+// wait state after the store on gfx9.  The compiler's hazard pass does not
+// see a store inside inline asm, so the asm carries the wait states itself
+// (without them, following VALU code overwrote the data before the store
+// read it).
+__device__ __forceinline__ void st8_stream_wt(half_t* p, h8 v) {
+    asm volatile("global_store_dwordx4 %0, %1, off nt sc1\n\ts_nop 1" : : "v"(p), "v"(v)
+                 : "memory");
+}
+// Store selected per kernel at compile time.
+template <bool WT>
+__device__ __forceinline__ void st8_out(half_t* p, h8 v) {
+    if constexpr (WT) st8_stream_wt(p, v); else st8_stream(p, v);
+}
 
 // Round-to-nearest-even fp32 -> fp16 (v_cvt_f16_f32 under the default mode).
 __device__ __forceinline__ half_t to_half(float f) { return (half_t)f; }

@@ -38,6 +38,9 @@
 #define MI_RMS_MAX_THREADS 256
 #endif
 
+#ifndef MI_WT_RMSS
+#define MI_WT_RMSS 1
+#endif
 namespace mi {
 namespace {
 
@@ -153,7 +156,7 @@ __global__ __launch_bounds__(256) void rms_small_kernel(const half_t* x, half_t*
         if constexpr (FUSED) {
 #pragma unroll
             for (int k = 0; k < 8; ++k) a[q][k] = to_half((float)r[q][k] + (float)a[q][k]);
-            if (ok) st8_stream(residual + row * D + lane * 8, a[q]);
+            if (ok) st8_out<MI_WT_RMSS>(residual + row * D + lane * 8, a[q]);
         }
         float ss = 0.0f;
 #pragma unroll
@@ -168,7 +171,7 @@ __global__ __launch_bounds__(256) void rms_small_kernel(const half_t* x, half_t*
             h8 o;
 #pragma unroll
             for (int k = 0; k < 8; ++k) o[k] = to_half((float)a[q][k] * rrms * ((float)wv[k] + w_bias));
-            st8_stream(y + row * D + lane * 8, o);
+            st8_out<MI_WT_RMSS>(y + row * D + lane * 8, o);
         }
     }
 }

@@ -31,6 +31,12 @@
 #include "mi_host.h"
 #include "rope_sincos.h"
 
+#ifndef MI_WT_ROPE
+#define MI_WT_ROPE 1
+#endif
+#ifndef MI_WT_QKNR
+#define MI_WT_QKNR 1
+#endif
 namespace mi {
 namespace {
 
@@ -184,8 +190,8 @@ __global__ __launch_bounds__(256) void rope_kernel(const half_t* q_in, half_t* q
             set_elem<VEC>(y2, k, fp32_rounded(b * cv + a * sv));
         }
         if constexpr (VEC == 8) {
-            st8_stream(dst, y1);
-            st8_stream(dst + half, y2);
+            st8_out<MI_WT_ROPE>(dst, y1);
+            st8_out<MI_WT_ROPE>(dst + half, y2);
         } else {
             V::store(dst, y1);
             V::store(dst + half, y2);
@@ -302,8 +308,8 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(half_t* q, int Hq, ha
             y1[e] = to_half(fp32_rounded(n1 * cv - n2 * sv));
             y2[e] = to_half(fp32_rounded(n2 * cv + n1 * sv));
         }
-        st8_stream(hp + c * 8, y1);
-        st8_stream(hp + HALF + c * 8, y2);
+        st8_out<MI_WT_QKNR>(hp + c * 8, y1);
+        st8_out<MI_WT_QKNR>(hp + HALF + c * 8, y2);
     };
 #pragma unroll
     for (int p = 0; p < TPW; ++p) process(threadIdx.x + p * 256, x1[p], x2[p]);
@@ -440,8 +446,8 @@ __global__ __launch_bounds__(256) void qk_norm_rope_pipe_kernel(
                 y2[e] = to_half(fp32_rounded(v2 * cv + v1 * sv));
             }
             half_t* hp = slot_ptr(p, tok0);
-            st8_stream(hp, y1);
-            st8_stream(hp + HALF, y2);
+            st8_out<MI_WT_QKNR>(hp, y1);
+            st8_out<MI_WT_QKNR>(hp + HALF, y2);
         }
     };
 

@@ -29,6 +29,9 @@
 #include "mi_device.h"
 #include "mi_host.h"
 
+#ifndef MI_WT_SM
+#define MI_WT_SM 0
+#endif
 namespace mi {
 namespace {
 
@@ -144,7 +147,7 @@ __device__ __forceinline__ void write_range(const half_t* xr, half_t* yr, int64_
                     h8 o;
 #pragma unroll
                     for (int k = 0; k < 8; ++k) o[k] = to_half(fast_exp((float)h[j][k] - m) * inv);
-                    st8_stream(yr + i, o);
+                    st8_out<MI_WT_SM>(yr + i, o);
                 }
             }
         } else {
@@ -367,7 +370,7 @@ __global__ __launch_bounds__(256) void softmax_onepass_kernel(const half_t* x, h
             h8 o;
 #pragma unroll
             for (int k = 0; k < 8; ++k) o[k] = to_half(fast_exp((float)a[j][k] - M) * inv);
-            st8_stream(yr + i, o);
+            st8_out<MI_WT_SM>(yr + i, o);
         }
     }
 }
