@@ -291,7 +291,8 @@ int64_t argmax_splits(int64_t B, int64_t V, int64_t& chunk) {
 // One-launch split rows (mi_greedy_argmax_ws_f16): every chunk workgroup
 // publishes its best key to a fixed per-row record and exits; only chunk 0
 // of each row waits, polls the row's records, and writes the index.  The
-// record scheme is the one-pass softmax's (epoch word, slots tagged epoch + 1,
+// record scheme is the one-pass softmax's (64-bit epoch, slots tagged with the
+// low 32 bits of epoch + 1,
 // chunk 0 raises the epoch once it has seen every slot; a poll that runs out
 // makes chunk 0 scan the whole row itself and raise the epoch by 2).  A key
 // travels as two 64-bit words {tag << 32 | key >> 32}, {tag << 32 | key
@@ -310,12 +311,12 @@ __global__ __launch_bounds__(256) void argmax_onepass_kernel(const half_t* __res
                                                              int32_t* __restrict__ out,
                                                              int poll_limit) {
     __shared__ uint64_t slots[256 / kWave];
-    __shared__ uint32_t epoch_sh;
+    __shared__ uint64_t epoch_sh;
     __shared__ int fallback_sh;
     const int split = blockIdx.x, splits = gridDim.x;
     const int64_t row = blockIdx.y;
     unsigned char* rec = ws + row * kArgmaxRecordBytes;
-    uint32_t* epoch = reinterpret_cast<uint32_t*>(rec);
+    uint64_t* epoch = reinterpret_cast<uint64_t*>(rec);
     uint64_t* slot = reinterpret_cast<uint64_t*>(rec + 16);
     const half_t* xr = x + row * V;
     const int64_t b = split * kArgmaxOnePassChunk;
@@ -323,7 +324,8 @@ __global__ __launch_bounds__(256) void argmax_onepass_kernel(const half_t* __res
     if (threadIdx.x == 0)
         epoch_sh = __hip_atomic_load(epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     const uint64_t best = chunk_best<8, 4>(xr, b, e, slots);  // barrier inside
-    const uint32_t tag = epoch_sh + 1;
+    const uint64_t E = epoch_sh;
+    const uint32_t tag = static_cast<uint32_t>(E + 1);
     if (threadIdx.x == 0) {
         __hip_atomic_store(&slot[2 * split], (static_cast<uint64_t>(tag) << 32) | (best >> 32),
                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -365,7 +367,7 @@ __global__ __launch_bounds__(256) void argmax_onepass_kernel(const half_t* __res
         if (threadIdx.x == 0) out[row] = key_index(k);
     }
     if (threadIdx.x == 0)
-        __hip_atomic_fetch_max(epoch, fallback ? tag + 1 : tag, __ATOMIC_RELAXED,
+        __hip_atomic_fetch_max(epoch, fallback ? E + 2 : E + 1, __ATOMIC_RELAXED,
                                __HIP_MEMORY_SCOPE_AGENT);
 }
 

@@ -234,13 +234,16 @@ __global__ __launch_bounds__(256) void softmax_finish_kernel(const half_t* x, ha
 // no atomics on a contended address.
 //
 // Workspace (zero before first use; every call leaves it valid for the
-// next): row r owns a fixed record at r * kRowRecordBytes -- an epoch word,
-// then kOnePassMaxSplits slots of two 64-bit words {tag << 32 | bits(max)},
-// {tag << 32 | bits(sum)}.  A call reads the row's epoch E; every chunk
-// publishes its pair tagged E + 1 and polls the row's slots until all carry
-// E + 1.  Because slots are fixed per (row, chunk) whatever the call's shape,
-// and a row's epoch only grows, a slot left by an earlier call never carries
-// the tag a later call waits for:
+// next): row r owns a fixed record at r * kRowRecordBytes -- a 64-bit epoch
+// word (16-byte header), then kOnePassMaxSplits slots of two 64-bit words
+// {tag << 32 | bits(max)}, {tag << 32 | bits(sum)}, tag = the low 32 bits of
+// epoch + 1.  A call reads the row's epoch E; every chunk publishes its pair
+// tagged E + 1 and polls the row's slots until all carry that tag.  Because
+// slots are fixed per (row, chunk) whatever the call's shape, and a row's
+// epoch only grows (64 bits: it cannot wrap), a slot left by an earlier call
+// never carries the tag a later call waits for -- short of a slot left
+// unwritten for 2^32 of its row's epochs and read again at exactly a
+// multiple of 2^32 later:
 //   * the chunk-0 workgroup raises the epoch to E + 1 (atomic max, one per
 //     row) after it has seen every slot tagged E + 1 -- so every workgroup of
 //     the row has already read E;
@@ -267,11 +270,11 @@ __global__ __launch_bounds__(256) void softmax_onepass_kernel(const half_t* x, h
     constexpr int U = 4;
     __shared__ float slots[256 / kWave];
     __shared__ float row_stats[3];  // M, S, fallback flag
-    __shared__ uint32_t epoch_sh;
+    __shared__ uint64_t epoch_sh;
     const int split = blockIdx.x, splits = gridDim.x;
     const int64_t row = blockIdx.y;
     unsigned char* rec = ws + row * kRowRecordBytes;
-    uint32_t* epoch = reinterpret_cast<uint32_t*>(rec);
+    uint64_t* epoch = reinterpret_cast<uint64_t*>(rec);
     uint64_t* slot = reinterpret_cast<uint64_t*>(rec + 16);
     const half_t* xr = x + row * D;
     const int64_t b = split * kOnePassChunk;
@@ -303,11 +306,12 @@ __global__ __launch_bounds__(256) void softmax_onepass_kernel(const half_t* x, h
         m = -INFINITY;  // NaN-free lane maximum of an all -inf (or NaN) lane
     }
     block_merge(m, s, slots);  // barriers: epoch_sh is visible after this
-    const uint32_t E = epoch_sh;
+    const uint64_t E = epoch_sh;
+    const uint32_t tag = static_cast<uint32_t>(E + 1);
     if (threadIdx.x == 0) {
-        __hip_atomic_store(&slot[2 * split], tagged(E + 1, m), __ATOMIC_RELAXED,
+        __hip_atomic_store(&slot[2 * split], tagged(tag, m), __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(&slot[2 * split + 1], tagged(E + 1, s), __ATOMIC_RELAXED,
+        __hip_atomic_store(&slot[2 * split + 1], tagged(tag, s), __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_AGENT);
     }
     if (threadIdx.x < kWave) {
@@ -322,8 +326,8 @@ __global__ __launch_bounds__(256) void softmax_onepass_kernel(const half_t* x, h
                                                       __HIP_MEMORY_SCOPE_AGENT);
                 const uint64_t w1 = __hip_atomic_load(&slot[2 * lane + 1], __ATOMIC_RELAXED,
                                                       __HIP_MEMORY_SCOPE_AGENT);
-                mine = static_cast<uint32_t>(w0 >> 32) == E + 1 &&
-                       static_cast<uint32_t>(w1 >> 32) == E + 1;
+                mine = static_cast<uint32_t>(w0 >> 32) == tag &&
+                       static_cast<uint32_t>(w1 >> 32) == tag;
                 mj = __builtin_bit_cast(float, static_cast<uint32_t>(w0));
                 sj = __builtin_bit_cast(float, static_cast<uint32_t>(w1));
             }

@@ -179,3 +179,22 @@ def test_greedy_argmax_onepass_forced_fallback(mk, orc, dev):
         x2 = normal_f16(rng, (64, 152064), 0, 4)
         got = to_host(mk.greedy_argmax(to_dev(x2, dev), workspace=ws))
         assert (got == orc.greedy_argmax(x2)).all(), f"call {i} after the fallback"
+
+
+def test_greedy_argmax_onepass_epoch_past_32_bits(mk, orc, dev):
+    """Row epochs are 64-bit: started just below 2^32, successive calls on new
+    logits return the new rows' maxima and the epoch grows past 2^32."""
+    _case("argmax one-pass epoch past 2^32")
+    import torch
+    rng = np.random.default_rng(59)
+    B, V, rec = 8, 40000, 1040 // 8
+    ws = torch.zeros(mk.greedy_argmax_workspace_bytes(B, V), dtype=torch.uint8, device=dev)
+    e64 = ws[: 512 * 1040].view(torch.int64)
+    start = (1 << 32) - 3
+    e64[0:B * rec:rec] = start
+    for i in range(5):
+        x = normal_f16(rng, (B, V), 0, 4)
+        got = to_host(mk.greedy_argmax(to_dev(x, dev), workspace=ws))
+        assert (got == orc.greedy_argmax(x)).all(), f"call {i}"
+    epochs = e64[0:B * rec:rec].cpu().numpy()
+    assert (epochs == start + 5).all(), epochs

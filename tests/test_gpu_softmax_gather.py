@@ -178,3 +178,24 @@ def test_softmax_graph_replay(mk, orc, dev):
         assert_bits_equal(to_host(y), ref, what=f"replay {i}")
         mk.softmax(xd, workspace=ws)  # eager call between replays
     assert_close(ref, orc.softmax(x, nthreads=8), what="vs oracle")
+
+
+def test_softmax_onepass_epoch_past_32_bits(mk, orc, dev):
+    """Row epochs are 64-bit: started just below 2^32 (as after ~4e9 calls on
+    a row), successive calls on new logits stay right and the epoch keeps
+    growing past 2^32 (a 32-bit epoch would stick at 2^32 - 1 and let the
+    next call take the previous call's slots as fresh)."""
+    _case("softmax one-pass epoch past 2^32")
+    import torch
+    rng = np.random.default_rng(58)
+    N, D, rec = 8, 40000, 1040 // 8
+    ws = torch.zeros(mk.softmax_workspace_bytes(N, D), dtype=torch.uint8, device=dev)
+    e64 = ws[: 512 * 1040].view(torch.int64)
+    start = (1 << 32) - 3
+    e64[0:N * rec:rec] = start
+    for i in range(5):
+        x = normal_f16(rng, (N, D), 0, 4)
+        assert_close(to_host(mk.softmax(to_dev(x, dev), workspace=ws)), orc.softmax(x),
+                     what=f"call {i}")
+    epochs = e64[0:N * rec:rec].cpu().numpy()
+    assert (epochs == start + 5).all(), epochs
