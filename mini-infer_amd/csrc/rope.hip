@@ -230,19 +230,17 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(half_t* q, int Hq, ha
     constexpr int HALF = CPH * 8;
     constexpr int HD = 2 * HALF;
     __shared__ float cs[TPW][2 * kMaxHalf];
+    __shared__ h8 wl[2][HD / 8];  // Q and K weights, read at use (no registers held)
     const int64_t tok0 = static_cast<int64_t>(blockIdx.x) * TPW;
     const int ntok = static_cast<int>(T - tok0 < TPW ? T - tok0 : TPW);
     const int upt = (Hq + Hkv) * CPH;  // units per token
     const int units = ntok * upt;
     const int c = threadIdx.x & (CPH - 1);  // a lane's slice is the same for every unit
 
-    // this lane's weight slices, for a Q head and for a K head
-    const h8 wq1 = ld8(wq + c * 8), wq2 = ld8(wq + HALF + c * 8);
-    h8 wk1 = h8(0), wk2 = h8(0);
-    if (Hkv > 0) {
-        wk1 = ld8(wk + c * 8);
-        wk2 = ld8(wk + HALF + c * 8);
-    }
+    if (threadIdx.x < HD / 8)
+        wl[0][threadIdx.x] = ld8(wq + threadIdx.x * 8);
+    else if (threadIdx.x < HD / 4 && Hkv > 0)
+        wl[1][threadIdx.x - HD / 8] = ld8(wk + (threadIdx.x - HD / 8) * 8);
 
     // unit u -> (token, head); returns the head's base pointer
     auto head_ptr = [&](int u, bool& is_k, int& t) -> half_t* {
@@ -296,7 +294,7 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(half_t* q, int Hq, ha
         int t;
         half_t* hp = head_ptr(u, is_k, t);
         const float rrms = rsqrtf(ss / static_cast<float>(HD) + eps);
-        const h8 w1 = is_k ? wk1 : wq1, w2 = is_k ? wk2 : wq2;
+        const h8 w1 = wl[is_k][c], w2 = wl[is_k][CPH + c];
         const float* cst = &cs[t][0];
         h8 y1, y2;
 #pragma unroll
