@@ -300,7 +300,11 @@ int64_t argmax_splits(int64_t B, int64_t V, int64_t& chunk) {
 // must be zero before its first use.
 // ---------------------------------------------------------------------------
 constexpr int kArgmaxOnePassMaxSplits = 64;
-constexpr int64_t kArgmaxOnePassChunk = 8192;  // 4 vectors per lane
+#ifndef MI_ARGMAX_ONEPASS_U
+#define MI_ARGMAX_ONEPASS_U 4
+#endif
+constexpr int kArgmaxOnePassU = MI_ARGMAX_ONEPASS_U;             // vectors per lane
+constexpr int64_t kArgmaxOnePassChunk = 2048 * kArgmaxOnePassU;  // elements per workgroup
 constexpr int64_t kArgmaxRecordBytes = 16 + kArgmaxOnePassMaxSplits * 16;
 constexpr int64_t kArgmaxRecordRegion = kArgmaxSplitMaxRows * kArgmaxRecordBytes;
 constexpr int kArgmaxPollLimit = 1 << 16;
@@ -323,7 +327,7 @@ __global__ __launch_bounds__(256) void argmax_onepass_kernel(const half_t* __res
     const int64_t e = b + kArgmaxOnePassChunk < V ? b + kArgmaxOnePassChunk : V;
     if (threadIdx.x == 0)
         epoch_sh = __hip_atomic_load(epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const uint64_t best = chunk_best<8, 4>(xr, b, e, slots);  // barrier inside
+    const uint64_t best = chunk_best<8, kArgmaxOnePassU>(xr, b, e, slots);  // barrier inside
     const uint64_t E = epoch_sh;
     const uint32_t tag = static_cast<uint32_t>(E + 1);
     if (threadIdx.x == 0) {

@@ -255,7 +255,11 @@ __global__ __launch_bounds__(256) void softmax_finish_kernel(const half_t* x, ha
 // stores, L2-bypassing loads), so a tag always travels with its value.
 // ---------------------------------------------------------------------------
 constexpr int kOnePassMaxSplits = 64;
-constexpr int64_t kOnePassChunk = 8192;  // 4 vectors per lane
+#ifndef MI_SOFTMAX_ONEPASS_U
+#define MI_SOFTMAX_ONEPASS_U 4
+#endif
+constexpr int kOnePassU = MI_SOFTMAX_ONEPASS_U;     // vectors per lane
+constexpr int64_t kOnePassChunk = 2048 * kOnePassU;  // elements per workgroup
 constexpr int64_t kRowRecordBytes = 16 + kOnePassMaxSplits * 16;
 constexpr int kPollLimit = 1 << 16;
 std::atomic<int> g_poll_limit{kPollLimit};  // mi_softmax_test_poll_limit
@@ -267,7 +271,7 @@ __device__ __forceinline__ uint64_t tagged(uint32_t tag, float v) {
 __global__ __launch_bounds__(256) void softmax_onepass_kernel(const half_t* x, half_t* y,
                                                               unsigned char* ws, int64_t D,
                                                               int poll_limit) {
-    constexpr int U = 4;
+    constexpr int U = kOnePassU;
     __shared__ float slots[256 / kWave];
     __shared__ float row_stats[3];  // M, S, fallback flag
     __shared__ uint64_t epoch_sh;
