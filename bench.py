@@ -326,15 +326,16 @@ def all_kernels(mk, dev, iters, warmup):
     bt = torch.from_numpy(rng.permutation(mb).astype(np.int32)).to(dev).view(1, mb)
     sl = torch.tensor([T], dtype=torch.int32, device=dev)
     sp = torch.tensor([0], dtype=torch.int32, device=dev)
-    ksrc = randn16((1, T, H, hd), gen, dev)
-    vsrc = randn16((1, T, H, hd), gen, dev)
-    kc = torch.empty((1, mb, H, bs, hd), dtype=f16, device=dev)
-    vc = torch.empty_like(kc)
     nb = 2 * 2 * T * H * hd * 2 + (mb + 2) * 4
-    sec = time_launches(lambda i: mk.paged_kv_scatter(ksrc, kc, bt, sl, sp, 0, bs, v_src=vsrc,
-                                                      v_cache=vc), 1, iters, warmup)
+    ns = rotations(nb, max_sets=32)
+    kv = [(randn16((1, T, H, hd), gen, dev), randn16((1, T, H, hd), gen, dev),
+           torch.empty((1, mb, H, bs, hd), dtype=f16, device=dev),
+           torch.empty((1, mb, H, bs, hd), dtype=f16, device=dev)) for _ in range(ns)]
+    sec = time_launches(lambda i: mk.paged_kv_scatter(kv[i][0], kv[i][2], bt, sl, sp, 0, bs,
+                                                      v_src=kv[i][1], v_cache=kv[i][3]),
+                        ns, iters, warmup)
     out.append(report("paged_kv_scatter_kv", "chain K+V [6064,4,128] bs=16", nb, sec, T))
-    del ksrc, vsrc, kc, vc
+    del kv
     torch.cuda.synchronize()
     for r in out:
         if r["bytes"] >= 8 << 20:

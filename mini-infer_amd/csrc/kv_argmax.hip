@@ -31,7 +31,7 @@
 #include "mi_host.h"
 
 #ifndef MI_WT_KV
-#define MI_WT_KV 1
+#define MI_WT_KV 0
 #endif
 namespace mi {
 namespace {
@@ -44,6 +44,22 @@ constexpr int kKvTokensPerWg = 4;  // one wave per token
 struct KvGeometry {
     int64_t B, S;
     int64_t layer, num_blocks, H_kv, D, block_size, max_blocks_per_seq;
+};
+
+// 16-byte vectors (streamed) or single elements.
+template <int VEC>
+struct HVecKv;
+template <>
+struct HVecKv<8> {
+    typedef h8 T;
+    __device__ static T load(const half_t* p) { return ld8_stream(p); }
+    __device__ static void store(half_t* p, T v) { st8_out<MI_WT_KV>(p, v); }
+};
+template <>
+struct HVecKv<1> {
+    typedef half_t T;
+    __device__ static T load(const half_t* p) { return *p; }
+    __device__ static void store(half_t* p, T v) { *p = v; }
 };
 
 template <int VEC>
@@ -59,6 +75,19 @@ __global__ __launch_bounds__(256) void kv_scatter_kernel(const half_t* __restric
     const int lane = threadIdx.x & (kWave - 1);
     const int64_t tok = static_cast<int64_t>(blockIdx.x) * kKvTokensPerWg + wave;
     if (tok >= g.B * g.S) return;  // wave-uniform; no cross-lane work follows
+    const int64_t row = g.H_kv * g.D;               // halves per token
+    const int64_t nv = row / VEC;                   // vectors per token
+    const half_t* s0 = src0 + tok * row;
+    const half_t* s1 = src1 ? src1 + tok * row : nullptr;
+    // The source row depends only on the token: its first vectors are in
+    // flight while the destination is resolved (two dependent lookups:
+    // start_pos / seq_len, then the block table).  Loads of a token that
+    // turns out to be skipped read valid source memory and are dropped.
+    typename HVecKv<VEC>::T a0{}, c0{};
+    if (lane < nv) {
+        a0 = HVecKv<VEC>::load(s0 + lane * VEC);
+        if (s1) c0 = HVecKv<VEC>::load(s1 + lane * VEC);
+    }
     const int64_t b = tok / g.S;
     const int64_t s = tok - b * g.S;
     const int64_t pos = static_cast<int64_t>(start_pos[b]) + s;
@@ -69,28 +98,20 @@ __global__ __launch_bounds__(256) void kv_scatter_kernel(const half_t* __restric
     if (phys < 0 || phys >= g.num_blocks) return;
     const int64_t slot = pos - blk * g.block_size;
 
-    const int64_t row = g.H_kv * g.D;               // halves per token
     const int64_t per_head = g.D / VEC;             // vectors per head
-    const int64_t nv = row / VEC;                   // vectors per token
     const int64_t head_stride = g.block_size * g.D; // halves between heads in a block
     const int64_t dst_base =
         ((g.layer * g.num_blocks + phys) * g.H_kv) * head_stride + slot * g.D;
-    const half_t* s0 = src0 + tok * row;
-    const half_t* s1 = src1 ? src1 + tok * row : nullptr;
     for (int64_t v = lane; v < nv; v += kWave) {
         const int64_t h = v / per_head;
         const int64_t d = (v - h * per_head) * VEC;
         const int64_t dst = dst_base + h * head_stride + d;
-        if constexpr (VEC == 8) {
-            const h8 a = ld8_stream(s0 + v * 8);
-            h8 c;
-            if (s1) c = ld8_stream(s1 + v * 8);
-            st8_out<MI_WT_KV>(cache0 + dst, a);
-            if (s1) st8_out<MI_WT_KV>(cache1 + dst, c);
-        } else {
-            cache0[dst] = s0[v];
-            if (s1) cache1[dst] = s1[v];
+        if (v != lane) {
+            a0 = HVecKv<VEC>::load(s0 + v * VEC);
+            if (s1) c0 = HVecKv<VEC>::load(s1 + v * VEC);
         }
+        HVecKv<VEC>::store(cache0 + dst, a0);
+        if (s1) HVecKv<VEC>::store(cache1 + dst, c0);
     }
 }
 
