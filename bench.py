@@ -39,7 +39,7 @@ def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
 
-def rotations(set_bytes, min_sets=2, max_sets=16):
+def rotations(set_bytes, min_sets=2, max_sets=64):
     """Enough buffer sets that a full rotation is >= 3x the Infinity Cache."""
     return int(min(max_sets, max(min_sets, math.ceil(3 * MALL_BYTES / max(set_bytes, 1)))))
 
@@ -311,14 +311,17 @@ def all_kernels(mk, dev, iters, warmup):
     sec = time_launches(lambda i: mk.softmax(sets[i][0], y=sets[i][1], workspace=ws), ns, iters,
                         warmup)
     out.append(report("softmax", "[64,152064]", nb, sec, N))
-    # 5g. greedy argmax over the same logits (the step after the LM head)
+    del sets
+    # 5g. greedy argmax over logits of the same shape (the step after the LM head)
     nb = N * V * 2 + N * 4
+    ns = rotations(N * V * 2)
+    xs = [randn16((N, V), gen, dev, 0.0, 4.0) for _ in range(ns)]
     wsa = torch.zeros(max(1, mk.greedy_argmax_workspace_bytes(N, V)), dtype=torch.uint8, device=dev)
     outi = torch.empty(N, dtype=torch.int32, device=dev)
-    sec = time_launches(lambda i: mk.greedy_argmax(sets[i][0], out=outi, workspace=wsa), ns, iters,
+    sec = time_launches(lambda i: mk.greedy_argmax(xs[i], out=outi, workspace=wsa), ns, iters,
                         warmup)
     out.append(report("greedy_argmax", "[64,152064]", nb, sec, N))
-    del sets
+    del xs
     # 5h. paged KV scatter of the chain's K and V [6064, 4, 128], block size
     # 16, as one 6064-token sequence into shuffled physical blocks
     H, hd, bs = 4, 128, 16
