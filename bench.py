@@ -17,7 +17,7 @@ test arithmetic, oracle/libmi_oracle.so) on the host, on a bounded sample of
 the same workload.  The oracle is the checker, never the thing measured on
 the GPU.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-kernels] [--no-cpu]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-kernels] [--no-cpu] [--no-chain]
 """
 import argparse
 import json
@@ -584,6 +584,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-kernels", action="store_true", help="skip the per-config table")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-chain", action="store_true",
+                    help="skip the whole-chain rows (profiling runs: one row per kernel and grid)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--cpu-seconds-per-config", type=float, default=1.0,
                     help="CPU oracle time per kernel-table config")
@@ -618,7 +620,8 @@ def main():
     if not args.no_kernels:
         log("[bench] per-config kernel table")
         kernels = all_kernels(mk, dev, max(20, args.steps // 2), max(5, args.warmup // 2))
-        kernels += decoder_chain(mk, dev, max(10, args.steps // 8), max(3, args.warmup // 4))
+        if not args.no_chain:
+            kernels += decoder_chain(mk, dev, max(10, args.steps // 8), max(3, args.warmup // 4))
         for k in kernels:
             floor = (f"  copy floor {k['copy_floor_us']:7.2f} us ({100 * k['frac_of_copy_floor']:5.1f}%)"
                      if "copy_floor_us" in k else "")
