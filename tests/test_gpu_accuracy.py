@@ -1,0 +1,99 @@
+"""GPU accuracy margins at the BASELINE shapes: how far inside the parity bar
+the fp32-math kernels land.
+
+The parity bar is rtol = atol = 1e-3 against the fp32 oracle
+(tests/verify/verify.py:142).  These tests hold the kernels to tighter
+margins on the full-size workloads, so a change that loses accuracy fails
+here while it is still inside the bar:
+* worst |ours - ref| / (atol + rtol |ref|) <= 0.5;
+* at most 1 fp16 ulp from RN16(ref) in the normal fp16 range (for
+  gelu_tanh / GeGLU against a float64 evaluation, see _gelu64); below 2^-14
+  the subnormal spacing (6e-8) makes ulps meaningless and the first bound
+  covers those outputs;
+* at most 0.1% of outputs differ from RN16(ref) at all.
+Each case prints its figures.
+"""
+import numpy as np
+import pytest
+
+from helpers import normal_f16, to_dev, to_host, ulp_diff
+
+pytestmark = pytest.mark.gpu
+RTOL = ATOL = 1e-3
+
+
+def _margins(name, ours_f16, ref_f32, max_ulp=1, exact=None):
+    """`exact`: a float64 evaluation to measure ulps against instead of the
+    oracle (gelu: see _gelu64)."""
+    o = np.asarray(ours_f16).astype(np.float32)
+    r = np.asarray(ref_f32, dtype=np.float32)
+    ratio = float((np.abs(o - r) / (ATOL + RTOL * np.abs(r))).max())
+    if exact is not None:
+        r = np.asarray(exact, dtype=np.float64).astype(np.float32)
+    u = ulp_diff(np.asarray(ours_f16, dtype=np.float16), r.astype(np.float16))
+    off = float((u > 0).mean())
+    normal = np.abs(r) >= 2.0 ** -14  # fp16 subnormals are 6e-8 apart: ulps there say little
+    un = int(u[normal].max()) if normal.any() else 0
+    us = int(u[~normal].max()) if (~normal).any() else 0
+    print(f"[accuracy] {name}: max err/tol {ratio:.3f}, max ulp {un} (normal range; "
+          f"{us} below 2^-14), {100 * off:.4f}% != RN16(ref)", flush=True)
+    assert ratio <= 0.5, f"{name}: max err/tol {ratio:.3f}"
+    assert un <= max_ulp, f"{name}: {un} ulp"
+    assert off <= 1e-3, f"{name}: {100 * off:.4f}% of outputs differ from RN16(ref)"
+
+
+def _gelu64(x):
+    """gelu_tanh in float64.  The oracle follows the reference's fp32 formula
+    0.5 x (1 + tanhf(u)) (src/kernels/gelu_kernel.cuh:11), in which 1 + tanh
+    cancels for x below about -3: the oracle's own relative error there
+    reaches ~1e-3, while the kernel's x / (1 + exp(-2u)) form has none.  The
+    ulp bound is therefore taken against this exact evaluation; the tolerance
+    bound stays against the oracle."""
+    x = np.asarray(x, dtype=np.float64)
+    return 0.5 * x * (1.0 + np.tanh(np.sqrt(2.0 / np.pi) * (x + 0.044715 * x ** 3)))
+
+
+def test_accuracy_norms(mk, orc, dev):
+    print("[case] accuracy: RMSNorm [16,3584], fused add+RMSNorm [8192,3584], Q-norm", flush=True)
+    rng = np.random.default_rng(123)
+    x, w = normal_f16(rng, (16, 3584)), normal_f16(rng, (3584,), 1, 0.1)
+    _margins("RMSNorm [16,3584]", to_host(mk.rmsnorm(to_dev(x, dev), to_dev(w, dev))),
+             orc.rmsnorm(x, w))
+    _margins("RMSNorm (1+w) [16,3584]",
+             to_host(mk.rmsnorm(to_dev(x, dev), to_dev(w, dev), add_one=True)),
+             orc.rmsnorm(x, w, add_one=True))
+    x, r = normal_f16(rng, (8192, 3584)), normal_f16(rng, (8192, 3584))
+    y = to_host(mk.fused_add_rmsnorm(to_dev(x, dev), to_dev(r, dev), to_dev(w, dev)))
+    _margins("fused add+RMSNorm [8192,3584]", y, orc.fused_add_rmsnorm(x, r, w, nthreads=8)[1])
+    q, wq = normal_f16(rng, (6064 * 28, 128)), normal_f16(rng, (128,), 1, 0.1)
+    _margins("Q RMSNorm [6064*28,128]", to_host(mk.rmsnorm(to_dev(q, dev), to_dev(wq, dev))),
+             orc.rmsnorm(q, wq, nthreads=8))
+
+
+def test_accuracy_activations(mk, orc, dev):
+    print("[case] accuracy: SwiGLU [4096,18944], GeGLU / gelu_tanh [4096,14336]", flush=True)
+    rng = np.random.default_rng(124)
+    g, u = normal_f16(rng, (4096, 18944)), normal_f16(rng, (4096, 18944))
+    _margins("SwiGLU [4096,18944]", to_host(mk.swiglu(to_dev(g, dev), to_dev(u, dev))),
+             orc.swiglu(g, u, nthreads=8))
+    g, u = normal_f16(rng, (4096, 14336)), normal_f16(rng, (4096, 14336))
+    g64 = _gelu64(g)
+    _margins("GeGLU [4096,14336]", to_host(mk.geglu(to_dev(g, dev), to_dev(u, dev))),
+             orc.geglu(g, u, nthreads=8), exact=g64 * u.astype(np.float64))
+    _margins("gelu_tanh [4096,14336]", to_host(mk.gelu_tanh(to_dev(g, dev))),
+             orc.gelu_tanh(g, nthreads=8), exact=g64)
+
+
+def test_accuracy_softmax(mk, orc, dev):
+    print("[case] accuracy: softmax [64,152064] one and two launches, [57344,512]", flush=True)
+    import torch
+    rng = np.random.default_rng(125)
+    lg = normal_f16(rng, (64, 152064), 0, 4)
+    ref = orc.softmax(lg, nthreads=8)
+    ws = torch.zeros(mk.softmax_workspace_bytes(64, 152064), dtype=torch.uint8, device=dev)
+    _margins("softmax [64,152064] one launch",
+             to_host(mk.softmax(to_dev(lg, dev), workspace=ws)), ref)
+    _margins("softmax [64,152064] two launches", to_host(mk.softmax(to_dev(lg, dev))), ref)
+    lg = normal_f16(rng, (57344, 512), 0, 4)
+    _margins("softmax [57344,512]", to_host(mk.softmax(to_dev(lg, dev))),
+             orc.softmax(lg, nthreads=8))
