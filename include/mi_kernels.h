@@ -135,7 +135,13 @@ int mi_scale_inplace_f16(void* y, float scale, int64_t n, void* stream);
 
 /* Row softmax, fp32 math: y = exp(x - max) / sum(exp(x - max)).
  * x, y: [N, D]; y may equal x.  Replaces launch_softmax
- * (src/kernels/softmax_kernel.cuh:12). */
+ * (src/kernels/softmax_kernel.cuh:12).  Few long rows (N < 512, D >= 8192)
+ * are split across workgroups.  On the legacy default stream (0, the
+ * reference's callers' stream) out-of-place aligned calls run in one launch,
+ * using 532,480 bytes of row records that the library allocates and zeroes
+ * once per device, on first use, and keeps until the process ends.  On other
+ * streams, or in place, they take two launches with a stream-ordered
+ * workspace for the call. */
 int mi_softmax_f16(const void* x, void* y, int64_t N, int64_t D, void* stream);
 
 /* Bytes of device workspace mi_softmax_ws_f16 needs for [N, D]: 0 when rows
@@ -199,8 +205,11 @@ int mi_paged_kv_scatter_kv_f16(const void* k_src, const void* v_src, void* k_cac
  * with nothing above -inf gives -1.
  * Replaces launch_greedy_sample / launch_greedy_sample_batched
  * (src/kernels/sampling_kernel.cuh:17-30; src/kernels/sampling_kernel.cu:14-76).
- * For B < 512 rows of V >= 8192 it takes <= 256 KiB of stream-ordered
- * workspace for the call, as mi_softmax_f16 does. */
+ * B < 512 rows of V >= 8192 are split across workgroups: on stream 0 (V % 16
+ * == 0, aligned) in one launch with 532,480 bytes of row records the library
+ * holds per device (allocated and zeroed on first use, kept until the process
+ * ends), otherwise in two launches with <= 256 KiB of stream-ordered
+ * workspace for the call. */
 int mi_greedy_argmax_f16(const void* logits, int64_t B, int64_t V, int32_t* out, void* stream);
 
 /* Workspace bytes mi_greedy_argmax_ws_f16 needs: 0 when rows are not split,

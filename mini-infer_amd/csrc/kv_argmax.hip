@@ -415,8 +415,23 @@ int64_t argmax_ws_bytes(int64_t B, int64_t V) {
 #define MI_ARGMAX_ONEPASS 1
 #endif
 
+// What a workspace handed to argmax() holds.
+enum class Ws {
+    kKeys,             // the two-launch keys only (allocating entry point)
+    kRecordsThenKeys,  // argmax_ws_bytes() layout (mi_greedy_argmax_ws_f16)
+    kRecords,          // the one-launch row records only (library-held, stream 0)
+};
+
+// Whether [B, V] runs as the one-launch split form given row records.
+bool argmax_onepass_ok(const void* logits, int64_t B, int64_t V) {
+    if (!MI_ARGMAX_ONEPASS || B <= 0 || V <= 0 || B > 65535 || V > 0x7fffffff) return false;
+    int64_t chunk;
+    return argmax_splits(B, V, chunk) > 1 && V % 16 == 0 && aligned16(logits) &&
+           ceil_div(V, kArgmaxOnePassChunk) <= kArgmaxOnePassMaxSplits;
+}
+
 int argmax(const void* logits, int64_t B, int64_t V, int32_t* out, void* ws, int64_t ws_bytes,
-           bool onepass_ws, void* stream) {
+           Ws layout, void* stream) {
     if (B < 0 || V < 0 || ws_bytes < 0) return MI_ERR_INVALID_ARGUMENT;
     if (B == 0) return MI_OK;
     if (!logits || !out) return MI_ERR_INVALID_ARGUMENT;
@@ -426,7 +441,13 @@ int argmax(const void* logits, int64_t B, int64_t V, int32_t* out, void* ws, int
     const int64_t splits = V == 0 ? 1 : argmax_splits(B, V, chunk);
     if (V == 0) chunk = 0;
     const int64_t keys = splits > 1 ? B * splits * 8 : 0;
-    const int64_t need = keys > 0 && onepass_ws ? kArgmaxRecordRegion + keys : keys;
+    const bool onepass = layout != Ws::kKeys && argmax_onepass_ok(logits, B, V);
+    if (layout == Ws::kRecords && keys > 0 && !onepass)
+        return MI_ERR_UNSUPPORTED;  // no keys to fall back on (callers check argmax_onepass_ok)
+    const int64_t need = keys == 0 ? 0
+                         : layout == Ws::kKeys ? keys
+                         : layout == Ws::kRecords ? kArgmaxRecordRegion
+                                                  : kArgmaxRecordRegion + keys;
     if (need > 0) {
         if (!ws || ws_bytes < need) return MI_ERR_INVALID_ARGUMENT;
         if (reinterpret_cast<uintptr_t>(ws) % 16 != 0) return MI_ERR_INVALID_ARGUMENT;
@@ -436,15 +457,16 @@ int argmax(const void* logits, int64_t B, int64_t V, int32_t* out, void* ws, int
     const hipStream_t st = as_stream(stream);
     const auto* x = static_cast<const half_t*>(logits);
     const bool vec = V % 16 == 0 && aligned16(logits);
-    const int64_t sp1 = ceil_div(V, kArgmaxOnePassChunk);
-    if (MI_ARGMAX_ONEPASS && onepass_ws && splits > 1 && vec && sp1 <= kArgmaxOnePassMaxSplits) {
+    if (onepass) {
+        const int64_t sp1 = ceil_div(V, kArgmaxOnePassChunk);
         argmax_onepass_kernel<<<dim3(static_cast<unsigned>(sp1), static_cast<unsigned>(B)),
                                 dim3(256), 0, st>>>(x, V, static_cast<unsigned char*>(ws), out,
                                                     g_argmax_poll_limit.load());
         return launch_status();
     }
-    auto* w = reinterpret_cast<uint64_t*>(static_cast<unsigned char*>(ws) +
-                                          (onepass_ws && keys > 0 ? kArgmaxRecordRegion : 0));
+    auto* w = reinterpret_cast<uint64_t*>(
+        static_cast<unsigned char*>(ws) +
+        (layout == Ws::kRecordsThenKeys && keys > 0 ? kArgmaxRecordRegion : 0));
     const dim3 g(static_cast<unsigned>(splits), static_cast<unsigned>(B));
     const bool two = splits == 1 || argmax_tile(B, V) == 4096;
     if (vec) {
@@ -491,7 +513,8 @@ extern "C" int64_t mi_greedy_argmax_workspace_bytes(int64_t B, int64_t V) {
 
 extern "C" int mi_greedy_argmax_ws_f16(const void* logits, int64_t B, int64_t V, int32_t* out,
                                        void* workspace, int64_t workspace_bytes, void* stream) {
-    return mi::argmax(logits, B, V, out, workspace, workspace_bytes, true, stream);
+    return mi::argmax(logits, B, V, out, workspace, workspace_bytes, mi::Ws::kRecordsThenKeys,
+                      stream);
 }
 
 extern "C" int mi_greedy_argmax_test_poll_limit(int limit) {
@@ -501,15 +524,24 @@ extern "C" int mi_greedy_argmax_test_poll_limit(int limit) {
 
 extern "C" int mi_greedy_argmax_f16(const void* logits, int64_t B, int64_t V, int32_t* out,
                                     void* stream) {
-    // a fresh pool allocation is not zeroed: the two-launch form
     const int64_t need = (B > 0 && V > 0) ? mi::argmax_keys_bytes(B, V) : 0;
-    if (need == 0) return mi::argmax(logits, B, V, out, nullptr, 0, false, stream);
+    if (need == 0) return mi::argmax(logits, B, V, out, nullptr, 0, mi::Ws::kKeys, stream);
     if (!logits || !out) return MI_ERR_INVALID_ARGUMENT;
     const hipStream_t s = mi::as_stream(stream);
+    // Few long rows on the default stream (the reference's callers pass 0):
+    // one launch, with row records the library holds for stream 0.
+    if (mi::argmax_onepass_ok(logits, B, V)) {
+        void* rec = mi::default_stream_region(mi::kRegionArgmax, mi::kArgmaxRecordRegion, s);
+        if (rec)
+            return mi::argmax(logits, B, V, out, rec, mi::kArgmaxRecordRegion, mi::Ws::kRecords,
+                              stream);
+    }
+    // Otherwise two launches with a stream-ordered keys workspace (a fresh
+    // pool allocation is not zeroed, which the two-launch form does not need).
     void* ws = nullptr;
     hipError_t e = hipMallocAsync(&ws, static_cast<size_t>(need), s);
     if (e != hipSuccess) return static_cast<int>(e);
-    const int st = mi::argmax(logits, B, V, out, ws, need, false, stream);
+    const int st = mi::argmax(logits, B, V, out, ws, need, mi::Ws::kKeys, stream);
     e = hipFreeAsync(ws, s);
     if (st != MI_OK) return st;
     return e == hipSuccess ? MI_OK : static_cast<int>(e);

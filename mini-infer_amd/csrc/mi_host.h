@@ -54,6 +54,44 @@ inline int64_t resident_workgroups(const void* kernel, int threads) {
     return cap;
 }
 
+// A zeroed device region of `bytes` that the library holds for the current
+// device's legacy default stream (stream 0), one per `tag`: allocated and
+// zeroed on stream 0 at its first use, never freed.  Calls on stream 0 run in
+// order, so a region that each call leaves valid for the next (the one-launch
+// softmax / argmax row records) can be shared by all of them.  Other streams
+// get nullptr -- a stream handle can be reused by a new stream while work of
+// the old one is pending, and hipStreamPerThread names a different stream in
+// every thread -- as do runtime errors (the error is cleared, so it is not
+// reported by a later launch).  The caller then takes a path that needs no
+// such region.
+inline void* default_stream_region(int tag, int64_t bytes, hipStream_t s) {
+    if (s != nullptr || bytes <= 0) return nullptr;
+    static std::mutex mu;
+    static std::map<std::pair<int, int>, void*> regions;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) {
+        (void)hipGetLastError();
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lock(mu);
+    const auto key = std::make_pair(dev, tag);
+    auto it = regions.find(key);
+    if (it != regions.end()) return it->second;
+    void* p = nullptr;
+    if (hipMalloc(&p, static_cast<size_t>(bytes)) != hipSuccess) {
+        (void)hipGetLastError();
+        return nullptr;
+    }
+    if (hipMemsetAsync(p, 0, static_cast<size_t>(bytes), nullptr) != hipSuccess) {
+        (void)hipGetLastError();
+        (void)hipFree(p);
+        return nullptr;
+    }
+    regions[key] = p;
+    return p;
+}
+enum RegionTag { kRegionSoftmax = 1, kRegionArgmax = 2 };
+
 // How full the GPU's last round of workgroups is when `groups` workgroups
 // run `cap` at a time: groups / (rounds * cap), 1.0 = no idle tail.
 inline double round_fill(int64_t groups, int64_t cap) {

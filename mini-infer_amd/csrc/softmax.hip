@@ -10,10 +10,11 @@
 //   * Many rows (N >= 512): one workgroup per row; the write pass re-reads the
 //     row, which the workgroup has just streamed through L2.
 //   * Few long rows (the LM-head case, 64 x 152064): one workgroup per row
-//     would light up 64 of 256 CUs, so each row is cut into chunks.  With a
-//     caller workspace and y != x, one launch (softmax_onepass_kernel, below):
-//     chunks stay in registers and exchange their (max, sum) through tagged
-//     per-row records.  Otherwise two launches, with `splits` chunks:
+//     would light up 64 of 256 CUs, so each row is cut into chunks.  With
+//     row records -- a caller workspace, or on stream 0 a region the library
+//     holds -- and y != x, one launch (softmax_onepass_kernel, below): chunks
+//     stay in registers and exchange their (max, sum) through tagged per-row
+//     records.  Otherwise two launches, with `splits` chunks:
 //     Kernel 1 writes a (max, sum) pair per chunk to a small stream-ordered
 //     workspace (8 bytes per chunk), from tiles whose loads are all issued
 //     first (one HBM wait per tile), a packed fp16 lane maximum and one exp
@@ -428,66 +429,81 @@ int64_t workspace_bytes(int64_t N, int64_t D) {
 #define MI_SOFTMAX_ONEPASS 1
 #endif
 
-// onepass_ws: a workspace laid out as workspace_bytes() describes (zero
-// before first use), else nullptr and `ws` holds only the two-pass pairs.
+// What a workspace handed to softmax_checked holds.
+enum class Ws {
+    kPairs,             // the two-pass (max, sum) pairs only (allocating entry point)
+    kRecordsThenPairs,  // workspace_bytes() layout (mi_softmax_ws_f16)
+    kRecords,           // the one-pass row records only (library-held, stream 0)
+};
+
+// Whether [N, D] runs as the one-launch split form given row records: every
+// chunk workgroup of the grid resident at once (no chunk polls for a
+// row-mate still queued), aligned rows, and y != x (the fallback re-reads x).
+bool onepass_ok(const void* x, const void* y, int64_t N, int64_t D) {
+    int64_t splits, chunk;
+    if (!MI_SOFTMAX_ONEPASS || plan(N, D, splits, chunk) != Plan::kTwoPass) return false;
+    const int64_t sp1 = ceil_div(D, kOnePassChunk);
+    return D % 8 == 0 && aligned16(x) && aligned16(y) && x != y && sp1 <= kOnePassMaxSplits &&
+           N <= 65535 &&
+           sp1 * N <= resident_workgroups(reinterpret_cast<const void*>(softmax_onepass_kernel),
+                                          256);
+}
+
 int softmax_checked(const void* x, void* y, int64_t N, int64_t D, void* ws, int64_t ws_bytes,
-                    bool onepass_ws, void* stream) {
+                    Ws layout, void* stream) {
     if (N < 0 || D < 0 || ws_bytes < 0) return MI_ERR_INVALID_ARGUMENT;
     if (N == 0 || D == 0) return MI_OK;
     if (!x || !y) return MI_ERR_INVALID_ARGUMENT;
     if (N > kMaxGridX) return MI_ERR_UNSUPPORTED;
     const int64_t bytes = N * D * 2;
     if (x != y && overlaps(x, bytes, y, bytes)) return MI_ERR_ALIASING;
-    const int64_t need = onepass_ws ? workspace_bytes(N, D) : twopass_bytes(N, D);
+    int64_t splits, chunk;
+    const Plan p = plan(N, D, splits, chunk);
+    const bool onepass = layout != Ws::kPairs && onepass_ok(x, y, N, D);
+    if (layout == Ws::kRecords && p == Plan::kTwoPass && !onepass)
+        return MI_ERR_UNSUPPORTED;  // no pairs to fall back on (callers check onepass_ok)
+    const int64_t need = p == Plan::kRow ? 0
+                         : layout == Ws::kPairs ? twopass_bytes(N, D)
+                         : layout == Ws::kRecords ? kOnePassRegion
+                                                  : workspace_bytes(N, D);
     if (need > 0) {
         if (!ws || ws_bytes < need) return MI_ERR_INVALID_ARGUMENT;
         if (overlaps(ws, need, x, bytes) || overlaps(ws, need, y, bytes)) return MI_ERR_ALIASING;
-        if (onepass_ws && reinterpret_cast<uintptr_t>(ws) % 16 != 0) return MI_ERR_INVALID_ARGUMENT;
+        if (layout != Ws::kPairs && reinterpret_cast<uintptr_t>(ws) % 16 != 0)
+            return MI_ERR_INVALID_ARGUMENT;
     }
     const auto* xh = static_cast<const half_t*>(x);
     auto* yh = static_cast<half_t*>(y);
-    auto* part = reinterpret_cast<float*>(static_cast<unsigned char*>(ws) +
-                                          (onepass_ws && need > 0 ? kOnePassRegion : 0));
     const hipStream_t s = as_stream(stream);
     const bool vec = D % 8 == 0 && aligned16(x) && aligned16(y);
-    int64_t splits, chunk;
-    switch (plan(N, D, splits, chunk)) {
-        case Plan::kRow: {
-            const int64_t want = ceil_div(D, vec ? 8 : 1);
-            const int threads = static_cast<int>(ceil_div(want < 1024 ? want : 1024, kWave) * kWave);
-            if (vec)
-                softmax_row_kernel<8><<<dim3(static_cast<unsigned>(N)), dim3(threads), 0, s>>>(xh, yh, D);
-            else
-                softmax_row_kernel<1><<<dim3(static_cast<unsigned>(N)), dim3(threads), 0, s>>>(xh, yh, D);
-            break;
-        }
-        case Plan::kTwoPass: {
-            const int64_t sp1 = ceil_div(D, kOnePassChunk);
-            // one launch when every chunk workgroup of the grid can be
-            // resident at once (no chunk polls for a row-mate still queued)
-            if (MI_SOFTMAX_ONEPASS && onepass_ws && vec && x != y && sp1 <= kOnePassMaxSplits &&
-                N <= 65535 &&
-                sp1 * N <= resident_workgroups(
-                               reinterpret_cast<const void*>(softmax_onepass_kernel), 256)) {
-                softmax_onepass_kernel<<<dim3(static_cast<unsigned>(sp1), static_cast<unsigned>(N)),
-                                         dim3(256), 0, s>>>(xh, yh,
-                                                            static_cast<unsigned char*>(ws), D,
-                                                            g_poll_limit.load());
-                break;
-            }
-            const dim3 g(static_cast<unsigned>(splits), static_cast<unsigned>(N));
-            if (vec) {
-                if (split_tile(N, D) == 4096)
-                    softmax_partial_kernel<8, 2><<<g, dim3(256), 0, s>>>(xh, part, D, chunk);
-                else
-                    softmax_partial_kernel<8, 1><<<g, dim3(256), 0, s>>>(xh, part, D, chunk);
-                softmax_finish_kernel<8><<<g, dim3(256), 0, s>>>(xh, yh, part, D, chunk);
-            } else {
-                softmax_partial_kernel<1, 1><<<g, dim3(256), 0, s>>>(xh, part, D, chunk);
-                softmax_finish_kernel<1><<<g, dim3(256), 0, s>>>(xh, yh, part, D, chunk);
-            }
-            break;
-        }
+    if (p == Plan::kRow) {
+        const int64_t want = ceil_div(D, vec ? 8 : 1);
+        const int threads = static_cast<int>(ceil_div(want < 1024 ? want : 1024, kWave) * kWave);
+        if (vec)
+            softmax_row_kernel<8><<<dim3(static_cast<unsigned>(N)), dim3(threads), 0, s>>>(xh, yh, D);
+        else
+            softmax_row_kernel<1><<<dim3(static_cast<unsigned>(N)), dim3(threads), 0, s>>>(xh, yh, D);
+        return launch_status();
+    }
+    if (onepass) {
+        const int64_t sp1 = ceil_div(D, kOnePassChunk);
+        softmax_onepass_kernel<<<dim3(static_cast<unsigned>(sp1), static_cast<unsigned>(N)),
+                                 dim3(256), 0, s>>>(xh, yh, static_cast<unsigned char*>(ws), D,
+                                                    g_poll_limit.load());
+        return launch_status();
+    }
+    auto* part = reinterpret_cast<float*>(static_cast<unsigned char*>(ws) +
+                                          (layout == Ws::kRecordsThenPairs ? kOnePassRegion : 0));
+    const dim3 g(static_cast<unsigned>(splits), static_cast<unsigned>(N));
+    if (vec) {
+        if (split_tile(N, D) == 4096)
+            softmax_partial_kernel<8, 2><<<g, dim3(256), 0, s>>>(xh, part, D, chunk);
+        else
+            softmax_partial_kernel<8, 1><<<g, dim3(256), 0, s>>>(xh, part, D, chunk);
+        softmax_finish_kernel<8><<<g, dim3(256), 0, s>>>(xh, yh, part, D, chunk);
+    } else {
+        softmax_partial_kernel<1, 1><<<g, dim3(256), 0, s>>>(xh, part, D, chunk);
+        softmax_finish_kernel<1><<<g, dim3(256), 0, s>>>(xh, yh, part, D, chunk);
     }
     return launch_status();
 }
@@ -502,22 +518,31 @@ extern "C" int64_t mi_softmax_workspace_bytes(int64_t N, int64_t D) {
 
 extern "C" int mi_softmax_ws_f16(const void* x, void* y, int64_t N, int64_t D, void* workspace,
                                  int64_t workspace_bytes, void* stream) {
-    return mi::softmax_checked(x, y, N, D, workspace, workspace_bytes, true, stream);
+    return mi::softmax_checked(x, y, N, D, workspace, workspace_bytes,
+                               mi::Ws::kRecordsThenPairs, stream);
 }
 
 extern "C" int mi_softmax_f16(const void* x, void* y, int64_t N, int64_t D, void* stream) {
-    // a fresh pool allocation is not zeroed: the two-pass form, which needs
-    // no state between calls
     const int64_t need = (N > 0 && D > 0) ? mi::twopass_bytes(N, D) : 0;
-    if (need == 0) return mi::softmax_checked(x, y, N, D, nullptr, 0, false, stream);
-    // Few long rows: a stream-ordered workspace from the device's default
-    // pool (concurrent calls on other streams get their own).
+    if (need == 0) return mi::softmax_checked(x, y, N, D, nullptr, 0, mi::Ws::kPairs, stream);
     if (!x || !y) return MI_ERR_INVALID_ARGUMENT;
     const hipStream_t s = mi::as_stream(stream);
+    // Few long rows on the default stream (every caller in the reference
+    // passes 0): one launch, with row records the library holds for stream 0.
+    if (mi::onepass_ok(x, y, N, D)) {
+        void* rec = mi::default_stream_region(mi::kRegionSoftmax, mi::kOnePassRegion, s);
+        if (rec)
+            return mi::softmax_checked(x, y, N, D, rec, mi::kOnePassRegion, mi::Ws::kRecords,
+                                       stream);
+    }
+    // Otherwise two launches with a stream-ordered workspace from the
+    // device's default pool (concurrent calls on other streams get their
+    // own; a fresh pool allocation is not zeroed, which the two-pass form
+    // does not need).
     void* ws = nullptr;
     hipError_t e = hipMallocAsync(&ws, static_cast<size_t>(need), s);
     if (e != hipSuccess) return static_cast<int>(e);
-    const int st = mi::softmax_checked(x, y, N, D, ws, need, false, stream);
+    const int st = mi::softmax_checked(x, y, N, D, ws, need, mi::Ws::kPairs, stream);
     e = hipFreeAsync(ws, s);
     if (st != MI_OK) return st;
     return e == hipSuccess ? MI_OK : static_cast<int>(e);

@@ -353,7 +353,9 @@ def softmax(x, y=None, workspace=None, stream=None):
     """Row softmax of x [N, D].  With `workspace` (a device tensor of at least
     softmax_workspace_bytes(N, D) bytes, zero before its first use and kept
     for softmax calls only) nothing is allocated per call, and out-of-place
-    split rows run in one launch."""
+    split rows run in one launch.  Without it, split rows run in one launch on
+    stream 0 (row records held by the library) and in two launches with a
+    per-call workspace on other streams."""
     _need(x, _f16(), "x")
     if x.dim() != 2:
         raise ValueError("x must be 2-D [N, D]")

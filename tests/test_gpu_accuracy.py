@@ -93,7 +93,12 @@ def test_accuracy_softmax(mk, orc, dev):
     ws = torch.zeros(mk.softmax_workspace_bytes(64, 152064), dtype=torch.uint8, device=dev)
     _margins("softmax [64,152064] one launch",
              to_host(mk.softmax(to_dev(lg, dev), workspace=ws)), ref)
-    _margins("softmax [64,152064] two launches", to_host(mk.softmax(to_dev(lg, dev))), ref)
+    side = torch.cuda.Stream()  # not stream 0: the allocating entry's two-launch form
+    xd = to_dev(lg, dev)
+    side.wait_stream(torch.cuda.current_stream())
+    y2 = mk.softmax(xd, stream=side)
+    torch.cuda.current_stream().wait_stream(side)
+    _margins("softmax [64,152064] two launches", to_host(y2), ref)
     lg = normal_f16(rng, (57344, 512), 0, 4)
     _margins("softmax [57344,512]", to_host(mk.softmax(to_dev(lg, dev))),
              orc.softmax(lg, nthreads=8))

@@ -198,3 +198,30 @@ def test_greedy_argmax_onepass_epoch_past_32_bits(mk, orc, dev):
         assert (got == orc.greedy_argmax(x)).all(), f"call {i}"
     epochs = e64[0:B * rec:rec].cpu().numpy()
     assert (epochs == start + 5).all(), epochs
+
+
+def test_greedy_argmax_allocating_entry_paths(mk, orc, dev):
+    """mi_greedy_argmax_f16 at split shapes: one launch on stream 0 with the
+    library's row records (fresh logits each call, a forced fallback in the
+    middle), two launches on another stream."""
+    _case("argmax allocating entry: stream 0 one launch, side stream two launches")
+    import torch
+    rng = np.random.default_rng(62)
+    assert torch.cuda.current_stream().cuda_stream == 0
+    for i, (B, V) in enumerate([(64, 152064), (8, 40000), (64, 152064), (3, 65536)]):
+        x = normal_f16(rng, (B, V), 0, 4)
+        prev = mk.greedy_argmax_test_poll_limit(0) if i == 2 else None
+        try:
+            got = to_host(mk.greedy_argmax(to_dev(x, dev)))
+        finally:
+            if prev is not None:
+                mk.greedy_argmax_test_poll_limit(prev)
+        assert (got == orc.greedy_argmax(x)).all(), f"stream 0, call {i} [{B},{V}]"
+    side = torch.cuda.Stream()
+    for B, V in [(64, 152064), (8, 40000)]:
+        x = normal_f16(rng, (B, V), 0, 4)
+        xd = to_dev(x, dev)
+        side.wait_stream(torch.cuda.current_stream())
+        got = mk.greedy_argmax(xd, stream=side)
+        torch.cuda.current_stream().wait_stream(side)
+        assert (to_host(got) == orc.greedy_argmax(x)).all(), f"side stream [{B},{V}]"

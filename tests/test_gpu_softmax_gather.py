@@ -199,3 +199,31 @@ def test_softmax_onepass_epoch_past_32_bits(mk, orc, dev):
                      what=f"call {i}")
     epochs = e64[0:N * rec:rec].cpu().numpy()
     assert (epochs == start + 5).all(), epochs
+
+
+def test_softmax_allocating_entry_paths(mk, orc, dev):
+    """mi_softmax_f16 at split shapes: on stream 0 (the reference's callers'
+    stream) one launch with row records the library holds -- fresh logits on
+    every call, a forced-fallback call in the middle -- and on another stream
+    two launches with a stream-ordered workspace."""
+    _case("softmax allocating entry: stream 0 one launch, side stream two launches")
+    import torch
+    rng = np.random.default_rng(61)
+    assert torch.cuda.current_stream().cuda_stream == 0
+    for i, (N, D) in enumerate([(64, 152064), (8, 40000), (64, 152064), (3, 65536)]):
+        x = normal_f16(rng, (N, D), 0, 4)
+        prev = mk.softmax_test_poll_limit(0) if i == 2 else None
+        try:
+            y = to_host(mk.softmax(to_dev(x, dev)))
+        finally:
+            if prev is not None:
+                mk.softmax_test_poll_limit(prev)
+        assert_close(y, orc.softmax(x, nthreads=8), what=f"stream 0, call {i} [{N},{D}]")
+    side = torch.cuda.Stream()
+    for N, D in [(64, 152064), (8, 40000)]:
+        x = normal_f16(rng, (N, D), 0, 4)
+        xd = to_dev(x, dev)
+        side.wait_stream(torch.cuda.current_stream())
+        y = mk.softmax(xd, stream=side)
+        torch.cuda.current_stream().wait_stream(side)
+        assert_close(to_host(y), orc.softmax(x, nthreads=8), what=f"side stream [{N},{D}]")
