@@ -5,6 +5,9 @@
 // rejects a launch, so a bad shape or a failed launch cannot pass silently.
 #include <hip/hip_runtime.h>
 
+#include <cstring>
+#include <map>
+#include <mutex>
 #include <stdexcept>
 #include <string>
 
@@ -32,6 +35,70 @@ void hip_check(hipError_t e, const char* what) {
 
 void* sv(hipStream_t s) { return reinterpret_cast<void*>(s); }
 
+// Host positions reach the table kernel through pinned staging buffers the
+// library holds: a ring of kSlots per device, each guarded by an event.  A
+// call copies the caller's positions into a slot on the host, so the
+// caller's buffer is free on return, and the table kernel reads them from the
+// pinned slot directly (no device copy, no host wait); the slot's event,
+// recorded after the kernel, keeps a later call from overwriting it early.
+// The host waits only when a slot's previous kernel is still running.  Slots
+// grow to the largest call seen and are kept until the process ends.
+class PositionStager {
+  public:
+    static PositionStager& for_current_device() {
+        static std::mutex mu;
+        static std::map<int, PositionStager*> stagers;
+        int dev = 0;
+        hip_check(hipGetDevice(&dev), "launch_rope_precompute: hipGetDevice");
+        std::lock_guard<std::mutex> lock(mu);
+        PositionStager*& p = stagers[dev];
+        if (!p) p = new PositionStager();
+        return *p;
+    }
+
+    // Copies n positions into the next free slot and runs `use` with it
+    // (device-readable pinned memory); then records the slot's event on s.
+    template <typename Use>
+    void run(const int64_t* src, int64_t n, hipStream_t s, Use use) {
+        std::lock_guard<std::mutex> lock(mu_);
+        Slot& slot = slots_[next_];
+        next_ = (next_ + 1) % kSlots;
+        if (slot.pending)
+            hip_check(hipEventSynchronize(slot.ev), "launch_rope_precompute: slot wait");
+        slot.pending = false;
+        const size_t bytes = static_cast<size_t>(n) * sizeof(int64_t);
+        if (slot.cap < bytes) {
+            if (slot.host) hip_check(hipHostFree(slot.host), "launch_rope_precompute: hipHostFree");
+            slot.host = nullptr;
+            slot.cap = 0;
+            const size_t cap = bytes < 4096 ? 4096 : bytes;
+            hip_check(hipHostMalloc(reinterpret_cast<void**>(&slot.host), cap,
+                                    hipHostMallocDefault),
+                      "launch_rope_precompute: hipHostMalloc");
+            slot.cap = cap;
+        }
+        if (!slot.ev)
+            hip_check(hipEventCreateWithFlags(&slot.ev, hipEventDisableTiming),
+                      "launch_rope_precompute: hipEventCreate");
+        std::memcpy(slot.host, src, bytes);
+        use(static_cast<const int64_t*>(slot.host));
+        hip_check(hipEventRecord(slot.ev, s), "launch_rope_precompute: hipEventRecord");
+        slot.pending = true;
+    }
+
+  private:
+    static constexpr int kSlots = 4;
+    struct Slot {
+        int64_t* host = nullptr;
+        size_t cap = 0;
+        hipEvent_t ev = nullptr;
+        bool pending = false;
+    };
+    std::mutex mu_;
+    Slot slots_[kSlots];
+    int next_ = 0;
+};
+
 }  // namespace
 
 void launch_rmsnorm(const __half* x, const __half* weight, __half* y, int N, int D, float eps,
@@ -53,26 +120,25 @@ void launch_rope(const __half* x, const __half* cos_t, const __half* sin_t, __ha
 void launch_rope_precompute_batched(const float* inv_freq_h, const int64_t* positions_h,
                                     __half* cos_d, __half* sin_d, int B, int S, int half,
                                     hipStream_t stream) {
-    // The reference takes host positions; they are staged to the device in a
-    // stream-ordered allocation (the table kernel reads device positions, and
-    // inv_freq travels by value in the kernel arguments).
+    // The reference takes host positions (src/kernels/rope_kernel.cu:87-102
+    // copies them with a per-call cudaMalloc and a synchronous copy).  Here
+    // the table kernel reads them from the pinned staging ring: no device
+    // allocation, copy or host wait (inv_freq travels by value in the kernel
+    // arguments).
     const int64_t n = static_cast<int64_t>(B) * S;
     if (n <= 0 || half <= 0) return;
     if (!positions_h) throw std::runtime_error("launch_rope_precompute: null positions");
-    void* pos_d = nullptr;
-    const size_t bytes = static_cast<size_t>(n) * sizeof(int64_t);
-    hip_check(hipMallocAsync(&pos_d, bytes, stream), "launch_rope_precompute: hipMallocAsync");
-    hipError_t e = hipMemcpyAsync(pos_d, positions_h, bytes, hipMemcpyHostToDevice, stream);
-    // the caller's host buffer may be released on return: wait for the copy
-    if (e == hipSuccess) e = hipStreamSynchronize(stream);
-    const int st = e == hipSuccess
-                       ? mi_rope_tables_f16(inv_freq_h, static_cast<const int64_t*>(pos_d), cos_d,
-                                            sin_d, n, half, sv(stream))
-                       : MI_OK;
-    const hipError_t fe = hipFreeAsync(pos_d, stream);
-    hip_check(e, "launch_rope_precompute: positions upload");
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    hip_check(hipStreamIsCapturing(stream, &cap), "launch_rope_precompute: hipStreamIsCapturing");
+    if (cap != hipStreamCaptureStatusNone)
+        throw std::runtime_error(
+            "launch_rope_precompute: host positions cannot be captured in a graph (a replay "
+            "would re-read a reused staging buffer); use launch_rope_qk with device positions");
+    int st = MI_OK;
+    PositionStager::for_current_device().run(positions_h, n, stream, [&](const int64_t* pos) {
+        st = mi_rope_tables_f16(inv_freq_h, pos, cos_d, sin_d, n, half, sv(stream));
+    });
     check(st, "launch_rope_precompute");
-    hip_check(fe, "launch_rope_precompute: hipFreeAsync");
 }
 
 void launch_rope_precompute(const float* inv_freq_h, const int64_t* positions_h, __half* cos_d,

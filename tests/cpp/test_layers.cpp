@@ -9,6 +9,7 @@
 // Links oracle/libmi_oracle.so as the checker.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdio>
 #include <cstring>
@@ -175,6 +176,37 @@ void gpu_checks() {
         EXPECT(bit_equal(q, ref16.data(), "RoPE::forward_qk_inplace"), "rope fused");
         EXPECT(throws([&] { rope.forward(xd, std::vector<int64_t>(S + 1)); }), "bad positions");
         EXPECT(throws([] { mini_infer::RoPE bad(7); }), "odd head_dim");
+    }
+    // --- launch_rope_precompute_batched: host positions through the pinned
+    // staging ring.  Ten calls back to back (more than the ring's slots, so
+    // slots are reused while earlier copies may be in flight), each caller
+    // buffer overwritten as soon as the call returns; every table must match.
+    {
+        const int n = 3000, half = 64, calls = 10;
+        std::vector<float> inv(half);
+        mio_rope_inv_freq(inv.data(), 2 * half, 1e6f);
+        std::vector<Tensor> cs, ss;
+        std::vector<std::vector<int64_t>> used;
+        std::vector<int64_t> host(n);
+        for (int c = 0; c < calls; ++c) {
+            mio_fill_uniform_int64(host.data(), n, 7000 + c, 0, 1 << 20);
+            used.push_back(host);
+            cs.push_back(Tensor::empty({n, half}, DType::FP16, Device::cuda(0)));
+            ss.push_back(Tensor::empty({n, half}, DType::FP16, Device::cuda(0)));
+            mini_infer::kernels::launch_rope_precompute_batched(inv.data(), host.data(),
+                                              static_cast<__half*>(cs.back().data()),
+                                              static_cast<__half*>(ss.back().data()), 1, n, half,
+                                              0);
+            std::fill(host.begin(), host.end(), int64_t{-1});  // the caller reuses its buffer
+        }
+        bool ok = true;
+        for (int c = 0; c < calls; ++c) {
+            std::vector<uint16_t> rc(n * half), rs(n * half);
+            mio_rope_tables(inv.data(), used[c].data(), rc.data(), rs.data(), n, half);
+            ok = bit_equal(cs[c], rc.data(), "launch_rope_precompute (staged) cos") && ok;
+            ok = bit_equal(ss[c], rs.data(), "launch_rope_precompute (staged) sin") && ok;
+        }
+        EXPECT(ok, "rope precompute staging ring");
     }
     // --- fused Q/K RMSNorm + RoPE (src/layers/attention.cpp:754-780) -------
     {
