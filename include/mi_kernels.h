@@ -71,7 +71,8 @@ int mi_rope_neox_f16(const void* x, const void* cos_t, const void* sin_t,
                      void* y, int64_t B, int64_t S, int64_t H, int64_t D,
                      void* stream);
 
-/* cos/sin tables [N, half] for the positions in DEVICE memory:
+/* cos/sin tables [N, half] for positions the device can read (device memory,
+ * or pinned host memory from hipHostMalloc written before the call):
  * cos_t[n, i] = half(cos(float(positions[n]) * inv_freq[i])), likewise sin.
  * inv_freq is a HOST array of `half` floats (<= 256), passed to the kernel by
  * value, so nothing is allocated or copied.  Device part of
