@@ -7,7 +7,9 @@
 // if p < seq_len[b], is copied to block block_table[b, p / BS], slot p % BS
 // of the cache laid out [L, num_blocks, H_kv, BS, D].  Bit-exact copy.  One
 // wave per token moves its H_kv * D halves as 16-byte vectors (H_kv = 4,
-// D = 128: 64 vectors = one per lane); block-table reads are wave-uniform.
+// D = 128: 64 vectors = one per lane).  The source loads are issued first:
+// they depend only on the token, while the destination takes two dependent
+// lookups (start_pos / seq_len, then the block table; wave-uniform).
 // Entries that would leave the cache (block index past max_blocks_per_seq,
 // physical block outside [0, num_blocks)) are skipped, where the reference
 // would write out of bounds.  A K+V form moves both tensors in one launch.
@@ -23,16 +25,21 @@
 // that order is one 64-bit key per element --
 //   [ordered fp16 value : 16 | 255 - bitrev8(i mod 256) : 16 | ~i : 32]
 // -- larger is better, 0 = not eligible, so any reduction order gives the
-// reference's answer.  Few long rows are split into chunks: kernel 1 writes
-// each chunk's best key, kernel 2 reduces a row's keys in one wave.
+// reference's answer.  Few long rows are split into chunks.  With row records
+// (a caller workspace, or on stream 0 a region the library holds) one launch:
+// every chunk publishes its best key to its row's record and chunk 0 combines
+// them.  Otherwise two: kernel 1 writes each chunk's best key, kernel 2
+// reduces a row's keys in one wave.
 #include <atomic>
 
 #include "mi_device.h"
 #include "mi_host.h"
 
+// KV stores: plain non-temporal (1 = write-through "nt sc1"; measured neutral).
 #ifndef MI_WT_KV
 #define MI_WT_KV 0
 #endif
+
 namespace mi {
 namespace {
 

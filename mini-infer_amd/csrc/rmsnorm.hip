@@ -38,9 +38,13 @@
 #define MI_RMS_MAX_THREADS 256
 #endif
 
+// Stores of rms_small_kernel (per-head Q/K norm, in place): write-through
+// ("nt sc1", st8_stream_wt) measured 1.5 points faster; the row kernels keep
+// plain non-temporal stores.
 #ifndef MI_WT_RMSS
 #define MI_WT_RMSS 1
 #endif
+
 namespace mi {
 namespace {
 

@@ -31,12 +31,15 @@
 #include "mi_host.h"
 #include "rope_sincos.h"
 
+// Stores of the in-place RoPE and fused Q/K-norm + RoPE kernels: write-through
+// ("nt sc1", st8_stream_wt) measured 1-3 points faster than plain non-temporal.
 #ifndef MI_WT_ROPE
 #define MI_WT_ROPE 1
 #endif
 #ifndef MI_WT_QKNR
 #define MI_WT_QKNR 1
 #endif
+
 namespace mi {
 namespace {
 

@@ -30,9 +30,11 @@
 #include "mi_device.h"
 #include "mi_host.h"
 
+// Softmax stores: plain non-temporal (1 = write-through "nt sc1"; measured neutral).
 #ifndef MI_WT_SM
 #define MI_WT_SM 0
 #endif
+
 namespace mi {
 namespace {
 
