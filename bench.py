@@ -384,6 +384,43 @@ def cpu_baseline(budget_s=10.0):
     }
 
 
+def cpu_torch_baseline(budget_s=5.0):
+    """The reference's kernel tests check their GPU output against torch on
+    the CPU (tests/verify/verify.py:30-42: fp32 x * rsqrt(mean(x^2) + eps) * w).
+    This times that arithmetic, restated here in torch (verify.py is not run),
+    on the headline workload: the residual add rounded to fp16 as the
+    reference's add kernel does, then the fp32 RMSNorm of the result.  Threads:
+    torch's intra-op pool, capped at 16."""
+    import torch
+    cores = max(1, min(16, os.cpu_count() or 1))
+    torch.set_num_threads(cores)
+    T, D = 8192, 3584
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn((T, D), generator=g).half()
+    r = torch.randn((T, D), generator=g).half()
+    w = (torch.randn(D, generator=g) * 0.1 + 1).half()
+
+    def step():
+        res = (r.float() + x.float()).half()
+        xf, wf = res.float(), w.float()
+        return res, (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + 1e-6) * wf).half()
+
+    step()
+    n, t0 = 0, time.perf_counter()
+    while True:
+        step()
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s:
+            break
+    sec = el / n
+    nbytes = 4 * T * D * 2 + D * 2
+    return {"value": round(nbytes / sec / 1e9, 3), "unit": "GB/s", "threads": cores,
+            "sample": (f"torch {torch.__version__} CPU fp32 residual add + RMSNorm on the full "
+                       f"[8192,3584] workload (the reference tests' torch arithmetic, restated), "
+                       f"{n} passes in {el:.1f} s; {sec * 1e3:.1f} ms/pass")}
+
+
 def cpu_kernel_table(budget_s=1.0):
     """The CPU oracle timed at every config of the kernel table (the
     cpu_baseline leg, per config): the same workload shapes, seeded host
@@ -628,10 +665,13 @@ def main():
             log(f"[bench]   {k['kernel']:<18} {k['config']:<38} {k['us']:>9.2f} us "
                 f"{k['GBps']:>8.1f} GB/s  {100 * k['frac']:5.1f}%{floor}")
 
-    cpu = None
+    cpu = cpu_torch = None
     if not args.no_cpu:
         log("[bench] CPU baseline (oracle on host cores)")
         cpu = cpu_baseline(args.cpu_seconds)
+        cpu_torch = cpu_torch_baseline(min(5.0, args.cpu_seconds))
+        log(f"[bench] CPU oracle {cpu['value']} GB/s, torch CPU {cpu_torch['value']} GB/s "
+            f"({cpu['cores']} threads)")
         if kernels is not None:
             cores, cpu_rows = cpu_kernel_table(args.cpu_seconds_per_config)
             by_key = {(r["kernel"], r["config"]): r for r in cpu_rows}
@@ -678,6 +718,7 @@ def main():
             "traffic": traffic,
         },
         "cpu_baseline": cpu,
+        "cpu_torch": cpu_torch,
         "timing": ("eager launches; HIP events on the launch stream" if EAGER else
                    "HIP graph replay of back-to-back launches; HIP events on the replay stream"),
         "copy_calibration_GBps": round(copy_gbps, 1),
