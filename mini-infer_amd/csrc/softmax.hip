@@ -172,6 +172,116 @@ __device__ __forceinline__ void block_merge(float& m, float& s, float* slots) {
     m = M;
 }
 
+// Register-resident rows (16-byte vectors, D <= G * VPT * 8): G lanes per
+// row -- G <= 64: 256 / G rows per workgroup and DPP-only reductions;
+// G = 256 or 1024: one row per workgroup and one LDS exchange per
+// reduction -- with VPT vectors per lane.  x is read once: a packed fp16
+// lane maximum, the row maximum, one exp per element (kept in registers when
+// VPT <= 4, recomputed at the write otherwise), the row sum, then the scaled
+// write.  Lanes past the row hold -inf, whose exp is 0.  No lane returns
+// early, so every group reduction sees all of its lanes.
+template <int G, int VPT>
+__global__ __launch_bounds__(G > 256 ? G : 256) void softmax_reg_kernel(const half_t* x,
+                                                                        half_t* y, int64_t N,
+                                                                        int64_t D) {
+    constexpr int kThreads = G > 256 ? G : 256;
+    constexpr int kRows = kThreads / G;
+    constexpr bool kKeepExp = VPT <= 4;
+    __shared__ float smax[kThreads / kWave], ssum[kThreads / kWave];
+    const int gl = threadIdx.x & (G - 1);
+    const int64_t row = static_cast<int64_t>(blockIdx.x) * kRows + threadIdx.x / G;
+    const bool live = row < N;
+    const int64_t nv = D >> 3;
+    const half_t* xr = x + row * D;
+    h8 a[VPT];
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+        const int64_t v = gl + j * G;
+        a[j] = live && v < nv ? ld8_stream(xr + v * 8) : h8(-__builtin_huge_valf16());
+    }
+    h2 m2 = h2(-__builtin_huge_valf16());
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+#pragma unroll
+        for (int k = 0; k < 8; k += 2) m2 = __builtin_elementwise_max(m2, h2{a[j][k], a[j][k + 1]});
+    }
+    float m = (float)__builtin_elementwise_max(m2.x, m2.y);
+    if constexpr (G <= 64)
+        m = group_max<G>(m);
+    else
+        m = block_max(m, smax);
+    float e[kKeepExp ? VPT : 1][8];
+    float s = 0.0f;
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const float t = fast_exp((float)a[j][k] - m);
+            if constexpr (kKeepExp) e[j][k] = t;
+            s += t;
+        }
+    }
+    if constexpr (G <= 64)
+        s = group_sum<G>(s);
+    else
+        s = block_sum(s, ssum);
+    const float inv = 1.0f / s;
+    half_t* yr = y + row * D;
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+        const int64_t v = gl + j * G;
+        if (live && v < nv) {
+            h8 o;
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const float t = kKeepExp ? e[kKeepExp ? j : 0][k] : fast_exp((float)a[j][k] - m);
+                o[k] = to_half(t * inv);
+            }
+            st8_out<MI_WT_SM>(yr + v * 8, o);
+        }
+    }
+}
+
+// Launch shape for softmax_reg_kernel: the fewest lanes per row (8, 16, 32,
+// 64, then 256 or 1024 as whole workgroups) that hold the row in at most
+// kRegVpt vectors each, else 1024 lanes with up to 8.  Returns false when
+// the row needs more than 1024 x 8 vectors.
+#ifndef MI_SOFTMAX_REG_VPT
+#define MI_SOFTMAX_REG_VPT 4
+#endif
+constexpr int kRegVpt = MI_SOFTMAX_REG_VPT;
+bool reg_shape(int64_t nv, int& G, int& VPT) {
+    static const int kG[] = {8, 16, 32, 64, 256, 1024};
+    G = 0;
+    for (int g : kG)
+        if (nv <= static_cast<int64_t>(kRegVpt) * g) {
+            G = g;
+            break;
+        }
+    if (G == 0) {
+        if (nv > 1024 * 8) return false;
+        G = 1024;
+    }
+    const int64_t v = ceil_div(nv, G);
+    VPT = v <= 1 ? 1 : v <= 2 ? 2 : v <= 4 ? 4 : 8;
+    if (G < 64 && VPT > 4) return false;  // not instantiated (kRegVpt > 4 only)
+    return true;
+}
+
+template <int G>
+void launch_reg(const half_t* x, half_t* y, int64_t N, int64_t D, int VPT, hipStream_t s) {
+    constexpr int kThreads = G > 256 ? G : 256;
+    const dim3 g(static_cast<unsigned>(ceil_div(N, kThreads / G))), b(kThreads);
+    if (VPT == 1)
+        softmax_reg_kernel<G, 1><<<g, b, 0, s>>>(x, y, N, D);
+    else if (VPT == 2)
+        softmax_reg_kernel<G, 2><<<g, b, 0, s>>>(x, y, N, D);
+    else if (VPT == 4 || G < 64)  // reg_shape gives fewer than 64 lanes at most 4 vectors
+        softmax_reg_kernel<G, 4><<<g, b, 0, s>>>(x, y, N, D);
+    else if constexpr (G >= 64)
+        softmax_reg_kernel<G, 8><<<g, b, 0, s>>>(x, y, N, D);
+}
+
 template <int VEC>
 __global__ __launch_bounds__(1024) void softmax_row_kernel(const half_t* x, half_t* y, int64_t D) {
     __shared__ float slots[1024 / kWave];
@@ -430,6 +540,9 @@ int64_t workspace_bytes(int64_t N, int64_t D) {
 #ifndef MI_SOFTMAX_ONEPASS
 #define MI_SOFTMAX_ONEPASS 1
 #endif
+#ifndef MI_SOFTMAX_REG
+#define MI_SOFTMAX_REG 1
+#endif
 
 // What a workspace handed to softmax_checked holds.
 enum class Ws {
@@ -479,6 +592,19 @@ int softmax_checked(const void* x, void* y, int64_t N, int64_t D, void* ws, int6
     const hipStream_t s = as_stream(stream);
     const bool vec = D % 8 == 0 && aligned16(x) && aligned16(y);
     if (p == Plan::kRow) {
+        int G = 0, VPT = 0;
+        if (MI_SOFTMAX_REG && vec && reg_shape(D / 8, G, VPT) &&
+            ceil_div(N, (G > 256 ? G : 256) / G) <= kMaxGridX) {
+            switch (G) {
+                case 8: launch_reg<8>(xh, yh, N, D, VPT, s); break;
+                case 16: launch_reg<16>(xh, yh, N, D, VPT, s); break;
+                case 32: launch_reg<32>(xh, yh, N, D, VPT, s); break;
+                case 64: launch_reg<64>(xh, yh, N, D, VPT, s); break;
+                case 256: launch_reg<256>(xh, yh, N, D, VPT, s); break;
+                default: launch_reg<1024>(xh, yh, N, D, VPT, s); break;
+            }
+            return launch_status();
+        }
         const int64_t want = ceil_div(D, vec ? 8 : 1);
         const int threads = static_cast<int>(ceil_div(want < 1024 ? want : 1024, kWave) * kWave);
         if (vec)
