@@ -585,9 +585,9 @@ int launch_rope(const half_t* q_in, half_t* q_out, int64_t Hq, const half_t* k_i
 #define MI_QKN_PIPE 1
 #endif
 
-// Pipelined launch: P register slots per lane (the fewest that hold one
-// token's units), G tokens per group (as many as the slots and the table
-// hold), and a grid of the resident capacity, so every workgroup stays
+// Pipelined launch: P register slots per lane (launched with P = 1, a
+// token's units in one slot), G tokens per group (as many as the slots and
+// the table hold), and a grid of the resident capacity, so every workgroup stays
 // resident and walks ngroups / grid groups.  Measured at T = 6064, Qwen2.5
 // heads: 63% of HBM peak against 56% for the one-round kernel; two tokens
 // per step (P = 2) and a grid of twice the capacity both measured lower.
@@ -614,19 +614,14 @@ template <int CPH>
 int launch_qk_norm_rope_t(half_t* q, int hq, half_t* k, int hk, const half_t* wq,
                           const half_t* wk, const int64_t* positions, int64_t T, float eps,
                           float w_bias, const InvFreq& inv, hipStream_t s) {
-    if (MI_QKN_PIPE) {
-        const int upt = (hq + hk) * CPH;
-        if (upt <= 256)
-            return launch_qk_norm_rope_pipe<CPH, 1>(q, hq, k, hk, wq, wk, positions, T, eps,
-                                                    w_bias, inv, s);
-        if (upt <= 512)
-            return launch_qk_norm_rope_pipe<CPH, 2>(q, hq, k, hk, wq, wk, positions, T, eps,
-                                                    w_bias, inv, s);
-        if (upt <= 1024)
-            return launch_qk_norm_rope_pipe<CPH, 4>(q, hq, k, hk, wq, wk, positions, T, eps,
-                                                    w_bias, inv, s);
-        // more than 1024 units per token: the one-round kernel below
-    }
+    // The pipelined kernel when a token's units fit one register slot per
+    // lane (<= 256 units).  With 2 or 4 slots (P = 2, 4) its register use
+    // (128 / 194 VGPRs) cost more occupancy than the pipelining gained: the
+    // one-round kernel below measured 2-11 points faster for 32|8, 32|32,
+    // 16|8 x 256 and 64|8 heads, so only P = 1 is launched.
+    if (MI_QKN_PIPE && (hq + hk) * CPH <= 256)
+        return launch_qk_norm_rope_pipe<CPH, 1>(q, hq, k, hk, wq, wk, positions, T, eps, w_bias,
+                                                inv, s);
     const int tpw = pick_tokens_per_wg(T, qk_norm_rope_kernel<CPH, 1>, qk_norm_rope_kernel<CPH, 2>,
                                        qk_norm_rope_kernel<CPH, 4>, qk_norm_rope_kernel<CPH, 8>);
     const int64_t grid = ceil_div(T, tpw);

@@ -196,10 +196,11 @@ def _assert_norm_rope_close(ours, ref, n16, what):
 def test_qk_norm_rope(mk, orc, dev, T, Hq, Hkv, hd):
     """Fused Q/K RMSNorm + RoPE == the reference's norm-then-rope composition
     (src/layers/attention.cpp:754-780), within rtol = atol = 1e-3.  Shapes
-    cover both launch forms: token groups of 1 to 32 tokens with a ragged
-    last group, groups walked several times per workgroup (T = 20000, 6064),
-    2 and 4 register slots per lane (48 and 96 heads of 128), and the
-    one-round kernel (144 heads of 128: more than 1024 lanes per token)."""
+    cover both launch forms: the pipelined kernel (at most 256 lanes per
+    token) with token groups of 1 to 32 tokens, a ragged last group and
+    groups walked several times per workgroup (T = 20000, 6064); and the
+    one-round kernel at 48, 96 and 144 heads of 128 (384 to 1152 lanes per
+    token, one to five units per lane)."""
     _case(f"qk_norm_rope T={T} Hq={Hq} Hkv={Hkv} hd={hd}")
     rng = np.random.default_rng(T * 7 + hd)
     q = normal_f16(rng, (T, Hq, hd))
