@@ -98,7 +98,7 @@ __device__ __forceinline__ void set_elem(typename HVec<VEC>::T& v, int k, float 
 }
 
 // Tokens per 256-lane workgroup, chosen per launch from {1, 2, 4, 8} (see
-// pick_tokens_per_wg); each lane issues the loads of TPW units (one per
+// fill_tokens_per_wg); each lane issues the loads of TPW units (one per
 // token for a 256-unit token, the Qwen2.5 case) before the table work.
 
 // TPW tokens per 256-lane workgroup.  Sources q_in/k_in, destinations
@@ -506,14 +506,25 @@ bool load_inv_freq(const float* host, int64_t half, InvFreq& out) {
     return true;
 }
 
-// Tokens per workgroup: the candidate whose grid leaves the least idle tail
-// in the GPU's last round of resident workgroups, with a small charge per
-// extra round (each round repeats the load-latency / table / barrier ramp).
-// With residencies of 2048/1792/1280/1024 workgroups for 1/2/4/8 tokens this
-// picks 1 token at T = 4096 (two full rounds) and at T = 6064 (three rounds,
-// 99% full).  The charge matters when residency is lower: with 1280 at
-// 4 tokens, T = 6064 in 1516 workgroups leaves a second round 18% full, and
-// taking 8 tokens in one round instead measured 58% -> 68% of HBM peak.
+// Tokens per 256-lane workgroup for the one-round kernels: the fewest (1, 2,
+// 4 or 8) whose units give every lane at least one, when a token has fewer
+// than 256.  Measured across head layouts (28|4, 32|8, 32|32 x 128, 16|8 x
+// 256, 32|4 and 8|1 x 64), this matched or beat choosing by the fill of the
+// last round of resident workgroups (pick_tokens_per_wg): one token per
+// workgroup whenever a token has 256 units or more.
+inline int fill_tokens_per_wg(int units_per_token) {
+    int tpw = 1;
+    while (tpw < 8 && tpw * units_per_token < 256) tpw *= 2;
+    return tpw;
+}
+
+// Tokens per workgroup for the one-round fused Q/K-norm + RoPE kernel: the
+// candidate whose grid leaves the least idle tail in the GPU's last round of
+// resident workgroups, with a small charge per extra round (each round
+// repeats the load-latency / table / barrier ramp).  (The RoPE kernel used
+// this rule until the lane-fill rule above measured as good or better there;
+// under the library sincosf's residencies it once took T = 6064 from 58% to
+// 68% by avoiding a second round 18% full.)
 template <typename K1, typename K2, typename K4, typename K8>
 int pick_tokens_per_wg(int64_t T, K1 k1, K2 k2, K4 k4, K8 k8) {
     const void* ks[4] = {reinterpret_cast<const void*>(k1), reinterpret_cast<const void*>(k2),
@@ -536,10 +547,7 @@ template <int VEC, bool FROM_POS>
 int launch_rope_t(const half_t* q_in, half_t* q_out, int hq, const half_t* k_in, half_t* k_out,
                   int hk, const int64_t* positions, const half_t* cos_t, const half_t* sin_t,
                   int64_t T, int d, const InvFreq& inv, hipStream_t s) {
-    const int tpw = pick_tokens_per_wg(T, rope_kernel<VEC, FROM_POS, 1>,
-                                       rope_kernel<VEC, FROM_POS, 2>,
-                                       rope_kernel<VEC, FROM_POS, 4>,
-                                       rope_kernel<VEC, FROM_POS, 8>);
+    const int tpw = fill_tokens_per_wg((hq + hk) * (d / 2 / VEC));
     const int64_t grid = ceil_div(T, tpw);
     if (grid > kMaxGridX) return MI_ERR_UNSUPPORTED;
     const dim3 g(static_cast<unsigned>(grid)), b(256);
@@ -622,6 +630,7 @@ int launch_qk_norm_rope_t(half_t* q, int hq, half_t* k, int hk, const half_t* wq
     if (MI_QKN_PIPE && (hq + hk) * CPH <= 256)
         return launch_qk_norm_rope_pipe<CPH, 1>(q, hq, k, hk, wq, wk, positions, T, eps, w_bias,
                                                 inv, s);
+    // (the lane-fill rule of the RoPE kernel measured 2-3 points lower here)
     const int tpw = pick_tokens_per_wg(T, qk_norm_rope_kernel<CPH, 1>, qk_norm_rope_kernel<CPH, 2>,
                                        qk_norm_rope_kernel<CPH, 4>, qk_norm_rope_kernel<CPH, 8>);
     const int64_t grid = ceil_div(T, tpw);
