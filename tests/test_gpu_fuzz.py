@@ -13,13 +13,15 @@ The bar is the same as everywhere: bit-exact for copies, RoPE and argmax;
 rtol = atol = 1e-3 for the fp32-math outputs (norm-then-rope with its
 documented one-ulp intermediate allowance).
 """
+import os
+
 import numpy as np
 import pytest
 
 from helpers import assert_bits_equal, assert_close, normal_f16, to_host
 
 pytestmark = pytest.mark.gpu
-CASES = 32
+CASES = int(os.environ.get("MI_FUZZ_CASES", "32"))  # a deeper run: MI_FUZZ_CASES=256
 
 
 def _case(msg):
@@ -136,19 +138,25 @@ def test_fuzz_softmax(mk, orc, dev, seed):
     split = bool(rng.integers(0, 2))
     N = int(rng.integers(1, 64)) if split else int(rng.integers(1, 700))
     D = (int(rng.integers(8192, 300000)) if split
-         else int(rng.choice([int(rng.integers(1, 64)), int(rng.integers(64, 8192))])))
+         else int(rng.choice([int(rng.integers(1, 64)), int(rng.integers(64, 8192)),
+                              8 * int(rng.integers(1, 1024))])))
+    if not split and rng.integers(0, 4) == 0:  # many rows of up to 65536 (register rows)
+        N, D = int(rng.integers(512, 1200)), 8 * int(rng.integers(1, 8193))
     mis = bool(rng.integers(0, 4) == 0)
-    _case(f"softmax seed={seed} N={N} D={D} misaligned={mis}")
+    inplace = bool(rng.integers(0, 4) == 0)
+    _case(f"softmax seed={seed} N={N} D={D} misaligned={mis} inplace={inplace}")
     x = normal_f16(rng, (N, D), 0.0, 4.0)
-    y = mk.softmax(_dev_array(x, dev, mis))
-    assert_close(to_host(y), orc.softmax(x), what="softmax")
+    xd = _dev_array(x, dev, mis)
+    y = mk.softmax(xd, y=xd if inplace else None)
+    assert_close(to_host(y), orc.softmax(x, nthreads=8), what="softmax")
 
 
 @pytest.mark.parametrize("seed", range(CASES))
 def test_fuzz_gather(mk, orc, dev, seed):
     rng = np.random.default_rng(7000 + seed)
     T = int(rng.integers(1, 500))
-    H = int(rng.choice([int(rng.integers(1, 300)), 8 * int(rng.integers(1, 600))]))
+    H = int(rng.choice([int(rng.integers(1, 300)), 8 * int(rng.integers(1, 600)),
+                        8 * int(rng.integers(600, 2100))]))  # up to 4 waves per row
     V = int(rng.integers(1, 3000))
     mis = bool(rng.integers(0, 4) == 0)
     _case(f"gather seed={seed} T={T} H={H} V={V} misaligned={mis}")
