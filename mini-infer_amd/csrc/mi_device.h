@@ -166,6 +166,15 @@ __device__ __forceinline__ float block_max(float v, float* slots) {
     return t;
 }
 
+// floor(u / d) for integers 0 <= u < 2^22 and d >= 1, given inv_d = 1.0f / d
+// (correctly rounded): (u + 0.5) * inv_d lies within (u + 0.5) * 2^-23 of
+// (u + 0.5) / d, which is less than the 0.5 / d separating that value from
+// the integers on either side.  A few instructions instead of a runtime
+// integer division.
+__device__ __forceinline__ int small_div(int u, float inv_d) {
+    return static_cast<int>((static_cast<float>(u) + 0.5f) * inv_d);
+}
+
 // exp(x) through the hardware base-2 exponential (v_exp_f32, ~1 ulp).
 __device__ __forceinline__ float fast_exp(float x) {
     return __builtin_amdgcn_exp2f(x * 1.4426950408889634f);

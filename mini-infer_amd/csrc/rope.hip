@@ -105,8 +105,11 @@ __device__ __forceinline__ void set_elem(typename HVec<VEC>::T& v, int k, float 
 // q_out/k_out (may equal the sources).  FROM_POS: cos/sin from positions +
 // inv_freq, else from fp16 tables [T, half].  A unit is one (token, head,
 // VEC-element slice) pair: x[i..i+VEC) and x[h+i..h+i+VEC).
+// (8 tokens: held to 128 VGPRs, 4 waves per SIMD; the compiler otherwise
+// settles at 130 and the residency drops to 3)
 template <int VEC, bool FROM_POS, int TPW>
-__global__ __launch_bounds__(256) void rope_kernel(const half_t* q_in, half_t* q_out, int Hq,
+__global__ __launch_bounds__(256)
+__attribute__((amdgpu_waves_per_eu(TPW == 8 ? 4 : 1))) void rope_kernel(const half_t* q_in, half_t* q_out, int Hq,
                                                    const half_t* k_in, half_t* k_out, int Hkv,
                                                    const int64_t* __restrict__ positions,
                                                    const half_t* __restrict__ cos_t,
@@ -121,10 +124,13 @@ __global__ __launch_bounds__(256) void rope_kernel(const half_t* q_in, half_t* q
     const int upt = (Hq + Hkv) * cph;          // units per token
     const int units = ntok * upt;
 
+    const float inv_upt = 1.0f / static_cast<float>(upt);
+    const float inv_cph = 1.0f / static_cast<float>(cph);
+    // units < 2^22 (checked at launch), so small_div is exact
     auto locate = [&](int u, const half_t*& src, half_t*& dst) {
-        const int t = u / upt;
+        const int t = small_div(u, inv_upt);
         const int rem = u - t * upt;
-        const int h = rem / cph;
+        const int h = small_div(rem, inv_cph);
         const int c = rem - h * cph;
         const int64_t tok = tok0 + t;
         if (h < Hq) {
@@ -245,9 +251,11 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(half_t* q, int Hq, ha
     else if (threadIdx.x < HD / 4 && Hkv > 0)
         wl[1][threadIdx.x - HD / 8] = ld8(wk + (threadIdx.x - HD / 8) * 8);
 
-    // unit u -> (token, head); returns the head's base pointer
+    // unit u -> (token, head); returns the head's base pointer (units < 2^22,
+    // checked at launch, so small_div is exact)
+    const float inv_upt = 1.0f / static_cast<float>(upt);
     auto head_ptr = [&](int u, bool& is_k, int& t) -> half_t* {
-        t = u / upt;
+        t = small_div(u, inv_upt);
         const int h = (u - t * upt) / CPH;
         const int64_t tok = tok0 + t;
         is_k = h >= Hq;
@@ -550,6 +558,8 @@ int launch_rope_t(const half_t* q_in, half_t* q_out, int hq, const half_t* k_in,
     const int tpw = fill_tokens_per_wg((hq + hk) * (d / 2 / VEC));
     const int64_t grid = ceil_div(T, tpw);
     if (grid > kMaxGridX) return MI_ERR_UNSUPPORTED;
+    if (static_cast<int64_t>(tpw) * (hq + hk) * (d / 2 / VEC) >= (int64_t{1} << 22))
+        return MI_ERR_UNSUPPORTED;  // units per workgroup: small_div's exact range
     const dim3 g(static_cast<unsigned>(grid)), b(256);
     switch (tpw) {
 #define MI_ROPE_CASE(P)                                                                        \
@@ -635,6 +645,8 @@ int launch_qk_norm_rope_t(half_t* q, int hq, half_t* k, int hk, const half_t* wq
                                        qk_norm_rope_kernel<CPH, 4>, qk_norm_rope_kernel<CPH, 8>);
     const int64_t grid = ceil_div(T, tpw);
     if (grid > kMaxGridX) return MI_ERR_UNSUPPORTED;
+    if (static_cast<int64_t>(tpw) * (hq + hk) * CPH >= (int64_t{1} << 22))
+        return MI_ERR_UNSUPPORTED;  // units per workgroup: small_div's exact range
     const dim3 g(static_cast<unsigned>(grid)), b(256);
     switch (tpw) {
 #define MI_QKN_CASE(P)                                                                          \
