@@ -7,7 +7,9 @@
 // if p < seq_len[b], is copied to block block_table[b, p / BS], slot p % BS
 // of the cache laid out [L, num_blocks, H_kv, BS, D].  Bit-exact copy.  One
 // wave per token moves its H_kv * D halves as 16-byte vectors (H_kv = 4,
-// D = 128: 64 vectors = one per lane).  The source loads are issued first:
+// D = 128: 64 vectors = one per lane; a token of 32 or fewer vectors shares
+// its wave with others, e.g. 4 tokens per wave for one KV head of 128).  The
+// source loads are issued first:
 // they depend only on the token, while the destination takes two dependent
 // lookups (start_pos / seq_len, then the block table; wave-uniform).
 // Entries that would leave the cache (block index past max_blocks_per_seq,
@@ -46,7 +48,6 @@ namespace {
 // ---------------------------------------------------------------------------
 // Paged KV scatter
 // ---------------------------------------------------------------------------
-constexpr int kKvTokensPerWg = 4;  // one wave per token
 
 struct KvGeometry {
     int64_t B, S;
@@ -69,7 +70,10 @@ struct HVecKv<1> {
     __device__ static void store(half_t* p, T v) { *p = v; }
 };
 
-template <int VEC>
+// L lanes per token (64, or 32 / 16 / 8 when a token has that few vectors,
+// so a wave moves 2 / 4 / 8 tokens: one KV head of 128 is 16 vectors),
+// 256 / L tokens per workgroup.
+template <int VEC, int L>
 __global__ __launch_bounds__(256) void kv_scatter_kernel(const half_t* __restrict__ src0,
                                                          half_t* __restrict__ cache0,
                                                          const half_t* __restrict__ src1,
@@ -78,10 +82,11 @@ __global__ __launch_bounds__(256) void kv_scatter_kernel(const half_t* __restric
                                                          const int* __restrict__ seq_len,
                                                          const int* __restrict__ start_pos,
                                                          KvGeometry g) {
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-    const int lane = threadIdx.x & (kWave - 1);
-    const int64_t tok = static_cast<int64_t>(blockIdx.x) * kKvTokensPerWg + wave;
-    if (tok >= g.B * g.S) return;  // wave-uniform; no cross-lane work follows
+    int tl = threadIdx.x / L;  // token within the workgroup
+    if constexpr (L == kWave) tl = __builtin_amdgcn_readfirstlane(tl);  // wave-uniform
+    const int lane = threadIdx.x & (L - 1);
+    const int64_t tok = static_cast<int64_t>(blockIdx.x) * (256 / L) + tl;
+    if (tok >= g.B * g.S) return;  // no cross-lane work follows
     const int64_t row = g.H_kv * g.D;               // halves per token
     const int64_t nv = row / VEC;                   // vectors per token
     const half_t* s0 = src0 + tok * row;
@@ -109,8 +114,10 @@ __global__ __launch_bounds__(256) void kv_scatter_kernel(const half_t* __restric
     const int64_t head_stride = g.block_size * g.D; // halves between heads in a block
     const int64_t dst_base =
         ((g.layer * g.num_blocks + phys) * g.H_kv) * head_stride + slot * g.D;
-    for (int64_t v = lane; v < nv; v += kWave) {
-        const int64_t h = v / per_head;
+    const float inv_per_head = 1.0f / static_cast<float>(per_head);
+    for (int64_t v = lane; v < nv; v += L) {
+        // nv < 2^22 (checked at launch): small_div is exact
+        const int64_t h = small_div(static_cast<int>(v), inv_per_head);
         const int64_t d = (v - h * per_head) * VEC;
         const int64_t dst = dst_base + h * head_stride + d;
         if (v != lane) {
@@ -134,8 +141,13 @@ int kv_scatter(const void* src0, void* cache0, const void* src1, void* cache1,
     if (!src0 || !cache0 || !block_table || !seq_len || !start_pos) return MI_ERR_INVALID_ARGUMENT;
     if ((src1 == nullptr) != (cache1 == nullptr)) return MI_ERR_INVALID_ARGUMENT;
     const int64_t tokens = B * S;
-    const int64_t grid = ceil_div(tokens, kKvTokensPerWg);
+    const bool vec = D % 8 == 0 && aligned16(src0) && aligned16(cache0) &&
+                     (!src1 || (aligned16(src1) && aligned16(cache1)));
+    const int64_t nv = H_kv * D / (vec ? 8 : 1);  // vectors per token
+    const int L = nv > 32 ? 64 : nv > 16 ? 32 : nv > 8 ? 16 : 8;
+    const int64_t grid = ceil_div(tokens, 256 / L);
     if (grid > kMaxGridX) return MI_ERR_UNSUPPORTED;
+    if (H_kv * D >= (int64_t{1} << 22)) return MI_ERR_UNSUPPORTED;  // elements per token
     const int64_t src_bytes = tokens * H_kv * D * 2;
     const int64_t cache_bytes = (layer + 1) * num_blocks * H_kv * block_size * D * 2;
     if (overlaps(src0, src_bytes, cache0, cache_bytes)) return MI_ERR_ALIASING;
@@ -143,19 +155,26 @@ int kv_scatter(const void* src0, void* cache0, const void* src1, void* cache1,
                  overlaps(cache0, cache_bytes, cache1, cache_bytes)))
         return MI_ERR_ALIASING;
     const KvGeometry g{B, S, layer, num_blocks, H_kv, D, block_size, max_blocks_per_seq};
-    const bool vec = D % 8 == 0 && aligned16(src0) && aligned16(cache0) &&
-                     (!src1 || (aligned16(src1) && aligned16(cache1)));
     const hipStream_t st = as_stream(stream);
     const auto* s0 = static_cast<const half_t*>(src0);
     const auto* s1 = static_cast<const half_t*>(src1);
     auto* c0 = static_cast<half_t*>(cache0);
     auto* c1 = static_cast<half_t*>(cache1);
-    if (vec)
-        kv_scatter_kernel<8><<<dim3(static_cast<unsigned>(grid)), dim3(256), 0, st>>>(
-            s0, c0, s1, c1, block_table, seq_len, start_pos, g);
-    else
-        kv_scatter_kernel<1><<<dim3(static_cast<unsigned>(grid)), dim3(256), 0, st>>>(
-            s0, c0, s1, c1, block_table, seq_len, start_pos, g);
+    const dim3 gr(static_cast<unsigned>(grid)), b(256);
+#define MI_KV_CASE(V, LL)                                                                      \
+    kv_scatter_kernel<V, LL><<<gr, b, 0, st>>>(s0, c0, s1, c1, block_table, seq_len, start_pos, g)
+    if (vec) {
+        if (L == 64) MI_KV_CASE(8, 64);
+        else if (L == 32) MI_KV_CASE(8, 32);
+        else if (L == 16) MI_KV_CASE(8, 16);
+        else MI_KV_CASE(8, 8);
+    } else {
+        if (L == 64) MI_KV_CASE(1, 64);
+        else if (L == 32) MI_KV_CASE(1, 32);
+        else if (L == 16) MI_KV_CASE(1, 16);
+        else MI_KV_CASE(1, 8);
+    }
+#undef MI_KV_CASE
     return launch_status();
 }
 
