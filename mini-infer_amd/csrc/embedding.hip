@@ -2,12 +2,11 @@
 //
 // out[t, :] = table[ids[t], :] (src/kernels/model_utils_kernel.cu:45-56).
 //
-// Design (HBM-bound: 2 x H x 2 bytes + 8 bytes of id per token): one wave per
-// token row (two or four for rows of more than 512 vectors), four rows per
-// 256-lane workgroup.  The id is read once per wave into a scalar register;
-// each lane then moves 16-byte vectors, issuing up to kBatch loads before the
-// matching stores, so a whole row (7 KiB at H = 3584, 16 KiB at H = 8192 over
-// two waves) is in flight at once.  An id outside [0, vocab) (when vocab > 0) produces a zero
+// Design (HBM-bound: 2 x H x 2 bytes + 8 bytes of id per token): 16 to 256
+// lanes per token row -- the fewest that hold the row at kBatch 16-byte
+// vectors per lane -- so one wave at H = 3584 or 4096, two at H = 8192, and
+// two rows per wave at H = 2048.  Each lane issues its loads before the
+// matching stores, so a whole row is in flight at once.  An id outside [0, vocab) (when vocab > 0) produces a zero
 // row rather than an out-of-bounds read.
 #include "mi_device.h"
 #include "mi_host.h"
@@ -17,19 +16,20 @@ namespace {
 
 constexpr int kBatch = 8;
 
-// W waves per token row, 4 / W rows per 256-lane workgroup: a row of up to
-// W * 64 * kBatch vectors is in flight at once (one batch; a second batch
-// would wait for the first one's stores to drain).
-template <int VEC, int W>
+// kLanes lanes per token row (16 .. 256), 256 / kLanes rows per workgroup:
+// a row of up to kLanes * kBatch vectors is in flight at once (one batch; a
+// second batch would wait for the first one's stores to drain), and narrow
+// rows share a wave instead of leaving lanes idle.
+template <int VEC, int kLanes>
 __global__ __launch_bounds__(256) void gather_kernel(const int64_t* __restrict__ ids,
                                                      const half_t* __restrict__ table,
                                                      half_t* __restrict__ out, int64_t T,
                                                      int64_t H, int64_t vocab) {
-    constexpr int kLanes = W * kWave;  // lanes per row
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    int r = threadIdx.x / kLanes;  // row within the workgroup
+    if constexpr (kLanes >= kWave) r = __builtin_amdgcn_readfirstlane(r);  // wave-uniform
     const int lane = threadIdx.x & (kLanes - 1);
-    const int64_t t = static_cast<int64_t>(blockIdx.x) * (4 / W) + wave / W;
-    if (t >= T) return;  // wave-uniform exit; no cross-lane work follows
+    const int64_t t = static_cast<int64_t>(blockIdx.x) * (256 / kLanes) + r;
+    if (t >= T) return;  // no cross-lane work follows
     const int64_t id = ids[t];
     const bool valid = id >= 0 && (vocab <= 0 || id < vocab);
     const half_t* src = table + (valid ? id : 0) * H;
@@ -64,24 +64,25 @@ __global__ __launch_bounds__(256) void gather_kernel(const int64_t* __restrict__
     }
 }
 
-// Waves per row: the fewest (1, 2, 4) that hold the row in one batch.
-inline int gather_waves(int64_t nv) {
-    return nv <= kWave * kBatch ? 1 : nv <= 2 * kWave * kBatch ? 2 : 4;
+// Lanes per row: the fewest power of two (16 .. 256) that hold the row in
+// one batch of kBatch vectors per lane.
+inline int gather_lanes(int64_t nv) {
+    int l = 16;
+    while (l < 256 && static_cast<int64_t>(l) * kBatch < nv) l *= 2;
+    return l;
 }
 
 template <int VEC>
 void launch_gather(const int64_t* ids, const half_t* tb, half_t* o, int64_t T, int64_t H,
-                   int64_t vocab, int W, hipStream_t s) {
-    const dim3 b(256);
-    if (W == 1)
-        gather_kernel<VEC, 1><<<dim3(static_cast<unsigned>(ceil_div(T, 4))), b, 0, s>>>(
-            ids, tb, o, T, H, vocab);
-    else if (W == 2)
-        gather_kernel<VEC, 2><<<dim3(static_cast<unsigned>(ceil_div(T, 2))), b, 0, s>>>(
-            ids, tb, o, T, H, vocab);
-    else
-        gather_kernel<VEC, 4><<<dim3(static_cast<unsigned>(T)), b, 0, s>>>(ids, tb, o, T, H,
-                                                                          vocab);
+                   int64_t vocab, int L, hipStream_t s) {
+    const dim3 g(static_cast<unsigned>(ceil_div(T, 256 / L))), b(256);
+    switch (L) {
+        case 16: gather_kernel<VEC, 16><<<g, b, 0, s>>>(ids, tb, o, T, H, vocab); break;
+        case 32: gather_kernel<VEC, 32><<<g, b, 0, s>>>(ids, tb, o, T, H, vocab); break;
+        case 64: gather_kernel<VEC, 64><<<g, b, 0, s>>>(ids, tb, o, T, H, vocab); break;
+        case 128: gather_kernel<VEC, 128><<<g, b, 0, s>>>(ids, tb, o, T, H, vocab); break;
+        default: gather_kernel<VEC, 256><<<g, b, 0, s>>>(ids, tb, o, T, H, vocab); break;
+    }
 }
 
 }  // namespace
@@ -93,15 +94,15 @@ extern "C" int mi_embedding_gather_f16(const int64_t* ids, const void* table, vo
     if (T == 0 || H == 0) return MI_OK;
     if (!ids || !table || !out) return MI_ERR_INVALID_ARGUMENT;
     const bool vec = H % 8 == 0 && mi::aligned16(table) && mi::aligned16(out);
-    const int W = mi::gather_waves(vec ? H / 8 : H);
-    if (mi::ceil_div(T, 4 / W) > mi::kMaxGridX) return MI_ERR_UNSUPPORTED;
+    const int L = mi::gather_lanes(vec ? H / 8 : H);
+    if (mi::ceil_div(T, 256 / L) > mi::kMaxGridX) return MI_ERR_UNSUPPORTED;
     if (vocab > 0 && mi::overlaps(out, T * H * 2, table, vocab * H * 2)) return MI_ERR_ALIASING;
     const auto* tb = static_cast<const mi::half_t*>(table);
     auto* o = static_cast<mi::half_t*>(out);
     const hipStream_t s = mi::as_stream(stream);
     if (vec)
-        mi::launch_gather<8>(ids, tb, o, T, H, vocab, W, s);
+        mi::launch_gather<8>(ids, tb, o, T, H, vocab, L, s);
     else
-        mi::launch_gather<1>(ids, tb, o, T, H, vocab, W, s);
+        mi::launch_gather<1>(ids, tb, o, T, H, vocab, L, s);
     return mi::launch_status();
 }
