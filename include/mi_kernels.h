@@ -136,8 +136,8 @@ int mi_scale_inplace_f16(void* y, float scale, int64_t n, void* stream);
 
 /* Row softmax, fp32 math: y = exp(x - max) / sum(exp(x - max)).
  * x, y: [N, D]; y may equal x.  Replaces launch_softmax
- * (src/kernels/softmax_kernel.cuh:12).  Few long rows (N < 512, D >= 8192)
- * are split across workgroups.  On the legacy default stream (0, the
+ * (src/kernels/softmax_kernel.cuh:12).  Few long rows (N < 512, D >= 8192;
+ * N < 256 when D <= 65536) are split across workgroups.  On the legacy default stream (0, the
  * reference's callers' stream) out-of-place aligned calls run in one launch,
  * using 532,480 bytes of row records that the library allocates and zeroes
  * once per device, on first use, and keeps until the process ends.  On other
@@ -146,7 +146,8 @@ int mi_scale_inplace_f16(void* y, float scale, int64_t n, void* stream);
 int mi_softmax_f16(const void* x, void* y, int64_t N, int64_t D, void* stream);
 
 /* Bytes of device workspace mi_softmax_ws_f16 needs for [N, D]: 0 when rows
- * are processed one workgroup each (N >= 512 or D < 8192), else 532,480 bytes
+ * are processed whole (N >= 512, D < 8192, or N >= 256 with D <= 65536),
+ * else 532,480 bytes
  * of one-pass row records (fixed: 512 rows x 1040 B) plus one fp32 (max, sum)
  * pair per row chunk for the two-pass form. */
 int64_t mi_softmax_workspace_bytes(int64_t N, int64_t D);
