@@ -172,6 +172,8 @@ def test_fuzz_argmax(mk, orc, dev, seed):
     split = bool(rng.integers(0, 2))
     B = int(rng.integers(1, 64)) if split else int(rng.integers(1, 700))
     V = int(rng.integers(8192, 200000)) if split else int(rng.integers(1, 8192))
+    if not split and rng.integers(0, 4) == 0:  # whole long rows (deep tiles)
+        B, V = int(rng.integers(512, 700)), int(rng.integers(16384, 70000))
     levels = int(rng.choice([0, 1, 3, 50]))
     _case(f"argmax seed={seed} B={B} V={V} levels={levels}")
     if levels:

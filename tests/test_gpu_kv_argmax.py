@@ -70,7 +70,8 @@ def test_kv_scatter_odd_head_dim(mk, orc, dev):
 
 @pytest.mark.parametrize("B,V,levels", [(64, 152064, None), (64, 152064, 7), (1, 152064, None),
                                         (600, 4096, 5), (3, 1000, 3), (5, 100003, 9),
-                                        (2, 17, None), (512, 152064, None)])
+                                        (2, 17, None), (512, 152064, None),
+                                        (512, 152064, 3), (700, 65536, 5), (513, 16392, None)])
 def test_greedy_argmax_vs_oracle(mk, orc, dev, B, V, levels):
     """levels: values drawn from a few integers, so maxima tie often and the
     reference's tie order decides."""
