@@ -18,6 +18,7 @@ the same workload.  The oracle is the checker, never the thing measured on
 the GPU.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-kernels] [--no-cpu] [--no-chain]
+       [--shapes]
 """
 import argparse
 import json
@@ -614,6 +615,95 @@ def decoder_chain(mk, dev, iters, warmup):
     return rows
 
 
+def shape_table(mk, dev, iters=40, warmup=5):
+    """Beyond the BASELINE configs (`--shapes`): each kernel across common
+    LLM shapes, ~100-260 MB per launch unless the shape is small by nature,
+    timed like the kernel table (graph replay, buffers rotated past the
+    Infinity Cache).  Rows: kernel, shape, us, % of HBM peak."""
+    import numpy as np
+    import torch
+    gen = torch.Generator(device=dev).manual_seed(7)
+    rng = np.random.default_rng(7)
+    f16 = torch.float16
+    R = randn16
+    rows = []
+
+    def run(kernel, shape, nbytes, fn, ns):
+        sec = time_launches(fn, ns, iters, warmup)
+        rows.append({"kernel": kernel, "shape": shape, "us": round(sec * 1e6, 2),
+                     "frac": round(nbytes / sec / HBM_PEAK, 4)})
+        log(f"[shapes]   {kernel:<20} {shape:<26} {sec * 1e6:9.2f} us {100 * nbytes / sec / HBM_PEAK:6.1f}%")
+
+    for D in (1024, 2048, 4096, 5120, 8192, 16384):
+        T = max(1, int(200e6 / (4 * D * 2)))
+        ns = rotations(3 * T * D * 2)
+        w = R((D,), gen, dev, 1, 0.1)
+        sets = [(R((T, D), gen, dev), R((T, D), gen, dev), torch.empty((T, D), dtype=f16, device=dev))
+                for _ in range(ns)]
+        run("fused_add_rmsnorm", f"[{T},{D}]", 4 * T * D * 2,
+            lambda i: mk.fused_add_rmsnorm(sets[i][0], sets[i][1], w, y=sets[i][2]), ns)
+        del sets
+    for (Hq, Hkv, hd) in ((28, 4, 128), (32, 8, 128), (32, 32, 128), (16, 8, 256), (64, 8, 128),
+                          (32, 4, 64), (8, 1, 64)):
+        T = int(100e6 / ((Hq + Hkv) * hd * 4))
+        ns = rotations(T * (Hq + Hkv) * hd * 2)
+        pos = torch.from_numpy(rng.integers(0, 32000, T).astype(np.int64)).to(dev)
+        inv = mk.rope_inv_freq(hd)
+        qs = [R((T, Hq, hd), gen, dev) for _ in range(ns)]
+        ks = [R((T, Hkv, hd), gen, dev) for _ in range(ns)]
+        wq, wk = R((hd,), gen, dev, 1, 0.1), R((hd,), gen, dev, 1, 0.1)
+        nb = 2 * T * (Hq + Hkv) * hd * 2 + T * 8
+        run("rope_neox_qk", f"T={T} {Hq}|{Hkv}x{hd}", nb,
+            lambda i: mk.rope_neox_qk(qs[i], ks[i], pos, inv), ns)
+        run("qk_norm_rope", f"T={T} {Hq}|{Hkv}x{hd}", nb,
+            lambda i: mk.qk_norm_rope(qs[i], ks[i], wq, wk, pos, inv), ns)
+        del qs, ks
+    for N, D in ((57344, 512), (16384, 2048), (8192, 4096), (2048, 32000), (256, 65536),
+                 (512, 152064)):
+        nb = 2 * N * D * 2
+        ns = rotations(nb)
+        sets = [(R((N, D), gen, dev, 0, 4), torch.empty((N, D), dtype=f16, device=dev))
+                for _ in range(ns)]
+        ws = torch.zeros(max(1, mk.softmax_workspace_bytes(N, D)), dtype=torch.uint8, device=dev)
+        run("softmax", f"[{N},{D}]", nb,
+            lambda i: mk.softmax(sets[i][0], y=sets[i][1], workspace=ws), ns)
+        del sets
+    for B, V in ((256, 152064), (512, 152064), (1024, 152064), (2048, 32000)):
+        nb = B * V * 2
+        ns = rotations(nb)
+        xs = [R((B, V), gen, dev, 0, 4) for _ in range(ns)]
+        ws = torch.zeros(max(1, mk.greedy_argmax_workspace_bytes(B, V)), dtype=torch.uint8,
+                         device=dev)
+        o = torch.empty(B, dtype=torch.int32, device=dev)
+        run("greedy_argmax", f"[{B},{V}]", nb,
+            lambda i: mk.greedy_argmax(xs[i], out=o, workspace=ws), ns)
+        del xs
+    for V, H, T in ((128256, 4096, 8192), (152064, 8192, 4096), (32000, 2048, 16384),
+                    (128256, 1024, 32768)):
+        table = R((V, H), gen, dev, 0, 0.02)
+        ids = [torch.from_numpy(rng.integers(0, V, T).astype(np.int64)).to(dev) for _ in range(8)]
+        outs = [torch.empty((T, H), dtype=f16, device=dev) for _ in range(8)]
+        run("embedding_gather", f"T={T} from [{V},{H}]", T * 8 + 2 * T * H * 2,
+            lambda i: mk.embedding_gather(ids[i], table, out=outs[i]), 8)
+        del table, outs
+    for T, H, hd, bs in ((8192, 8, 128, 16), (16384, 1, 128, 16), (4096, 8, 128, 32)):
+        mb = -(-T // bs)
+        bt = torch.from_numpy(rng.permutation(mb).astype(np.int32)).to(dev).view(1, mb)
+        sl = torch.tensor([T], dtype=torch.int32, device=dev)
+        sp = torch.tensor([0], dtype=torch.int32, device=dev)
+        nb = 2 * 2 * T * H * hd * 2
+        ns = rotations(nb)
+        kv = [(R((1, T, H, hd), gen, dev), R((1, T, H, hd), gen, dev),
+               torch.empty((1, mb, H, bs, hd), dtype=f16, device=dev),
+               torch.empty((1, mb, H, bs, hd), dtype=f16, device=dev)) for _ in range(ns)]
+        run("paged_kv_scatter_kv", f"T={T} {H}x{hd} bs={bs}", nb,
+            lambda i: mk.paged_kv_scatter(kv[i][0], kv[i][2], bt, sl, sp, 0, bs, v_src=kv[i][1],
+                                          v_cache=kv[i][3]), ns)
+        del kv
+    torch.cuda.synchronize()
+    return rows
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawTextHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -621,6 +711,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-kernels", action="store_true", help="skip the per-config table")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--shapes", action="store_true",
+                    help="also time each kernel across common LLM shapes beyond the configs")
     ap.add_argument("--no-chain", action="store_true",
                     help="skip the whole-chain rows (profiling runs: one row per kernel and grid)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
@@ -664,6 +756,11 @@ def main():
                      if "copy_floor_us" in k else "")
             log(f"[bench]   {k['kernel']:<18} {k['config']:<38} {k['us']:>9.2f} us "
                 f"{k['GBps']:>8.1f} GB/s  {100 * k['frac']:5.1f}%{floor}")
+
+    shapes = None
+    if args.shapes:
+        log("[bench] shape table")
+        shapes = shape_table(mk, dev)
 
     cpu = cpu_torch = None
     if not args.no_cpu:
@@ -724,6 +821,8 @@ def main():
         "copy_calibration_GBps": round(copy_gbps, 1),
         "kernels": kernels,
     }
+    if shapes is not None:
+        line["shapes"] = shapes
     print(json.dumps(line), flush=True)
 
 
