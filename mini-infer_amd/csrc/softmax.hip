@@ -197,10 +197,15 @@ __global__ __launch_bounds__(G > 256 ? G : 256) void softmax_reg_kernel(const ha
     const int64_t nv = D >> 3;
     const half_t* xr = x + row * D;
     h8 a[VPT];
+    // vector j of this lane: a uniform base per j (xr + j * G * 8) plus the
+    // lane's 32-bit offset, so deep rows need no 64-bit address per load
+    const uint32_t lo = static_cast<uint32_t>(gl) * 16u;  // byte offset
 #pragma unroll
     for (int j = 0; j < VPT; ++j) {
         const int64_t v = gl + j * G;
-        a[j] = live && v < nv ? ld8_stream(xr + v * 8) : h8(-__builtin_huge_valf16());
+        const char* base = reinterpret_cast<const char*>(xr + static_cast<int64_t>(j) * G * 8);
+        a[j] = live && v < nv ? __builtin_nontemporal_load(reinterpret_cast<const h8*>(base + lo))
+                              : h8(-__builtin_huge_valf16());
     }
     h2 m2 = h2(-__builtin_huge_valf16());
 #pragma unroll
@@ -229,6 +234,11 @@ __global__ __launch_bounds__(G > 256 ? G : 256) void softmax_reg_kernel(const ha
     else
         s = block_sum(s, ssum);
     const float inv = 1.0f / s;
+    // Recomputing the exps (VPT > 4): an opaque copy of m keeps the compiler
+    // from reusing the sum loop's exps, which would hold 8 * VPT fp32 values
+    // live instead of the 4 * VPT registers of fp16 data.
+    float mw = m;
+    if constexpr (!kKeepExp) asm volatile("" : "+v"(mw));
     half_t* yr = y + row * D;
 #pragma unroll
     for (int j = 0; j < VPT; ++j) {
@@ -237,10 +247,13 @@ __global__ __launch_bounds__(G > 256 ? G : 256) void softmax_reg_kernel(const ha
             h8 o;
 #pragma unroll
             for (int k = 0; k < 8; ++k) {
-                const float t = kKeepExp ? e[kKeepExp ? j : 0][k] : fast_exp((float)a[j][k] - m);
+                const float t = kKeepExp ? e[kKeepExp ? j : 0][k] : fast_exp((float)a[j][k] - mw);
                 o[k] = to_half(t * inv);
             }
-            st8_out<MI_WT_SM>(yr + v * 8, o);
+            st8_out<MI_WT_SM>(
+                reinterpret_cast<half_t*>(
+                    reinterpret_cast<char*>(yr + static_cast<int64_t>(j) * G * 8) + lo),
+                o);
         }
     }
 }
@@ -253,6 +266,10 @@ __global__ __launch_bounds__(G > 256 ? G : 256) void softmax_reg_kernel(const ha
 #define MI_SOFTMAX_REG_VPT 4
 #endif
 constexpr int kRegVpt = MI_SOFTMAX_REG_VPT;
+// At most 8 vectors per lane (rows <= 1024 x 8 x 8 = 65536).  12 fit in
+// 110 VGPRs but measured mixed: [256, 98304] 51% -> 57%, [300, 70000]
+// 45% -> 36% (idle lanes and a 17%-full second round); 16 or more spill.
+constexpr int kRegVptMax = 8;
 bool reg_shape(int64_t nv, int& G, int& VPT) {
     static const int kG[] = {8, 16, 32, 64, 256, 1024};
     G = 0;
@@ -262,7 +279,7 @@ bool reg_shape(int64_t nv, int& G, int& VPT) {
             break;
         }
     if (G == 0) {
-        if (nv > 1024 * 8) return false;
+        if (nv > 1024 * kRegVptMax) return false;
         G = 1024;
     }
     const int64_t v = ceil_div(nv, G);
@@ -517,7 +534,7 @@ Plan plan(int64_t N, int64_t D, int64_t& splits, int64_t& chunk) {
     // 256 rows or more that register rows hold (D <= 1024 x 8 x 8): one
     // 1024-lane workgroup per row beat splitting them (measured at [256,
     // 32000] 45% -> 49%, [256, 65536] 49% -> 56%, [384, 16384] 39% -> 47%)
-    if (N >= MI_SOFTMAX_REG_ROWS && D <= 65536) return Plan::kRow;
+    if (N >= MI_SOFTMAX_REG_ROWS && D <= 1024 * kRegVptMax * 8) return Plan::kRow;
     const int64_t tile = split_tile(N, D);
     int64_t sp = ceil_div(kSplitTargetWgs, N);
     if (sp > kMaxSplits) sp = kMaxSplits;
