@@ -198,13 +198,14 @@ __global__ __launch_bounds__(G > 256 ? G : 256) void softmax_reg_kernel(const ha
     const half_t* xr = x + row * D;
     h8 a[VPT];
     // vector j of this lane: a uniform base per j (xr + j * G * 8) plus the
-    // lane's 32-bit offset, so deep rows need no 64-bit address per load
-    const uint32_t lo = static_cast<uint32_t>(gl) * 16u;  // byte offset
+    // lane's 32-bit byte offset (with the forced recompute below, 8-vector
+    // rows went from 90-115 to 78-88 VGPRs)
+    const uint32_t lo = static_cast<uint32_t>(gl) * 16u;
 #pragma unroll
     for (int j = 0; j < VPT; ++j) {
         const int64_t v = gl + j * G;
         const char* base = reinterpret_cast<const char*>(xr + static_cast<int64_t>(j) * G * 8);
-        a[j] = live && v < nv ? __builtin_nontemporal_load(reinterpret_cast<const h8*>(base + lo))
+        a[j] = live && v < nv ? ld8_stream(reinterpret_cast<const half_t*>(base + lo))
                               : h8(-__builtin_huge_valf16());
     }
     h2 m2 = h2(-__builtin_huge_valf16());
