@@ -137,19 +137,23 @@ int mi_scale_inplace_f16(void* y, float scale, int64_t n, void* stream);
 /* Row softmax, fp32 math: y = exp(x - max) / sum(exp(x - max)).
  * x, y: [N, D]; y may equal x.  Replaces launch_softmax
  * (src/kernels/softmax_kernel.cuh:12).  Few long rows (N < 512, D >= 8192;
- * N < 256 when D <= 65536) are split across workgroups.  On the legacy default stream (0, the
- * reference's callers' stream) out-of-place aligned calls run in one launch,
- * using 532,480 bytes of row records that the library allocates and zeroes
- * once per device, on first use, and keeps until the process ends.  On other
- * streams, or in place, they take two launches with a stream-ordered
- * workspace for the call. */
+ * N < 256 when D <= 65536) are split across workgroups, and so are many rows
+ * longer than 32768 (N >= 512, or N >= 256 up to 65536; at most 64 x 8192
+ * elements) when the call can run in one launch.  On the legacy default
+ * stream (0, the reference's callers' stream) out-of-place aligned calls of
+ * these shapes run in one launch, using 1,056,768 bytes of row records that
+ * the library allocates and zeroes once per device, on first use, and keeps
+ * until the process ends.  On other streams, or in place, few long rows take
+ * two launches with a stream-ordered workspace for the call, and many long
+ * rows one workgroup per row. */
 int mi_softmax_f16(const void* x, void* y, int64_t N, int64_t D, void* stream);
 
 /* Bytes of device workspace mi_softmax_ws_f16 needs for [N, D]: 0 when rows
- * are processed whole (N >= 512, D < 8192, or N >= 256 with D <= 65536),
- * else 532,480 bytes
- * of one-pass row records (fixed: 512 rows x 1040 B) plus one fp32 (max, sum)
- * pair per row chunk for the two-pass form. */
+ * are processed whole (N >= 512 or N >= 256 with D <= 65536, unless D is in
+ * 32769 .. 64 x 8192; and D < 8192); 1,056,768 bytes of row records (fixed:
+ * 512 rows x 2064 B) for many rows longer than 32768; for few long rows, the
+ * records plus one fp32 (max, sum) pair per row chunk for the two-launch
+ * form. */
 int64_t mi_softmax_workspace_bytes(int64_t N, int64_t D);
 
 /* mi_softmax_f16 with a caller-provided device workspace of at least
@@ -159,9 +163,11 @@ int64_t mi_softmax_workspace_bytes(int64_t N, int64_t D);
  * used only by this function (any shapes); each call leaves it valid for the
  * next.  With y != x and aligned rows of <= 64 x 8192 elements, split rows
  * run in ONE launch: chunks exchange (max, sum) through tagged per-row
- * records, with no atomics on a shared address; in place, or otherwise, the
- * two-launch form runs.  Calls that share one workspace must not overlap in
- * time. */
+ * records, with no atomics on a shared address -- every chunk of the grid
+ * resident at once, or, for more rows than that, a resident grid that walks
+ * the rows in rounds.  In place, or otherwise, few long rows take the
+ * two-launch form and many long rows one workgroup per row.  Calls that share
+ * one workspace must not overlap in time. */
 int mi_softmax_ws_f16(const void* x, void* y, int64_t N, int64_t D, void* workspace,
                       int64_t workspace_bytes, void* stream);
 

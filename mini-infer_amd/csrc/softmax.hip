@@ -7,8 +7,14 @@
 //   * Each lane keeps an online (max, sum) pair over its 16-byte vectors,
 //     rescaling the sum when the max grows, so statistics need ONE read of x
 //     (the reference makes separate max and sum passes, then a third to write).
-//   * Many rows (N >= 512): one workgroup per row; the write pass re-reads the
-//     row, which the workgroup has just streamed through L2.
+//   * Many rows (N >= 512; N >= 256 up to 65536): whole rows, in registers
+//     where they fit (softmax_reg_kernel), else one workgroup per row whose
+//     write pass re-reads the row through L2.
+//   * Many rows longer than 32768 (N >= 512, or N >= 256 up to 65536, or
+//     too many rows for the one-launch grid below): with row records and
+//     y != x, softmax_stream_kernel -- a resident grid of chunk workgroups
+//     walking the rows in rounds, one read of x, the next row's loads in
+//     flight during each exchange.
 //   * Few long rows (the LM-head case, 64 x 152064): one workgroup per row
 //     would light up 64 of 256 CUs, so each row is cut into chunks.  With
 //     row records -- a caller workspace, or on stream 0 a region the library
@@ -394,12 +400,123 @@ constexpr int kOnePassMaxSplits = 64;
 #endif
 constexpr int kOnePassU = MI_SOFTMAX_ONEPASS_U;     // vectors per lane
 constexpr int64_t kOnePassChunk = 2048 * kOnePassU;  // elements per workgroup
-constexpr int64_t kRowRecordBytes = 16 + kOnePassMaxSplits * 16;
+// header, then two sets of slot pairs (the persistent kernel alternates
+// them by round; the one-pass kernel uses the first)
+constexpr int64_t kRowRecordBytes = 16 + 2 * kOnePassMaxSplits * 16;
 constexpr int kPollLimit = 1 << 16;
 std::atomic<int> g_poll_limit{kPollLimit};  // mi_softmax_test_poll_limit
 
 __device__ __forceinline__ uint64_t tagged(uint32_t tag, float v) {
     return (static_cast<uint64_t>(tag) << 32) | __builtin_bit_cast(uint32_t, v);
+}
+
+// The pieces of a one-launch chunk workgroup.
+// Loads the chunk [b, e) of a row, U vectors per lane, -inf past e.
+template <int U>
+__device__ __forceinline__ void chunk_load(const half_t* xr, int64_t b, int64_t e, h8 (&a)[U]) {
+#pragma unroll
+    for (int j = 0; j < U; ++j) {
+        const int64_t i = b + (threadIdx.x + j * 256) * 8;
+        a[j] = i < e ? ld8(xr + i) : h8(-__builtin_huge_valf16());
+    }
+}
+// The lane's (max, sum) over its vectors: packed fp16 maximum, one exp per
+// element.
+template <int U>
+__device__ __forceinline__ void chunk_lane_stats(const h8 (&a)[U], float& m, float& s) {
+    h2 m2 = h2(-__builtin_huge_valf16());
+#pragma unroll
+    for (int j = 0; j < U; ++j) {
+#pragma unroll
+        for (int k = 0; k < 8; k += 2) m2 = __builtin_elementwise_max(m2, h2{a[j][k], a[j][k + 1]});
+    }
+    m = (float)__builtin_elementwise_max(m2.x, m2.y);
+    s = 0.0f;
+    if (m > -INFINITY) {
+#pragma unroll
+        for (int j = 0; j < U; ++j) {
+#pragma unroll
+            for (int k = 0; k < 8; ++k) s += fast_exp((float)a[j][k] - m);
+        }
+    } else {
+        m = -INFINITY;  // NaN-free lane maximum of an all -inf (or NaN) lane
+    }
+}
+// Thread `who` publishes the chunk's pair into slot pair `split` of `slots`.
+__device__ __forceinline__ void chunk_publish(uint64_t* slots, int split, uint32_t tag, float m,
+                                              float s, unsigned who) {
+    if (threadIdx.x == who) {
+        __hip_atomic_store(&slots[2 * split], tagged(tag, m), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(&slots[2 * split + 1], tagged(tag, s), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+// One wave (the caller's choice) polls the row's `splits` slot pairs (lane j
+// reads chunk j) until all carry `tag`, at most poll_limit rounds, and leaves
+// the row's (M, S) in row_stats[0..1] and row_stats[2] = 0, or
+// row_stats[2] = 1 when polling ran out.  The caller's barrier publishes
+// row_stats.
+__device__ __forceinline__ void row_poll(const uint64_t* slots, int splits, uint32_t tag,
+                                         int poll_limit, float* row_stats) {
+    const int lane = threadIdx.x & (kWave - 1);
+    float mj = -INFINITY, sj = 0.0f;
+    bool all = false;
+    for (int it = 0; it < poll_limit && !all; ++it) {
+        bool mine = true;
+        if (lane < splits) {
+            const uint64_t w0 = __hip_atomic_load(&slots[2 * lane], __ATOMIC_RELAXED,
+                                                  __HIP_MEMORY_SCOPE_AGENT);
+            const uint64_t w1 = __hip_atomic_load(&slots[2 * lane + 1], __ATOMIC_RELAXED,
+                                                  __HIP_MEMORY_SCOPE_AGENT);
+            mine = static_cast<uint32_t>(w0 >> 32) == tag && static_cast<uint32_t>(w1 >> 32) == tag;
+            mj = __builtin_bit_cast(float, static_cast<uint32_t>(w0));
+            sj = __builtin_bit_cast(float, static_cast<uint32_t>(w1));
+        }
+        all = __all(mine);
+        if (!all) __builtin_amdgcn_s_sleep(2);
+    }
+    if (all) {
+        if (lane >= splits) {
+            mj = -INFINITY;
+            sj = 0.0f;
+        }
+        const float M = group_max<kWave>(mj);
+        const float S = group_sum<kWave>(mj == -INFINITY ? 0.0f : sj * fast_exp(mj - M));
+        if (lane == 0) {
+            row_stats[0] = M;
+            row_stats[1] = S;
+            row_stats[2] = 0.0f;
+        }
+    } else if (lane == 0) {
+        row_stats[2] = 1.0f;
+    }
+}
+// The row's statistics from x itself (the fallback when polling runs out; x
+// is not written: y != x).  Barriers: called by the whole workgroup.
+// Lanes 0..255 read x; other lanes of the workgroup only join the merge.
+__device__ __forceinline__ void row_stats_from_x(const half_t* xr, int64_t D, float& M, float& S,
+                                                 float* slots) {
+    float fm = -INFINITY, fs = 0.0f;
+    if (threadIdx.x < 256) tile_stats<2>(xr, 0, D, fm, fs);
+    __syncthreads();  // slots reused
+    block_merge(fm, fs, slots);
+    M = fm;
+    S = fs;
+}
+template <int U>
+__device__ __forceinline__ void chunk_store(const h8 (&a)[U], half_t* yr, int64_t b, int64_t e,
+                                            float M, float inv) {
+#pragma unroll
+    for (int j = 0; j < U; ++j) {
+        const int64_t i = b + (threadIdx.x + j * 256) * 8;
+        if (i < e) {
+            h8 o;
+#pragma unroll
+            for (int k = 0; k < 8; ++k) o[k] = to_half(fast_exp((float)a[j][k] - M) * inv);
+            st8_out<MI_WT_SM>(yr + i, o);
+        }
+    }
 }
 
 __global__ __launch_bounds__(256) void softmax_onepass_kernel(const half_t* x, half_t* y,
@@ -420,104 +537,147 @@ __global__ __launch_bounds__(256) void softmax_onepass_kernel(const half_t* x, h
 
     if (threadIdx.x == 0)
         epoch_sh = __hip_atomic_load(epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    // the chunk, all loads first (-inf past the end of the row)
     h8 a[U];
-#pragma unroll
-    for (int j = 0; j < U; ++j) {
-        const int64_t i = b + (threadIdx.x + j * 256) * 8;
-        a[j] = i < e ? ld8(xr + i) : h8(-__builtin_huge_valf16());
-    }
-    h2 m2 = h2(-__builtin_huge_valf16());
-#pragma unroll
-    for (int j = 0; j < U; ++j) {
-#pragma unroll
-        for (int k = 0; k < 8; k += 2) m2 = __builtin_elementwise_max(m2, h2{a[j][k], a[j][k + 1]});
-    }
-    float m = (float)__builtin_elementwise_max(m2.x, m2.y), s = 0.0f;
-    if (m > -INFINITY) {
-#pragma unroll
-        for (int j = 0; j < U; ++j) {
-#pragma unroll
-            for (int k = 0; k < 8; ++k) s += fast_exp((float)a[j][k] - m);
-        }
-    } else {
-        m = -INFINITY;  // NaN-free lane maximum of an all -inf (or NaN) lane
-    }
+    chunk_load<U>(xr, b, e, a);
+    float m, s;
+    chunk_lane_stats<U>(a, m, s);
     block_merge(m, s, slots);  // barriers: epoch_sh is visible after this
     const uint64_t E = epoch_sh;
     const uint32_t tag = static_cast<uint32_t>(E + 1);
-    if (threadIdx.x == 0) {
-        __hip_atomic_store(&slot[2 * split], tagged(tag, m), __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(&slot[2 * split + 1], tagged(tag, s), __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
-    }
-    if (threadIdx.x < kWave) {
-        // wave 0 polls the row's slots: lane j reads chunk j
-        const int lane = threadIdx.x;
-        float mj = -INFINITY, sj = 0.0f;
-        bool all = false;
-        for (int it = 0; it < poll_limit && !all; ++it) {
-            bool mine = true;
-            if (lane < splits) {
-                const uint64_t w0 = __hip_atomic_load(&slot[2 * lane], __ATOMIC_RELAXED,
-                                                      __HIP_MEMORY_SCOPE_AGENT);
-                const uint64_t w1 = __hip_atomic_load(&slot[2 * lane + 1], __ATOMIC_RELAXED,
-                                                      __HIP_MEMORY_SCOPE_AGENT);
-                mine = static_cast<uint32_t>(w0 >> 32) == tag &&
-                       static_cast<uint32_t>(w1 >> 32) == tag;
-                mj = __builtin_bit_cast(float, static_cast<uint32_t>(w0));
-                sj = __builtin_bit_cast(float, static_cast<uint32_t>(w1));
-            }
-            all = __all(mine);
-            if (!all) __builtin_amdgcn_s_sleep(2);
-        }
-        if (all) {
-            if (lane >= splits) {
-                mj = -INFINITY;
-                sj = 0.0f;
-            }
-            const float M = group_max<kWave>(mj);
-            const float S = group_sum<kWave>(mj == -INFINITY ? 0.0f : sj * fast_exp(mj - M));
-            if (lane == 0) {
-                row_stats[0] = M;
-                row_stats[1] = S;
-                row_stats[2] = 0.0f;
-            }
-        } else if (lane == 0) {
-            row_stats[2] = 1.0f;
-        }
-    }
+    chunk_publish(slot, split, tag, m, s, 0);
+    if (threadIdx.x < kWave) row_poll(slot, splits, tag, poll_limit, row_stats);
     __syncthreads();
     float M = row_stats[0], S = row_stats[1];
     const bool fallback = row_stats[2] != 0.0f;
-    if (fallback) {
-        // the row's statistics from x itself (x is not written: y != x)
-        float fm = -INFINITY, fs = 0.0f;
-        tile_stats<2>(xr, 0, D, fm, fs);
-        __syncthreads();  // slots reused
-        block_merge(fm, fs, slots);
-        M = fm;
-        S = fs;
-    }
+    if (fallback) row_stats_from_x(xr, D, M, S, slots);
     if (threadIdx.x == 0 && (split == 0 || fallback))
         __hip_atomic_fetch_max(epoch, fallback ? E + 2 : E + 1, __ATOMIC_RELAXED,
                                __HIP_MEMORY_SCOPE_AGENT);
-    const float inv = 1.0f / S;
-    half_t* yr = y + row * D;
+    chunk_store<U>(a, y + row * D, b, e, M, 1.0f / S);
+}
+
+// ---------------------------------------------------------------------------
+// Persistent one-launch form, for more rows than can hold every chunk
+// workgroup resident at once (softmax_onepass_kernel's condition): a grid of
+// `splits` x R workgroups, all resident, where row slot r (blockIdx.y) walks
+// rows r, r + R, r + 2R, ...  While a round's chunk statistics are exchanged,
+// the workgroup already has the loads of its next row's chunk in flight, so
+// the exchange latency overlaps HBM reads instead of idling the CU.
+//
+// Records: row slot r uses the record of row r (same header and epoch as the
+// one-pass kernel), with two sets of slot pairs used by round parity.  A
+// workgroup can only publish round k + 2 into a set after it has seen every
+// chunk's round k + 1 pair, which its row-mates publish after they have read
+// round k: no pair is overwritten before it is read.  Round k's tag is the
+// low 32 bits of E + 1 + k (E = the epoch read at the start); the chunk-0
+// workgroup raises the epoch to E + K after the last (K-th) round, when every
+// workgroup of the slot has published it (and so has read E).  A workgroup
+// whose polling runs out computes that row's statistics from x and raises
+// the epoch to E + K + 1 at once, past every tag this launch writes for the
+// slot: a workgroup that starts after that reads the higher epoch, its tags
+// then match nobody's and it takes the same fallback for its rows --
+// slower, still correct, and bounded.
+// ---------------------------------------------------------------------------
+// The persistent kernel's per-lane view of its chunk: the same in every
+// round, so one 32-bit byte offset (rows are < 2^31 bytes) and a valid flag
+// per vector, against a row base that is uniform across the workgroup.
+template <int U>
+__device__ __forceinline__ void lane_load(const half_t* row, uint32_t lo, const bool (&ok)[U],
+                                          h8 (&a)[U]) {
+    const char* base = reinterpret_cast<const char*>(row) + lo;
 #pragma unroll
     for (int j = 0; j < U; ++j) {
-        const int64_t i = b + (threadIdx.x + j * 256) * 8;
-        if (i < e) {
+        const half_t* p = reinterpret_cast<const half_t*>(base + j * 256 * 16);
+        a[j] = ok[j] ? ld8_stream(p) : h8(-__builtin_huge_valf16());
+    }
+}
+template <int U>
+__device__ __forceinline__ void lane_store(const h8 (&a)[U], half_t* row, uint32_t lo,
+                                           const bool (&ok)[U], float M, float inv) {
+    char* base = reinterpret_cast<char*>(row) + lo;
+#pragma unroll
+    for (int j = 0; j < U; ++j) {
+        if (ok[j]) {
             h8 o;
 #pragma unroll
             for (int k = 0; k < 8; ++k) o[k] = to_half(fast_exp((float)a[j][k] - M) * inv);
-            st8_out<MI_WT_SM>(yr + i, o);
+            st8_out<MI_WT_SM>(reinterpret_cast<half_t*>(base + j * 256 * 16), o);
         }
     }
 }
 
-enum class Plan { kRow, kTwoPass };
+// 64 VGPRs, so 8 workgroups per CU (per-lane 32-bit offsets, not 64-bit
+// indices: 68 VGPRs and 7 workgroups per CU with them measured 5-10 points
+// lower; amdgpu_waves_per_eu(8) also measured ~8 points lower at the same
+// 64 VGPRs); wave 0 publishes and polls.
+__global__ __launch_bounds__(256) void softmax_stream_kernel(const half_t* x, half_t* y,
+                                                             unsigned char* ws, int64_t N,
+                                                             int64_t D, int poll_limit) {
+    constexpr int U = kOnePassU;
+    __shared__ float slots[256 / kWave];
+    __shared__ float row_stats[3];  // M, S, fallback flag
+    __shared__ uint64_t epoch_sh;
+    const int split = blockIdx.x, splits = gridDim.x;
+    const int64_t r0 = blockIdx.y, R = gridDim.y;
+    unsigned char* rec = ws + r0 * kRowRecordBytes;
+    uint64_t* epoch = reinterpret_cast<uint64_t*>(rec);
+    uint64_t* sets = reinterpret_cast<uint64_t*>(rec + 16);
+    const int64_t K = (N - r0 + R - 1) / R;  // rounds of this row slot (>= 1)
+    const int64_t b = split * kOnePassChunk;
+    const int64_t e = b + kOnePassChunk < D ? b + kOnePassChunk : D;
+    const uint32_t lo = static_cast<uint32_t>(b + threadIdx.x * 8) * 2;
+    bool ok[U];
+#pragma unroll
+    for (int j = 0; j < U; ++j) ok[j] = b + (threadIdx.x + j * 256) * 8 < e;
+
+    if (threadIdx.x == 0)
+        epoch_sh = __hip_atomic_load(epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    h8 a[U], n[U];
+    lane_load<U>(x + r0 * D, lo, ok, a);
+    for (int64_t k = 0; k < K; ++k) {
+        const int64_t row = r0 + k * R;
+        // The guard is always true (256 lanes); written out, it keeps the
+        // statistics in a block of their own, which measured 64 VGPRs with
+        // no spill against 80 without it.
+        float m = -INFINITY, s = 0.0f;
+        if (threadIdx.x < 256) chunk_lane_stats<U>(a, m, s);
+        block_merge(m, s, slots);  // barriers: epoch_sh (first round) is visible after this
+        const uint64_t E = epoch_sh;
+        const uint32_t tag = static_cast<uint32_t>(E + 1 + k);
+        uint64_t* set = sets + (k & 1) * (2 * kOnePassMaxSplits);
+        chunk_publish(set, split, tag, m, s, 0);
+        if (k + 1 < K) lane_load<U>(x + (row + R) * D, lo, ok, n);
+        if (threadIdx.x < kWave) row_poll(set, splits, tag, poll_limit, row_stats);
+        __syncthreads();
+        float M = row_stats[0], S = row_stats[1];
+        const bool fallback = row_stats[2] != 0.0f;
+        if (fallback) row_stats_from_x(x + row * D, D, M, S, slots);
+        if (threadIdx.x == 0 && (fallback || (split == 0 && k + 1 == K)))
+            __hip_atomic_fetch_max(epoch, fallback ? E + K + 1 : E + K, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+        lane_store<U>(a, y + row * D, lo, ok, M, 1.0f / S);
+        if (k + 1 < K) {
+#pragma unroll
+            for (int j = 0; j < U; ++j) a[j] = n[j];
+        }
+    }
+}
+
+// kStream: many rows long enough that chunking them beats a workgroup per
+// row; with row records and y != x they run as softmax_stream_kernel,
+// otherwise as kRow.
+enum class Plan { kRow, kTwoPass, kStream };
+
+#ifndef MI_SOFTMAX_STREAM
+#define MI_SOFTMAX_STREAM 1
+#endif
+#ifndef MI_SOFTMAX_STREAM_MIN_D
+#define MI_SOFTMAX_STREAM_MIN_D 32769
+#endif
+bool stream_shape(int64_t D) {
+    return MI_SOFTMAX_STREAM && D >= MI_SOFTMAX_STREAM_MIN_D &&
+           D <= kOnePassMaxSplits * kOnePassChunk;
+}
 
 // Few long rows are split into chunks: aim at ~2048 workgroups (a 19.5 MB
 // read-and-reduce measured flat at 5.0-5.5 us from 1216 to 4800 workgroups)
@@ -531,11 +691,12 @@ int64_t split_tile(int64_t N, int64_t D) { return N * ceil_div(D, 4096) >= 1024 
 Plan plan(int64_t N, int64_t D, int64_t& splits, int64_t& chunk) {
     splits = 1;
     chunk = D;
-    if (N >= kSplitMaxRows || D < 8192) return Plan::kRow;
+    if (N >= kSplitMaxRows || D < 8192) return stream_shape(D) ? Plan::kStream : Plan::kRow;
     // 256 rows or more that register rows hold (D <= 1024 x 8 x 8): one
     // 1024-lane workgroup per row beat splitting them (measured at [256,
     // 32000] 45% -> 49%, [256, 65536] 49% -> 56%, [384, 16384] 39% -> 47%)
-    if (N >= MI_SOFTMAX_REG_ROWS && D <= 1024 * kRegVptMax * 8) return Plan::kRow;
+    if (N >= MI_SOFTMAX_REG_ROWS && D <= 1024 * kRegVptMax * 8)
+        return stream_shape(D) ? Plan::kStream : Plan::kRow;
     const int64_t tile = split_tile(N, D);
     int64_t sp = ceil_div(kSplitTargetWgs, N);
     if (sp > kMaxSplits) sp = kMaxSplits;
@@ -549,7 +710,7 @@ Plan plan(int64_t N, int64_t D, int64_t& splits, int64_t& chunk) {
 // Workspace of the two-pass split plan: one (max, sum) pair per chunk.
 int64_t twopass_bytes(int64_t N, int64_t D) {
     int64_t splits, chunk;
-    if (plan(N, D, splits, chunk) == Plan::kRow) return 0;
+    if (plan(N, D, splits, chunk) != Plan::kTwoPass) return 0;
     return N * splits * 2 * static_cast<int64_t>(sizeof(float));
 }
 
@@ -558,6 +719,8 @@ int64_t twopass_bytes(int64_t N, int64_t D) {
 // same place), then the two-pass pairs (in-place or unaligned calls).
 constexpr int64_t kOnePassRegion = kSplitMaxRows * kRowRecordBytes;
 int64_t workspace_bytes(int64_t N, int64_t D) {
+    int64_t splits, chunk;
+    if (plan(N, D, splits, chunk) == Plan::kStream) return kOnePassRegion;
     const int64_t two = twopass_bytes(N, D);
     return two > 0 ? kOnePassRegion + two : 0;
 }
@@ -589,6 +752,34 @@ bool onepass_ok(const void* x, const void* y, int64_t N, int64_t D) {
                                           256);
 }
 
+// Rows of the persistent kernel's grid: as many as stay resident next to
+// each other with every chunk of a row (at most the record rows).
+int64_t stream_rows(int64_t N, int64_t D) {
+    const int64_t sp1 = ceil_div(D, kOnePassChunk);
+    int64_t R = resident_workgroups(reinterpret_cast<const void*>(softmax_stream_kernel), 256) / sp1;
+    if (R > N) R = N;
+    if (R > kSplitMaxRows) R = kSplitMaxRows;
+    return R;
+}
+
+// Whether [N, D] runs as softmax_stream_kernel given row records: a kStream
+// shape, or a split shape too large for the one-pass grid; aligned rows,
+// y != x (the fallback re-reads x), 2..64 chunks per row.
+bool stream_ok(const void* x, const void* y, int64_t N, int64_t D) {
+    int64_t splits, chunk;
+    const Plan p = plan(N, D, splits, chunk);
+    if (!MI_SOFTMAX_STREAM || p == Plan::kRow) return false;
+    if (p == Plan::kTwoPass && onepass_ok(x, y, N, D)) return false;
+    const int64_t sp1 = ceil_div(D, kOnePassChunk);
+    return D % 8 == 0 && aligned16(x) && aligned16(y) && x != y && sp1 >= 2 &&
+           sp1 <= kOnePassMaxSplits && stream_rows(N, D) >= 1;
+}
+
+// Whether a call of this shape uses row records (one-pass or persistent).
+bool records_ok(const void* x, const void* y, int64_t N, int64_t D) {
+    return onepass_ok(x, y, N, D) || stream_ok(x, y, N, D);
+}
+
 int softmax_checked(const void* x, void* y, int64_t N, int64_t D, void* ws, int64_t ws_bytes,
                     Ws layout, void* stream) {
     if (N < 0 || D < 0 || ws_bytes < 0) return MI_ERR_INVALID_ARGUMENT;
@@ -600,9 +791,11 @@ int softmax_checked(const void* x, void* y, int64_t N, int64_t D, void* ws, int6
     int64_t splits, chunk;
     const Plan p = plan(N, D, splits, chunk);
     const bool onepass = layout != Ws::kPairs && onepass_ok(x, y, N, D);
-    if (layout == Ws::kRecords && p == Plan::kTwoPass && !onepass)
-        return MI_ERR_UNSUPPORTED;  // no pairs to fall back on (callers check onepass_ok)
+    const bool persistent = layout != Ws::kPairs && stream_ok(x, y, N, D);
+    if (layout == Ws::kRecords && p == Plan::kTwoPass && !onepass && !persistent)
+        return MI_ERR_UNSUPPORTED;  // no pairs to fall back on (callers check records_ok)
     const int64_t need = p == Plan::kRow ? 0
+                         : p == Plan::kStream ? (persistent ? kOnePassRegion : 0)
                          : layout == Ws::kPairs ? twopass_bytes(N, D)
                          : layout == Ws::kRecords ? kOnePassRegion
                                                   : workspace_bytes(N, D);
@@ -616,7 +809,7 @@ int softmax_checked(const void* x, void* y, int64_t N, int64_t D, void* ws, int6
     auto* yh = static_cast<half_t*>(y);
     const hipStream_t s = as_stream(stream);
     const bool vec = D % 8 == 0 && aligned16(x) && aligned16(y);
-    if (p == Plan::kRow) {
+    if (p == Plan::kRow || (p == Plan::kStream && !persistent)) {
         int G = 0, VPT = 0;
         if (MI_SOFTMAX_REG && vec && reg_shape(D / 8, G, VPT) &&
             ceil_div(N, (G > 256 ? G : 256) / G) <= kMaxGridX) {
@@ -636,6 +829,14 @@ int softmax_checked(const void* x, void* y, int64_t N, int64_t D, void* ws, int6
             softmax_row_kernel<8><<<dim3(static_cast<unsigned>(N)), dim3(threads), 0, s>>>(xh, yh, D);
         else
             softmax_row_kernel<1><<<dim3(static_cast<unsigned>(N)), dim3(threads), 0, s>>>(xh, yh, D);
+        return launch_status();
+    }
+    if (persistent) {
+        const int64_t sp1 = ceil_div(D, kOnePassChunk);
+        const int64_t R = stream_rows(N, D);
+        softmax_stream_kernel<<<dim3(static_cast<unsigned>(sp1), static_cast<unsigned>(R)),
+                                dim3(256), 0, s>>>(xh, yh, static_cast<unsigned char*>(ws), N, D,
+                                                   g_poll_limit.load());
         return launch_status();
     }
     if (onepass) {
@@ -677,17 +878,17 @@ extern "C" int mi_softmax_ws_f16(const void* x, void* y, int64_t N, int64_t D, v
 
 extern "C" int mi_softmax_f16(const void* x, void* y, int64_t N, int64_t D, void* stream) {
     const int64_t need = (N > 0 && D > 0) ? mi::twopass_bytes(N, D) : 0;
-    if (need == 0) return mi::softmax_checked(x, y, N, D, nullptr, 0, mi::Ws::kPairs, stream);
-    if (!x || !y) return MI_ERR_INVALID_ARGUMENT;
     const hipStream_t s = mi::as_stream(stream);
-    // Few long rows on the default stream (every caller in the reference
+    // Long split rows on the default stream (every caller in the reference
     // passes 0): one launch, with row records the library holds for stream 0.
-    if (mi::onepass_ok(x, y, N, D)) {
+    if (x && y && N > 0 && D > 0 && N <= mi::kMaxGridX && mi::records_ok(x, y, N, D)) {
         void* rec = mi::default_stream_region(mi::kRegionSoftmax, mi::kOnePassRegion, s);
         if (rec)
             return mi::softmax_checked(x, y, N, D, rec, mi::kOnePassRegion, mi::Ws::kRecords,
                                        stream);
     }
+    if (need == 0) return mi::softmax_checked(x, y, N, D, nullptr, 0, mi::Ws::kPairs, stream);
+    if (!x || !y) return MI_ERR_INVALID_ARGUMENT;
     // Otherwise two launches with a stream-ordered workspace from the
     // device's default pool (concurrent calls on other streams get their
     // own; a fresh pool allocation is not zeroed, which the two-pass form

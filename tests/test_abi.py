@@ -108,14 +108,25 @@ def test_product_path_has_no_oracle_dependency():
 def test_softmax_workspace_sizes(lib):
     lib.mi_softmax_workspace_bytes.argtypes = [ctypes.c_int64, ctypes.c_int64]
     lib.mi_softmax_workspace_bytes.restype = ctypes.c_int64
-    # 64 rows of 152064: the one-pass records (512 rows x 1040 B), then for
-    # the two-launch form chunks of one 4096-element tile (the whole number
-    # of tiles nearest 152064 / 32), 38 per row, one (max, sum) pair each
-    assert lib.mi_softmax_workspace_bytes(64, 152064) == 512 * 1040 + 64 * 38 * 8
+    # Row records: 512 rows x 2064 B (16 B header, two sets of 64 slot pairs).
+    # 64 rows of 152064: the records, then for the two-launch form chunks of
+    # one 4096-element tile (the whole number of tiles nearest 152064 / 32),
+    # 38 per row, one (max, sum) pair each
+    rec = 512 * 2064
+    assert lib.mi_softmax_workspace_bytes(64, 152064) == rec + 64 * 38 * 8
+    # 512 rows or more (256 or more up to 65536) longer than 32768: the
+    # records only (persistent one-launch form; a workgroup per row when a
+    # call cannot use them)
+    assert lib.mi_softmax_workspace_bytes(512, 152064) == rec
+    assert lib.mi_softmax_workspace_bytes(4096, 32769) == rec
+    assert lib.mi_softmax_workspace_bytes(256, 65536) == rec
+    assert lib.mi_softmax_workspace_bytes(512, 32768) == 0
+    assert lib.mi_softmax_workspace_bytes(256, 32768) == 0
+    assert lib.mi_softmax_workspace_bytes(512, 600000) == 0  # more than 64 chunks per row
     assert lib.mi_softmax_workspace_bytes(57344, 512) == 0
     assert lib.mi_softmax_workspace_bytes(8, 1024) == 0
     assert lib.mi_softmax_workspace_bytes(0, 5) == 0
-    assert 0 < lib.mi_softmax_workspace_bytes(511, 10**6) <= 512 * 1040 + 256 * 1024
+    assert 0 < lib.mi_softmax_workspace_bytes(511, 10**6) <= rec + 256 * 1024
 
 
 def test_argmax_workspace_sizes(lib):

@@ -6,7 +6,8 @@ tests pin one at a time:
 * vector (16-byte) and scalar paths: sizes not a multiple of 8, and buffers
   misaligned by one fp16 element (a contiguous view at storage offset 1);
 * in-place and out-of-place calls;
-* split and whole rows for softmax / argmax;
+* split and whole rows for softmax / argmax, and many long softmax rows
+  (the persistent one-launch form, rows in rounds);
 * invalid ids and KV blocks;
 * ties, NaN and -inf in argmax rows.
 The bar is the same as everywhere: bit-exact for copies, RoPE and argmax;
@@ -140,8 +141,13 @@ def test_fuzz_softmax(mk, orc, dev, seed):
     D = (int(rng.integers(8192, 300000)) if split
          else int(rng.choice([int(rng.integers(1, 64)), int(rng.integers(64, 8192)),
                               8 * int(rng.integers(1, 1024))])))
-    if not split and rng.integers(0, 4) == 0:  # many rows of up to 65536 (register rows)
+    pick = int(rng.integers(0, 8)) if not split else -1
+    if pick in (0, 1):  # many rows of up to 65536 (register rows, or persistent past 32768)
         N, D = int(rng.integers(512, 1200)), 8 * int(rng.integers(1, 8193))
+    elif pick == 2:  # many long rows (persistent one-launch form; rounds of rows)
+        N, D = int(rng.integers(100, 900)), int(rng.integers(32769, 200000))
+        if rng.integers(0, 2):
+            D -= D % 8
     mis = bool(rng.integers(0, 4) == 0)
     inplace = bool(rng.integers(0, 4) == 0)
     _case(f"softmax seed={seed} N={N} D={D} misaligned={mis} inplace={inplace}")

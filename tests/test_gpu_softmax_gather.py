@@ -188,9 +188,9 @@ def test_softmax_onepass_epoch_past_32_bits(mk, orc, dev):
     _case("softmax one-pass epoch past 2^32")
     import torch
     rng = np.random.default_rng(58)
-    N, D, rec = 8, 40000, 1040 // 8
+    N, D, rec = 8, 40000, 2064 // 8  # 2064-byte row records
     ws = torch.zeros(mk.softmax_workspace_bytes(N, D), dtype=torch.uint8, device=dev)
-    e64 = ws[: 512 * 1040].view(torch.int64)
+    e64 = ws[: 512 * 2064].view(torch.int64)
     start = (1 << 32) - 3
     e64[0:N * rec:rec] = start
     for i in range(5):
@@ -227,3 +227,84 @@ def test_softmax_allocating_entry_paths(mk, orc, dev):
         y = mk.softmax(xd, stream=side)
         torch.cuda.current_stream().wait_stream(side)
         assert_close(to_host(y), orc.softmax(x, nthreads=8), what=f"side stream [{N},{D}]")
+
+
+def test_softmax_persistent_rows(mk, orc, dev):
+    """Many long rows in the persistent one-launch form (a resident grid of
+    chunk workgroups walking rows in rounds, the next row's loads in flight
+    during each exchange): the caller-workspace entry and the allocating
+    entry on stream 0, ragged last rounds, rows too many for the one-pass
+    grid below 512 rows, -inf entries, and an in-place call (a workgroup
+    per row)."""
+    _case("softmax persistent rows")
+    import torch
+    rng = np.random.default_rng(62)
+    shapes = ((512, 152064), (200, 152064), (1000, 70000), (700, 65544), (513, 100008),
+              (4100, 65600), (300, 40000), (256, 32776), (2048, 40000))
+    nb = max(mk.softmax_workspace_bytes(N, D) for N, D in shapes)
+    ws = torch.zeros(nb, dtype=torch.uint8, device=dev)
+    for N, D in shapes:
+        print(f"[case] persistent [{N},{D}]", flush=True)
+        x = normal_f16(rng, (N, D), 0, 4)
+        x[:, rng.integers(0, D, 16)] = -np.inf
+        ref = orc.softmax(x, nthreads=8)
+        xd = to_dev(x, dev)
+        assert_close(to_host(mk.softmax(xd, workspace=ws)), ref, what=f"workspace [{N},{D}]")
+        assert_close(to_host(mk.softmax(xd)), ref, what=f"stream 0 [{N},{D}]")
+        del xd
+    x = normal_f16(rng, (512, 152064), 0, 4)
+    ref = orc.softmax(x, nthreads=8)
+    xd = to_dev(x, dev)
+    assert_close(to_host(mk.softmax(xd, y=xd, workspace=ws)), ref, what="in place")
+
+
+def test_softmax_persistent_forced_fallback(mk, orc, dev):
+    """The persistent form with the poll bound forced to 0 from the host:
+    every chunk of every round computes its row's statistics from x.  Calls
+    afterwards, persistent and one-pass on the same records, stay right."""
+    _case("softmax persistent forced fallback")
+    import torch
+    rng = np.random.default_rng(63)
+    nb = max(mk.softmax_workspace_bytes(N, D) for N, D in ((64, 152064), (300, 152064)))
+    ws = torch.zeros(nb, dtype=torch.uint8, device=dev)
+    x = normal_f16(rng, (600, 100000), 0, 4)
+    ref = orc.softmax(x, nthreads=8)
+    xd = to_dev(x, dev)
+    prev = mk.softmax_test_poll_limit(0)
+    try:
+        assert_close(to_host(mk.softmax(xd, workspace=ws)), ref, what="forced fallback")
+    finally:
+        mk.softmax_test_poll_limit(prev)
+    for N, D in ((600, 100000), (64, 152064), (600, 100000), (300, 152064)):
+        x2 = normal_f16(rng, (N, D), 0, 4)
+        assert_close(to_host(mk.softmax(to_dev(x2, dev), workspace=ws)),
+                     orc.softmax(x2, nthreads=8), what=f"after fallback [{N},{D}]")
+
+
+def test_softmax_persistent_graph_replay(mk, orc, dev):
+    """The persistent form inside a captured graph, replayed several times
+    with eager calls on the same records in between."""
+    _case("softmax persistent graph replay [512,152064]")
+    import torch
+    rng = np.random.default_rng(64)
+    x = normal_f16(rng, (512, 152064), 0, 4)
+    xd = to_dev(x, dev)
+    ws = torch.zeros(mk.softmax_workspace_bytes(512, 152064), dtype=torch.uint8, device=dev)
+    y = torch.empty_like(xd)
+    ref = to_host(mk.softmax(xd, workspace=ws))
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        mk.softmax(xd, y=y, workspace=ws)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        mk.softmax(xd, y=y, workspace=ws)
+    for i in range(4):
+        y.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        assert_bits_equal(to_host(y), ref, what=f"replay {i}")
+        mk.softmax(xd, workspace=ws)
+    assert_close(ref, orc.softmax(x, nthreads=8), what="vs oracle")
