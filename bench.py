@@ -659,7 +659,7 @@ def shape_table(mk, dev, iters=40, warmup=5):
             lambda i: mk.qk_norm_rope(qs[i], ks[i], wq, wk, pos, inv), ns)
         del qs, ks
     for N, D in ((57344, 512), (16384, 2048), (8192, 4096), (2048, 32000), (256, 65536),
-                 (512, 152064)):
+                 (2048, 40000), (128, 152064), (512, 152064), (1024, 128256)):
         nb = 2 * N * D * 2
         ns = rotations(nb)
         sets = [(R((N, D), gen, dev, 0, 4), torch.empty((N, D), dtype=f16, device=dev))
