@@ -10,17 +10,17 @@
 //   * Many rows (N >= 512; N >= 256 up to 65536): whole rows, in registers
 //     where they fit (softmax_reg_kernel), else one workgroup per row whose
 //     write pass re-reads the row through L2.
-//   * Many rows longer than 32768 (N >= 512, or N >= 256 up to 65536, or
-//     too many rows for the one-launch grid below): with row records and
-//     y != x, softmax_stream_kernel -- a resident grid of chunk workgroups
-//     walking the rows in rounds, one read of x, the next row's loads in
-//     flight during each exchange.
-//   * Few long rows (the LM-head case, 64 x 152064): one workgroup per row
-//     would light up 64 of 256 CUs, so each row is cut into chunks.  With
-//     row records -- a caller workspace, or on stream 0 a region the library
-//     holds -- and y != x, one launch (softmax_onepass_kernel, below): chunks
-//     stay in registers and exchange their (max, sum) through tagged per-row
-//     records.  Otherwise two launches, with `splits` chunks:
+//   * Few long rows (the LM-head case, 64 x 152064), and many rows longer
+//     than 32768 (N >= 512, or N >= 256 up to 65536): one workgroup per row
+//     would light up few CUs or re-read the row, so each row is cut into
+//     8192-element chunks.  With row records -- a caller workspace, or on
+//     stream 0 a region the library holds -- and y != x, one launch
+//     (softmax_stream_kernel, below): a resident grid of chunk workgroups
+//     holds the chunks in registers and exchanges their (max, sum) through
+//     tagged per-row records, walking the rows in rounds when they are more
+//     than the grid holds, with the next row's loads in flight during each
+//     exchange.  Otherwise many rows take a workgroup per row, and few rows
+//     two launches with `splits` chunks:
 //     Kernel 1 writes a (max, sum) pair per chunk to a small stream-ordered
 //     workspace (8 bytes per chunk), from tiles whose loads are all issued
 //     first (one HBM wait per tile), a packed fp16 lane maximum and one exp
@@ -368,31 +368,40 @@ __global__ __launch_bounds__(256) void softmax_finish_kernel(const half_t* x, ha
 }
 
 // ---------------------------------------------------------------------------
-// One-pass split rows (mi_softmax_ws_f16 with x != y): each workgroup holds
-// its 8192-element chunk in registers, publishes the chunk's (max, sum), and
-// reads every chunk's pair of its row to finish -- one launch, one read of x,
-// no atomics on a contended address.
+// One-launch split rows (row records: mi_softmax_ws_f16, or stream 0; x != y):
+// each workgroup holds an 8192-element chunk of a row in registers, publishes
+// the chunk's (max, sum), and reads every chunk's pair of its row to finish --
+// one launch, one read of x, no atomics on a contended address.  The grid is
+// `chunks per row` x R row slots, all resident; slot r handles rows r, r + R,
+// ... in rounds (one round when every row fits), and issues its next row's
+// loads before it polls for the current row's statistics.
 //
 // Workspace (zero before first use; every call leaves it valid for the
-// next): row r owns a fixed record at r * kRowRecordBytes -- a 64-bit epoch
-// word (16-byte header), then kOnePassMaxSplits slots of two 64-bit words
-// {tag << 32 | bits(max)}, {tag << 32 | bits(sum)}, tag = the low 32 bits of
-// epoch + 1.  A call reads the row's epoch E; every chunk publishes its pair
-// tagged E + 1 and polls the row's slots until all carry that tag.  Because
-// slots are fixed per (row, chunk) whatever the call's shape, and a row's
-// epoch only grows (64 bits: it cannot wrap), a slot left by an earlier call
-// never carries the tag a later call waits for -- short of a slot left
-// unwritten for 2^32 of its row's epochs and read again at exactly a
-// multiple of 2^32 later:
-//   * the chunk-0 workgroup raises the epoch to E + 1 (atomic max, one per
-//     row) after it has seen every slot tagged E + 1 -- so every workgroup of
-//     the row has already read E;
+// next): row slot r owns a fixed record at r * kRowRecordBytes -- a 64-bit
+// epoch word (16-byte header), then two sets of kOnePassMaxSplits slots of
+// two 64-bit words {tag << 32 | bits(max)}, {tag << 32 | bits(sum)}.  A call
+// reads the slot's epoch E; round k publishes into set k & 1 with tag = the
+// low 32 bits of E + 1 + k and polls the set until every chunk's pair carries
+// that tag.  Because slots are fixed per (row slot, chunk) whatever the
+// call's shape, and an epoch only grows (64 bits: it cannot wrap), a slot
+// left by an earlier call never carries the tag a later call waits for --
+// short of a slot left unwritten for 2^32 of its epochs and read again at
+// exactly a multiple of 2^32 later:
+//   * the chunk-0 workgroup raises the epoch to E + K (atomic max) after the
+//     last (K-th) round, when every workgroup of the slot has published it --
+//     so every one of them has already read E;
 //   * a workgroup whose polling runs out (kPollLimit; not expected when the
-//     grid fits the GPU) computes the row's statistics itself from x and
-//     raises the epoch to E + 2, so no tag written in this call can pass for
-//     fresh later.  Polling is bounded: no workgroup can wait forever.
-// Each 64-bit word is stored and loaded whole at device scope (write-through
-// stores, L2-bypassing loads), so a tag always travels with its value.
+//     grid fits the GPU) computes that row's statistics itself from x and
+//     raises the epoch to E + K + 1 at once, past every tag the launch writes
+//     for the slot.  A workgroup that starts after that reads the higher
+//     epoch, its tags match nobody's, and it takes the same fallback for its
+//     rows: slower, still correct.  Polling is bounded: no workgroup can wait
+//     forever.
+// A workgroup publishes round k + 2 into a set only after it has seen every
+// chunk's round k + 1 pair, which its row-mates publish after they have read
+// round k: no pair is overwritten before it is read.  Each 64-bit word is
+// stored and loaded whole at device scope (write-through stores, L2-bypassing
+// loads), so a tag always travels with its value.
 // ---------------------------------------------------------------------------
 constexpr int kOnePassMaxSplits = 64;
 #ifndef MI_SOFTMAX_ONEPASS_U
@@ -400,8 +409,7 @@ constexpr int kOnePassMaxSplits = 64;
 #endif
 constexpr int kOnePassU = MI_SOFTMAX_ONEPASS_U;     // vectors per lane
 constexpr int64_t kOnePassChunk = 2048 * kOnePassU;  // elements per workgroup
-// header, then two sets of slot pairs (the persistent kernel alternates
-// them by round; the one-pass kernel uses the first)
+// header, then two sets of slot pairs (alternated by round)
 constexpr int64_t kRowRecordBytes = 16 + 2 * kOnePassMaxSplits * 16;
 constexpr int kPollLimit = 1 << 16;
 std::atomic<int> g_poll_limit{kPollLimit};  // mi_softmax_test_poll_limit
@@ -411,15 +419,6 @@ __device__ __forceinline__ uint64_t tagged(uint32_t tag, float v) {
 }
 
 // The pieces of a one-launch chunk workgroup.
-// Loads the chunk [b, e) of a row, U vectors per lane, -inf past e.
-template <int U>
-__device__ __forceinline__ void chunk_load(const half_t* xr, int64_t b, int64_t e, h8 (&a)[U]) {
-#pragma unroll
-    for (int j = 0; j < U; ++j) {
-        const int64_t i = b + (threadIdx.x + j * 256) * 8;
-        a[j] = i < e ? ld8(xr + i) : h8(-__builtin_huge_valf16());
-    }
-}
 // The lane's (max, sum) over its vectors: packed fp16 maximum, one exp per
 // element.
 template <int U>
@@ -504,80 +503,6 @@ __device__ __forceinline__ void row_stats_from_x(const half_t* xr, int64_t D, fl
     M = fm;
     S = fs;
 }
-template <int U>
-__device__ __forceinline__ void chunk_store(const h8 (&a)[U], half_t* yr, int64_t b, int64_t e,
-                                            float M, float inv) {
-#pragma unroll
-    for (int j = 0; j < U; ++j) {
-        const int64_t i = b + (threadIdx.x + j * 256) * 8;
-        if (i < e) {
-            h8 o;
-#pragma unroll
-            for (int k = 0; k < 8; ++k) o[k] = to_half(fast_exp((float)a[j][k] - M) * inv);
-            st8_out<MI_WT_SM>(yr + i, o);
-        }
-    }
-}
-
-__global__ __launch_bounds__(256) void softmax_onepass_kernel(const half_t* x, half_t* y,
-                                                              unsigned char* ws, int64_t D,
-                                                              int poll_limit) {
-    constexpr int U = kOnePassU;
-    __shared__ float slots[256 / kWave];
-    __shared__ float row_stats[3];  // M, S, fallback flag
-    __shared__ uint64_t epoch_sh;
-    const int split = blockIdx.x, splits = gridDim.x;
-    const int64_t row = blockIdx.y;
-    unsigned char* rec = ws + row * kRowRecordBytes;
-    uint64_t* epoch = reinterpret_cast<uint64_t*>(rec);
-    uint64_t* slot = reinterpret_cast<uint64_t*>(rec + 16);
-    const half_t* xr = x + row * D;
-    const int64_t b = split * kOnePassChunk;
-    const int64_t e = b + kOnePassChunk < D ? b + kOnePassChunk : D;
-
-    if (threadIdx.x == 0)
-        epoch_sh = __hip_atomic_load(epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    h8 a[U];
-    chunk_load<U>(xr, b, e, a);
-    float m, s;
-    chunk_lane_stats<U>(a, m, s);
-    block_merge(m, s, slots);  // barriers: epoch_sh is visible after this
-    const uint64_t E = epoch_sh;
-    const uint32_t tag = static_cast<uint32_t>(E + 1);
-    chunk_publish(slot, split, tag, m, s, 0);
-    if (threadIdx.x < kWave) row_poll(slot, splits, tag, poll_limit, row_stats);
-    __syncthreads();
-    float M = row_stats[0], S = row_stats[1];
-    const bool fallback = row_stats[2] != 0.0f;
-    if (fallback) row_stats_from_x(xr, D, M, S, slots);
-    if (threadIdx.x == 0 && (split == 0 || fallback))
-        __hip_atomic_fetch_max(epoch, fallback ? E + 2 : E + 1, __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
-    chunk_store<U>(a, y + row * D, b, e, M, 1.0f / S);
-}
-
-// ---------------------------------------------------------------------------
-// Persistent one-launch form, for more rows than can hold every chunk
-// workgroup resident at once (softmax_onepass_kernel's condition): a grid of
-// `splits` x R workgroups, all resident, where row slot r (blockIdx.y) walks
-// rows r, r + R, r + 2R, ...  While a round's chunk statistics are exchanged,
-// the workgroup already has the loads of its next row's chunk in flight, so
-// the exchange latency overlaps HBM reads instead of idling the CU.
-//
-// Records: row slot r uses the record of row r (same header and epoch as the
-// one-pass kernel), with two sets of slot pairs used by round parity.  A
-// workgroup can only publish round k + 2 into a set after it has seen every
-// chunk's round k + 1 pair, which its row-mates publish after they have read
-// round k: no pair is overwritten before it is read.  Round k's tag is the
-// low 32 bits of E + 1 + k (E = the epoch read at the start); the chunk-0
-// workgroup raises the epoch to E + K after the last (K-th) round, when every
-// workgroup of the slot has published it (and so has read E).  A workgroup
-// whose polling runs out computes that row's statistics from x and raises
-// the epoch to E + K + 1 at once, past every tag this launch writes for the
-// slot: a workgroup that starts after that reads the higher epoch, its tags
-// then match nobody's and it takes the same fallback for its rows --
-// slower, still correct, and bounded.
-// ---------------------------------------------------------------------------
 // The persistent kernel's per-lane view of its chunk: the same in every
 // round, so one 32-bit byte offset (rows are < 2^31 bytes) and a valid flag
 // per vector, against a row base that is uniform across the workgroup.
@@ -739,22 +664,9 @@ enum class Ws {
     kRecords,           // the one-pass row records only (library-held, stream 0)
 };
 
-// Whether [N, D] runs as the one-launch split form given row records: every
-// chunk workgroup of the grid resident at once (no chunk polls for a
-// row-mate still queued), aligned rows, and y != x (the fallback re-reads x).
-bool onepass_ok(const void* x, const void* y, int64_t N, int64_t D) {
-    int64_t splits, chunk;
-    if (!MI_SOFTMAX_ONEPASS || plan(N, D, splits, chunk) != Plan::kTwoPass) return false;
-    const int64_t sp1 = ceil_div(D, kOnePassChunk);
-    return D % 8 == 0 && aligned16(x) && aligned16(y) && x != y && sp1 <= kOnePassMaxSplits &&
-           N <= 65535 &&
-           sp1 * N <= resident_workgroups(reinterpret_cast<const void*>(softmax_onepass_kernel),
-                                          256);
-}
-
-// Rows of the persistent kernel's grid: as many as stay resident next to
-// each other with every chunk of a row (at most the record rows).
-int64_t stream_rows(int64_t N, int64_t D) {
+// Rows of the one-launch grid: as many as stay resident next to each other
+// with every chunk of a row (at most the record rows).
+int64_t onelaunch_rows(int64_t N, int64_t D) {
     const int64_t sp1 = ceil_div(D, kOnePassChunk);
     int64_t R = resident_workgroups(reinterpret_cast<const void*>(softmax_stream_kernel), 256) / sp1;
     if (R > N) R = N;
@@ -762,22 +674,14 @@ int64_t stream_rows(int64_t N, int64_t D) {
     return R;
 }
 
-// Whether [N, D] runs as softmax_stream_kernel given row records: a kStream
-// shape, or a split shape too large for the one-pass grid; aligned rows,
-// y != x (the fallback re-reads x), 2..64 chunks per row.
-bool stream_ok(const void* x, const void* y, int64_t N, int64_t D) {
+// Whether [N, D] runs as the one-launch form given row records: a split or
+// kStream shape, aligned rows, y != x (the fallback re-reads x), at most 64
+// chunks per row.
+bool onelaunch_ok(const void* x, const void* y, int64_t N, int64_t D) {
     int64_t splits, chunk;
-    const Plan p = plan(N, D, splits, chunk);
-    if (!MI_SOFTMAX_STREAM || p == Plan::kRow) return false;
-    if (p == Plan::kTwoPass && onepass_ok(x, y, N, D)) return false;
-    const int64_t sp1 = ceil_div(D, kOnePassChunk);
-    return D % 8 == 0 && aligned16(x) && aligned16(y) && x != y && sp1 >= 2 &&
-           sp1 <= kOnePassMaxSplits && stream_rows(N, D) >= 1;
-}
-
-// Whether a call of this shape uses row records (one-pass or persistent).
-bool records_ok(const void* x, const void* y, int64_t N, int64_t D) {
-    return onepass_ok(x, y, N, D) || stream_ok(x, y, N, D);
+    if (!MI_SOFTMAX_ONEPASS || plan(N, D, splits, chunk) == Plan::kRow) return false;
+    return D % 8 == 0 && aligned16(x) && aligned16(y) && x != y &&
+           ceil_div(D, kOnePassChunk) <= kOnePassMaxSplits && onelaunch_rows(N, D) >= 1;
 }
 
 int softmax_checked(const void* x, void* y, int64_t N, int64_t D, void* ws, int64_t ws_bytes,
@@ -790,12 +694,11 @@ int softmax_checked(const void* x, void* y, int64_t N, int64_t D, void* ws, int6
     if (x != y && overlaps(x, bytes, y, bytes)) return MI_ERR_ALIASING;
     int64_t splits, chunk;
     const Plan p = plan(N, D, splits, chunk);
-    const bool onepass = layout != Ws::kPairs && onepass_ok(x, y, N, D);
-    const bool persistent = layout != Ws::kPairs && stream_ok(x, y, N, D);
-    if (layout == Ws::kRecords && p == Plan::kTwoPass && !onepass && !persistent)
-        return MI_ERR_UNSUPPORTED;  // no pairs to fall back on (callers check records_ok)
+    const bool onelaunch = layout != Ws::kPairs && onelaunch_ok(x, y, N, D);
+    if (layout == Ws::kRecords && p == Plan::kTwoPass && !onelaunch)
+        return MI_ERR_UNSUPPORTED;  // no pairs to fall back on (callers check onelaunch_ok)
     const int64_t need = p == Plan::kRow ? 0
-                         : p == Plan::kStream ? (persistent ? kOnePassRegion : 0)
+                         : p == Plan::kStream ? (onelaunch ? kOnePassRegion : 0)
                          : layout == Ws::kPairs ? twopass_bytes(N, D)
                          : layout == Ws::kRecords ? kOnePassRegion
                                                   : workspace_bytes(N, D);
@@ -809,7 +712,7 @@ int softmax_checked(const void* x, void* y, int64_t N, int64_t D, void* ws, int6
     auto* yh = static_cast<half_t*>(y);
     const hipStream_t s = as_stream(stream);
     const bool vec = D % 8 == 0 && aligned16(x) && aligned16(y);
-    if (p == Plan::kRow || (p == Plan::kStream && !persistent)) {
+    if (p == Plan::kRow || (p == Plan::kStream && !onelaunch)) {
         int G = 0, VPT = 0;
         if (MI_SOFTMAX_REG && vec && reg_shape(D / 8, G, VPT) &&
             ceil_div(N, (G > 256 ? G : 256) / G) <= kMaxGridX) {
@@ -831,19 +734,12 @@ int softmax_checked(const void* x, void* y, int64_t N, int64_t D, void* ws, int6
             softmax_row_kernel<1><<<dim3(static_cast<unsigned>(N)), dim3(threads), 0, s>>>(xh, yh, D);
         return launch_status();
     }
-    if (persistent) {
+    if (onelaunch) {
         const int64_t sp1 = ceil_div(D, kOnePassChunk);
-        const int64_t R = stream_rows(N, D);
+        const int64_t R = onelaunch_rows(N, D);
         softmax_stream_kernel<<<dim3(static_cast<unsigned>(sp1), static_cast<unsigned>(R)),
                                 dim3(256), 0, s>>>(xh, yh, static_cast<unsigned char*>(ws), N, D,
                                                    g_poll_limit.load());
-        return launch_status();
-    }
-    if (onepass) {
-        const int64_t sp1 = ceil_div(D, kOnePassChunk);
-        softmax_onepass_kernel<<<dim3(static_cast<unsigned>(sp1), static_cast<unsigned>(N)),
-                                 dim3(256), 0, s>>>(xh, yh, static_cast<unsigned char*>(ws), D,
-                                                    g_poll_limit.load());
         return launch_status();
     }
     auto* part = reinterpret_cast<float*>(static_cast<unsigned char*>(ws) +
@@ -881,7 +777,7 @@ extern "C" int mi_softmax_f16(const void* x, void* y, int64_t N, int64_t D, void
     const hipStream_t s = mi::as_stream(stream);
     // Long split rows on the default stream (every caller in the reference
     // passes 0): one launch, with row records the library holds for stream 0.
-    if (x && y && N > 0 && D > 0 && N <= mi::kMaxGridX && mi::records_ok(x, y, N, D)) {
+    if (x && y && N > 0 && D > 0 && N <= mi::kMaxGridX && mi::onelaunch_ok(x, y, N, D)) {
         void* rec = mi::default_stream_region(mi::kRegionSoftmax, mi::kOnePassRegion, s);
         if (rec)
             return mi::softmax_checked(x, y, N, D, rec, mi::kOnePassRegion, mi::Ws::kRecords,
