@@ -338,10 +338,10 @@ int64_t argmax_splits(int64_t B, int64_t V, int64_t& chunk) {
 // One-launch split rows (mi_greedy_argmax_ws_f16): every chunk workgroup
 // publishes its best key to a fixed per-row record and exits; only chunk 0
 // of each row waits, polls the row's records, and writes the index.  The
-// record scheme is the one-pass softmax's (64-bit epoch, slots tagged with the
-// low 32 bits of epoch + 1,
-// chunk 0 raises the epoch once it has seen every slot; a poll that runs out
-// makes chunk 0 scan the whole row itself and raise the epoch by 2).  A key
+// record scheme is the one-launch softmax's with a single round and a single
+// slot set (64-bit epoch E, slots tagged with the low 32 bits of E + 1;
+// chunk 0 raises the epoch to E + 1 once it has seen every slot; a poll that
+// runs out makes chunk 0 scan the whole row itself and raise it to E + 2).  A key
 // travels as two 64-bit words {tag << 32 | key >> 32}, {tag << 32 | key
 // & 0xffffffff}, each stored and loaded whole at device scope.  The workspace
 // must be zero before its first use.
