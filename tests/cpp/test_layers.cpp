@@ -16,6 +16,7 @@
 #include <functional>
 #include <stdexcept>
 #include <string>
+#include <utility>
 #include <vector>
 
 #include "core/tensor.h"
@@ -265,6 +266,23 @@ void gpu_checks() {
         mini_infer::kernels::launch_softmax(static_cast<const __half*>(xd.data()),
                                             static_cast<__half*>(yd.data()), N, D, 0);
         EXPECT(close(yd, ref, "launch_softmax [8,1024]"), "softmax");
+        // split rows on stream 0: one launch with the library-held row records
+        // (few long rows in one round; many long rows in rounds)
+        for (const auto& nd : {std::pair<int, int>{64, 152064}, std::pair<int, int>{300, 40000}}) {
+            const int n = nd.first, d = nd.second;
+            Tensor lx = reftest_f16({n, d}, 4.0f, 556);
+            std::vector<float> lref(static_cast<size_t>(n) * d);
+            mio_softmax(bits(lx), lref.data(), n, d, 8);
+            Tensor lxd = lx.to(Device::cuda(0));
+            Tensor lyd = Tensor::empty({n, d}, DType::FP16, Device::cuda(0));
+            for (int rep = 0; rep < 2; ++rep) {  // the records carry over between calls
+                mini_infer::kernels::launch_softmax(static_cast<const __half*>(lxd.data()),
+                                                    static_cast<__half*>(lyd.data()), n, d, 0);
+                char what[64];
+                std::snprintf(what, sizeof what, "launch_softmax [%d,%d] call %d", n, d, rep);
+                EXPECT(close(lyd, lref, what), "softmax split rows");
+            }
+        }
 
         Tensor gx = reftest_f16({4096}, 2.0f, 13);  // tests/test_gelu/main.cpp:64-67
         std::vector<float> gref(4096);
