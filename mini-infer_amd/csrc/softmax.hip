@@ -441,17 +441,17 @@ __device__ __forceinline__ void chunk_lane_stats(const h8 (&a)[U], float& m, flo
         m = -INFINITY;  // NaN-free lane maximum of an all -inf (or NaN) lane
     }
 }
-// Thread `who` publishes the chunk's pair into slot pair `split` of `slots`.
+// Thread 0 publishes the chunk's pair into slot pair `split` of `slots`.
 __device__ __forceinline__ void chunk_publish(uint64_t* slots, int split, uint32_t tag, float m,
-                                              float s, unsigned who) {
-    if (threadIdx.x == who) {
+                                              float s) {
+    if (threadIdx.x == 0) {
         __hip_atomic_store(&slots[2 * split], tagged(tag, m), __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_AGENT);
         __hip_atomic_store(&slots[2 * split + 1], tagged(tag, s), __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_AGENT);
     }
 }
-// One wave (the caller's choice) polls the row's `splits` slot pairs (lane j
+// Wave 0 (the caller calls it there) polls the row's `splits` slot pairs (lane j
 // reads chunk j) until all carry `tag`, at most poll_limit rounds, and leaves
 // the row's (M, S) in row_stats[0..1] and row_stats[2] = 0, or
 // row_stats[2] = 1 when polling ran out.  The caller's barrier publishes
@@ -493,11 +493,10 @@ __device__ __forceinline__ void row_poll(const uint64_t* slots, int splits, uint
 }
 // The row's statistics from x itself (the fallback when polling runs out; x
 // is not written: y != x).  Barriers: called by the whole workgroup.
-// Lanes 0..255 read x; other lanes of the workgroup only join the merge.
 __device__ __forceinline__ void row_stats_from_x(const half_t* xr, int64_t D, float& M, float& S,
                                                  float* slots) {
     float fm = -INFINITY, fs = 0.0f;
-    if (threadIdx.x < 256) tile_stats<2>(xr, 0, D, fm, fs);
+    tile_stats<2>(xr, 0, D, fm, fs);
     __syncthreads();  // slots reused
     block_merge(fm, fs, slots);
     M = fm;
@@ -570,7 +569,7 @@ __global__ __launch_bounds__(256) void softmax_stream_kernel(const half_t* x, ha
         const uint64_t E = epoch_sh;
         const uint32_t tag = static_cast<uint32_t>(E + 1 + k);
         uint64_t* set = sets + (k & 1) * (2 * kOnePassMaxSplits);
-        chunk_publish(set, split, tag, m, s, 0);
+        chunk_publish(set, split, tag, m, s);
         if (k + 1 < K) lane_load<U>(x + (row + R) * D, lo, ok, n);
         if (threadIdx.x < kWave) row_poll(set, splits, tag, poll_limit, row_stats);
         __syncthreads();
