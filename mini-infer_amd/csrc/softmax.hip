@@ -534,10 +534,12 @@ __device__ __forceinline__ void lane_store(const h8 (&a)[U], half_t* row, uint32
 // indices: 68 VGPRs and 7 workgroups per CU with them measured 5-10 points
 // lower; amdgpu_waves_per_eu(8) also measured ~8 points lower at the same
 // 64 VGPRs); wave 0 publishes and polls.
+// U vectors per lane: chunks of 2048 * U elements.
+template <int U>
 __global__ __launch_bounds__(256) void softmax_stream_kernel(const half_t* x, half_t* y,
                                                              unsigned char* ws, int64_t N,
                                                              int64_t D, int poll_limit) {
-    constexpr int U = kOnePassU;
+    constexpr int64_t kChunk = 2048 * U;
     __shared__ float slots[256 / kWave];
     __shared__ float row_stats[3];  // M, S, fallback flag
     __shared__ uint64_t epoch_sh;
@@ -547,8 +549,8 @@ __global__ __launch_bounds__(256) void softmax_stream_kernel(const half_t* x, ha
     uint64_t* epoch = reinterpret_cast<uint64_t*>(rec);
     uint64_t* sets = reinterpret_cast<uint64_t*>(rec + 16);
     const int64_t K = (N - r0 + R - 1) / R;  // rounds of this row slot (>= 1)
-    const int64_t b = split * kOnePassChunk;
-    const int64_t e = b + kOnePassChunk < D ? b + kOnePassChunk : D;
+    const int64_t b = split * kChunk;
+    const int64_t e = b + kChunk < D ? b + kChunk : D;
     const uint32_t lo = static_cast<uint32_t>(b + threadIdx.x * 8) * 2;
     bool ok[U];
 #pragma unroll
@@ -663,11 +665,32 @@ enum class Ws {
     kRecords,           // the one-pass row records only (library-held, stream 0)
 };
 
+// Vectors per lane of the one-launch chunks: kOnePassU (8192 elements), or
+// half that when the larger chunks would leave fewer than
+// MI_SOFTMAX_SMALL_CHUNK_WGS workgroups in the launch (measured +1.4 to +2.2
+// points at [200, 32000], [100, 40000], [32, 152064]; 2048 cost [64, 152064]
+// 6 points, as its 38 smaller chunks per row no longer fit in one round).
+#ifndef MI_SOFTMAX_SMALL_CHUNK_WGS
+#define MI_SOFTMAX_SMALL_CHUNK_WGS 1024
+#endif
+int onelaunch_u(int64_t N, int64_t D) {
+    constexpr int kSmall = kOnePassU / 2;
+    if (N * ceil_div(D, kOnePassChunk) < MI_SOFTMAX_SMALL_CHUNK_WGS &&
+        ceil_div(D, 2048 * kSmall) <= kOnePassMaxSplits)
+        return kSmall;
+    return kOnePassU;
+}
+const void* onelaunch_kernel(int u) {
+    return u == kOnePassU ? reinterpret_cast<const void*>(softmax_stream_kernel<kOnePassU>)
+                          : reinterpret_cast<const void*>(softmax_stream_kernel<kOnePassU / 2>);
+}
+
 // Rows of the one-launch grid: as many as stay resident next to each other
 // with every chunk of a row (at most the record rows).
 int64_t onelaunch_rows(int64_t N, int64_t D) {
-    const int64_t sp1 = ceil_div(D, kOnePassChunk);
-    int64_t R = resident_workgroups(reinterpret_cast<const void*>(softmax_stream_kernel), 256) / sp1;
+    const int u = onelaunch_u(N, D);
+    const int64_t sp1 = ceil_div(D, 2048 * u);
+    int64_t R = resident_workgroups(onelaunch_kernel(u), 256) / sp1;
     if (R > N) R = N;
     if (R > kSplitMaxRows) R = kSplitMaxRows;
     return R;
@@ -680,7 +703,8 @@ bool onelaunch_ok(const void* x, const void* y, int64_t N, int64_t D) {
     int64_t splits, chunk;
     if (!MI_SOFTMAX_ONEPASS || plan(N, D, splits, chunk) == Plan::kRow) return false;
     return D % 8 == 0 && aligned16(x) && aligned16(y) && x != y &&
-           ceil_div(D, kOnePassChunk) <= kOnePassMaxSplits && onelaunch_rows(N, D) >= 1;
+           ceil_div(D, 2048 * onelaunch_u(N, D)) <= kOnePassMaxSplits &&
+           onelaunch_rows(N, D) >= 1;
 }
 
 int softmax_checked(const void* x, void* y, int64_t N, int64_t D, void* ws, int64_t ws_bytes,
@@ -734,11 +758,16 @@ int softmax_checked(const void* x, void* y, int64_t N, int64_t D, void* ws, int6
         return launch_status();
     }
     if (onelaunch) {
-        const int64_t sp1 = ceil_div(D, kOnePassChunk);
-        const int64_t R = onelaunch_rows(N, D);
-        softmax_stream_kernel<<<dim3(static_cast<unsigned>(sp1), static_cast<unsigned>(R)),
-                                dim3(256), 0, s>>>(xh, yh, static_cast<unsigned char*>(ws), N, D,
-                                                   g_poll_limit.load());
+        const int u = onelaunch_u(N, D);
+        const dim3 g(static_cast<unsigned>(ceil_div(D, 2048 * u)),
+                     static_cast<unsigned>(onelaunch_rows(N, D)));
+        auto* rec = static_cast<unsigned char*>(ws);
+        if (u == kOnePassU)
+            softmax_stream_kernel<kOnePassU><<<g, dim3(256), 0, s>>>(xh, yh, rec, N, D,
+                                                                    g_poll_limit.load());
+        else
+            softmax_stream_kernel<kOnePassU / 2><<<g, dim3(256), 0, s>>>(xh, yh, rec, N, D,
+                                                                        g_poll_limit.load());
         return launch_status();
     }
     auto* part = reinterpret_cast<float*>(static_cast<unsigned char*>(ws) +
