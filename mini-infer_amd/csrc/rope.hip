@@ -45,6 +45,18 @@ namespace {
 
 constexpr int kMaxHalf = 256;  // head_dim <= 512
 
+// LDS position of element i of a half-row of n entries (n a multiple of 8),
+// for lanes that each read the 8 entries c*8 .. c*8+7 as two 16-byte LDS
+// reads: entries 0-3 of every lane's group sit together in the first n/2
+// slots and entries 4-7 in the second, so lane c reads slots 4c .. 4c+3 and
+// n/2 + 4c .. n/2 + 4c+3.  Eight consecutive lanes then cover 32 distinct
+// banks per read; with the plain layout (lane c at 8c) lanes c and c+4 fall
+// on the same banks and every read took a second pass (rocprof
+// LdsBankConflict 0.97 conflicts per access).
+__device__ __forceinline__ int quad_split(int i, int n) {
+    return ((i & 4) ? (n >> 1) : 0) + ((i >> 3) << 2) + (i & 3);
+}
+
 // Host-computed inverse frequencies travel by value in the kernel arguments.
 struct InvFreq {
     float v[kMaxHalf];
@@ -142,7 +154,8 @@ __attribute__((amdgpu_waves_per_eu(TPW == 8 ? 4 : 1))) void rope_kernel(const ha
             src = k_in + base;
             dst = k_out + base;
         }
-        return t * (2 * kMaxHalf) + c * VEC;  // offset of this unit's cos in cs
+        // offset of this unit's first cos entry in cs (quad_split layout for VEC = 8)
+        return t * (2 * kMaxHalf) + (VEC == 8 ? c * 4 : c * VEC);
     };
 
     // 1. issue up to TPW units' loads per lane before the table work,
@@ -178,8 +191,9 @@ __attribute__((amdgpu_waves_per_eu(TPW == 8 ? 4 : 1))) void rope_kernel(const ha
             hc = cos_t[tok * half + i];
             hs = sin_t[tok * half + i];
         }
-        cs[t][i] = (float)hc;
-        cs[t][kMaxHalf + i] = (float)hs;
+        const int li = VEC == 8 ? quad_split(i, half) : i;
+        cs[t][li] = (float)hc;
+        cs[t][kMaxHalf + li] = (float)hs;
     }
     __syncthreads();
 
@@ -192,8 +206,10 @@ __attribute__((amdgpu_waves_per_eu(TPW == 8 ? 4 : 1))) void rope_kernel(const ha
         typename V::T y1, y2;
 #pragma unroll
         for (int k = 0; k < VEC; ++k) {
-            const float cv = csf[off + k];
-            const float sv = csf[off + kMaxHalf + k];
+            // VEC = 8: entries 4-7 sit half/2 slots on (quad_split)
+            const int kk = (VEC == 8 && (k & 4)) ? ((half >> 3) << 2) + (k & 3) : k;
+            const float cv = csf[off + kk];
+            const float sv = csf[off + kMaxHalf + kk];
             const float a = elem<VEC>(a1, k), b = elem<VEC>(a2, k);
             set_elem<VEC>(y1, k, fp32_rounded(a * cv - b * sv));
             set_elem<VEC>(y2, k, fp32_rounded(b * cv + a * sv));
@@ -373,7 +389,9 @@ __global__ __launch_bounds__(256) void qk_norm_rope_pipe_kernel(
     __shared__ float wt[2][HD];
     for (int i = threadIdx.x; i < 2 * HD; i += 256) {
         const int r = i / HD, j = i - r * HD;
-        wt[r][j] = (r == 0 || Hkv > 0) ? (float)(r == 0 ? wq : wk)[j] + w_bias : 0.0f;
+        const int hh = j >= HALF ? HALF : 0;  // quad_split within each half
+        wt[r][hh + quad_split(j - hh, HALF)] =
+            (r == 0 || Hkv > 0) ? (float)(r == 0 ? wq : wk)[j] + w_bias : 0.0f;
     }
     const int upt = (Hq + Hkv) * CPH;
     const int c = threadIdx.x & (CPH - 1);
@@ -425,8 +443,9 @@ __global__ __launch_bounds__(256) void qk_norm_rope_pipe_kernel(
         if (tab_on) {
             half_t hc, hs;
             cos_sin_half(static_cast<float>(pos) * tab_f, hc, hs);
-            tab[threadIdx.x] = (float)hc;
-            tab[kTab + threadIdx.x] = (float)hs;
+            const int li = tab_t * HALF + quad_split(threadIdx.x - tab_t * HALF, HALF);
+            tab[li] = (float)hc;
+            tab[kTab + li] = (float)hs;
         }
     };
     auto process = [&](int64_t g, const float* tab, const h8* a1, const h8* a2) {
@@ -443,14 +462,17 @@ __global__ __launch_bounds__(256) void qk_norm_rope_pipe_kernel(
             ss = group_sum<CPH>(ss);
             if (!slot_on[p] || tok0 + slot_t[p] >= T) continue;
             const float rrms = rsqrtf(ss / static_cast<float>(HD) + eps);
-            const float* w = &wt[slot_k[p] ? 1 : 0][c * 8];
-            const float* cst = tab + slot_t[p] * HALF + c * 8;
+            // weights and table in the quad_split layout: entry e of this
+            // lane's group at c*4 + (e & 3), plus HALF/2 for e >= 4
+            const float* w = &wt[slot_k[p] ? 1 : 0][c * 4];
+            const float* cst = tab + slot_t[p] * HALF + c * 4;
             h8 y1, y2;
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
-                const float v1 = (float)to_half((float)a1[p][e] * rrms * w[e]);
-                const float v2 = (float)to_half((float)a2[p][e] * rrms * w[HALF + e]);
-                const float cv = cst[e], sv = cst[kTab + e];
+                const int le = (e & 4) ? HALF / 2 + (e & 3) : e;
+                const float v1 = (float)to_half((float)a1[p][e] * rrms * w[le]);
+                const float v2 = (float)to_half((float)a2[p][e] * rrms * w[HALF + le]);
+                const float cv = cst[le], sv = cst[kTab + le];
                 y1[e] = to_half(fp32_rounded(v1 * cv - v2 * sv));
                 y2[e] = to_half(fp32_rounded(v2 * cv + v1 * sv));
             }
