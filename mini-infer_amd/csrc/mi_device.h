@@ -61,8 +61,11 @@ __device__ __forceinline__ void st8_stream(half_t* p, h8 v) {
 // see a store inside inline asm, so the asm carries the wait states itself
 // (without them, following VALU code overwrote the data before the store
 // read it).
+#ifndef MI_WT_BITS
+#define MI_WT_BITS "nt sc1"
+#endif
 __device__ __forceinline__ void st8_stream_wt(half_t* p, h8 v) {
-    asm volatile("global_store_dwordx4 %0, %1, off nt sc1\n\ts_nop 1" : : "v"(p), "v"(v)
+    asm volatile("global_store_dwordx4 %0, %1, off " MI_WT_BITS "\n\ts_nop 1" : : "v"(p), "v"(v)
                  : "memory");
 }
 // Store selected per kernel at compile time.
