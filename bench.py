@@ -106,31 +106,135 @@ def randn16(shape, gen, dev, mean=0.0, std=1.0):
     return (torch.randn(shape, generator=gen, device=dev, dtype=torch.float32) * std + mean).half()
 
 
+# ---------------------------------------------------------------------------
+# Floors: calibration streams that move the same bytes and do nothing else
+# (mini-infer_amd/bench/floors.hip -> libmi_floors.so), timed like the
+# kernels (graph replay, buffers rotated past the Infinity Cache).  Each floor
+# is the fastest of a few plain forms (16-byte vectors per lane per step
+# 1/2/4/8, one workgroup per tile or a resident grid-stride grid), so it is
+# the time a no-work kernel of this library's style needs for those bytes.
+# ---------------------------------------------------------------------------
+
+FLOOR_FORMS = [(v, p) for v in (1, 2, 4, 8) for p in (0, 1)]
+_FLOORS_LIB = None
 _FLOOR = {}
 
 
-def copy_floor(mk, dev, nbytes, iters=50):
-    """Seconds for a plain device copy moving the same bytes (half read, half
-    written), through the library's gather kernel with identity ids, buffers
-    rotated past the Infinity Cache like the kernel under test.  Small
-    transfers pay a fixed launch / ramp cost, so this is the practical floor
-    for a kernel of that size."""
+def floors_lib():
+    import ctypes
+    global _FLOORS_LIB
+    if _FLOORS_LIB is None:
+        path = ROOT / "mini-infer_amd" / "libmi_floors.so"
+        if not path.exists():
+            raise RuntimeError(f"{path} is missing: run `make -C mini-infer_amd`")
+        lib = ctypes.CDLL(str(path))
+        i64, vp, ci = ctypes.c_int64, ctypes.c_void_p, ctypes.c_int
+        lib.mi_floor_copy.argtypes = [vp, vp, i64, ci, ci, vp]
+        lib.mi_floor_inplace.argtypes = [vp, i64, ci, ci, vp]
+        lib.mi_floor_read.argtypes = [vp, i64, ci, ci, vp, i64, vp]
+        lib.mi_floor_empty.argtypes = [vp]
+        _FLOORS_LIB = lib
+    return _FLOORS_LIB
+
+
+def _floor_launcher(kind, bufs, sink, nbytes, vpl, persistent):
     import torch
-    H = 3584
-    rows = max(1, int(round(nbytes / (4 * H))))
-    if rows in _FLOOR:
-        return _FLOOR[rows]
-    ns = rotations(2 * rows * H * 2)
-    ids = torch.arange(rows, dtype=torch.int64, device=dev)
-    src = [torch.zeros((rows, H), dtype=torch.float16, device=dev) for _ in range(ns)]
-    dst = [torch.empty((rows, H), dtype=torch.float16, device=dev) for _ in range(ns)]
-    sec = time_launches(lambda i: mk.embedding_gather(ids, src[i], out=dst[i]), ns, iters, 5)
-    del src, dst
-    _FLOOR[rows] = sec
-    return sec
+    lib = floors_lib()
+
+    def go(i):
+        st = torch.cuda.current_stream().cuda_stream
+        if kind == "copy":
+            rc = lib.mi_floor_copy(bufs[i][0].data_ptr(), bufs[i][1].data_ptr(), nbytes, vpl,
+                                   persistent, st)
+        elif kind == "inplace":
+            rc = lib.mi_floor_inplace(bufs[i][0].data_ptr(), nbytes, vpl, persistent, st)
+        else:
+            rc = lib.mi_floor_read(bufs[i][0].data_ptr(), nbytes, vpl, persistent,
+                                   sink.data_ptr(), sink.numel(), st)
+        if rc != 0:
+            raise RuntimeError(f"floor {kind} failed: {rc}")
+    return go
 
 
-def report(name, cfg, nbytes, seconds, tokens, floor=None):
+def floor_time(dev, kind, nbytes, iters=40, warmup=5, forms=None):
+    """Fastest time of the `kind` stream ("copy": read nbytes + write nbytes
+    elsewhere; "inplace": read and rewrite nbytes; "read": read nbytes) over
+    FLOOR_FORMS; returns (seconds, {form: seconds})."""
+    import torch
+    nbytes = max(16, (int(nbytes) + 15) // 16 * 16)
+    key = (kind, nbytes)
+    if key in _FLOOR and forms is None:
+        return _FLOOR[key]
+    nb = nbytes // 2
+    ns = rotations(2 * nbytes if kind == "copy" else nbytes)
+    bufs = [(torch.empty(nbytes, dtype=torch.uint8, device=dev).fill_(1),
+             torch.empty(nbytes, dtype=torch.uint8, device=dev) if kind == "copy" else None)
+            for _ in range(ns)]
+    sink = torch.zeros(1 << 20, dtype=torch.int32, device=dev)
+    per = {}
+    for vpl, pers in (forms or FLOOR_FORMS):
+        per[(vpl, pers)] = time_launches(_floor_launcher(kind, bufs, sink, nbytes, vpl, pers), ns,
+                                         iters, warmup)
+    del bufs, nb
+    best = min(per.values())
+    if forms is None:
+        _FLOOR[key] = (best, per)
+    return best, per
+
+
+def empty_launch_time(iters=400, warmup=20):
+    """Average time per launch of an empty one-workgroup kernel, replayed
+    back to back like the kernel rows: the launch floor of a tiny kernel."""
+    import torch
+    lib = floors_lib()
+
+    def go(i):
+        if lib.mi_floor_empty(torch.cuda.current_stream().cuda_stream) != 0:
+            raise RuntimeError("empty launch failed")
+    return time_launches(go, 1, iters, warmup)
+
+
+# Which floors apply to a kernel row: (read bytes, written bytes) -> the
+# out-of-place copy and the in-place stream of half the row's bytes each
+# (every row), and the read stream for rows that write next to nothing.
+def attach_floors(dev, row, read_only=False):
+    half = row["bytes"] // 2
+    oop, _ = floor_time(dev, "copy", half)
+    inp, _ = floor_time(dev, "inplace", half)
+    row["oop_floor_us"] = round(oop * 1e6, 3)
+    row["inplace_floor_us"] = round(inp * 1e6, 3)
+    if read_only:
+        rd, _ = floor_time(dev, "read", row["bytes"])
+        row["read_floor_us"] = round(rd * 1e6, 3)
+        row["frac_of_floor"] = round(rd / (row["us"] * 1e-6), 4)
+        row["floor_kind"] = "read"
+    else:
+        kind = row.get("floor_kind", "copy")
+        f = inp if kind == "inplace" else oop
+        row["frac_of_floor"] = round(f / (row["us"] * 1e-6), 4)
+        row["floor_kind"] = kind
+
+
+def floor_sweep(dev, sizes_mb=(8, 20, 40, 67, 100, 174, 235, 465)):
+    """--floors: every form of every stream at a range of sizes (us and % of
+    HBM peak of the bytes moved), to compare the forms with each other."""
+    rows = []
+    for mb in sizes_mb:
+        nbytes = int(mb * 1e6) // 2 // 16 * 16
+        for kind in ("copy", "inplace", "read"):
+            moved = nbytes if kind == "read" else 2 * nbytes
+            n = moved if kind == "read" else nbytes
+            _, per = floor_time(dev, kind, n, forms=FLOOR_FORMS)
+            for (v, p), sec in per.items():
+                rows.append({"kind": kind, "moved_bytes": moved, "vpl": v, "persistent": p,
+                             "us": round(sec * 1e6, 3),
+                             "frac": round(moved / sec / HBM_PEAK, 4)})
+                log(f"[floors] {kind:<8} {moved / 1e6:8.1f} MB vpl={v} persistent={p} "
+                    f"{sec * 1e6:9.2f} us {100 * moved / sec / HBM_PEAK:6.1f}%")
+    return rows
+
+
+def report(name, cfg, nbytes, seconds, tokens, floor_kind=None):
     r = {
         "kernel": name,
         "config": cfg,
@@ -140,9 +244,8 @@ def report(name, cfg, nbytes, seconds, tokens, floor=None):
         "frac": round(nbytes / seconds / HBM_PEAK, 4),
         "tokens_per_s": round(tokens / seconds, 1),
     }
-    if floor is not None:
-        r["copy_floor_us"] = round(floor * 1e6, 3)
-        r["frac_of_copy_floor"] = round(floor / seconds, 4)
+    if floor_kind:
+        r["floor_kind"] = floor_kind
     return r
 
 
@@ -212,6 +315,8 @@ def all_kernels(mk, dev, iters, warmup):
     ys = [torch.empty_like(xs[0]) for _ in range(4)]
     sec = time_launches(lambda i: mk.rmsnorm(xs[i], w, y=ys[i]), 4, iters * 4, warmup)
     out.append(report("rmsnorm", "[16,3584]", nb, sec, T))
+    # launch-bound: set beside an empty launch replayed the same way
+    out[-1]["empty_launch_us"] = round(empty_launch_time() * 1e6, 3)
     del xs, ys
 
     # 2. fused residual-add + RMSNorm [8192, 3584]
@@ -233,7 +338,7 @@ def all_kernels(mk, dev, iters, warmup):
     qs = [randn16((T, Hq, hd), gen, dev) for _ in range(ns)]
     ks = [randn16((T, Hkv, hd), gen, dev) for _ in range(ns)]
     sec = time_launches(lambda i: mk.rope_neox_qk(qs[i], ks[i], pos, inv), ns, iters, warmup)
-    out.append(report("rope_neox_qk", "Q[4096,28,128]+K[4096,4,128]", nb, sec, T))
+    out.append(report("rope_neox_qk", "Q[4096,28,128]+K[4096,4,128]", nb, sec, T, "inplace"))
     del qs, ks
 
     # 4a/4b. SwiGLU [4096,18944], GeGLU [4096,14336]
@@ -279,19 +384,19 @@ def all_kernels(mk, dev, iters, warmup):
         mk.rmsnorm(qs[i], wq, y=qs[i])
         mk.rmsnorm(ks[i], wk, y=ks[i])
     sec = time_launches(qk, ns, iters, warmup)
-    out.append(report("qk_rmsnorm", "chain Q[6064*28,128]+K[6064*4,128]", nb, sec, T))
+    out.append(report("qk_rmsnorm", "chain Q[6064*28,128]+K[6064*4,128]", nb, sec, T, "inplace"))
     # 5d. RoPE on the same Q/K (fused Q+K launch)
     nb = 2 * T * 32 * 128 * 2 + T * 8
     pos = torch.from_numpy(chain_positions(rng)).to(dev)
     inv = rope_inv(128)
     sec = time_launches(lambda i: mk.rope_neox_qk(qs[i].view(T, 28, 128), ks[i].view(T, 4, 128),
                                                   pos, inv), ns, iters, warmup)
-    out.append(report("rope_neox_qk", "chain Q[6064,28,128]+K[6064,4,128]", nb, sec, T))
+    out.append(report("rope_neox_qk", "chain Q[6064,28,128]+K[6064,4,128]", nb, sec, T, "inplace"))
     # 5c+5d fused: Q/K RMSNorm + RoPE in one pass (replaces the two rows above)
     nb = 2 * T * 32 * 128 * 2 + T * 8 + 2 * 128 * 2
     sec = time_launches(lambda i: mk.qk_norm_rope(qs[i].view(T, 28, 128), ks[i].view(T, 4, 128),
                                                   wq, wk, pos, inv), ns, iters, warmup)
-    out.append(report("qk_norm_rope", "chain Q[6064,28,128]+K[6064,4,128]", nb, sec, T))
+    out.append(report("qk_norm_rope", "chain Q[6064,28,128]+K[6064,4,128]", nb, sec, T, "inplace"))
     del qs, ks
     # 5e. SwiGLU [6064, 18944]
     nb = 3 * T * I * 2
@@ -343,9 +448,7 @@ def all_kernels(mk, dev, iters, warmup):
     torch.cuda.synchronize()
     for r in out:
         if r["bytes"] >= 8 << 20:
-            f = copy_floor(mk, dev, r["bytes"])
-            r["copy_floor_us"] = round(f * 1e6, 3)
-            r["frac_of_copy_floor"] = round(f / (r["us"] * 1e-6), 4)
+            attach_floors(dev, r, read_only=r["kernel"] == "greedy_argmax")
     return out
 
 
@@ -515,102 +618,88 @@ def cpu_kernel_table(budget_s=1.0):
     return cores, rows
 
 
+def chain_bytes(s, segments_tokens):
+    """Algorithmic HBM bytes of one chain step (each input read once, each
+    output written once), from the workload's shapes."""
+    T, D, I, V, N = s["T"], s["hidden_size"], s["intermediate_size"], s["vocab"], s["logit_rows"]
+    Hq, Hkv, hd = s["num_heads"], s["num_kv_heads"], s["head_dim"]
+    return ((T * 8 + 2 * T * D * 2)                                   # gather
+            + (2 * T * D * 2 + D * 2)                                 # input norm
+            + (2 * T * (Hq + Hkv) * hd * 2 + T * 8 + 2 * hd * 2)      # qk-norm + rope
+            + (2 * 2 * segments_tokens * Hkv * hd * 2)                # K + V scatter
+            + 2 * (4 * T * D * 2 + D * 2)                             # 2x residual add + norm
+            + 3 * T * I * 2                                           # SwiGLU
+            + 2 * N * V * 2 + (N * V * 2 + N * 4))                    # softmax, argmax
+
+
 def decoder_chain(mk, dev, iters, warmup):
-    """BASELINE config 5 as one step: the non-GEMM launches of a decoder layer
-    at T = 6064 (64 decode tokens + two 3000-token prefills), then the LM-head
-    side, all captured back to back:
-      gather -> residual-add + RMSNorm -> Q/K-norm + RoPE -> paged K+V scatter
-      -> SwiGLU [6064,18944] -> softmax [64,152064] -> greedy argmax.
-    Timed twice: with this library's fused entry points, and as the
-    reference's caller composes the same steps from its unfused launchers
-    (src/model/transformer_model.cpp:414-424, :448; src/layers/attention.cpp:
-    754-780): add in place, a device copy, RMSNorm; Q-norm and K-norm; cos/sin
-    tables, then RoPE of Q and of K from the tables; one scatter for K and one
-    for V.  Both run this library's kernels, so the difference is the fusion
-    alone.  Bytes are the fused step's algorithmic bytes."""
-    import numpy as np
+    """BASELINE config 5 as one step: the C++ decoder chain (include/mi_chain.h)
+    over one non-GEMM decoder layer at T = 6064 (64 decode tokens at random
+    positions + two 3000-token prefills), then the sampling step:
+      gather -> input RMSNorm -> Q/K-norm + RoPE -> paged K+V scatter ->
+      residual add + RMSNorm -> SwiGLU [6064,18944] -> residual add + final
+      RMSNorm -> softmax [64,152064] -> greedy argmax,
+    with seeded stand-ins for the GEMM outputs, captured as one graph.  Also
+    timed: the same steps as the reference's caller composes them from its
+    unfused launchers (src/model/transformer_model.cpp:578-660;
+    src/layers/attention.cpp:743-846): a device copy and RMSNorm, Q-norm and
+    K-norm, cos/sin tables then RoPE of Q and of K, one scatter for K and one
+    for V per segment, add in place + copy + RMSNorm twice.  Both run this
+    library's kernels, so the difference is the fusion alone.  Bytes are the
+    fused step's algorithmic bytes.  Two workloads alternate, so consecutive
+    steps stream from HBM rather than the Infinity Cache."""
     import torch
-    gen = torch.Generator(device=dev).manual_seed(5)
-    rng = np.random.default_rng(5)
-    f16 = torch.float16
-    T, D, I, V, N = 6064, 3584, 18944, 152064, 64
-    Hq, Hkv, hd, bs = 28, 4, 128, 16
-    table = randn16((V, D), gen, dev, 0.0, 0.02)
-    w1 = randn16((D,), gen, dev, 1.0, 0.1)
-    wq, wk = randn16((hd,), gen, dev, 1.0, 0.1), randn16((hd,), gen, dev, 1.0, 0.1)
+    import mi_chain
+    ws = [mi_chain.Workload(dev, seed=5 + i, host=False) for i in range(2)]
+    s = ws[0].shapes
+    T, D, V, N = s["T"], s["hidden_size"], s["vocab"], s["logit_rows"]
+    Hq, Hkv, hd = s["num_heads"], s["num_kv_heads"], s["head_dim"]
     inv = mk.rope_inv_freq(hd)
-    pos = torch.from_numpy(chain_positions(rng)).to(dev)
-    mb = -(-T // bs)
-    bt = torch.from_numpy(rng.permutation(mb).astype(np.int32)).to(dev).view(1, mb)
-    sl = torch.tensor([T], dtype=torch.int32, device=dev)
-    sp = torch.tensor([0], dtype=torch.int32, device=dev)
-    cos_t = torch.empty((T, hd // 2), dtype=f16, device=dev)
+    cos_t = torch.empty((T, hd // 2), dtype=torch.float16, device=dev)
     sin_t = torch.empty_like(cos_t)
-    wss = torch.zeros(max(1, mk.softmax_workspace_bytes(N, V)), dtype=torch.uint8, device=dev)
-    wsa = torch.zeros(max(1, mk.greedy_argmax_workspace_bytes(N, V)), dtype=torch.uint8,
-                      device=dev)
-    am = torch.empty(N, dtype=torch.int32, device=dev)
-
-    def make_set():
-        return {
-            "ids": torch.from_numpy(rng.integers(0, V, T).astype(np.int64)).to(dev),
-            "hidden": torch.empty((T, D), dtype=f16, device=dev),
-            "attn": randn16((T, D), gen, dev),
-            "hid2d": torch.empty((T, D), dtype=f16, device=dev),
-            "normed": torch.empty((T, D), dtype=f16, device=dev),
-            "q": randn16((T, Hq, hd), gen, dev), "k": randn16((T, Hkv, hd), gen, dev),
-            "v": randn16((T, Hkv, hd), gen, dev),
-            "kc": torch.empty((1, mb, Hkv, bs, hd), dtype=f16, device=dev),
-            "vc": torch.empty((1, mb, Hkv, bs, hd), dtype=f16, device=dev),
-            "g": randn16((T, I), gen, dev), "u": randn16((T, I), gen, dev),
-            "act": torch.empty((T, I), dtype=f16, device=dev),
-            "logits": randn16((N, V), gen, dev, 0.0, 4.0),
-            "probs": torch.empty((N, V), dtype=f16, device=dev),
-        }
-    sets = [make_set() for _ in range(2)]  # ~1.1 GB of streamed data per step
-
-    def tail(b):
-        mk.swiglu(b["g"], b["u"], out=b["act"])
-        mk.softmax(b["logits"], y=b["probs"], workspace=wss)
-        mk.greedy_argmax(b["logits"], out=am, workspace=wsa)
+    tmp = torch.empty((T, D), dtype=torch.float16, device=dev)
 
     def fused(i):
-        b = sets[i]
-        mk.embedding_gather(b["ids"], table, out=b["hidden"])
-        mk.fused_add_rmsnorm(b["attn"], b["hidden"], w1, y=b["normed"])
-        mk.qk_norm_rope(b["q"], b["k"], wq, wk, pos, inv)
-        mk.paged_kv_scatter(b["k"].view(1, T, Hkv, hd), b["kc"], bt, sl, sp, 0, bs,
-                            v_src=b["v"].view(1, T, Hkv, hd), v_cache=b["vc"])
-        tail(b)
+        ws[i].run()
 
     def unfused(i):
-        b = sets[i]
-        mk.embedding_gather(b["ids"], table, out=b["hidden"])
-        mk.add_inplace(b["hidden"], b["attn"])
-        b["hid2d"].copy_(b["hidden"])
-        mk.rmsnorm(b["hid2d"], w1, y=b["normed"])
-        q2, k2 = b["q"].view(T * Hq, hd), b["k"].view(T * Hkv, hd)
-        mk.rmsnorm(q2, wq, y=q2)
-        mk.rmsnorm(k2, wk, y=k2)
-        mk.rope_tables(inv, pos, cos_t=cos_t, sin_t=sin_t)
-        q4, k4 = b["q"].view(1, T, Hq, hd), b["k"].view(1, T, Hkv, hd)
+        w = ws[i]
+        t = w.t
+        mk.embedding_gather(t["ids"], t["embed"], out=t["hidden"])
+        tmp.copy_(t["hidden"])
+        mk.rmsnorm(tmp, t["input_norm"], y=t["normed"])
+        q2, k2 = t["q"].view(T * Hq, hd), t["k"].view(T * Hkv, hd)
+        mk.rmsnorm(q2, t["q_norm"], y=q2)
+        mk.rmsnorm(k2, t["k_norm"], y=k2)
+        mk.rope_tables(inv, t["positions"], cos_t=cos_t, sin_t=sin_t)
+        q4, k4 = t["q"].view(1, T, Hq, hd), t["k"].view(1, T, Hkv, hd)
         mk.rope_neox(q4, cos_t, sin_t, y=q4)
         mk.rope_neox(k4, cos_t, sin_t, y=k4)
-        mk.paged_kv_scatter(k4, b["kc"], bt, sl, sp, 0, bs)
-        mk.paged_kv_scatter(b["v"].view(1, T, Hkv, hd), b["vc"], bt, sl, sp, 0, bs)
-        tail(b)
+        for g in w.segments:
+            o, B, S = g["token_offset"], g["B"], g["S"]
+            for src, cache in ((t["k"], t["k_cache"]), (t["v"], t["v_cache"])):
+                mk.paged_kv_scatter(src[o:o + B * S].view(B, S, Hkv, hd), cache, g["block_table"],
+                                    g["seq_len"], g["start_pos"], s["layer"], s["block_size"])
+        for x, wt, y in ((t["attn_out"], t["post_attn_norm"], t["post_normed"]),
+                         (t["mlp_out"], t["final_norm"], t["final_normed"])):
+            mk.add_inplace(t["hidden"], x)
+            tmp.copy_(t["hidden"])
+            mk.rmsnorm(tmp, wt, y=y)
+            if y is t["post_normed"]:
+                mk.swiglu(t["gate"], t["up"], out=t["act_out"])
+        mk.softmax(t["logits"], y=t["probs"], workspace=t["softmax_ws"])
+        mk.greedy_argmax(t["logits"], out=t["next_tokens"], workspace=t["argmax_ws"])
 
-    nb = ((T * 8 + 2 * T * D * 2) + (4 * T * D * 2 + D * 2)
-          + (2 * T * (Hq + Hkv) * hd * 2 + T * 8 + 2 * hd * 2)
-          + (2 * 2 * T * Hkv * hd * 2 + (mb + 2) * 4) + 3 * T * I * 2
-          + 2 * N * V * 2 + (N * V * 2 + N * 4))
-    cfg = "gather+add&norm+qk-norm&rope+kv+swiglu+softmax+argmax T=6064"
+    nb = chain_bytes(s, sum(g["B"] * g["S"] for g in ws[0].segments))
+    cfg = ("gather+norm+qk-norm&rope+kv+add&norm+swiglu+add&norm+softmax+argmax "
+           f"T={T} (64 decode + 2x3000 prefill)")
     rows = []
-    for name, fn in (("decoder_chain_fused", fused), ("decoder_chain_unfused", unfused)):
-        sec = time_launches(fn, len(sets), iters, warmup)
+    for name, fn in (("decoder_chain", fused), ("decoder_chain_unfused", unfused)):
+        sec = time_launches(fn, len(ws), iters, warmup)
         rows.append(report(name, cfg, nb, sec, T))
     rows[0]["speedup_over_unfused"] = round(rows[1]["us"] / rows[0]["us"], 3)
-    del sets, table
+    rows[0]["impl"] = "C++ DecoderChain (mi_decoder_chain_run), one graph"
+    del ws
     torch.cuda.synchronize()
     return rows
 
@@ -713,6 +802,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--shapes", action="store_true",
                     help="also time each kernel across common LLM shapes beyond the configs")
+    ap.add_argument("--floors", action="store_true",
+                    help="also print every calibration-stream form at a range of sizes")
     ap.add_argument("--no-chain", action="store_true",
                     help="skip the whole-chain rows (profiling runs: one row per kernel and grid)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
@@ -752,10 +843,20 @@ def main():
         if not args.no_chain:
             kernels += decoder_chain(mk, dev, max(10, args.steps // 8), max(3, args.warmup // 4))
         for k in kernels:
-            floor = (f"  copy floor {k['copy_floor_us']:7.2f} us ({100 * k['frac_of_copy_floor']:5.1f}%)"
-                     if "copy_floor_us" in k else "")
+            floor = ""
+            if "frac_of_floor" in k:
+                floor = (f"  floors oop {k['oop_floor_us']:7.2f} inplace {k['inplace_floor_us']:7.2f}"
+                         + (f" read {k['read_floor_us']:7.2f}" if "read_floor_us" in k else "")
+                         + f" us -> {100 * k['frac_of_floor']:5.1f}% of {k['floor_kind']}")
+            elif "empty_launch_us" in k:
+                floor = f"  empty launch {k['empty_launch_us']:.2f} us"
             log(f"[bench]   {k['kernel']:<18} {k['config']:<38} {k['us']:>9.2f} us "
                 f"{k['GBps']:>8.1f} GB/s  {100 * k['frac']:5.1f}%{floor}")
+
+    floors = None
+    if args.floors:
+        log("[bench] floor sweep")
+        floors = floor_sweep(dev)
 
     shapes = None
     if args.shapes:
@@ -823,6 +924,8 @@ def main():
     }
     if shapes is not None:
         line["shapes"] = shapes
+    if floors is not None:
+        line["floors"] = floors
     print(json.dumps(line), flush=True)
 
 

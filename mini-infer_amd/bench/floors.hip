@@ -1,0 +1,138 @@
+// floors.hip -- calibration streams for the benchmark (libmi_floors.so).
+//
+// Kernels that move bytes and do nothing else, so a layer kernel's time can
+// be set beside the time the same bytes take with no arithmetic, no
+// reduction and no exchange:
+//   * copy     : dst[i] = src[i]            (read n, write n, out of place)
+//   * inplace  : buf[i] = buf[i] ^ pattern  (read n, write n, same address;
+//                the XOR keeps the write from being a no-op store of the value
+//                just read, and each call flips the buffer back and forth)
+//   * read     : one 32-bit word per workgroup folded from its slice
+//                (read n, write ~nothing)
+//   * empty    : a one-workgroup kernel that returns at once (launch floor)
+// Each stream kernel moves 16-byte vectors, VPL of them per lane per step,
+// all loads of a step issued before its stores, with non-temporal loads
+// and stores; `persistent` selects a grid of the resident capacity walking
+// the buffer with a grid stride instead of one workgroup per tile.  The
+// benchmark takes the fastest of a few (VPL, persistent) forms as the floor.
+// Not part of the layer-kernel library: nothing here is reached from
+// include/mi_kernels.h.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace {
+
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ u4 ld(const u4* p) { return __builtin_nontemporal_load(p); }
+__device__ __forceinline__ void st(u4* p, u4 v) { __builtin_nontemporal_store(v, p); }
+
+constexpr int kThreads = 256;
+
+enum Kind { kCopy = 0, kInplace = 1, kRead = 2 };
+
+template <int KIND, int VPL>
+__global__ __launch_bounds__(kThreads) void stream_kernel(const u4* src, u4* dst, int64_t nvec,
+                                                          uint32_t pattern, uint32_t* sink) {
+    const int64_t tile = static_cast<int64_t>(kThreads) * VPL;
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * tile;
+    uint32_t acc = 0;
+    for (int64_t base = static_cast<int64_t>(blockIdx.x) * tile + threadIdx.x; base < nvec;
+         base += stride) {
+        u4 v[VPL];
+#pragma unroll
+        for (int j = 0; j < VPL; ++j) {
+            const int64_t i = base + static_cast<int64_t>(j) * kThreads;
+            if (i < nvec) v[j] = ld(src + i);
+        }
+#pragma unroll
+        for (int j = 0; j < VPL; ++j) {
+            const int64_t i = base + static_cast<int64_t>(j) * kThreads;
+            if (i < nvec) {
+                if constexpr (KIND == kCopy) st(dst + i, v[j]);
+                if constexpr (KIND == kInplace) st(dst + i, v[j] ^ pattern);
+                if constexpr (KIND == kRead) acc ^= v[j].x ^ v[j].y ^ v[j].z ^ v[j].w;
+            }
+        }
+    }
+    if constexpr (KIND == kRead) {
+        // one word per workgroup, so the loads cannot be dropped
+        __shared__ uint32_t red;
+        if (threadIdx.x == 0) red = 0;
+        __syncthreads();
+        atomicXor(&red, acc);
+        __syncthreads();
+        if (threadIdx.x == 0) sink[blockIdx.x] = red;
+    }
+}
+
+__global__ void empty_kernel() {}
+
+template <int KIND, int VPL>
+int launch_vpl(const void* src, void* dst, int64_t nvec, int persistent, uint32_t* sink,
+               int64_t sink_words, hipStream_t s) {
+    const auto k = stream_kernel<KIND, VPL>;
+    const int64_t tiles = (nvec + kThreads * VPL - 1) / (kThreads * VPL);
+    int64_t grid = tiles;
+    if (persistent) {
+        int per_cu = 0, cus = 0, dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k, kThreads, 0) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+            return -2;
+        const int64_t cap = static_cast<int64_t>(per_cu) * cus;
+        if (cap > 0 && cap < grid) grid = cap;
+    }
+    if (grid < 1) grid = 1;
+    if (grid > 2147483647) return -2;
+    if (KIND == kRead && grid > sink_words) return -1;
+    k<<<dim3(static_cast<unsigned>(grid)), dim3(kThreads), 0, s>>>(
+        static_cast<const u4*>(src), static_cast<u4*>(dst), nvec, 0x3c003c00u, sink);
+    return hipGetLastError() == hipSuccess ? 0 : 1;
+}
+
+template <int KIND>
+int launch(const void* src, void* dst, int64_t bytes, int vpl, int persistent, uint32_t* sink,
+           int64_t sink_words, void* stream) {
+    if (bytes <= 0 || bytes % 16 != 0 || !src || (KIND != kRead && !dst) ||
+        (KIND == kRead && !sink))
+        return -1;
+    if ((reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(dst)) & 15u) return -1;
+    const int64_t nvec = bytes / 16;
+    const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    switch (vpl) {
+        case 1: return launch_vpl<KIND, 1>(src, dst, nvec, persistent, sink, sink_words, s);
+        case 2: return launch_vpl<KIND, 2>(src, dst, nvec, persistent, sink, sink_words, s);
+        case 4: return launch_vpl<KIND, 4>(src, dst, nvec, persistent, sink, sink_words, s);
+        case 8: return launch_vpl<KIND, 8>(src, dst, nvec, persistent, sink, sink_words, s);
+        default: return -1;
+    }
+}
+
+}  // namespace
+
+// Out-of-place copy of `bytes` (a multiple of 16, 16-byte aligned buffers).
+extern "C" int mi_floor_copy(const void* src, void* dst, int64_t bytes, int vpl, int persistent,
+                             void* stream) {
+    return launch<kCopy>(src, dst, bytes, vpl, persistent, nullptr, 0, stream);
+}
+
+// In-place read-then-write of `bytes` of buf (each 32-bit word XOR-ed with
+// a fixed pattern, so two calls restore it).
+extern "C" int mi_floor_inplace(void* buf, int64_t bytes, int vpl, int persistent, void* stream) {
+    return launch<kInplace>(buf, buf, bytes, vpl, persistent, nullptr, 0, stream);
+}
+
+// Read of `bytes` of src, one 32-bit word per workgroup into sink (which
+// holds sink_words words; the grid must fit).
+extern "C" int mi_floor_read(const void* src, int64_t bytes, int vpl, int persistent,
+                             uint32_t* sink, int64_t sink_words, void* stream) {
+    return launch<kRead>(src, nullptr, bytes, vpl, persistent, sink, sink_words, stream);
+}
+
+// An empty one-workgroup launch.
+extern "C" int mi_floor_empty(void* stream) {
+    empty_kernel<<<dim3(1), dim3(64), 0, reinterpret_cast<hipStream_t>(stream)>>>();
+    return hipGetLastError() == hipSuccess ? 0 : 1;
+}

@@ -7,8 +7,9 @@
 //   gelu   : y = half(0.5 x (1 + tanh(sqrt(2/pi)(x + 0.044715 x^3))))
 //            (src/kernels/gelu_kernel.cu:23-35), evaluated as x / (1 + exp(-2u)),
 //            which is the same function since 0.5 (1 + tanh(u)) = sigmoid(2u)
-//   geglu  : out = half(gelu(g) * u) -- the reference runs gelu then
-//            mul_inplace (src/layers/mlp.cpp:282-291), rounding twice
+//   geglu  : out = half(half(gelu(g)) * u) -- the reference runs gelu then
+//            mul_inplace (src/layers/mlp.cpp:282-291), rounding twice; the
+//            fused pass keeps both roundings at one pass's traffic
 //   add    : y = half(y + x)   (src/kernels/model_utils_kernel.cu:31-35)
 //   mul    : y = half(y * x)   (:82-86)
 //   scale  : y = half(y * s)   (:68-72)
@@ -31,7 +32,9 @@ template <int OP>
 __device__ __forceinline__ float apply(float a, float b, float scale) {
     if constexpr (OP == kSwiglu) return silu_mul(a, b);
     if constexpr (OP == kGelu) return gelu_tanh(a);
-    if constexpr (OP == kGeglu) return gelu_tanh(a) * b;
+    // gelu rounded to fp16 before the multiply, as the reference's
+    // launch_gelu_tanh + launch_mul_inplace pair stores it in between
+    if constexpr (OP == kGeglu) return (float)to_half(gelu_tanh(a)) * b;
     if constexpr (OP == kAdd) return a + b;
     if constexpr (OP == kMul) return a * b;
     if constexpr (OP == kScale) return a * scale;

@@ -389,7 +389,10 @@ __global__ __launch_bounds__(256) void argmax_onepass_kernel(const half_t* __res
         const int lane = threadIdx.x;
         uint64_t k = 0;
         bool all = false;
+        // also bounded by 20000 ticks (200 us) of the 100 MHz constant clock
+        const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
         for (int it = 0; it < poll_limit && !all; ++it) {
+            if (it > 0 && __builtin_amdgcn_s_memrealtime() - t0 > 20000) break;
             bool mine = true;
             k = 0;
             if (lane < splits) {

@@ -74,17 +74,21 @@ __device__ __forceinline__ void st8_out(half_t* p, h8 v) {
     if constexpr (WT) st8_stream_wt(p, v); else st8_stream(p, v);
 }
 
-// Round-to-nearest-even fp32 -> fp16 (v_cvt_f16_f32 under the default mode).
-__device__ __forceinline__ half_t to_half(float f) { return (half_t)f; }
-
 // Pins a value to an fp32 register.  The compiler may otherwise fold
-// "fp32 result, then fp16 conversion" into one mixed-precision FMA that rounds
-// the exact result straight to fp16; reference kernels round to fp32 first
-// (e.g. __float2half(a * b - c * d)), and the two differ in rare ties.
+// "fp32 result, then fp16 conversion" into one mixed-precision FMA
+// (v_fma_mixlo_f16 a, b, 0) that rounds the exact product straight to fp16;
+// reference kernels round to fp32 first (e.g. __float2half(a * b - c * d)),
+// and the two differ in rare ties -- and in the sign of a zero product,
+// since the fused form adds +0 to it.
 __device__ __forceinline__ float fp32_rounded(float f) {
     asm volatile("" : "+v"(f));
     return f;
 }
+
+// Round-to-nearest-even fp32 -> fp16 of a value first rounded to fp32
+// (v_cvt_f16_f32 under the default mode): RN16(RN32(expression)), as the
+// reference's __float2half(expression) computes it.
+__device__ __forceinline__ half_t to_half(float f) { return (half_t)fp32_rounded(f); }
 
 // --- DPP helpers ------------------------------------------------------------
 // dpp_ctrl encodings (GFX9 DPP): quad_perm = 8-bit lane map within a quad,

@@ -300,7 +300,9 @@ int rmsnorm_dispatch(const void* xv, void* rv, const void* wv, void* yv, int64_t
     half_t* r = static_cast<half_t*>(rv);
     const half_t* w = static_cast<const half_t*>(wv);
     half_t* y = static_cast<half_t*>(yv);
-    const float bias = add_one ? 1.0f : 0.0f;
+    // -0.0f, not +0.0f: w + (-0) == w for every w including -0, so the
+    // sign of a zero output follows x * rrms * w as the reference computes it
+    const float bias = add_one ? 1.0f : -0.0f;
     const hipStream_t s = as_stream(stream);
 
     const bool vec = (D % 8 == 0) && aligned16(x) && aligned16(w) && aligned16(y) &&

@@ -802,5 +802,5 @@ extern "C" int mi_qk_norm_rope_f16(void* q, void* k, const void* q_weight, const
     return mi::launch_qk_norm_rope(static_cast<half_t*>(q), Hq, static_cast<half_t*>(k), Hkv,
                                    static_cast<const half_t*>(q_weight),
                                    static_cast<const half_t*>(k_weight), positions, T, head_dim,
-                                   eps, add_one ? 1.0f : 0.0f, inv, mi::as_stream(stream));
+                                   eps, add_one ? 1.0f : -0.0f, inv, mi::as_stream(stream));
 }

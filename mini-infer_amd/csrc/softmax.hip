@@ -390,13 +390,17 @@ __global__ __launch_bounds__(256) void softmax_finish_kernel(const half_t* x, ha
 //   * the chunk-0 workgroup raises the epoch to E + K (atomic max) after the
 //     last (K-th) round, when every workgroup of the slot has published it --
 //     so every one of them has already read E;
-//   * a workgroup whose polling runs out (kPollLimit; not expected when the
-//     grid fits the GPU) computes that row's statistics itself from x and
+//   * a workgroup whose polling runs out (kPollLimit polls or kPollTicks of
+//     the 100 MHz constant clock, whichever comes first; not expected when
+//     the grid fits the GPU) computes that row's statistics itself from x and
 //     raises the epoch to E + K + 1 at once, past every tag the launch writes
 //     for the slot.  A workgroup that starts after that reads the higher
 //     epoch, its tags match nobody's, and it takes the same fallback for its
-//     rows: slower, still correct.  Polling is bounded: no workgroup can wait
-//     forever.
+//     rows: slower, still correct.  A workgroup that has fallen back once
+//     stops polling for its remaining rounds (its row-mates may be out of
+//     step with it for good), so a late start costs at most one poll bound
+//     per workgroup, not one per round.  Polling is bounded: no workgroup
+//     can wait forever.
 // A workgroup publishes round k + 2 into a set only after it has seen every
 // chunk's round k + 1 pair, which its row-mates publish after they have read
 // round k: no pair is overwritten before it is read.  Each 64-bit word is
@@ -412,6 +416,9 @@ constexpr int64_t kOnePassChunk = 2048 * kOnePassU;  // elements per workgroup
 // header, then two sets of slot pairs (alternated by round)
 constexpr int64_t kRowRecordBytes = 16 + 2 * kOnePassMaxSplits * 16;
 constexpr int kPollLimit = 1 << 16;
+// Wall-clock bound of one row's polling: 20000 ticks of the 100 MHz
+// constant clock (s_memrealtime) = 200 us, some 100 times a normal exchange.
+constexpr uint64_t kPollTicks = 20000;
 std::atomic<int> g_poll_limit{kPollLimit};  // mi_softmax_test_poll_limit
 
 __device__ __forceinline__ uint64_t tagged(uint32_t tag, float v) {
@@ -461,7 +468,9 @@ __device__ __forceinline__ void row_poll(const uint64_t* slots, int splits, uint
     const int lane = threadIdx.x & (kWave - 1);
     float mj = -INFINITY, sj = 0.0f;
     bool all = false;
+    const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
     for (int it = 0; it < poll_limit && !all; ++it) {
+        if (it > 0 && __builtin_amdgcn_s_memrealtime() - t0 > kPollTicks) break;
         bool mine = true;
         if (lane < splits) {
             const uint64_t w0 = __hip_atomic_load(&slots[2 * lane], __ATOMIC_RELAXED,
@@ -560,6 +569,7 @@ __global__ __launch_bounds__(256) void softmax_stream_kernel(const half_t* x, ha
         epoch_sh = __hip_atomic_load(epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     h8 a[U], n[U];
     lane_load<U>(x + r0 * D, lo, ok, a);
+    bool gave_up = false;  // workgroup-uniform: set after the first fallback
     for (int64_t k = 0; k < K; ++k) {
         const int64_t row = r0 + k * R;
         // The guard is always true (256 lanes); written out, it keeps the
@@ -573,10 +583,15 @@ __global__ __launch_bounds__(256) void softmax_stream_kernel(const half_t* x, ha
         uint64_t* set = sets + (k & 1) * (2 * kOnePassMaxSplits);
         chunk_publish(set, split, tag, m, s);
         if (k + 1 < K) lane_load<U>(x + (row + R) * D, lo, ok, n);
-        if (threadIdx.x < kWave) row_poll(set, splits, tag, poll_limit, row_stats);
+        if (gave_up) {
+            if (threadIdx.x == 0) row_stats[2] = 1.0f;
+        } else if (threadIdx.x < kWave) {
+            row_poll(set, splits, tag, poll_limit, row_stats);
+        }
         __syncthreads();
         float M = row_stats[0], S = row_stats[1];
         const bool fallback = row_stats[2] != 0.0f;
+        gave_up = gave_up || fallback;
         if (fallback) row_stats_from_x(x + row * D, D, M, S, slots);
         if (threadIdx.x == 0 && (fallback || (split == 0 && k + 1 == K)))
             __hip_atomic_fetch_max(epoch, fallback ? E + K + 1 : E + K, __ATOMIC_RELAXED,

@@ -98,7 +98,7 @@ def test_fuzz_rope_qk(mk, orc, dev, seed):
 
 @pytest.mark.parametrize("seed", range(CASES))
 def test_fuzz_qk_norm_rope(mk, orc, dev, seed):
-    from test_gpu_rope import _assert_norm_rope_close, _qk_norm_rope_ref
+    from helpers import assert_norm_rope_close, qk_norm_rope_ref
     rng = np.random.default_rng(4000 + seed)
     T = int(rng.integers(1, 400))
     hd = int(rng.choice([16, 32, 64, 128, 256, 512]))
@@ -114,9 +114,9 @@ def test_fuzz_qk_norm_rope(mk, orc, dev, seed):
     mk.qk_norm_rope(qd, kd if Hkv else None, _dev_array(wq, dev), _dev_array(wk, dev),
                     _dev_array(pos, dev), inv)
     if Hq:
-        _assert_norm_rope_close(to_host(qd), *_qk_norm_rope_ref(orc, q, wq, pos, inv), what="q")
+        assert_norm_rope_close(to_host(qd), *qk_norm_rope_ref(orc, q, wq, pos, inv), what="q")
     if Hkv:
-        _assert_norm_rope_close(to_host(kd), *_qk_norm_rope_ref(orc, k, wk, pos, inv), what="k")
+        assert_norm_rope_close(to_host(kd), *qk_norm_rope_ref(orc, k, wk, pos, inv), what="k")
 
 
 @pytest.mark.parametrize("seed", range(CASES))

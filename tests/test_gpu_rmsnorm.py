@@ -134,3 +134,27 @@ def test_argument_errors(mk, dev):
         mk.fused_add_rmsnorm(x, x, w)  # residual aliases x
     with pytest.raises(RuntimeError, match="status -3"):
         mk.rmsnorm(x, w, y=y)
+
+
+@pytest.mark.parametrize("N,D", [(64, 128), (16, 3584), (5, 3583)])
+def test_signed_zero_weights(mk, orc, dev, N, D):
+    """Weights of -0 and +0 give zero outputs whose sign is that of
+    x * rrms * w, as the reference computes it (rmsnorm_kernel.cu:61-65):
+    the Gemma bias is only added when add_one is set.  Small-row, long-row
+    and scalar kernels, plain and fused."""
+    _case(f"rmsnorm signed-zero weights [{N},{D}]")
+    rng = np.random.default_rng(D)
+    x = normal_f16(rng, (N, D))
+    r = normal_f16(rng, (N, D))
+    w = normal_f16(rng, (D,), 1.0, 0.1)
+    w[0::4] = np.float16(-0.0)
+    w[1::4] = np.float16(0.0)
+    zero = np.zeros((N, D), bool)
+    zero[:, 0::4] = zero[:, 1::4] = True
+    y = to_host(mk.rmsnorm(to_dev(x, dev), to_dev(w, dev)))
+    ref = orc.f32_to_f16(orc.rmsnorm(x, w))
+    assert_bits_equal(y[zero], ref[zero], what="signed zeros, plain")
+    assert_close(y, orc.rmsnorm(x, w), what="plain")
+    yf = to_host(mk.fused_add_rmsnorm(to_dev(x, dev), to_dev(r, dev), to_dev(w, dev)))
+    reff = orc.f32_to_f16(orc.fused_add_rmsnorm(x, r, w)[1])
+    assert_bits_equal(yf[zero], reff[zero], what="signed zeros, fused")

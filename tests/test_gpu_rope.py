@@ -13,7 +13,8 @@ from pathlib import Path
 import numpy as np
 import pytest
 
-from helpers import ATOL, RTOL, assert_bits_equal, assert_close, normal_f16, to_dev, to_host
+from helpers import (assert_bits_equal, assert_close, assert_norm_rope_close, normal_f16,
+                     qk_norm_rope_ref, to_dev, to_host)
 
 pytestmark = pytest.mark.gpu
 GOLD = np.load(Path(__file__).resolve().parent / "golden" / "ref_cases.npz")
@@ -150,44 +151,6 @@ def test_position_zero_is_identity(mk, orc, dev):
     assert_bits_equal(to_host(qd), q, what="identity")
 
 
-def _qk_norm_rope_ref(orc, x, w, pos, inv, eps=1e-6, add_one=False):
-    """Reference composition: per-head RMSNorm written as fp16, then RoPE."""
-    T, H, hd = x.shape
-    n = orc.rmsnorm(x.reshape(T * H, hd), w, eps, add_one, nthreads=8)
-    n16 = orc.f32_to_f16(n).reshape(T, H, hd)
-    c, s = orc.rope_tables(inv, pos)
-    return orc.rope_neox(n16, c, s, nthreads=8), n16
-
-
-def _ulp16(v):
-    return np.spacing(np.abs(np.asarray(v, np.float32)).astype(np.float16)).astype(np.float32)
-
-
-def _assert_norm_rope_close(ours, ref, n16, what):
-    """rtol = atol = 1e-3, except at elements whose fp16 normalised input sits
-    on a rounding boundary.  The oracle's statistics are exact (double sum of
-    squares, double 1/sqrt); a GPU kernel -- the reference's included --
-    sums in an fp32 tree and uses an fp32 reciprocal square root, so the fp16
-    value it hands to the rotation can be one ulp away there.  RoPE then
-    carries that ulp into an output that may be much smaller (x1 c - x2 s
-    cancels).  Such elements must be rare (< 1e-5 of the tensor) and within
-    one ulp of each rotated operand plus one output ulp."""
-    ours = np.asarray(ours).astype(np.float32)
-    ref = np.asarray(ref, np.float32)
-    diff = np.abs(ours - ref)
-    out = diff > ATOL + RTOL * np.abs(ref)
-    if not out.any():
-        return
-    half = n16.shape[-1] // 2
-    partner = np.concatenate([n16[..., half:], n16[..., :half]], axis=-1)
-    bound = _ulp16(n16) + _ulp16(partner) + _ulp16(ref)
-    worst = np.unravel_index(np.argmax(diff - bound), diff.shape)
-    assert (diff[out] <= bound[out]).all(), (
-        f"{what}: error beyond one ulp of the normalised operands at {worst}: "
-        f"ours={ours[worst]} ref={ref[worst]} bound={bound[worst]}")
-    assert out.mean() < 1e-5, f"{what}: {int(out.sum())} of {out.size} outside tolerance"
-
-
 @pytest.mark.parametrize("T,Hq,Hkv,hd", [(6064, 28, 4, 128), (37, 8, 2, 64), (5, 3, 1, 256),
                                          (9, 2, 2, 16), (3, 4, 0, 128), (4, 0, 2, 128),
                                          (2, 2, 1, 512), (11, 5, 3, 32), (20000, 8, 2, 64),
@@ -212,11 +175,11 @@ def test_qk_norm_rope(mk, orc, dev, T, Hq, Hkv, hd):
     qd, kd = to_dev(q, dev), to_dev(k, dev)
     mk.qk_norm_rope(qd, kd if Hkv else None, to_dev(wq, dev), to_dev(wk, dev), to_dev(pos, dev), inv)
     if Hq:
-        ref, n16 = _qk_norm_rope_ref(orc, q, wq, pos, inv)
-        _assert_norm_rope_close(to_host(qd), ref, n16, what="q")
+        ref, n16 = qk_norm_rope_ref(orc, q, wq, pos, inv)
+        assert_norm_rope_close(to_host(qd), ref, n16, what="q")
     if Hkv:
-        ref, n16 = _qk_norm_rope_ref(orc, k, wk, pos, inv)
-        _assert_norm_rope_close(to_host(kd), ref, n16, what="k")
+        ref, n16 = qk_norm_rope_ref(orc, k, wk, pos, inv)
+        assert_norm_rope_close(to_host(kd), ref, n16, what="k")
 
 
 def test_qk_norm_rope_huge_positions(mk, orc, dev):
@@ -230,8 +193,8 @@ def test_qk_norm_rope_huge_positions(mk, orc, dev):
     inv = orc.rope_inv_freq(hd, 1e4)
     qd, kd = to_dev(q, dev), to_dev(k, dev)
     mk.qk_norm_rope(qd, kd, to_dev(wq, dev), to_dev(wk, dev), to_dev(pos, dev), inv)
-    _assert_norm_rope_close(to_host(qd), *_qk_norm_rope_ref(orc, q, wq, pos, inv), what="q")
-    _assert_norm_rope_close(to_host(kd), *_qk_norm_rope_ref(orc, k, wk, pos, inv), what="k")
+    assert_norm_rope_close(to_host(qd), *qk_norm_rope_ref(orc, q, wq, pos, inv), what="q")
+    assert_norm_rope_close(to_host(kd), *qk_norm_rope_ref(orc, k, wk, pos, inv), what="k")
 
 
 def test_qk_norm_rope_vs_two_launches(mk, orc, dev):

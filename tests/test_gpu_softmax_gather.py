@@ -151,6 +151,38 @@ def test_softmax_onepass_forced_fallback(mk, orc, dev):
                      what=f"after fallback, call {i}")
 
 
+def test_softmax_multiround_fallback_is_bounded(mk, orc, dev):
+    """Persistent one-launch rows over several rounds per row slot, with a
+    poll bound small enough that some chunks give up: a chunk that has fallen
+    back computes every later round's statistics from x without polling
+    again, so the call stays correct and its time stays bounded (with the
+    bound 1, a chunk that kept polling each round would still finish; the
+    wall-time check guards the path that stops polling)."""
+    _case("softmax multi-round fallback [4096,65600] poll bound 1")
+    import time
+    import torch
+    rng = np.random.default_rng(58)
+    N, D = 4096, 65600
+    ws = torch.zeros(mk.softmax_workspace_bytes(N, D), dtype=torch.uint8, device=dev)
+    x = normal_f16(rng, (N, D), 0, 4)
+    xd = to_dev(x, dev)
+    ref = orc.softmax(x, nthreads=8)
+    for limit in (1, 0):
+        prev = mk.softmax_test_poll_limit(limit)
+        try:
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            y = mk.softmax(xd, workspace=ws)
+            torch.cuda.synchronize()
+            el = time.perf_counter() - t0
+        finally:
+            mk.softmax_test_poll_limit(prev)
+        print(f"[case]   poll bound {limit}: {el * 1e3:.2f} ms", flush=True)
+        assert el < 0.5, f"poll bound {limit}: {el:.3f} s"
+        assert_close(to_host(y), ref, what=f"poll bound {limit}")
+    assert_close(to_host(mk.softmax(xd, workspace=ws)), ref, what="after the fallbacks")
+
+
 def test_softmax_graph_replay(mk, orc, dev):
     """The split-row kernels inside a captured graph, replayed several times
     with eager work in between; every replay matches the eager call."""
