@@ -171,6 +171,19 @@ int64_t mi_softmax_workspace_bytes(int64_t N, int64_t D);
 int mi_softmax_ws_f16(const void* x, void* y, int64_t N, int64_t D, void* workspace,
                       int64_t workspace_bytes, void* stream);
 
+/* mi_softmax_f16 for callers that cannot allocate (no counterpart in the
+ * reference; for code under HIP graph capture, tight serving loops and
+ * harnesses that forbid hipMalloc): the same kernels as mi_softmax_ws_f16,
+ * with the workspace taken from a file-scope device array of 1,318,912 bytes
+ * per GPU (row records plus 256 KiB of two-pass pairs) that the library
+ * holds from load until the process ends.  Calls no hipMalloc / hipFree; on a
+ * device's first call it looks up the array's address and zeroes it with a
+ * kernel on `stream`.  Shapes whose workspace would exceed the array return
+ * MI_ERR_UNSUPPORTED.  Every call on one GPU shares that GPU's array, so
+ * calls that overlap in time on one GPU (different streams, or threads)
+ * race; calls in one stream's order do not. */
+int mi_softmax_noalloc_f16(const void* x, void* y, int64_t N, int64_t D, void* stream);
+
 /* Test hook (no counterpart in the reference): bound on the polls a one-pass
  * softmax chunk makes before computing its row's statistics from x itself;
  * 0 forces that fallback everywhere.  Returns the previous bound. */

@@ -32,6 +32,8 @@
 //     the full 2 bytes/element again); it is served from the 256 MB
 //     Infinity Cache when the logits are still resident there, else HBM.
 #include <atomic>
+#include <map>
+#include <mutex>
 
 #include "mi_device.h"
 #include "mi_host.h"
@@ -801,8 +803,83 @@ int softmax_checked(const void* x, void* y, int64_t N, int64_t D, void* ws, int6
     return launch_status();
 }
 
+// ---------------------------------------------------------------------------
+// Allocation-free entry (mi_softmax_noalloc_f16): the same plans and kernels
+// as mi_softmax_ws_f16, with the workspace taken from a file-scope device
+// array (`scratch`, below) instead of the caller or the runtime.  Its host
+// address comes from hipGetSymbolAddress once per device; it is zeroed by a
+// fill kernel on that device's first call (the row records must start at
+// zero) and then left to each call, which leaves it valid for the next.
+// ---------------------------------------------------------------------------
+constexpr int64_t kNoAllocPairBytes = 256 * 1024;  // two-pass (max, sum) pairs
+constexpr int64_t kScratchBytes = kOnePassRegion + kNoAllocPairBytes;
+
+__global__ __launch_bounds__(256) void zero_kernel(uint4* p, int64_t n) {
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n;
+         i += static_cast<int64_t>(gridDim.x) * 256)
+        p[i] = make_uint4(0, 0, 0, 0);
+}
+
 }  // namespace
 }  // namespace mi
+
+// 1,318,912 bytes per GPU, held from the library's load until the process
+// ends.  Host code never passes this name to a kernel or a copy: it is a
+// host-side stand-in; the device address comes from hipGetSymbolAddress.
+static __device__ __align__(256) unsigned char scratch[mi::kScratchBytes];
+
+namespace mi {
+namespace {
+
+// This device's address of `scratch` (nullptr with *err set when the
+// runtime cannot give it), looked up and zeroed on the device's first call.
+void* scratch_for_current_device(hipStream_t s, int* err) {
+    static std::mutex mu;
+    static std::map<int, void*> ptrs;
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) {
+        *err = static_cast<int>(e);
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lock(mu);
+    auto it = ptrs.find(dev);
+    if (it != ptrs.end()) return it->second;
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || ptr == nullptr) {
+        *err = static_cast<int>(e != hipSuccess ? e : hipErrorInvalidSymbol);
+        (void)hipGetLastError();
+        return nullptr;
+    }
+    zero_kernel<<<dim3(64), dim3(256), 0, s>>>(static_cast<uint4*>(ptr), kScratchBytes / 16);
+    e = hipGetLastError();
+    if (e != hipSuccess) {
+        *err = static_cast<int>(e);
+        return nullptr;
+    }
+    ptrs[dev] = ptr;
+    return ptr;
+}
+
+}  // namespace
+}  // namespace mi
+
+extern "C" int mi_softmax_noalloc_f16(const void* x, void* y, int64_t N, int64_t D,
+                                      void* stream) {
+    if (N < 0 || D < 0) return MI_ERR_INVALID_ARGUMENT;
+    if (N == 0 || D == 0) return MI_OK;
+    if (!x || !y) return MI_ERR_INVALID_ARGUMENT;
+    const int64_t need = mi::workspace_bytes(N, D);
+    if (need > mi::kScratchBytes) return MI_ERR_UNSUPPORTED;  // beyond the array
+    if (need == 0)
+        return mi::softmax_checked(x, y, N, D, nullptr, 0, mi::Ws::kRecordsThenPairs, stream);
+    int err = MI_OK;
+    void* ptr = mi::scratch_for_current_device(mi::as_stream(stream), &err);
+    if (!ptr) return err;
+    return mi::softmax_checked(x, y, N, D, ptr, mi::kScratchBytes, mi::Ws::kRecordsThenPairs,
+                               stream);
+}
 
 extern "C" int64_t mi_softmax_workspace_bytes(int64_t N, int64_t D) {
     if (N <= 0 || D <= 0) return 0;

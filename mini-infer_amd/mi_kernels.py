@@ -46,6 +46,7 @@ SIGNATURES = {
     "mi_softmax_f16": [_c_void_p, _c_void_p, _i64, _i64, _c_void_p],
     "mi_embedding_gather_f16": [_c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64, _c_void_p],
     "mi_softmax_ws_f16": [_c_void_p, _c_void_p, _i64, _i64, _c_void_p, _i64, _c_void_p],
+    "mi_softmax_noalloc_f16": [_c_void_p, _c_void_p, _i64, _i64, _c_void_p],
     "mi_paged_kv_scatter_f16": [_c_void_p] * 5 + [_i64] * 8 + [_c_void_p],
     "mi_paged_kv_scatter_kv_f16": [_c_void_p] * 7 + [_i64] * 8 + [_c_void_p],
     "mi_greedy_argmax_f16": [_c_void_p, _i64, _i64, _c_void_p, _c_void_p],
@@ -374,6 +375,24 @@ def softmax(x, y=None, workspace=None, stream=None):
     _check(load_library().mi_softmax_ws_f16(_ptr(x), _ptr(y), x.shape[0], x.shape[1],
                                             _ptr(workspace), nbytes, _stream(stream)),
            "mi_softmax_ws_f16")
+    return y
+
+
+def softmax_noalloc(x, y=None, stream=None):
+    """Row softmax through the allocation-free entry point
+    (mi_softmax_noalloc_f16): its workspace is a device array the library
+    holds, shared by every call on the GPU."""
+    torch = _torch()
+    _need(x, _f16(), "x")
+    x2 = x if x.dim() == 2 else x.view(-1, x.shape[-1])
+    N, D = x2.shape
+    if y is None:
+        y = torch.empty_like(x)
+    _need(y, _f16(), "y")
+    if y.numel() != x.numel():
+        raise ValueError("y must match x")
+    _check(load_library().mi_softmax_noalloc_f16(_ptr(x2), _ptr(y), N, D, _stream(stream)),
+           "mi_softmax_noalloc_f16")
     return y
 
 
