@@ -7,8 +7,8 @@
 //   * inplace  : buf[i] = buf[i] ^ pattern  (read n, write n, same address;
 //                the XOR keeps the write from being a no-op store of the value
 //                just read, and each call flips the buffer back and forth)
-//   * read     : one 32-bit word per workgroup folded from its slice
-//                (read n, write ~nothing)
+//   * read     : every word folded into a per-lane value that guards a store
+//                which never fires (read n, write nothing)
 //   * empty    : a one-workgroup kernel that returns at once (launch floor)
 // Each stream kernel moves 16-byte vectors, VPL of them per lane per step,
 // all loads of a step issued before its stores, with non-temporal loads
@@ -56,15 +56,11 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(const u4* src, u4* dst
             }
         }
     }
-    if constexpr (KIND == kRead) {
-        // one word per workgroup, so the loads cannot be dropped
-        __shared__ uint32_t red;
-        if (threadIdx.x == 0) red = 0;
-        __syncthreads();
-        atomicXor(&red, acc);
-        __syncthreads();
-        if (threadIdx.x == 0) sink[blockIdx.x] = red;
-    }
+    // The loaded values feed a store that a fixed pattern never triggers
+    // (the buffers hold 0x01 bytes), so no load can be dropped and no lane
+    // pays for a reduction.
+    if constexpr (KIND == kRead)
+        if (acc == pattern) sink[blockIdx.x] = acc;
 }
 
 __global__ void empty_kernel() {}
@@ -124,8 +120,9 @@ extern "C" int mi_floor_inplace(void* buf, int64_t bytes, int vpl, int persisten
     return launch<kInplace>(buf, buf, bytes, vpl, persistent, nullptr, 0, stream);
 }
 
-// Read of `bytes` of src, one 32-bit word per workgroup into sink (which
-// holds sink_words words; the grid must fit).
+// Read of `bytes` of src; sink (sink_words words, at least the grid) is only
+// written if the XOR of a lane's words equals the fixed pattern, which the
+// benchmark's 0x01-filled buffers never give.
 extern "C" int mi_floor_read(const void* src, int64_t bytes, int vpl, int persistent,
                              uint32_t* sink, int64_t sink_words, void* stream) {
     return launch<kRead>(src, nullptr, bytes, vpl, persistent, sink, sink_words, stream);
