@@ -111,11 +111,12 @@ def randn16(shape, gen, dev, mean=0.0, std=1.0):
 # (mini-infer_amd/bench/floors.hip -> libmi_floors.so), timed like the
 # kernels (graph replay, buffers rotated past the Infinity Cache).  Each floor
 # is the fastest of a few plain forms (16-byte vectors per lane per step
-# 1/2/4/8, one workgroup per tile or a resident grid-stride grid), so it is
+# 1/2/4/8, one workgroup per tile or a resident grid-stride grid,
+# non-temporal or plain loads), so it is
 # the time a no-work kernel of this library's style needs for those bytes.
 # ---------------------------------------------------------------------------
 
-FLOOR_FORMS = [(v, p) for v in (1, 2, 4, 8) for p in (0, 1)]
+FLOOR_FORMS = [(v, p, n) for v in (1, 2, 4, 8) for p in (0, 1) for n in (0, 1)]
 _FLOORS_LIB = None
 _FLOOR = {}
 
@@ -129,28 +130,28 @@ def floors_lib():
             raise RuntimeError(f"{path} is missing: run `make -C mini-infer_amd`")
         lib = ctypes.CDLL(str(path))
         i64, vp, ci = ctypes.c_int64, ctypes.c_void_p, ctypes.c_int
-        lib.mi_floor_copy.argtypes = [vp, vp, i64, ci, ci, vp]
-        lib.mi_floor_inplace.argtypes = [vp, i64, ci, ci, vp]
-        lib.mi_floor_read.argtypes = [vp, i64, ci, ci, vp, i64, vp]
+        lib.mi_floor_copy.argtypes = [vp, vp, i64, ci, vp]
+        lib.mi_floor_inplace.argtypes = [vp, i64, ci, vp]
+        lib.mi_floor_read.argtypes = [vp, i64, ci, vp, i64, vp]
         lib.mi_floor_empty.argtypes = [vp]
         _FLOORS_LIB = lib
     return _FLOORS_LIB
 
 
-def _floor_launcher(kind, bufs, sink, nbytes, vpl, persistent):
+def _floor_launcher(kind, bufs, sink, nbytes, vpl, persistent, plain):
     import torch
     lib = floors_lib()
+    form = vpl | (16 if persistent else 0) | (32 if plain else 0)
 
     def go(i):
         st = torch.cuda.current_stream().cuda_stream
         if kind == "copy":
-            rc = lib.mi_floor_copy(bufs[i][0].data_ptr(), bufs[i][1].data_ptr(), nbytes, vpl,
-                                   persistent, st)
+            rc = lib.mi_floor_copy(bufs[i][0].data_ptr(), bufs[i][1].data_ptr(), nbytes, form, st)
         elif kind == "inplace":
-            rc = lib.mi_floor_inplace(bufs[i][0].data_ptr(), nbytes, vpl, persistent, st)
+            rc = lib.mi_floor_inplace(bufs[i][0].data_ptr(), nbytes, form, st)
         else:
-            rc = lib.mi_floor_read(bufs[i][0].data_ptr(), nbytes, vpl, persistent,
-                                   sink.data_ptr(), sink.numel(), st)
+            rc = lib.mi_floor_read(bufs[i][0].data_ptr(), nbytes, form, sink.data_ptr(),
+                                   sink.numel(), st)
         if rc != 0:
             raise RuntimeError(f"floor {kind} failed: {rc}")
     return go
@@ -172,9 +173,9 @@ def floor_time(dev, kind, nbytes, iters=40, warmup=5, forms=None):
             for _ in range(ns)]
     sink = torch.zeros(1 << 20, dtype=torch.int32, device=dev)
     per = {}
-    for vpl, pers in (forms or FLOOR_FORMS):
-        per[(vpl, pers)] = time_launches(_floor_launcher(kind, bufs, sink, nbytes, vpl, pers), ns,
-                                         iters, warmup)
+    for vpl, pers, plain in (forms or FLOOR_FORMS):
+        per[(vpl, pers, plain)] = time_launches(
+            _floor_launcher(kind, bufs, sink, nbytes, vpl, pers, plain), ns, iters, warmup)
     del bufs, nb
     best = min(per.values())
     if forms is None:
@@ -225,12 +226,12 @@ def floor_sweep(dev, sizes_mb=(8, 20, 40, 67, 100, 174, 235, 465)):
             moved = nbytes if kind == "read" else 2 * nbytes
             n = moved if kind == "read" else nbytes
             _, per = floor_time(dev, kind, n, forms=FLOOR_FORMS)
-            for (v, p), sec in per.items():
+            for (v, p, pl), sec in per.items():
                 rows.append({"kind": kind, "moved_bytes": moved, "vpl": v, "persistent": p,
-                             "us": round(sec * 1e6, 3),
+                             "plain_loads": pl, "us": round(sec * 1e6, 3),
                              "frac": round(moved / sec / HBM_PEAK, 4)})
                 log(f"[floors] {kind:<8} {moved / 1e6:8.1f} MB vpl={v} persistent={p} "
-                    f"{sec * 1e6:9.2f} us {100 * moved / sec / HBM_PEAK:6.1f}%")
+                    f"plain_loads={pl} {sec * 1e6:9.2f} us {100 * moved / sec / HBM_PEAK:6.1f}%")
     return rows
 
 

@@ -11,9 +11,9 @@
 //                which never fires (read n, write nothing)
 //   * empty    : a one-workgroup kernel that returns at once (launch floor)
 // Each stream kernel moves 16-byte vectors, VPL of them per lane per step,
-// all loads of a step issued before its stores, with non-temporal loads
-// and stores; `persistent` selects a grid of the resident capacity walking
-// the buffer with a grid stride instead of one workgroup per tile.  The
+// all loads of a step issued before its stores, with non-temporal stores and
+// non-temporal or plain loads; a `form` also selects one workgroup per tile
+// or a grid of the resident capacity walking the buffer with a grid stride.  The
 // benchmark takes the fastest of a few (VPL, persistent) forms as the floor.
 // Not part of the layer-kernel library: nothing here is reached from
 // include/mi_kernels.h.
@@ -25,14 +25,17 @@ namespace {
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef uint32_t u4 __attribute__((ext_vector_type(4)));
 
-__device__ __forceinline__ u4 ld(const u4* p) { return __builtin_nontemporal_load(p); }
+template <bool NT>
+__device__ __forceinline__ u4 ld(const u4* p) {
+    if constexpr (NT) return __builtin_nontemporal_load(p); else return *p;
+}
 __device__ __forceinline__ void st(u4* p, u4 v) { __builtin_nontemporal_store(v, p); }
 
 constexpr int kThreads = 256;
 
 enum Kind { kCopy = 0, kInplace = 1, kRead = 2 };
 
-template <int KIND, int VPL>
+template <int KIND, int VPL, bool NT>
 __global__ __launch_bounds__(kThreads) void stream_kernel(const u4* src, u4* dst, int64_t nvec,
                                                           uint32_t pattern, uint32_t* sink) {
     const int64_t tile = static_cast<int64_t>(kThreads) * VPL;
@@ -44,7 +47,7 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(const u4* src, u4* dst
 #pragma unroll
         for (int j = 0; j < VPL; ++j) {
             const int64_t i = base + static_cast<int64_t>(j) * kThreads;
-            if (i < nvec) v[j] = ld(src + i);
+            if (i < nvec) v[j] = ld<NT>(src + i);
         }
 #pragma unroll
         for (int j = 0; j < VPL; ++j) {
@@ -65,10 +68,10 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(const u4* src, u4* dst
 
 __global__ void empty_kernel() {}
 
-template <int KIND, int VPL>
+template <int KIND, int VPL, bool NT>
 int launch_vpl(const void* src, void* dst, int64_t nvec, int persistent, uint32_t* sink,
                int64_t sink_words, hipStream_t s) {
-    const auto k = stream_kernel<KIND, VPL>;
+    const auto k = stream_kernel<KIND, VPL, NT>;
     const int64_t tiles = (nvec + kThreads * VPL - 1) / (kThreads * VPL);
     int64_t grid = tiles;
     if (persistent) {
@@ -88,44 +91,53 @@ int launch_vpl(const void* src, void* dst, int64_t nvec, int persistent, uint32_
     return hipGetLastError() == hipSuccess ? 0 : 1;
 }
 
+template <int KIND, bool NT>
+int launch_nt(const void* src, void* dst, int64_t nvec, int vpl, int persistent, uint32_t* sink,
+              int64_t sink_words, hipStream_t s) {
+    switch (vpl) {
+        case 1: return launch_vpl<KIND, 1, NT>(src, dst, nvec, persistent, sink, sink_words, s);
+        case 2: return launch_vpl<KIND, 2, NT>(src, dst, nvec, persistent, sink, sink_words, s);
+        case 4: return launch_vpl<KIND, 4, NT>(src, dst, nvec, persistent, sink, sink_words, s);
+        case 8: return launch_vpl<KIND, 8, NT>(src, dst, nvec, persistent, sink, sink_words, s);
+        default: return -1;
+    }
+}
+
+// form: vpl (1, 2, 4, 8) | 16 (resident grid-stride grid) | 32 (plain loads
+// instead of non-temporal ones)
 template <int KIND>
-int launch(const void* src, void* dst, int64_t bytes, int vpl, int persistent, uint32_t* sink,
+int launch(const void* src, void* dst, int64_t bytes, int form, uint32_t* sink,
            int64_t sink_words, void* stream) {
+    const int vpl = form & 15, persistent = (form >> 4) & 1, plain = (form >> 5) & 1;
     if (bytes <= 0 || bytes % 16 != 0 || !src || (KIND != kRead && !dst) ||
         (KIND == kRead && !sink))
         return -1;
     if ((reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(dst)) & 15u) return -1;
     const int64_t nvec = bytes / 16;
     const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-    switch (vpl) {
-        case 1: return launch_vpl<KIND, 1>(src, dst, nvec, persistent, sink, sink_words, s);
-        case 2: return launch_vpl<KIND, 2>(src, dst, nvec, persistent, sink, sink_words, s);
-        case 4: return launch_vpl<KIND, 4>(src, dst, nvec, persistent, sink, sink_words, s);
-        case 8: return launch_vpl<KIND, 8>(src, dst, nvec, persistent, sink, sink_words, s);
-        default: return -1;
-    }
+    return plain ? launch_nt<KIND, false>(src, dst, nvec, vpl, persistent, sink, sink_words, s)
+                 : launch_nt<KIND, true>(src, dst, nvec, vpl, persistent, sink, sink_words, s);
 }
 
 }  // namespace
 
 // Out-of-place copy of `bytes` (a multiple of 16, 16-byte aligned buffers).
-extern "C" int mi_floor_copy(const void* src, void* dst, int64_t bytes, int vpl, int persistent,
-                             void* stream) {
-    return launch<kCopy>(src, dst, bytes, vpl, persistent, nullptr, 0, stream);
+extern "C" int mi_floor_copy(const void* src, void* dst, int64_t bytes, int form, void* stream) {
+    return launch<kCopy>(src, dst, bytes, form, nullptr, 0, stream);
 }
 
 // In-place read-then-write of `bytes` of buf (each 32-bit word XOR-ed with
 // a fixed pattern, so two calls restore it).
-extern "C" int mi_floor_inplace(void* buf, int64_t bytes, int vpl, int persistent, void* stream) {
-    return launch<kInplace>(buf, buf, bytes, vpl, persistent, nullptr, 0, stream);
+extern "C" int mi_floor_inplace(void* buf, int64_t bytes, int form, void* stream) {
+    return launch<kInplace>(buf, buf, bytes, form, nullptr, 0, stream);
 }
 
 // Read of `bytes` of src; sink (sink_words words, at least the grid) is only
 // written if the XOR of a lane's words equals the fixed pattern, which the
 // benchmark's 0x01-filled buffers never give.
-extern "C" int mi_floor_read(const void* src, int64_t bytes, int vpl, int persistent,
-                             uint32_t* sink, int64_t sink_words, void* stream) {
-    return launch<kRead>(src, nullptr, bytes, vpl, persistent, sink, sink_words, stream);
+extern "C" int mi_floor_read(const void* src, int64_t bytes, int form, uint32_t* sink,
+                             int64_t sink_words, void* stream) {
+    return launch<kRead>(src, nullptr, bytes, form, sink, sink_words, stream);
 }
 
 // An empty one-workgroup launch.

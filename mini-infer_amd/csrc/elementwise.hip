@@ -16,9 +16,10 @@
 //
 // Design (HBM-bound; 6 bytes/element for the binary ops, 4 for unary): each
 // 256-lane workgroup owns a contiguous tile of kUnroll x 256 16-byte vectors
-// per operand; a lane issues all of its loads before any math.  kUnroll = 2
-// measured best at [4096, 18944] (78% of HBM peak vs 74% at 4 and 73% at 8).  Inputs and outputs are touched once,
-// so loads and stores carry the non-temporal hint.  A scalar kernel takes
+// per operand; a lane issues all of its loads before any math.  kUnroll = 1
+// measured best at [6064, 18944]: 80-81% of HBM peak against 77% at 2 (and
+// 74% at 4, 73% at 8 at [4096, 18944]).  Inputs and outputs are touched
+// once, so loads and stores carry the non-temporal hint.  A scalar kernel takes
 // the n % 8 tail and any unaligned buffer.
 #include "mi_device.h"
 #include "mi_host.h"
@@ -47,7 +48,7 @@ constexpr bool binary() {
 }
 
 #ifndef MI_EW_UNROLL
-#define MI_EW_UNROLL 2
+#define MI_EW_UNROLL 1
 #endif
 constexpr int kUnroll = MI_EW_UNROLL;
 constexpr int kThreads = 256;

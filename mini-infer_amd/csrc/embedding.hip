@@ -41,7 +41,10 @@ __global__ __launch_bounds__(256) void gather_kernel(const int64_t* __restrict__
 #pragma unroll
             for (int j = 0; j < kBatch; ++j) {
                 const int64_t c = c0 + j * kLanes + lane;
-                v[j] = (valid && c < nv) ? ld8_stream(src + c * 8) : h8(0);
+                // plain loads: the rows are scattered over a table far larger than
+                // the caches, and the non-temporal hint measured 66% -> 72% of peak
+                // slower at T = 6064 of [152064, 3584] (16.4 -> 15.1 us)
+                v[j] = (valid && c < nv) ? ld8(src + c * 8) : h8(0);
             }
 #pragma unroll
             for (int j = 0; j < kBatch; ++j) {
