@@ -71,6 +71,13 @@ int mi_rope_neox_f16(const void* x, const void* cos_t, const void* sin_t,
                      void* y, int64_t B, int64_t S, int64_t H, int64_t D,
                      void* stream);
 
+/* Positions (the tables entry below and the two fused entries after it):
+ * any int64 value.  The angle float(pos) * inv_freq[i] is an fp32 value and
+ * its cos/sin are evaluated to half(RN32(exact)) for every finite fp32 angle
+ * (an fp32 form up to 2^20, Cody-Waite in fp64 to 2^24, Payne-Hanek
+ * reduction above), so there is no range limit and nothing for the host to
+ * check in the device-resident positions. */
+
 /* cos/sin tables [N, half] for positions the device can read (device memory,
  * or pinned host memory from hipHostMalloc written before the call):
  * cos_t[n, i] = half(cos(float(positions[n]) * inv_freq[i])), likewise sin.

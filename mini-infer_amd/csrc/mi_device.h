@@ -61,12 +61,29 @@ __device__ __forceinline__ void st8_stream(half_t* p, h8 v) {
 // see a store inside inline asm, so the asm carries the wait states itself
 // (without them, following VALU code overwrote the data before the store
 // read it).
-#ifndef MI_WT_BITS
-#define MI_WT_BITS "nt sc1"
+// MI_WT_FORM picks the cache-policy bits of that store from the forms
+// measured on the GPU (no other text can reach the asm):
+//   0 = "nt sc1" (default: fastest for the in-place RoPE / Q/K-norm stores),
+//   1 = "sc1", 2 = "sc0 sc1", 3 = "sc0 sc1 nt", 4 = "sc0 nt".
+// Each form is followed by the same two wait states (s_nop 1).
+#ifndef MI_WT_FORM
+#define MI_WT_FORM 0
+#endif
+#if MI_WT_FORM == 0
+#define MI_WT_ASM "global_store_dwordx4 %0, %1, off nt sc1\n\ts_nop 1"
+#elif MI_WT_FORM == 1
+#define MI_WT_ASM "global_store_dwordx4 %0, %1, off sc1\n\ts_nop 1"
+#elif MI_WT_FORM == 2
+#define MI_WT_ASM "global_store_dwordx4 %0, %1, off sc0 sc1\n\ts_nop 1"
+#elif MI_WT_FORM == 3
+#define MI_WT_ASM "global_store_dwordx4 %0, %1, off sc0 sc1 nt\n\ts_nop 1"
+#elif MI_WT_FORM == 4
+#define MI_WT_ASM "global_store_dwordx4 %0, %1, off sc0 nt\n\ts_nop 1"
+#else
+#error "MI_WT_FORM must be 0-4"
 #endif
 __device__ __forceinline__ void st8_stream_wt(half_t* p, h8 v) {
-    asm volatile("global_store_dwordx4 %0, %1, off " MI_WT_BITS "\n\ts_nop 1" : : "v"(p), "v"(v)
-                 : "memory");
+    asm volatile(MI_WT_ASM : : "v"(p), "v"(v) : "memory");
 }
 // Store selected per kernel at compile time.
 template <bool WT>

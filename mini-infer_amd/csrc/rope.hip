@@ -65,8 +65,9 @@ struct InvFreq {
 // fp16 cos/sin of an fp32 angle, equal to half(RN32(exact)) (see file header).
 // |ang| <= 2^20: the fp32 Cody-Waite form, re-evaluated in fp64 when a value
 // lies within rope_guard_width of an fp16 rounding boundary; larger angles
-// (positions beyond 2^20 / inv_freq) go straight to the fp64 form, which holds
-// to |ang| <= 2^30.
+// (positions beyond 2^20 / inv_freq) go straight to the fp64 form
+// (rope_sincos_any: Cody-Waite to 2^24, Payne-Hanek above), which covers
+// every fp32 angle -- so every int64 position -- with no range limit.
 __device__ __forceinline__ bool near_half_boundary(float v) {
     const float d = rope_guard_width(v);
     return to_half(v - d) != to_half(v + d);
@@ -77,7 +78,7 @@ __device__ __forceinline__ void cos_sin_half(float ang, half_t& hc, half_t& hs) 
     rope_sincos_f32(ang, &s, &c);
     if (!rope_sincos_f32_ok(ang) || near_half_boundary(c) || near_half_boundary(s)) {
         double sd, cd;
-        rope_sincos_f64(static_cast<double>(ang), &sd, &cd);
+        rope_sincos_any(ang, &sd, &cd);
         c = static_cast<float>(cd);
         s = static_cast<float>(sd);
     }

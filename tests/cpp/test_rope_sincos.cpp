@@ -11,8 +11,12 @@
 //      fp32 value v holds RN32(exact) -- exact from libm's double sin/cos;
 //   2. the table value the kernels produce (fp32 form, fp64 re-evaluation
 //      near an fp16 rounding boundary, fp64 form above 2^20) equals
-//      half(RN32(exact)), the oracle's rule, bit for bit;
-//   3. the fp64 form stays within 2^-50 relative of long-double sin/cos.
+//      half(RN32(exact)), the oracle's rule, bit for bit -- also at and just
+//      beyond 2^24, where the fp64 form changes from Cody-Waite to the
+//      Payne-Hanek reduction, and for fp32 angles up to 2^63 (every int64
+//      position) and the largest finite fp32;
+//   3. the fp64 form stays within 2^-50 relative of long-double sin/cos, on
+//      both sides of 2^24 and up to 2^127.
 // Exit status 0 and "ALL OK" when every claim holds.
 #include <math.h>
 #include <stdint.h>
@@ -57,7 +61,7 @@ static void check_angle(float a) {
     };
     if (!fast_ok || near(c) || near(s)) {
         double sd, cd;
-        mi::rope_sincos_f64((double)a, &sd, &cd);
+        mi::rope_sincos_any(a, &sd, &cd);
         c = (float)cd;
         s = (float)sd;
         ++g_fallback;
@@ -74,6 +78,17 @@ int main() {
     for (uint32_t b = 0x80000000u; b <= 0xC9800000u; b += 4999) check_angle(bits_to_float(b));
     // above 2^20: the fp64 form alone (positions up to 2^24)
     for (uint32_t b = 0x49800001u; b <= 0x4B800000u; b += 997) check_angle(bits_to_float(b));
+    // at and just beyond 2^24 (the Cody-Waite / Payne-Hanek boundary), both signs
+    for (uint32_t b = 0x4B7FF000u; b <= 0x4B801000u; ++b) {
+        check_angle(bits_to_float(b));
+        check_angle(-bits_to_float(b));
+    }
+    // beyond 2^24: int64 positions (to 2^63) and the rest of the fp32 range
+    for (uint32_t b = 0x4B800001u; b <= 0x5F000000u; b += 1009) check_angle(bits_to_float(b));
+    for (uint32_t b = 0x5F000001u; b <= 0x7F7FFFFFu; b += 100003) check_angle(bits_to_float(b));
+    for (int64_t p : {int64_t{16777216}, int64_t{16777217}, int64_t{16777218}, int64_t{1} << 31,
+                      (int64_t{1} << 40) + 12345, int64_t{9223372036854775807}})
+        check_angle((float)p);
     for (double theta : {1.0e4, 1.0e6}) {
         for (int i = 0; i < 64; ++i) {
             const float inv = powf((float)theta, -(float)(2 * i) / 128.0f);
@@ -81,20 +96,28 @@ int main() {
         }
     }
     double worst64 = 0.0;
-    for (uint32_t b = 0x3f800000u; b <= 0x4b800000u; b += 40961) {
+    long fp64_checked = 0;
+    for (uint32_t b = 0x3f800000u; b <= 0x7F7FFFFFu; b += 40961) {
         const float a = bits_to_float(b);
         double s, c;
-        mi::rope_sincos_f64(a, &s, &c);
+        mi::rope_sincos_any(a, &s, &c);
         const long double es = sinl((long double)a), ec = cosl((long double)a);
-        const double rs = (double)(fabsl((long double)s - es) / fabsl(es));
-        const double rc = (double)(fabsl((long double)c - ec) / fabsl(ec));
-        if (rs > worst64) worst64 = rs;
-        if (rc > worst64) worst64 = rc;
+        // relative error, away from the zeros (where it measures the absolute
+        // error of the reduction, 2^-60 or better, not the value)
+        if (fabsl(es) > 0x1p-8L) {
+            const double rs = (double)(fabsl((long double)s - es) / fabsl(es));
+            if (rs > worst64) worst64 = rs;
+        }
+        if (fabsl(ec) > 0x1p-8L) {
+            const double rc = (double)(fabsl((long double)c - ec) / fabsl(ec));
+            if (rc > worst64) worst64 = rc;
+        }
+        ++fp64_checked;
     }
     printf("angles %ld, fp64 re-evaluations %ld (%.3f%%), guard failures %ld, table mismatches %ld, "
-           "fp64 worst relative error 2^%.1f\n",
+           "fp64 worst relative error 2^%.1f over %ld angles to 2^128\n",
            g_checked, g_fallback, 100.0 * g_fallback / g_checked, g_guard_fail, g_table_fail,
-           log2(worst64));
+           log2(worst64), fp64_checked);
     const bool ok = g_guard_fail == 0 && g_table_fail == 0 && worst64 < 0x1p-50;
     if (ok) printf("ALL OK\n");
     return ok ? 0 : 1;

@@ -62,12 +62,15 @@ def test_tables_large_positions(mk, orc, dev):
     assert_bits_equal(to_host(s), s_ref, what="sin")
 
 
-@pytest.mark.parametrize("lo,hi", [(1 << 20, 1 << 22), (1 << 22, 1 << 24)])
+@pytest.mark.parametrize("lo,hi", [(1 << 20, 1 << 22), (1 << 22, 1 << 24),
+                                   ((1 << 24) - 2048, (1 << 24) + 2048), (1 << 24, 1 << 40),
+                                   (1 << 40, 1 << 62), (-(1 << 62), 0)])
 def test_tables_huge_positions(mk, orc, dev, lo, hi):
     """Positions past 2^20 (angles beyond the fp32 sin/cos range, evaluated in
-    fp64 directly), theta 1e4 and 1e6: still bit-exact."""
+    fp64 directly; past 2^24 with the Payne-Hanek reduction), up to 2^62 and
+    negative, theta 1e4 and 1e6: still bit-exact."""
     _case(f"rope tables positions in [{lo}, {hi})")
-    rng = np.random.default_rng(lo)
+    rng = np.random.default_rng(abs(lo) % (1 << 32))
     pos = rng.integers(lo, hi, 4096).astype(np.int64)
     for theta in (1e4, 1e6):
         inv = orc.rope_inv_freq(128, theta)
@@ -183,13 +186,15 @@ def test_qk_norm_rope(mk, orc, dev, T, Hq, Hkv, hd):
 
 
 def test_qk_norm_rope_huge_positions(mk, orc, dev):
-    """Positions up to 2^23: the in-kernel table takes the fp64 path."""
-    _case("qk_norm_rope positions up to 2^23")
+    """Positions up to 2^23 and, every third token, up to 2^62: the in-kernel
+    table takes the fp64 paths."""
+    _case("qk_norm_rope positions up to 2^62")
     rng = np.random.default_rng(23)
     T, Hq, Hkv, hd = 300, 28, 4, 128
     q = normal_f16(rng, (T, Hq, hd)); k = normal_f16(rng, (T, Hkv, hd))
     wq = normal_f16(rng, (hd,), 1.0, 0.1); wk = normal_f16(rng, (hd,), 1.0, 0.1)
     pos = rng.integers(0, 1 << 23, T).astype(np.int64)
+    pos[::3] = rng.integers(1 << 24, 1 << 62, len(pos[::3]))  # Payne-Hanek path
     inv = orc.rope_inv_freq(hd, 1e4)
     qd, kd = to_dev(q, dev), to_dev(k, dev)
     mk.qk_norm_rope(qd, kd, to_dev(wq, dev), to_dev(wk, dev), to_dev(pos, dev), inv)
