@@ -199,14 +199,34 @@ __device__ __forceinline__ uint64_t argmax_key(uint16_t h, int64_t i) {
 
 __device__ __forceinline__ uint64_t max_u64(uint64_t a, uint64_t b) { return a > b ? a : b; }
 
-__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) {
-        const uint32_t lo = __shfl_xor(static_cast<uint32_t>(v), off, kWave);
-        const uint32_t hi = __shfl_xor(static_cast<uint32_t>(v >> 32), off, kWave);
-        v = max_u64(v, (static_cast<uint64_t>(hi) << 32) | lo);
+// The largest 64-bit key of the wave, in every lane: DPP within 16-lane
+// rows (both halves of the key move together), then the permlane swaps
+// across rows (no LDS).  Every lane must be active.
+template <int CTRL>
+__device__ __forceinline__ uint64_t dpp_u64(uint64_t v) {
+    const uint32_t lo = __builtin_amdgcn_mov_dpp(static_cast<int>(v), CTRL, 0xF, 0xF, false);
+    const uint32_t hi = __builtin_amdgcn_mov_dpp(static_cast<int>(v >> 32), CTRL, 0xF, 0xF, false);
+    return (static_cast<uint64_t>(hi) << 32) | lo;
+}
+template <int STRIDE>
+__device__ __forceinline__ uint64_t max_xor_u64(uint64_t v) {
+    uint32_t la, lb, ha, hb;
+    if constexpr (STRIDE == 16) {
+        pair_xor16(static_cast<uint32_t>(v), la, lb);
+        pair_xor16(static_cast<uint32_t>(v >> 32), ha, hb);
+    } else {
+        pair_xor32(static_cast<uint32_t>(v), la, lb);
+        pair_xor32(static_cast<uint32_t>(v >> 32), ha, hb);
     }
-    return v;
+    return max_u64((static_cast<uint64_t>(ha) << 32) | la, (static_cast<uint64_t>(hb) << 32) | lb);
+}
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+    v = max_u64(v, dpp_u64<0xB1>(v));   // xor 1
+    v = max_u64(v, dpp_u64<0x4E>(v));   // xor 2
+    v = max_u64(v, dpp_u64<0x141>(v));  // other quad of the half row
+    v = max_u64(v, dpp_u64<0x140>(v));  // other half of the row
+    v = max_xor_u64<16>(v);
+    return max_xor_u64<32>(v);
 }
 
 __device__ __forceinline__ int32_t key_index(uint64_t key) {

@@ -117,6 +117,27 @@ __device__ __forceinline__ float dpp_f(float v) {
         float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
 }
 
+// Lane i's value and lane (i ^ 16)'s, or (i ^ 32)'s, through gfx950's
+// v_permlane16_swap / v_permlane32_swap (VALU, no LDS round trip as a
+// ds_bpermute shuffle takes).  Swapping a register with itself leaves, in
+// the two results, lane i's own value and its partner's (in one order or the
+// other); callers combine them with a commutative operation, so both lanes
+// of a pair get the same bits.  Every lane of the wave must be active.
+// (Used by the 64-bit argmax reduction, where it replaced twelve shuffles:
+// 7.7 -> 7.3 us at [64, 152064].  For the fp32 reductions below it measured
+// no better -- softmax [64, 152064] 9.8 -> 10.2 us -- so they keep
+// __shfl_xor across rows.)
+__device__ __forceinline__ void pair_xor16(uint32_t v, uint32_t& a, uint32_t& b) {
+    const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    a = r[0];
+    b = r[1];
+}
+__device__ __forceinline__ void pair_xor32(uint32_t v, uint32_t& a, uint32_t& b) {
+    const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    a = r[0];
+    b = r[1];
+}
+
 // Sum across aligned groups of G lanes (G a power of two, 1..64); every lane
 // of a group receives the group total.
 template <int G>

@@ -175,6 +175,8 @@ __device__ __forceinline__ void write_range(const half_t* xr, half_t* yr, int64_
 }
 
 // Workgroup-wide merge of per-lane (m, s): max first, then rescaled sums.
+// (A one-barrier form -- wave (max, sum) pairs folded after a single barrier
+// -- measured no faster at [64, 152064].)  `slots` needs one float per wave.
 __device__ __forceinline__ void block_merge(float& m, float& s, float* slots) {
     const float M = block_max(m, slots);
     const float part = (m == -INFINITY) ? 0.0f : s * fast_exp(m - M);
@@ -510,6 +512,7 @@ __device__ __forceinline__ void row_stats_from_x(const half_t* xr, int64_t D, fl
     tile_stats<2>(xr, 0, D, fm, fs);
     __syncthreads();  // slots reused
     block_merge(fm, fs, slots);
+    __syncthreads();  // every wave has read slots before a later round writes them
     M = fm;
     S = fs;
 }
