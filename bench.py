@@ -364,7 +364,14 @@ def all_kernels(mk, dev, iters, warmup):
     sec = time_launches(lambda i: mk.embedding_gather(ids[i], table, out=outs[i]), ns, iters,
                         warmup)
     out.append(report("embedding_gather", "T=6064 from [152064,3584]", nb, sec, T))
-    del table, ids, outs
+    # 5a'. the gather fused with the input RMSNorm (writes hidden and normed)
+    nb = T * 8 + 3 * T * D * 2 + D * 2
+    w_in = randn16((D,), gen, dev, 1.0, 0.1)
+    nrm = [torch.empty((T, D), dtype=f16, device=dev) for _ in range(ns)]
+    sec = time_launches(lambda i: mk.embedding_rmsnorm(ids[i], table, w_in, hidden=outs[i],
+                                                       y=nrm[i]), ns, iters, warmup)
+    out.append(report("embedding_rmsnorm", "T=6064 from [152064,3584]", nb, sec, T))
+    del table, ids, outs, nrm
     # 5b. residual + RMSNorm
     nb = 4 * T * D * 2 + D * 2
     ns = rotations(3 * T * D * 2)
@@ -428,7 +435,14 @@ def all_kernels(mk, dev, iters, warmup):
     sec = time_launches(lambda i: mk.greedy_argmax(xs[i], out=outi, workspace=wsa), ns, iters,
                         warmup)
     out.append(report("greedy_argmax", "[64,152064]", nb, sec, N))
-    del xs
+    # 5g'. softmax and argmax of the same logits in one pass
+    nb = 2 * N * V * 2 + N * 4
+    ysm = [torch.empty((N, V), dtype=f16, device=dev) for _ in range(ns)]
+    wsf = torch.zeros(mk.softmax_argmax_workspace_bytes(N, V), dtype=torch.uint8, device=dev)
+    sec = time_launches(lambda i: mk.softmax_argmax(xs[i], wsf, probs=ysm[i], out=outi), ns,
+                        iters, warmup)
+    out.append(report("softmax_argmax", "[64,152064]", nb, sec, N))
+    del xs, ysm
     # 5h. paged KV scatter of the chain's K and V [6064, 4, 128], block size
     # 16, as one 6064-token sequence into shuffled physical blocks
     H, hd, bs = 4, 128, 16
@@ -624,26 +638,25 @@ def chain_bytes(s, segments_tokens):
     output written once), from the workload's shapes."""
     T, D, I, V, N = s["T"], s["hidden_size"], s["intermediate_size"], s["vocab"], s["logit_rows"]
     Hq, Hkv, hd = s["num_heads"], s["num_kv_heads"], s["head_dim"]
-    return ((T * 8 + 2 * T * D * 2)                                   # gather
-            + (2 * T * D * 2 + D * 2)                                 # input norm
+    return ((T * 8 + 3 * T * D * 2 + D * 2)                           # gather + input norm
             + (2 * T * (Hq + Hkv) * hd * 2 + T * 8 + 2 * hd * 2)      # qk-norm + rope
             + (2 * 2 * segments_tokens * Hkv * hd * 2)                # K + V scatter
             + 2 * (4 * T * D * 2 + D * 2)                             # 2x residual add + norm
             + 3 * T * I * 2                                           # SwiGLU
-            + 2 * N * V * 2 + (N * V * 2 + N * 4))                    # softmax, argmax
+            + (2 * N * V * 2 + N * 4))                                # softmax + argmax
 
 
 def decoder_chain(mk, dev, iters, warmup):
     """BASELINE config 5 as one step: the C++ decoder chain (include/mi_chain.h)
     over one non-GEMM decoder layer at T = 6064 (64 decode tokens at random
     positions + two 3000-token prefills), then the sampling step:
-      gather -> input RMSNorm -> Q/K-norm + RoPE -> paged K+V scatter ->
+      gather + input RMSNorm -> Q/K-norm + RoPE -> paged K+V scatter ->
       residual add + RMSNorm -> SwiGLU [6064,18944] -> residual add + final
-      RMSNorm -> softmax [64,152064] -> greedy argmax,
+      RMSNorm -> softmax + greedy argmax of the logits [64,152064],
     with seeded stand-ins for the GEMM outputs, captured as one graph.  Also
     timed: the same steps as the reference's caller composes them from its
-    unfused launchers (src/model/transformer_model.cpp:578-660;
-    src/layers/attention.cpp:743-846): a device copy and RMSNorm, Q-norm and
+    unfused launchers (src/model/transformer_model.cpp:561-660;
+    src/layers/attention.cpp:743-846): gather, a device copy and RMSNorm, Q-norm and
     K-norm, cos/sin tables then RoPE of Q and of K, one scatter for K and one
     for V per segment, add in place + copy + RMSNorm twice.  Both run this
     library's kernels, so the difference is the fusion alone.  Bytes are the
@@ -659,6 +672,9 @@ def decoder_chain(mk, dev, iters, warmup):
     cos_t = torch.empty((T, hd // 2), dtype=torch.float16, device=dev)
     sin_t = torch.empty_like(cos_t)
     tmp = torch.empty((T, D), dtype=torch.float16, device=dev)
+    wss = torch.zeros(max(16, mk.softmax_workspace_bytes(N, V)), dtype=torch.uint8, device=dev)
+    wsa = torch.zeros(max(16, mk.greedy_argmax_workspace_bytes(N, V)), dtype=torch.uint8,
+                      device=dev)
 
     def fused(i):
         ws[i].run()
@@ -688,11 +704,11 @@ def decoder_chain(mk, dev, iters, warmup):
             mk.rmsnorm(tmp, wt, y=y)
             if y is t["post_normed"]:
                 mk.swiglu(t["gate"], t["up"], out=t["act_out"])
-        mk.softmax(t["logits"], y=t["probs"], workspace=t["softmax_ws"])
-        mk.greedy_argmax(t["logits"], out=t["next_tokens"], workspace=t["argmax_ws"])
+        mk.softmax(t["logits"], y=t["probs"], workspace=wss)
+        mk.greedy_argmax(t["logits"], out=t["next_tokens"], workspace=wsa)
 
     nb = chain_bytes(s, sum(g["B"] * g["S"] for g in ws[0].segments))
-    cfg = ("gather+norm+qk-norm&rope+kv+add&norm+swiglu+add&norm+softmax+argmax "
+    cfg = ("gather&norm+qk-norm&rope+kv+add&norm+swiglu+add&norm+softmax&argmax "
            f"T={T} (64 decode + 2x3000 prefill)")
     rows = []
     for name, fn in (("decoder_chain", fused), ("decoder_chain_unfused", unfused)):

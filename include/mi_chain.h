@@ -7,8 +7,8 @@
  * copies between them and no allocation.
  *
  * The reference step, per layer, and what replaces each piece here:
- *   gather (+ embed scale)            -> mi_embedding_gather_f16 (+ mi_scale_inplace_f16)
- *   copy, input_layernorm, copy       -> mi_rmsnorm_f16 into `normed`
+ *   gather (+ embed scale), copy,     -> mi_embedding_rmsnorm_f16: hidden and `normed`
+ *   input_layernorm, copy                in one pass
  *   [QKV GEMMs]                       -> the caller's q, k, v
  *   copies, Q-norm, K-norm, 2x RoPE   -> mi_qk_norm_rope_f16 (or mi_rope_neox_qk_f16)
  *   2x launch_paged_kv_scatter        -> mi_paged_kv_scatter_kv_f16 per segment
@@ -23,7 +23,7 @@
  *                                        final norm stands where the next layer's input
  *                                        norm would)
  *   [LM head]                         -> the caller's logits
- *   sampling                          -> mi_softmax_ws_f16 and mi_greedy_argmax_ws_f16
+ *   sampling: softmax and argmax      -> mi_softmax_argmax_ws_f16 (one read of the logits)
  * The bracketed GEMM steps are not part of this library: their outputs are
  * buffers the caller fills (in the C++ interface, through hooks called at
  * those points; through this ABI, before the call).
@@ -96,10 +96,8 @@ typedef struct mi_chain_desc {
     void* logits;       /* [N, V] LM head output */
     void* probs;        /* [N, V] softmax */
     int32_t* next_tokens; /* [N] greedy argmax */
-    void* softmax_ws;   /* mi_softmax_workspace_bytes(N, V) bytes, zero before first use */
-    int64_t softmax_ws_bytes;
-    void* argmax_ws;    /* mi_greedy_argmax_workspace_bytes(N, V) bytes, zero before first use */
-    int64_t argmax_ws_bytes;
+    void* sample_ws;    /* mi_softmax_argmax_workspace_bytes(N, V) bytes, zero before first use */
+    int64_t sample_ws_bytes;
 } mi_chain_desc;
 
 /* Stages, in issue order; mi_decoder_chain_run stops after `last_stage`. */
@@ -111,7 +109,7 @@ enum {
     MI_CHAIN_POST_ATTN_NORM = 5, /* hidden += attn_out; post_normed = rmsnorm(hidden) */
     MI_CHAIN_ACTIVATION = 6,     /* act_out = act(gate) * up */
     MI_CHAIN_FINAL_NORM = 7,     /* hidden += mlp_out; final_normed = rmsnorm(hidden) */
-    MI_CHAIN_SAMPLE = 8          /* probs = softmax(logits); next_tokens = argmax(logits) */
+    MI_CHAIN_SAMPLE = 8          /* probs = softmax(logits), next_tokens = argmax(logits) */
 };
 
 /* Validates `d` against every stage up to last_stage (MI_ERR_* of

@@ -191,6 +191,21 @@ int mi_softmax_ws_f16(const void* x, void* y, int64_t N, int64_t D, void* worksp
  * race; calls in one stream's order do not. */
 int mi_softmax_noalloc_f16(const void* x, void* y, int64_t N, int64_t D, void* stream);
 
+/* The sampling step over one set of logits [N, V] in one pass: probs =
+ * softmax(logits) as mi_softmax_ws_f16 computes it, and out[n] = the greedy
+ * argmax of row n as mi_greedy_argmax_f16 computes it (the reference's tie
+ * order), reading the logits once.  Replaces launch_softmax + launch_greedy
+ * _sample_batched over the same logits (src/kernels/softmax_kernel.cuh:12,
+ * sampling_kernel.cuh:25-30).  Shapes the one-launch softmax takes (split
+ * or many long rows, aligned, probs != logits) run as one kernel whose chunks
+ * also publish their best key; others run the two entry points in turn.
+ * The workspace (mi_softmax_argmax_workspace_bytes(N, V) bytes, 16-byte
+ * aligned) must hold zeros before its first use and then serve only this
+ * function; calls sharing it must not overlap.  N <= 65535. */
+int64_t mi_softmax_argmax_workspace_bytes(int64_t N, int64_t V);
+int mi_softmax_argmax_ws_f16(const void* logits, void* probs, int32_t* out, int64_t N, int64_t V,
+                             void* workspace, int64_t workspace_bytes, void* stream);
+
 /* Test hook (no counterpart in the reference): bound on the polls a one-pass
  * softmax chunk makes before computing its row's statistics from x itself;
  * 0 forces that fallback everywhere.  Returns the previous bound. */
@@ -203,6 +218,20 @@ int mi_softmax_test_poll_limit(int limit);
  * (src/kernels/model_utils_kernel.cuh:14), where T = B*S. */
 int mi_embedding_gather_f16(const int64_t* ids, const void* table, void* out,
                             int64_t T, int64_t H, int64_t vocab, void* stream);
+
+/* Embedding gather fused with the first layer's input RMSNorm:
+ * hidden[t, :] = half(table[ids[t], :] * scale) (the row itself when scale is
+ * 1; ids outside [0, vocab) give a zero row when vocab > 0) and
+ * y = rmsnorm(hidden) with weight [D] (f(w) = w, or 1 + w when add_one), in
+ * one pass that writes hidden and y and never reads hidden back.  Equals
+ * mi_embedding_gather_f16, then mi_scale_inplace_f16 when scale != 1, then
+ * mi_rmsnorm_f16, bit for bit.  Replaces launch_embedding_gather (+
+ * launch_scale_inplace for Gemma) and the first input_layernorm at
+ * src/model/transformer_model.cpp:561-584 (with the device copies around
+ * that norm).  hidden and y must not overlap. */
+int mi_embedding_rmsnorm_f16(const int64_t* ids, const void* table, void* hidden,
+                             const void* weight, void* y, int64_t T, int64_t D, int64_t vocab,
+                             float scale, float eps, int add_one, void* stream);
 
 /* Paged KV-cache scatter: token (b, s) of src [B, S, H_kv, D] at global
  * position p = start_pos[b] + s is copied, when p < seq_len[b], into physical

@@ -88,8 +88,136 @@ void launch_gather(const int64_t* ids, const half_t* tb, half_t* o, int64_t T, i
     }
 }
 
+// ---------------------------------------------------------------------------
+// Gather fused with the first layer's input RMSNorm (and Gemma's embedding
+// scale): hidden[t] = half(table[ids[t]] * scale) (the gathered row itself
+// when scale == 1), y[t] = rmsnorm(hidden[t]), one workgroup per token row
+// held in registers -- the gathered row is written once and normalised
+// from registers instead of being read back by a second launch.  The
+// arithmetic is the rmsnorm kernels' (fp32 sum of squares, rsqrt,
+// half(h * rrms * f(w))) applied to the fp16 hidden value.
+// ---------------------------------------------------------------------------
+template <int VPT>
+__global__ __launch_bounds__(256) void embed_rms_kernel(const int64_t* __restrict__ ids,
+                                                        const half_t* __restrict__ table,
+                                                        half_t* __restrict__ hidden,
+                                                        const half_t* __restrict__ w,
+                                                        half_t* __restrict__ y, int64_t D,
+                                                        int64_t vocab, float scale, float eps,
+                                                        float w_bias) {
+    __shared__ float slots[256 / kWave];
+    const int64_t t = blockIdx.x;
+    const int64_t id = ids[t];
+    const bool valid = id >= 0 && (vocab <= 0 || id < vocab);
+    const half_t* src = table + (valid ? id : 0) * D;
+    const int64_t nv = D >> 3;
+    h8 v[VPT];
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+        const int64_t c = threadIdx.x + j * 256;
+        // plain loads, as in gather_kernel: the rows are scattered over the table
+        v[j] = (valid && c < nv) ? ld8(src + c * 8) : h8(0);
+    }
+    h8 wv[VPT];
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+        const int64_t c = threadIdx.x + j * 256;
+        wv[j] = c < nv ? ld8(w + c * 8) : h8(0);
+    }
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+        const int64_t c = threadIdx.x + j * 256;
+        if (scale != 1.0f) {
+#pragma unroll
+            for (int k = 0; k < 8; ++k) v[j][k] = to_half((float)v[j][k] * scale);
+        }
+        if (c < nv) st8_stream(hidden + t * D + c * 8, v[j]);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const float f = (float)v[j][k];
+            ss = fmaf(f, f, ss);
+        }
+    }
+    ss = block_sum(ss, slots);
+    const float rrms = rsqrtf(ss / static_cast<float>(D) + eps);
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+        const int64_t c = threadIdx.x + j * 256;
+        if (c < nv) {
+            h8 o;
+#pragma unroll
+            for (int k = 0; k < 8; ++k)
+                o[k] = to_half((float)v[j][k] * rrms * ((float)wv[j][k] + w_bias));
+            st8_stream(y + t * D + c * 8, o);
+        }
+    }
+}
+
+// Any D or alignment: one workgroup per row, two passes over the row (the
+// second re-reads the hidden values this workgroup's own lanes wrote).
+__global__ __launch_bounds__(256) void embed_rms_scalar_kernel(
+    const int64_t* __restrict__ ids, const half_t* __restrict__ table, half_t* hidden,
+    const half_t* __restrict__ w, half_t* __restrict__ y, int64_t D, int64_t vocab, float scale,
+    float eps, float w_bias) {
+    __shared__ float slots[256 / kWave];
+    const int64_t t = blockIdx.x;
+    const int64_t id = ids[t];
+    const bool valid = id >= 0 && (vocab <= 0 || id < vocab);
+    const half_t* src = table + (valid ? id : 0) * D;
+    half_t* hr = hidden + t * D;
+    float ss = 0.0f;
+    for (int64_t i = threadIdx.x; i < D; i += 256) {
+        half_t h = valid ? src[i] : half_t(0);
+        if (scale != 1.0f) h = to_half((float)h * scale);
+        hr[i] = h;
+        const float f = (float)h;
+        ss = fmaf(f, f, ss);
+    }
+    ss = block_sum(ss, slots);
+    const float rrms = rsqrtf(ss / static_cast<float>(D) + eps);
+    for (int64_t i = threadIdx.x; i < D; i += 256)
+        y[t * D + i] = to_half((float)hr[i] * rrms * ((float)w[i] + w_bias));
+}
+
 }  // namespace
 }  // namespace mi
+
+extern "C" int mi_embedding_rmsnorm_f16(const int64_t* ids, const void* table, void* hidden,
+                                        const void* weight, void* y, int64_t T, int64_t D,
+                                        int64_t vocab, float scale, float eps, int add_one,
+                                        void* stream) {
+    if (T < 0 || D < 0) return MI_ERR_INVALID_ARGUMENT;
+    if (T == 0 || D == 0) return MI_OK;
+    if (!ids || !table || !hidden || !weight || !y) return MI_ERR_INVALID_ARGUMENT;
+    if (T > mi::kMaxGridX) return MI_ERR_UNSUPPORTED;
+    const int64_t bytes = T * D * 2;
+    if (mi::overlaps(hidden, bytes, y, bytes)) return MI_ERR_ALIASING;
+    if (vocab > 0 && (mi::overlaps(hidden, bytes, table, vocab * D * 2) ||
+                      mi::overlaps(y, bytes, table, vocab * D * 2)))
+        return MI_ERR_ALIASING;
+    const auto* tb = static_cast<const mi::half_t*>(table);
+    const auto* w = static_cast<const mi::half_t*>(weight);
+    auto* h = static_cast<mi::half_t*>(hidden);
+    auto* yo = static_cast<mi::half_t*>(y);
+    const float bias = add_one ? 1.0f : -0.0f;  // -0: w + bias == w, signed zeros kept
+    const hipStream_t s = mi::as_stream(stream);
+    const dim3 g(static_cast<unsigned>(T)), b(256);
+    const bool vec = D % 8 == 0 && mi::aligned16(table) && mi::aligned16(hidden) &&
+                     mi::aligned16(weight) && mi::aligned16(y);
+    const int64_t vpt = mi::ceil_div(D / 8, 256);
+    if (vec && vpt <= 4) {
+        switch (vpt) {
+            case 1: mi::embed_rms_kernel<1><<<g, b, 0, s>>>(ids, tb, h, w, yo, D, vocab, scale, eps, bias); break;
+            case 2: mi::embed_rms_kernel<2><<<g, b, 0, s>>>(ids, tb, h, w, yo, D, vocab, scale, eps, bias); break;
+            case 3: mi::embed_rms_kernel<3><<<g, b, 0, s>>>(ids, tb, h, w, yo, D, vocab, scale, eps, bias); break;
+            default: mi::embed_rms_kernel<4><<<g, b, 0, s>>>(ids, tb, h, w, yo, D, vocab, scale, eps, bias); break;
+        }
+    } else {
+        mi::embed_rms_scalar_kernel<<<g, b, 0, s>>>(ids, tb, h, w, yo, D, vocab, scale, eps, bias);
+    }
+    return mi::launch_status();
+}
 
 extern "C" int mi_embedding_gather_f16(const int64_t* ids, const void* table, void* out, int64_t T,
                                        int64_t H, int64_t vocab, void* stream) {

@@ -34,6 +34,7 @@
 // reduces a row's keys in one wave.
 #include <atomic>
 
+#include "argmax_key.h"
 #include "mi_device.h"
 #include "mi_host.h"
 
@@ -185,119 +186,6 @@ typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
 
 constexpr int kArgmaxSplitMaxRows = 512;
 constexpr int kArgmaxMaxSplits = 1024;
-
-// Order key of element i with fp16 bits h (see the file header); 0 when the
-// element can never be chosen (NaN or -inf).
-__device__ __forceinline__ uint64_t argmax_key(uint16_t h, int64_t i) {
-    if ((h & 0x7fffu) > 0x7c00u || h == 0xfc00u) return 0;  // NaN, -inf
-    if (h == 0x8000u) h = 0;                                 // -0 == +0
-    const uint32_t ord = (h & 0x8000u) ? (~h & 0xffffu) : (h | 0x8000u);
-    const uint32_t tie = 255u - (__builtin_bitreverse32(static_cast<uint32_t>(i & 255)) >> 24);
-    return (static_cast<uint64_t>(ord) << 48) | (static_cast<uint64_t>(tie) << 32) |
-           static_cast<uint64_t>(~static_cast<uint32_t>(i));
-}
-
-__device__ __forceinline__ uint64_t max_u64(uint64_t a, uint64_t b) { return a > b ? a : b; }
-
-// The largest 64-bit key of the wave, in every lane: DPP within 16-lane
-// rows (both halves of the key move together), then the permlane swaps
-// across rows (no LDS).  Every lane must be active.
-template <int CTRL>
-__device__ __forceinline__ uint64_t dpp_u64(uint64_t v) {
-    const uint32_t lo = __builtin_amdgcn_mov_dpp(static_cast<int>(v), CTRL, 0xF, 0xF, false);
-    const uint32_t hi = __builtin_amdgcn_mov_dpp(static_cast<int>(v >> 32), CTRL, 0xF, 0xF, false);
-    return (static_cast<uint64_t>(hi) << 32) | lo;
-}
-template <int STRIDE>
-__device__ __forceinline__ uint64_t max_xor_u64(uint64_t v) {
-    uint32_t la, lb, ha, hb;
-    if constexpr (STRIDE == 16) {
-        pair_xor16(static_cast<uint32_t>(v), la, lb);
-        pair_xor16(static_cast<uint32_t>(v >> 32), ha, hb);
-    } else {
-        pair_xor32(static_cast<uint32_t>(v), la, lb);
-        pair_xor32(static_cast<uint32_t>(v >> 32), ha, hb);
-    }
-    return max_u64((static_cast<uint64_t>(ha) << 32) | la, (static_cast<uint64_t>(hb) << 32) | lb);
-}
-__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
-    v = max_u64(v, dpp_u64<0xB1>(v));   // xor 1
-    v = max_u64(v, dpp_u64<0x4E>(v));   // xor 2
-    v = max_u64(v, dpp_u64<0x141>(v));  // other quad of the half row
-    v = max_u64(v, dpp_u64<0x140>(v));  // other half of the row
-    v = max_xor_u64<16>(v);
-    return max_xor_u64<32>(v);
-}
-
-__device__ __forceinline__ int32_t key_index(uint64_t key) {
-    return key == 0 ? -1 : static_cast<int32_t>(~static_cast<uint32_t>(key));
-}
-
-// Best key of elements [begin, end) of a row, over the workgroup.  The range
-// is walked in tiles of 256 * VEC * U elements; every load of a tile is
-// issued before any arithmetic, so a workgroup whose chunk is one tile waits
-// for HBM once.  With VEC = 8, begin is a multiple of 2048 and end - begin a
-// multiple of 16.
-template <int VEC, int U>
-__device__ __forceinline__ uint64_t chunk_best(const half_t* xr, int64_t begin, int64_t end,
-                                               uint64_t* slots) {
-    uint64_t best = 0;
-    constexpr int64_t kTile = 256 * VEC * U;
-    for (int64_t t0 = begin; t0 < end; t0 += kTile) {
-        if constexpr (VEC == 8) {
-            // Lane maximum first (packed fp16 max, which passes over NaN),
-            // then the element equal to it that the tie order prefers: for
-            // i = t0 + (lane + 256 j) * 8 + k with t0 = 0 mod 256,
-            // bitrev8(i mod 256) = bitrev3(k) << 5 | bitrev5(lane mod 32), so
-            // within a lane a smaller bitrev3(k) wins, then a smaller j.  Only
-            // that one element's 64-bit key is formed.
-            h8 a[U];
-#pragma unroll
-            for (int j = 0; j < U; ++j) {
-                const int64_t i = t0 + (threadIdx.x + j * 256) * 8;
-                a[j] = i < end ? ld8_stream(xr + i) : h8(-__builtin_huge_valf16());
-            }
-            h2 m2 = h2(-__builtin_huge_valf16());
-#pragma unroll
-            for (int j = 0; j < U; ++j) {
-#pragma unroll
-                for (int k = 0; k < 8; k += 2) m2 = __builtin_elementwise_max(m2, h2{a[j][k], a[j][k + 1]});
-            }
-            const half_t M = __builtin_elementwise_max(m2.x, m2.y);
-            if (M > -__builtin_huge_valf16()) {  // false for NaN and -inf: nothing eligible
-                constexpr int kLowToHigh[8] = {7, 3, 5, 1, 6, 2, 4, 0};  // k by falling bitrev3
-                int code = 0;
-#pragma unroll
-                for (int q = 0; q < 8; ++q) {
-#pragma unroll
-                    for (int j = U - 1; j >= 0; --j)
-                        if (a[j][kLowToHigh[q]] == M) code = j * 8 + kLowToHigh[q];
-                }
-                const int64_t i = t0 + (threadIdx.x + (code >> 3) * 256) * 8 + (code & 7);
-                best = max_u64(best, argmax_key(__builtin_bit_cast(uint16_t, M), i));
-            }
-        } else {
-            uint16_t a[U];
-#pragma unroll
-            for (int j = 0; j < U; ++j) {
-                const int64_t i = t0 + threadIdx.x + j * 256;
-                a[j] = i < end ? __builtin_bit_cast(uint16_t, xr[i]) : uint16_t(0);
-            }
-#pragma unroll
-            for (int j = 0; j < U; ++j) {
-                const int64_t i = t0 + threadIdx.x + j * 256;
-                if (i < end) best = max_u64(best, argmax_key(a[j], i));
-            }
-        }
-    }
-    best = wave_max_u64(best);
-    const int wave = threadIdx.x / kWave;
-    if ((threadIdx.x & (kWave - 1)) == 0) slots[wave] = best;
-    __syncthreads();
-    uint64_t t = 0;
-    for (int w = 0; w < static_cast<int>(blockDim.x / kWave); ++w) t = max_u64(t, slots[w]);
-    return t;
-}
 
 // grid (splits, B).  With one split the index goes straight to `out`;
 // otherwise each chunk's key goes to ws[row * splits + split].

@@ -35,6 +35,7 @@
 #include <map>
 #include <mutex>
 
+#include "argmax_key.h"
 #include "mi_device.h"
 #include "mi_host.h"
 
@@ -417,8 +418,13 @@ constexpr int kOnePassMaxSplits = 64;
 #endif
 constexpr int kOnePassU = MI_SOFTMAX_ONEPASS_U;     // vectors per lane
 constexpr int64_t kOnePassChunk = 2048 * kOnePassU;  // elements per workgroup
-// header, then two sets of slot pairs (alternated by round)
+// header, then two sets of slots (alternated by round); a slot is the
+// chunk's tagged (max, sum) pair, plus its tagged argmax key (two words) in
+// the fused softmax + argmax pass
 constexpr int64_t kRowRecordBytes = 16 + 2 * kOnePassMaxSplits * 16;
+constexpr int64_t kRowRecordBytesAM = 16 + 2 * kOnePassMaxSplits * 32;
+template <bool AM>
+constexpr int64_t record_bytes() { return AM ? kRowRecordBytesAM : kRowRecordBytes; }
 constexpr int kPollLimit = 1 << 16;
 // Wall-clock bound of one row's polling: 20000 ticks of the 100 MHz
 // constant clock (s_memrealtime) = 200 us, some 100 times a normal exchange.
@@ -452,38 +458,57 @@ __device__ __forceinline__ void chunk_lane_stats(const h8 (&a)[U], float& m, flo
         m = -INFINITY;  // NaN-free lane maximum of an all -inf (or NaN) lane
     }
 }
-// Thread 0 publishes the chunk's pair into slot pair `split` of `slots`.
+// Thread 0 publishes the chunk's pair (and, AM, its argmax key) into slot
+// `split` of `slots` (SW = 2 or 4 words per slot).
+template <bool AM>
 __device__ __forceinline__ void chunk_publish(uint64_t* slots, int split, uint32_t tag, float m,
-                                              float s) {
+                                              float s, uint64_t key) {
+    constexpr int SW = AM ? 4 : 2;
     if (threadIdx.x == 0) {
-        __hip_atomic_store(&slots[2 * split], tagged(tag, m), __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(&slots[2 * split + 1], tagged(tag, s), __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
+        uint64_t* p = slots + SW * split;
+        __hip_atomic_store(&p[0], tagged(tag, m), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(&p[1], tagged(tag, s), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if constexpr (AM) {
+            const uint64_t t = static_cast<uint64_t>(tag) << 32;
+            __hip_atomic_store(&p[2], t | (key >> 32), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(&p[3], t | (key & 0xffffffffu), __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+        }
     }
 }
-// Wave 0 (the caller calls it there) polls the row's `splits` slot pairs (lane j
+// Wave 0 (the caller calls it there) polls the row's `splits` slots (lane j
 // reads chunk j) until all carry `tag`, at most poll_limit rounds, and leaves
-// the row's (M, S) in row_stats[0..1] and row_stats[2] = 0, or
-// row_stats[2] = 1 when polling ran out.  The caller's barrier publishes
-// row_stats.
+// the row's (M, S) in row_stats[0..1] (AM: its best key in *row_key) and
+// row_stats[2] = 0, or row_stats[2] = 1 when polling ran out.  The caller's
+// barrier publishes them.
+template <bool AM>
 __device__ __forceinline__ void row_poll(const uint64_t* slots, int splits, uint32_t tag,
-                                         int poll_limit, float* row_stats) {
+                                         int poll_limit, float* row_stats, uint64_t* row_key) {
+    constexpr int SW = AM ? 4 : 2;
     const int lane = threadIdx.x & (kWave - 1);
     float mj = -INFINITY, sj = 0.0f;
+    uint64_t kj = 0;
     bool all = false;
     const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
     for (int it = 0; it < poll_limit && !all; ++it) {
         if (it > 0 && __builtin_amdgcn_s_memrealtime() - t0 > kPollTicks) break;
         bool mine = true;
         if (lane < splits) {
-            const uint64_t w0 = __hip_atomic_load(&slots[2 * lane], __ATOMIC_RELAXED,
-                                                  __HIP_MEMORY_SCOPE_AGENT);
-            const uint64_t w1 = __hip_atomic_load(&slots[2 * lane + 1], __ATOMIC_RELAXED,
-                                                  __HIP_MEMORY_SCOPE_AGENT);
+            const uint64_t* p = slots + SW * lane;
+            const uint64_t w0 = __hip_atomic_load(&p[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const uint64_t w1 = __hip_atomic_load(&p[1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             mine = static_cast<uint32_t>(w0 >> 32) == tag && static_cast<uint32_t>(w1 >> 32) == tag;
             mj = __builtin_bit_cast(float, static_cast<uint32_t>(w0));
             sj = __builtin_bit_cast(float, static_cast<uint32_t>(w1));
+            if constexpr (AM) {
+                const uint64_t w2 = __hip_atomic_load(&p[2], __ATOMIC_RELAXED,
+                                                      __HIP_MEMORY_SCOPE_AGENT);
+                const uint64_t w3 = __hip_atomic_load(&p[3], __ATOMIC_RELAXED,
+                                                      __HIP_MEMORY_SCOPE_AGENT);
+                mine = mine && static_cast<uint32_t>(w2 >> 32) == tag &&
+                       static_cast<uint32_t>(w3 >> 32) == tag;
+                kj = (w2 << 32) | (w3 & 0xffffffffu);
+            }
         }
         all = __all(mine);
         if (!all) __builtin_amdgcn_s_sleep(2);
@@ -492,13 +517,16 @@ __device__ __forceinline__ void row_poll(const uint64_t* slots, int splits, uint
         if (lane >= splits) {
             mj = -INFINITY;
             sj = 0.0f;
+            kj = 0;
         }
         const float M = group_max<kWave>(mj);
         const float S = group_sum<kWave>(mj == -INFINITY ? 0.0f : sj * fast_exp(mj - M));
+        if constexpr (AM) kj = wave_max_u64(kj);
         if (lane == 0) {
             row_stats[0] = M;
             row_stats[1] = S;
             row_stats[2] = 0.0f;
+            if constexpr (AM) *row_key = kj;
         }
     } else if (lane == 0) {
         row_stats[2] = 1.0f;
@@ -548,18 +576,29 @@ __device__ __forceinline__ void lane_store(const h8 (&a)[U], half_t* row, uint32
 // indices: 68 VGPRs and 7 workgroups per CU with them measured 5-10 points
 // lower; amdgpu_waves_per_eu(8) also measured ~8 points lower at the same
 // 64 VGPRs); wave 0 publishes and polls.
-// U vectors per lane: chunks of 2048 * U elements.
-template <int U>
-__global__ __launch_bounds__(256) void softmax_stream_kernel(const half_t* x, half_t* y,
+// U vectors per lane: chunks of 2048 * U elements.  AM: the fused softmax +
+// greedy argmax pass -- each chunk also forms its best argmax key from the
+// registers it already holds, publishes it with its (max, sum), and chunk 0
+// writes the row's index to `out` (the fallback scans the row from x).
+// (AM: held to 5 waves per SIMD, <= 96 VGPRs, so that 1216 chunk workgroups
+// of [64, 152064] stay resident at once; the compiler otherwise settles at
+// 98 and the grid needs a second round.)
+template <int U, bool AM>
+__global__ __launch_bounds__(256)
+__attribute__((amdgpu_waves_per_eu(AM ? 5 : 1))) void softmax_stream_kernel(const half_t* x, half_t* y,
                                                              unsigned char* ws, int64_t N,
-                                                             int64_t D, int poll_limit) {
+                                                             int64_t D, int poll_limit,
+                                                             int32_t* out) {
     constexpr int64_t kChunk = 2048 * U;
+    constexpr int SW = AM ? 4 : 2;
     __shared__ float slots[256 / kWave];
     __shared__ float row_stats[3];  // M, S, fallback flag
     __shared__ uint64_t epoch_sh;
+    __shared__ uint64_t kslots[AM ? 256 / kWave : 1];  // per-wave keys (AM)
+    __shared__ uint64_t row_key;                        // the row's best key (AM)
     const int split = blockIdx.x, splits = gridDim.x;
     const int64_t r0 = blockIdx.y, R = gridDim.y;
-    unsigned char* rec = ws + r0 * kRowRecordBytes;
+    unsigned char* rec = ws + r0 * record_bytes<AM>();
     uint64_t* epoch = reinterpret_cast<uint64_t*>(rec);
     uint64_t* sets = reinterpret_cast<uint64_t*>(rec + 16);
     const int64_t K = (N - r0 + R - 1) / R;  // rounds of this row slot (>= 1)
@@ -582,22 +621,42 @@ __global__ __launch_bounds__(256) void softmax_stream_kernel(const half_t* x, ha
         // no spill against 80 without it.
         float m = -INFINITY, s = 0.0f;
         if (threadIdx.x < 256) chunk_lane_stats<U>(a, m, s);
-        block_merge(m, s, slots);  // barriers: epoch_sh (first round) is visible after this
+        if constexpr (AM) {
+            // vectors past the row hold -inf (lane_load), whose key is 0
+            const uint64_t kw = wave_max_u64(lane_best_key<U>(a, b));
+            if ((threadIdx.x & (kWave - 1)) == 0) kslots[threadIdx.x / kWave] = kw;
+        }
+        block_merge(m, s, slots);  // barriers: epoch_sh (first round) and kslots visible after
+        uint64_t key = 0;
+        if constexpr (AM) {
+#pragma unroll
+            for (int w = 0; w < 256 / kWave; ++w) key = max_u64(key, kslots[w]);
+        }
         const uint64_t E = epoch_sh;
         const uint32_t tag = static_cast<uint32_t>(E + 1 + k);
-        uint64_t* set = sets + (k & 1) * (2 * kOnePassMaxSplits);
-        chunk_publish(set, split, tag, m, s);
+        uint64_t* set = sets + (k & 1) * (SW * kOnePassMaxSplits);
+        chunk_publish<AM>(set, split, tag, m, s, key);
         if (k + 1 < K) lane_load<U>(x + (row + R) * D, lo, ok, n);
         if (gave_up) {
             if (threadIdx.x == 0) row_stats[2] = 1.0f;
         } else if (threadIdx.x < kWave) {
-            row_poll(set, splits, tag, poll_limit, row_stats);
+            row_poll<AM>(set, splits, tag, poll_limit, row_stats, &row_key);
         }
         __syncthreads();
         float M = row_stats[0], S = row_stats[1];
         const bool fallback = row_stats[2] != 0.0f;
         gave_up = gave_up || fallback;
         if (fallback) row_stats_from_x(x + row * D, D, M, S, slots);
+        if constexpr (AM) {
+            if (split == 0) {  // workgroup-uniform: chunk_best has barriers
+                uint64_t rk = row_key;
+                if (fallback) {
+                    rk = chunk_best<8, 4>(x + row * D, 0, D, kslots);
+                    __syncthreads();  // kslots are written again by the next round
+                }
+                if (threadIdx.x == 0) out[row] = key_index(rk);
+            }
+        }
         if (threadIdx.x == 0 && (fallback || (split == 0 && k + 1 == K)))
             __hip_atomic_fetch_max(epoch, fallback ? E + K + 1 : E + K, __ATOMIC_RELAXED,
                                    __HIP_MEMORY_SCOPE_AGENT);
@@ -700,17 +759,21 @@ int onelaunch_u(int64_t N, int64_t D) {
         return kSmall;
     return kOnePassU;
 }
-const void* onelaunch_kernel(int u) {
-    return u == kOnePassU ? reinterpret_cast<const void*>(softmax_stream_kernel<kOnePassU>)
-                          : reinterpret_cast<const void*>(softmax_stream_kernel<kOnePassU / 2>);
+const void* onelaunch_kernel(int u, bool am) {
+    if (am)
+        return u == kOnePassU
+                   ? reinterpret_cast<const void*>(softmax_stream_kernel<kOnePassU, true>)
+                   : reinterpret_cast<const void*>(softmax_stream_kernel<kOnePassU / 2, true>);
+    return u == kOnePassU ? reinterpret_cast<const void*>(softmax_stream_kernel<kOnePassU, false>)
+                          : reinterpret_cast<const void*>(softmax_stream_kernel<kOnePassU / 2, false>);
 }
 
 // Rows of the one-launch grid: as many as stay resident next to each other
 // with every chunk of a row (at most the record rows).
-int64_t onelaunch_rows(int64_t N, int64_t D) {
+int64_t onelaunch_rows(int64_t N, int64_t D, bool am = false) {
     const int u = onelaunch_u(N, D);
     const int64_t sp1 = ceil_div(D, 2048 * u);
-    int64_t R = resident_workgroups(onelaunch_kernel(u), 256) / sp1;
+    int64_t R = resident_workgroups(onelaunch_kernel(u, am), 256) / sp1;
     if (R > N) R = N;
     if (R > kSplitMaxRows) R = kSplitMaxRows;
     return R;
@@ -719,12 +782,12 @@ int64_t onelaunch_rows(int64_t N, int64_t D) {
 // Whether [N, D] runs as the one-launch form given row records: a split or
 // kStream shape, aligned rows, y != x (the fallback re-reads x), at most 64
 // chunks per row.
-bool onelaunch_ok(const void* x, const void* y, int64_t N, int64_t D) {
+bool onelaunch_ok(const void* x, const void* y, int64_t N, int64_t D, bool am = false) {
     int64_t splits, chunk;
     if (!MI_SOFTMAX_ONEPASS || plan(N, D, splits, chunk) == Plan::kRow) return false;
     return D % 8 == 0 && aligned16(x) && aligned16(y) && x != y &&
            ceil_div(D, 2048 * onelaunch_u(N, D)) <= kOnePassMaxSplits &&
-           onelaunch_rows(N, D) >= 1;
+           onelaunch_rows(N, D, am) >= 1;
 }
 
 int softmax_checked(const void* x, void* y, int64_t N, int64_t D, void* ws, int64_t ws_bytes,
@@ -783,11 +846,11 @@ int softmax_checked(const void* x, void* y, int64_t N, int64_t D, void* ws, int6
                      static_cast<unsigned>(onelaunch_rows(N, D)));
         auto* rec = static_cast<unsigned char*>(ws);
         if (u == kOnePassU)
-            softmax_stream_kernel<kOnePassU><<<g, dim3(256), 0, s>>>(xh, yh, rec, N, D,
-                                                                    g_poll_limit.load());
+            softmax_stream_kernel<kOnePassU, false><<<g, dim3(256), 0, s>>>(
+                xh, yh, rec, N, D, g_poll_limit.load(), nullptr);
         else
-            softmax_stream_kernel<kOnePassU / 2><<<g, dim3(256), 0, s>>>(xh, yh, rec, N, D,
-                                                                        g_poll_limit.load());
+            softmax_stream_kernel<kOnePassU / 2, false><<<g, dim3(256), 0, s>>>(
+                xh, yh, rec, N, D, g_poll_limit.load(), nullptr);
         return launch_status();
     }
     auto* part = reinterpret_cast<float*>(static_cast<unsigned char*>(ws) +
@@ -893,6 +956,60 @@ extern "C" int mi_softmax_ws_f16(const void* x, void* y, int64_t N, int64_t D, v
                                  int64_t workspace_bytes, void* stream) {
     return mi::softmax_checked(x, y, N, D, workspace, workspace_bytes,
                                mi::Ws::kRecordsThenPairs, stream);
+}
+
+// Fused softmax + greedy argmax: [fused row records | softmax workspace |
+// argmax workspace]; the one-launch fused kernel when the shape takes the
+// one-launch softmax, else the two entry points in turn on their parts.
+namespace {
+constexpr int64_t kFusedRegion = mi::kSplitMaxRows * mi::kRowRecordBytesAM;
+}
+
+extern "C" int64_t mi_softmax_argmax_workspace_bytes(int64_t N, int64_t V) {
+    if (N <= 0 || V <= 0) return 0;
+    return kFusedRegion + mi::workspace_bytes(N, V) + mi_greedy_argmax_workspace_bytes(N, V);
+}
+
+extern "C" int mi_softmax_argmax_ws_f16(const void* logits, void* probs, int32_t* out, int64_t N,
+                                        int64_t V, void* workspace, int64_t workspace_bytes,
+                                        void* stream) {
+    if (N < 0 || V < 0 || workspace_bytes < 0) return MI_ERR_INVALID_ARGUMENT;
+    if (N == 0 || V == 0) return MI_OK;
+    if (!logits || !probs || !out || !workspace) return MI_ERR_INVALID_ARGUMENT;
+    if (N > 65535) return MI_ERR_UNSUPPORTED;  // the argmax grid's rows
+    const int64_t need = mi_softmax_argmax_workspace_bytes(N, V);
+    if (workspace_bytes < need || reinterpret_cast<uintptr_t>(workspace) % 16 != 0)
+        return MI_ERR_INVALID_ARGUMENT;
+    const int64_t bytes = N * V * 2;
+    if (logits != probs && mi::overlaps(logits, bytes, probs, bytes)) return MI_ERR_ALIASING;
+    if (mi::overlaps(workspace, need, logits, bytes) || mi::overlaps(workspace, need, probs, bytes) ||
+        mi::overlaps(out, N * 4, logits, bytes) || mi::overlaps(out, N * 4, probs, bytes) ||
+        mi::overlaps(out, N * 4, workspace, need))
+        return MI_ERR_ALIASING;
+    auto* ws = static_cast<unsigned char*>(workspace);
+    const hipStream_t s = mi::as_stream(stream);
+    if (mi::onelaunch_ok(logits, probs, N, V, true)) {
+        const int u = mi::onelaunch_u(N, V);
+        const dim3 g(static_cast<unsigned>(mi::ceil_div(V, 2048 * u)),
+                     static_cast<unsigned>(mi::onelaunch_rows(N, V, true)));
+        const auto* xh = static_cast<const mi::half_t*>(logits);
+        auto* yh = static_cast<mi::half_t*>(probs);
+        if (u == mi::kOnePassU)
+            mi::softmax_stream_kernel<mi::kOnePassU, true><<<g, dim3(256), 0, s>>>(
+                xh, yh, ws, N, V, mi::g_poll_limit.load(), out);
+        else
+            mi::softmax_stream_kernel<mi::kOnePassU / 2, true><<<g, dim3(256), 0, s>>>(
+                xh, yh, ws, N, V, mi::g_poll_limit.load(), out);
+        return mi::launch_status();
+    }
+    // separately: argmax first (in place, softmax would overwrite the logits)
+    const int64_t sw = mi::workspace_bytes(N, V);
+    unsigned char* aw = ws + kFusedRegion + sw;
+    const int st = mi_greedy_argmax_ws_f16(logits, N, V, out, aw,
+                                           mi_greedy_argmax_workspace_bytes(N, V), stream);
+    if (st != MI_OK) return st;
+    return mi_softmax_ws_f16(logits, probs, N, V, sw > 0 ? ws + kFusedRegion : nullptr, sw,
+                             stream);
 }
 
 extern "C" int mi_softmax_f16(const void* x, void* y, int64_t N, int64_t D, void* stream) {

@@ -87,10 +87,10 @@ void DecoderChain::validate_() const {
     }
     if (L >= MI_CHAIN_SAMPLE) {
         need(d.logit_rows > 0 && d.logits && d.probs && d.next_tokens, "sample buffers");
-        const int64_t sw = mi_softmax_workspace_bytes(d.logit_rows, d.vocab);
-        const int64_t aw = mi_greedy_argmax_workspace_bytes(d.logit_rows, d.vocab);
-        need(sw == 0 || (d.softmax_ws && d.softmax_ws_bytes >= sw), "softmax workspace too small");
-        need(aw == 0 || (d.argmax_ws && d.argmax_ws_bytes >= aw), "argmax workspace too small");
+        need(d.logit_rows <= 65535, "logit_rows above 65535");
+        need(d.sample_ws && d.sample_ws_bytes >= mi_softmax_argmax_workspace_bytes(d.logit_rows,
+                                                                                  d.vocab),
+             "sample workspace too small");
     }
 }
 
@@ -103,16 +103,20 @@ void DecoderChain::run(hipStream_t s, DecoderChainHooks* hooks) const {
     const int add1 = d.norm_add_one;
     if (T == 0) return;
 
-    // 1. token embedding (+ Gemma's sqrt(D) scale), transformer_model.cpp:561-572
-    check(mi_embedding_gather_f16(d.ids, d.embed, d.hidden, T, D, d.vocab, sv(s)), "gather");
-    if (d.embed_scale)
-        check(mi_scale_inplace_f16(d.hidden, std::sqrt(static_cast<float>(D)), T * D, sv(s)),
-              "embed scale");
-    if (last_ == MI_CHAIN_EMBED) return;
-
-    // 2. input_layernorm straight from the residual stream (:578-584 copy
-    //    hidden into a 2-D tensor, normalise, copy back: no copies here)
-    check(mi_rmsnorm_f16(d.hidden, d.input_norm, d.normed, T, D, eps, add1, sv(s)), "input norm");
+    // 1-2. token embedding (+ Gemma's sqrt(D) scale) and the input_layernorm
+    //    (transformer_model.cpp:561-584: gather, scale, copy hidden into a
+    //    2-D tensor, normalise, copy back) in one pass that writes hidden and
+    //    normed; stopping after the embedding takes the gather alone
+    const float scale = d.embed_scale ? std::sqrt(static_cast<float>(D)) : 1.0f;
+    if (last_ == MI_CHAIN_EMBED) {
+        check(mi_embedding_gather_f16(d.ids, d.embed, d.hidden, T, D, d.vocab, sv(s)), "gather");
+        if (d.embed_scale)
+            check(mi_scale_inplace_f16(d.hidden, scale, T * D, sv(s)), "embed scale");
+        return;
+    }
+    check(mi_embedding_rmsnorm_f16(d.ids, d.embed, d.hidden, d.input_norm, d.normed, T, D,
+                                   d.vocab, scale, eps, add1, sv(s)),
+          "gather + input norm");
     if (last_ == MI_CHAIN_INPUT_NORM) return;
 
     // 3. QKV GEMMs, then Q/K-norm + RoPE in one in-place pass
@@ -181,14 +185,12 @@ void DecoderChain::run(hipStream_t s, DecoderChainHooks* hooks) const {
           "residual add + final norm");
     if (last_ == MI_CHAIN_FINAL_NORM) return;
 
-    // 8. LM head, then the sampling step over the logits rows
+    // 8. LM head, then the sampling step: softmax and greedy argmax of the
+    //    logits rows in one pass
     h.lm_head(d, s);
-    check(mi_softmax_ws_f16(d.logits, d.probs, d.logit_rows, d.vocab, d.softmax_ws,
-                            d.softmax_ws_bytes, sv(s)),
-          "softmax");
-    check(mi_greedy_argmax_ws_f16(d.logits, d.logit_rows, d.vocab, d.next_tokens, d.argmax_ws,
-                                  d.argmax_ws_bytes, sv(s)),
-          "greedy argmax");
+    check(mi_softmax_argmax_ws_f16(d.logits, d.probs, d.next_tokens, d.logit_rows, d.vocab,
+                                   d.sample_ws, d.sample_ws_bytes, sv(s)),
+          "softmax + greedy argmax");
 }
 
 }  // namespace mini_infer

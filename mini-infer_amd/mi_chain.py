@@ -52,8 +52,7 @@ class ChainDesc(ctypes.Structure):
                 + [(n, _vp) for n in _PTRS]
                 + [("num_kv_segments", _int), ("kv_segments", ctypes.POINTER(KvSegment))]
                 + [(n, _vp) for n in _BUFS]
-                + [("softmax_ws", _vp), ("softmax_ws_bytes", _i64), ("argmax_ws", _vp),
-                   ("argmax_ws_bytes", _i64)])
+                + [("sample_ws", _vp), ("sample_ws_bytes", _i64)])
 
 
 _lib = None
@@ -84,12 +83,11 @@ def make_desc(shapes: dict, tensors: dict, segments) -> tuple:
     for name, _ in ChainDesc._fields_:
         if name in shapes:
             setattr(d, name, shapes[name])
-    for name in _PTRS + _BUFS + ["softmax_ws", "argmax_ws"]:
+    for name in _PTRS + _BUFS + ["sample_ws"]:
         t = tensors.get(name)
         setattr(d, name, t.data_ptr() if t is not None else None)
-    for name in ("softmax_ws", "argmax_ws"):
-        t = tensors.get(name)
-        setattr(d, name + "_bytes", t.numel() * t.element_size() if t is not None else 0)
+    t = tensors.get("sample_ws")
+    d.sample_ws_bytes = t.numel() * t.element_size() if t is not None else 0
     segs = (KvSegment * max(1, len(segments)))()
     for i, g in enumerate(segments):
         bt = g["block_table"]
@@ -222,11 +220,8 @@ class Workload:
         t["k_cache"] = torch.zeros(cache, dtype=f16, device=dev)
         t["v_cache"] = torch.zeros(cache, dtype=f16, device=dev)
         t["next_tokens"] = torch.empty(logit_rows, dtype=torch.int32, device=dev)
-        t["softmax_ws"] = torch.zeros(max(16, mi_kernels.softmax_workspace_bytes(logit_rows, V)),
-                                      dtype=torch.uint8, device=dev)
-        t["argmax_ws"] = torch.zeros(
-            max(16, mi_kernels.greedy_argmax_workspace_bytes(logit_rows, V)), dtype=torch.uint8,
-            device=dev)
+        t["sample_ws"] = torch.zeros(mi_kernels.softmax_argmax_workspace_bytes(logit_rows, V),
+                                     dtype=torch.uint8, device=dev)
         self.groups = groups
         self.segments = [dict(token_offset=g["token_offset"], B=g["B"], S=g["S"],
                               block_table=torch.from_numpy(g["block_table"]).to(dev),

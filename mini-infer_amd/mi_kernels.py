@@ -45,8 +45,12 @@ SIGNATURES = {
     "mi_scale_inplace_f16": [_c_void_p, _f32, _i64, _c_void_p],
     "mi_softmax_f16": [_c_void_p, _c_void_p, _i64, _i64, _c_void_p],
     "mi_embedding_gather_f16": [_c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64, _c_void_p],
+    "mi_embedding_rmsnorm_f16": [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64,
+                                 _i64, _i64, _f32, _f32, _int, _c_void_p],
     "mi_softmax_ws_f16": [_c_void_p, _c_void_p, _i64, _i64, _c_void_p, _i64, _c_void_p],
     "mi_softmax_noalloc_f16": [_c_void_p, _c_void_p, _i64, _i64, _c_void_p],
+    "mi_softmax_argmax_ws_f16": [_c_void_p, _c_void_p, _c_void_p, _i64, _i64, _c_void_p, _i64,
+                                 _c_void_p],
     "mi_paged_kv_scatter_f16": [_c_void_p] * 5 + [_i64] * 8 + [_c_void_p],
     "mi_paged_kv_scatter_kv_f16": [_c_void_p] * 7 + [_i64] * 8 + [_c_void_p],
     "mi_greedy_argmax_f16": [_c_void_p, _i64, _i64, _c_void_p, _c_void_p],
@@ -77,6 +81,8 @@ def load_library(path: os.PathLike | str | None = None) -> ctypes.CDLL:
     lib.mi_greedy_argmax_workspace_bytes.restype = _i64
     lib.mi_softmax_workspace_bytes.argtypes = [_i64, _i64]
     lib.mi_softmax_workspace_bytes.restype = _i64
+    lib.mi_softmax_argmax_workspace_bytes.argtypes = [_i64, _i64]
+    lib.mi_softmax_argmax_workspace_bytes.restype = _i64
     lib.mi_status_string.argtypes = [_int]
     lib.mi_status_string.restype = ctypes.c_char_p
     if path is None:
@@ -378,6 +384,33 @@ def softmax(x, y=None, workspace=None, stream=None):
     return y
 
 
+def softmax_argmax_workspace_bytes(N: int, V: int) -> int:
+    return int(load_library().mi_softmax_argmax_workspace_bytes(N, V))
+
+
+def softmax_argmax(logits, workspace, probs=None, out=None, stream=None):
+    """probs = softmax(logits) and out = greedy argmax(logits) in one pass over
+    logits [N, V]; `workspace` (softmax_argmax_workspace_bytes bytes) must be
+    zero before its first use and kept for this function.  Returns (probs, out)."""
+    torch = _torch()
+    _need(logits, _f16(), "logits")
+    if logits.dim() != 2:
+        raise ValueError("logits must be 2-D [N, V]")
+    N, V = logits.shape
+    if probs is None:
+        probs = torch.empty_like(logits)
+    if out is None:
+        out = torch.empty(N, dtype=torch.int32, device=logits.device)
+    _need(probs, _f16(), "probs"); _need(out, torch.int32, "out")
+    if probs.shape != logits.shape or out.numel() != N:
+        raise ValueError("probs must match logits and out hold N entries")
+    nbytes = workspace.numel() * workspace.element_size()
+    _check(load_library().mi_softmax_argmax_ws_f16(_ptr(logits), _ptr(probs), _ptr(out), N, V,
+                                                   _ptr(workspace), nbytes, _stream(stream)),
+           "mi_softmax_argmax_ws_f16")
+    return probs, out
+
+
 def softmax_noalloc(x, y=None, stream=None):
     """Row softmax through the allocation-free entry point
     (mi_softmax_noalloc_f16): its workspace is a device array the library
@@ -426,6 +459,34 @@ def embedding_gather(ids, table, out=None, check_range: bool = True, stream=None
     _check(load_library().mi_embedding_gather_f16(_ptr(ids), _ptr(table), _ptr(out), T, H, vocab,
                                                   _stream(stream)), "mi_embedding_gather_f16")
     return out
+
+
+def embedding_rmsnorm(ids, table, weight, hidden=None, y=None, scale: float = 1.0,
+                      eps: float = 1e-6, add_one: bool = False, check_range: bool = True,
+                      stream=None):
+    """hidden[t] = half(table[ids[t]] * scale), y = rmsnorm(hidden) in one pass;
+    returns (hidden, y), each [*ids.shape, D]."""
+    torch = _torch()
+    _need(ids, torch.int64, "ids"); _need(table, _f16(), "table"); _need(weight, _f16(), "weight")
+    if table.dim() != 2:
+        raise ValueError("table must be 2-D [V, D]")
+    V, D = table.shape
+    T = ids.numel()
+    if weight.numel() != D:
+        raise ValueError("weight must hold D elements")
+    if hidden is None:
+        hidden = torch.empty((*ids.shape, D), dtype=torch.float16, device=table.device)
+    if y is None:
+        y = torch.empty((*ids.shape, D), dtype=torch.float16, device=table.device)
+    for t, n in ((hidden, "hidden"), (y, "y")):
+        _need(t, _f16(), n)
+        if t.numel() != T * D:
+            raise ValueError(f"{n} must hold T * D elements")
+    _check(load_library().mi_embedding_rmsnorm_f16(
+        _ptr(ids), _ptr(table), _ptr(hidden), _ptr(weight), _ptr(y), T, D,
+        V if check_range else 0, float(scale), float(eps), int(add_one), _stream(stream)),
+        "mi_embedding_rmsnorm_f16")
+    return hidden, y
 
 
 # ---------------------------------------------------------------------------

@@ -89,6 +89,37 @@ def test_gather_shapes_and_bad_ids(mk, orc, dev, H):
     assert (out[0, 0] == 0).all() and (out[1, 5] == 0).all()
 
 
+@pytest.mark.parametrize("D,scale,add_one", [(3584, 1.0, False), (3584, 3584 ** 0.5, True),
+                                             (8192, 1.0, False), (2048, 2048 ** 0.5, False),
+                                             (1000, 1.0, False), (3585, 59.87, True)])
+def test_embedding_rmsnorm(mk, orc, dev, D, scale, add_one):
+    """Gather fused with the input RMSNorm: hidden is the gathered row (scaled
+    and rounded as mi_scale_inplace_f16 does), bit for bit, and y the oracle's
+    RMSNorm of that fp16 hidden, rtol = atol = 1e-3.  Vector and scalar
+    paths, out-of-range ids (zero rows), Gemma's scale and (1 + w)."""
+    _case(f"embedding+rmsnorm D={D} scale={scale:.3f} add_one={add_one}")
+    rng = np.random.default_rng(D)
+    V, T = 700, 613
+    table = normal_f16(rng, (V, D), 0, 0.02)
+    w = normal_f16(rng, (D,), 0.0 if add_one else 1.0, 0.1)
+    ids = rng.integers(0, V, T).astype(np.int64)
+    ids[3] = -5
+    ids[10] = V
+    hid, y = mk.embedding_rmsnorm(to_dev(ids, dev), to_dev(table, dev), to_dev(w, dev),
+                                  scale=scale, eps=1e-6, add_one=add_one)
+    ref_h = orc.embedding_gather(ids, table)
+    if scale != 1.0:
+        ref_h = orc.scale(ref_h, np.float32(scale))
+    assert_bits_equal(to_host(hid), ref_h, what="hidden")
+    assert_close(to_host(y), orc.rmsnorm(ref_h, w, 1e-6, add_one), what="y")
+    # the unfused sequence on the GPU gives the same bits
+    g = mk.embedding_gather(to_dev(ids, dev), to_dev(table, dev))
+    if scale != 1.0:
+        mk.scale_inplace(g, scale)
+    y2 = mk.rmsnorm(g, to_dev(w, dev), eps=1e-6, add_one=add_one)
+    assert_bits_equal(to_host(y), to_host(y2), what="fused vs gather + scale + rmsnorm")
+
+
 def test_softmax_workspace_variant(mk, orc, dev):
     _case("softmax with caller workspace")
     import torch
@@ -340,3 +371,103 @@ def test_softmax_persistent_graph_replay(mk, orc, dev):
         assert_bits_equal(to_host(y), ref, what=f"replay {i}")
         mk.softmax(xd, workspace=ws)
     assert_close(ref, orc.softmax(x, nthreads=8), what="vs oracle")
+
+
+def _special_logits(rng, N, V):
+    x = normal_f16(rng, (N, V), 0, 4)
+    x[0, :] = -np.inf                       # nothing eligible: argmax -1
+    x[1, 5], x[1, V - 3] = 30.0, 30.0       # a tie across chunks
+    if N > 2:
+        x[2, ::7] = np.nan                  # NaN never chosen
+        x[2, V // 2] = 40.0
+    if N > 3:
+        x[3, :] = -0.0                      # all equal (signed zeros): the tie order decides
+        x[3, 1::2] = 0.0
+    return x
+
+
+@pytest.mark.parametrize("N,V,inplace", [(64, 152064, False), (600, 65544, False),
+                                         (5, 40000, False), (64, 152064, True), (7, 1000, False),
+                                         (300, 32768, False)])
+def test_softmax_argmax_fused(mk, orc, dev, N, V, inplace):
+    """Softmax and greedy argmax of the same logits in one pass: probs bit for
+    bit those of mi_softmax_ws_f16 (the same kernels' arithmetic), indices
+    exactly the oracle's (the reference's tie order), over one-launch split
+    rows, the persistent many-row form, and shapes that run the two entry
+    points in turn (in place, short rows)."""
+    _case(f"softmax+argmax [{N},{V}] inplace={inplace}")
+    import torch
+    rng = np.random.default_rng(N + V)
+    x = _special_logits(rng, N, V)
+    xd = to_dev(x, dev)
+    ws = torch.zeros(mk.softmax_argmax_workspace_bytes(N, V), dtype=torch.uint8, device=dev)
+    ref_idx = orc.greedy_argmax(x)
+    sws = torch.zeros(max(16, mk.softmax_workspace_bytes(N, V)), dtype=torch.uint8, device=dev)
+    xr = xd.clone()
+    ref_p = to_host(mk.softmax(xr, y=xr if inplace else None, workspace=sws))
+    for call in range(2):  # the workspace stays valid for the next call
+        xin = xd.clone() if inplace else xd
+        probs, idx = mk.softmax_argmax(xin, ws, probs=xin if inplace else None)
+        assert (to_host(idx) == ref_idx).all(), f"call {call}: argmax"
+        assert_bits_equal(to_host(probs), ref_p, what=f"call {call}: probs")
+    if not inplace:
+        assert_bits_equal(to_host(xd), x, what="logits untouched")
+
+
+def test_softmax_argmax_forced_fallback(mk, orc, dev):
+    """Poll bound 0: every chunk takes the fallback (statistics and the row's
+    key from x); results unchanged, and normal calls afterwards still right."""
+    _case("softmax+argmax forced fallback")
+    import torch
+    rng = np.random.default_rng(77)
+    N, V = 64, 152064
+    x = _special_logits(rng, N, V)
+    xd = to_dev(x, dev)
+    ws = torch.zeros(mk.softmax_argmax_workspace_bytes(N, V), dtype=torch.uint8, device=dev)
+    ref_p = orc.softmax(x, nthreads=8)
+    prev = mk.softmax_test_poll_limit(0)
+    try:
+        probs, idx = mk.softmax_argmax(xd, ws)
+        torch.cuda.synchronize()
+    finally:
+        mk.softmax_test_poll_limit(prev)
+    assert (to_host(idx) == orc.greedy_argmax(x)).all()
+    ok = np.isfinite(ref_p)
+    assert_close(to_host(probs)[ok], ref_p[ok], what="fallback probs")
+    x2 = normal_f16(rng, (N, V), 0, 4)
+    probs, idx = mk.softmax_argmax(to_dev(x2, dev), ws)
+    assert (to_host(idx) == orc.greedy_argmax(x2)).all()
+    assert_close(to_host(probs), orc.softmax(x2, nthreads=8), what="after fallback")
+
+
+def test_softmax_argmax_graph_replay(mk, orc, dev):
+    """The fused pass captured in a graph and replayed with eager work in
+    between: every replay matches the eager call."""
+    _case("softmax+argmax graph replay")
+    import torch
+    rng = np.random.default_rng(78)
+    N, V = 64, 152064
+    x = normal_f16(rng, (N, V), 0, 4)
+    xd = to_dev(x, dev)
+    ws = torch.zeros(mk.softmax_argmax_workspace_bytes(N, V), dtype=torch.uint8, device=dev)
+    p_ref, i_ref = (to_host(t) for t in mk.softmax_argmax(xd, ws))
+    probs = torch.empty_like(xd)
+    idx = torch.empty(N, dtype=torch.int32, device=dev)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        mk.softmax_argmax(xd, ws, probs=probs, out=idx)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=side):
+        mk.softmax_argmax(xd, ws, probs=probs, out=idx, stream=side)
+    for i in range(3):
+        probs.zero_()
+        idx.fill_(-7)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert_bits_equal(to_host(probs), p_ref, what=f"replay {i}")
+        assert (to_host(idx) == i_ref).all(), f"replay {i}"
+    del g
