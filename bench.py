@@ -112,11 +112,13 @@ def randn16(shape, gen, dev, mean=0.0, std=1.0):
 # kernels (graph replay, buffers rotated past the Infinity Cache).  Each floor
 # is the fastest of a few plain forms (16-byte vectors per lane per step
 # 1/2/4/8, one workgroup per tile or a resident grid-stride grid,
-# non-temporal or plain loads), so it is
-# the time a no-work kernel of this library's style needs for those bytes.
+# non-temporal or plain loads, stores issued back to back or each waiting for
+# the one before it -- the latter is faster at 40 MB), so it is the time a
+# no-work kernel of this library's style needs for those bytes.
 # ---------------------------------------------------------------------------
 
-FLOOR_FORMS = [(v, p, n) for v in (1, 2, 4, 8) for p in (0, 1) for n in (0, 1)]
+FLOOR_FORMS = ([(v, p, n, 0) for v in (1, 2, 4, 8) for p in (0, 1) for n in (0, 1)] +
+               [(v, p, 0, 1) for v in (1, 2, 4, 8) for p in (0, 1)])
 _FLOORS_LIB = None
 _FLOOR = {}
 
@@ -138,10 +140,10 @@ def floors_lib():
     return _FLOORS_LIB
 
 
-def _floor_launcher(kind, bufs, sink, nbytes, vpl, persistent, plain):
+def _floor_launcher(kind, bufs, sink, nbytes, vpl, persistent, plain, serial):
     import torch
     lib = floors_lib()
-    form = vpl | (16 if persistent else 0) | (32 if plain else 0)
+    form = vpl | (16 if persistent else 0) | (32 if plain else 0) | (64 if serial else 0)
 
     def go(i):
         st = torch.cuda.current_stream().cuda_stream
@@ -173,9 +175,11 @@ def floor_time(dev, kind, nbytes, iters=40, warmup=5, forms=None):
             for _ in range(ns)]
     sink = torch.zeros(1 << 20, dtype=torch.int32, device=dev)
     per = {}
-    for vpl, pers, plain in (forms or FLOOR_FORMS):
-        per[(vpl, pers, plain)] = time_launches(
-            _floor_launcher(kind, bufs, sink, nbytes, vpl, pers, plain), ns, iters, warmup)
+    for vpl, pers, plain, serial in (forms or FLOOR_FORMS):
+        if serial and kind == "read":
+            continue  # no stores
+        per[(vpl, pers, plain, serial)] = time_launches(
+            _floor_launcher(kind, bufs, sink, nbytes, vpl, pers, plain, serial), ns, iters, warmup)
     del bufs, nb
     best = min(per.values())
     if forms is None:
@@ -226,12 +230,13 @@ def floor_sweep(dev, sizes_mb=(8, 20, 40, 67, 100, 174, 235, 465)):
             moved = nbytes if kind == "read" else 2 * nbytes
             n = moved if kind == "read" else nbytes
             _, per = floor_time(dev, kind, n, forms=FLOOR_FORMS)
-            for (v, p, pl), sec in per.items():
+            for (v, p, pl, se), sec in per.items():
                 rows.append({"kind": kind, "moved_bytes": moved, "vpl": v, "persistent": p,
-                             "plain_loads": pl, "us": round(sec * 1e6, 3),
+                             "plain_loads": pl, "serial_stores": se, "us": round(sec * 1e6, 3),
                              "frac": round(moved / sec / HBM_PEAK, 4)})
                 log(f"[floors] {kind:<8} {moved / 1e6:8.1f} MB vpl={v} persistent={p} "
-                    f"plain_loads={pl} {sec * 1e6:9.2f} us {100 * moved / sec / HBM_PEAK:6.1f}%")
+                    f"plain_loads={pl} serial_stores={se} {sec * 1e6:9.2f} us "
+                    f"{100 * moved / sec / HBM_PEAK:6.1f}%")
     return rows
 
 

@@ -13,7 +13,8 @@
 // Each stream kernel moves 16-byte vectors, VPL of them per lane per step,
 // all loads of a step issued before its stores, with non-temporal stores and
 // non-temporal or plain loads; a `form` also selects one workgroup per tile
-// or a grid of the resident capacity walking the buffer with a grid stride.  The
+// or a grid of the resident capacity walking the buffer with a grid stride,
+// and stores issued back to back or each waiting for the one before it.  The
 // benchmark takes the fastest of a few (VPL, persistent) forms as the floor.
 // Not part of the layer-kernel library: nothing here is reached from
 // include/mi_kernels.h.
@@ -35,7 +36,7 @@ constexpr int kThreads = 256;
 
 enum Kind { kCopy = 0, kInplace = 1, kRead = 2 };
 
-template <int KIND, int VPL, bool NT>
+template <int KIND, int VPL, bool NT, bool SER = false>
 __global__ __launch_bounds__(kThreads) void stream_kernel(const u4* src, u4* dst, int64_t nvec,
                                                           uint32_t pattern, uint32_t* sink) {
     const int64_t tile = static_cast<int64_t>(kThreads) * VPL;
@@ -54,7 +55,9 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(const u4* src, u4* dst
             const int64_t i = base + static_cast<int64_t>(j) * kThreads;
             if (i < nvec) {
                 if constexpr (KIND == kCopy) st(dst + i, v[j]);
+                if constexpr (SER && KIND == kCopy) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
                 if constexpr (KIND == kInplace) st(dst + i, v[j] ^ pattern);
+                if constexpr (SER && KIND == kInplace) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
                 if constexpr (KIND == kRead) acc ^= v[j].x ^ v[j].y ^ v[j].z ^ v[j].w;
             }
         }
@@ -68,10 +71,10 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(const u4* src, u4* dst
 
 __global__ void empty_kernel() {}
 
-template <int KIND, int VPL, bool NT>
+template <int KIND, int VPL, bool NT, bool SER>
 int launch_vpl(const void* src, void* dst, int64_t nvec, int persistent, uint32_t* sink,
                int64_t sink_words, hipStream_t s) {
-    const auto k = stream_kernel<KIND, VPL, NT>;
+    const auto k = stream_kernel<KIND, VPL, NT, SER>;
     const int64_t tiles = (nvec + kThreads * VPL - 1) / (kThreads * VPL);
     int64_t grid = tiles;
     if (persistent) {
@@ -91,32 +94,36 @@ int launch_vpl(const void* src, void* dst, int64_t nvec, int persistent, uint32_
     return hipGetLastError() == hipSuccess ? 0 : 1;
 }
 
-template <int KIND, bool NT>
+template <int KIND, bool NT, bool SER>
 int launch_nt(const void* src, void* dst, int64_t nvec, int vpl, int persistent, uint32_t* sink,
               int64_t sink_words, hipStream_t s) {
     switch (vpl) {
-        case 1: return launch_vpl<KIND, 1, NT>(src, dst, nvec, persistent, sink, sink_words, s);
-        case 2: return launch_vpl<KIND, 2, NT>(src, dst, nvec, persistent, sink, sink_words, s);
-        case 4: return launch_vpl<KIND, 4, NT>(src, dst, nvec, persistent, sink, sink_words, s);
-        case 8: return launch_vpl<KIND, 8, NT>(src, dst, nvec, persistent, sink, sink_words, s);
+        case 1: return launch_vpl<KIND, 1, NT, SER>(src, dst, nvec, persistent, sink, sink_words, s);
+        case 2: return launch_vpl<KIND, 2, NT, SER>(src, dst, nvec, persistent, sink, sink_words, s);
+        case 4: return launch_vpl<KIND, 4, NT, SER>(src, dst, nvec, persistent, sink, sink_words, s);
+        case 8: return launch_vpl<KIND, 8, NT, SER>(src, dst, nvec, persistent, sink, sink_words, s);
         default: return -1;
     }
 }
 
 // form: vpl (1, 2, 4, 8) | 16 (resident grid-stride grid) | 32 (plain loads
-// instead of non-temporal ones)
+// instead of non-temporal ones) | 64 (each store waits for the one before)
 template <int KIND>
 int launch(const void* src, void* dst, int64_t bytes, int form, uint32_t* sink,
            int64_t sink_words, void* stream) {
-    const int vpl = form & 15, persistent = (form >> 4) & 1, plain = (form >> 5) & 1;
+    const int vpl = form & 15, persistent = (form >> 4) & 1, plain = (form >> 5) & 1,
+              ser = (form >> 6) & 1;
     if (bytes <= 0 || bytes % 16 != 0 || !src || (KIND != kRead && !dst) ||
         (KIND == kRead && !sink))
         return -1;
     if ((reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(dst)) & 15u) return -1;
     const int64_t nvec = bytes / 16;
     const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-    return plain ? launch_nt<KIND, false>(src, dst, nvec, vpl, persistent, sink, sink_words, s)
-                 : launch_nt<KIND, true>(src, dst, nvec, vpl, persistent, sink, sink_words, s);
+    if (ser)
+        return plain ? launch_nt<KIND, false, true>(src, dst, nvec, vpl, persistent, sink, sink_words, s)
+                     : launch_nt<KIND, true, true>(src, dst, nvec, vpl, persistent, sink, sink_words, s);
+    return plain ? launch_nt<KIND, false, false>(src, dst, nvec, vpl, persistent, sink, sink_words, s)
+                 : launch_nt<KIND, true, false>(src, dst, nvec, vpl, persistent, sink, sink_words, s);
 }
 
 }  // namespace

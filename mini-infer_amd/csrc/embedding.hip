@@ -42,8 +42,11 @@ __global__ __launch_bounds__(256) void gather_kernel(const int64_t* __restrict__
             for (int j = 0; j < kBatch; ++j) {
                 const int64_t c = c0 + j * kLanes + lane;
                 // plain loads: the rows are scattered over a table far larger than
-                // the caches, and the non-temporal hint measured 66% -> 72% of peak
-                // slower at T = 6064 of [152064, 3584] (16.4 -> 15.1 us)
+                // the caches; plain loads measured 72% of peak against 66% with the
+                // non-temporal hint at T = 6064 of [152064, 3584] (15.1 vs 16.4 us).
+                // (The stores below each wait for the one before them -- the
+                // counter is in order -- and measured faster that way: one
+                // explicit wait for all loads instead took 15.3 -> 17.0 us.)
                 v[j] = (valid && c < nv) ? ld8(src + c * 8) : h8(0);
             }
 #pragma unroll
@@ -124,20 +127,30 @@ __global__ __launch_bounds__(256) void embed_rms_kernel(const int64_t* __restric
         const int64_t c = threadIdx.x + j * 256;
         wv[j] = c < nv ? ld8(w + c * 8) : h8(0);
     }
-    float ss = 0.0f;
+    // Every load is waited for once, here, and every vector scaled and
+    // squared before the first store: with a store in flight, any later wait
+    // on the (in-order) vector-memory counter would also wait for the store.
+    __builtin_amdgcn_s_waitcnt(kDrainVmem);
+    if (scale != 1.0f) {
 #pragma unroll
-    for (int j = 0; j < VPT; ++j) {
-        const int64_t c = threadIdx.x + j * 256;
-        if (scale != 1.0f) {
+        for (int j = 0; j < VPT; ++j) {
 #pragma unroll
             for (int k = 0; k < 8; ++k) v[j][k] = to_half((float)v[j][k] * scale);
         }
-        if (c < nv) st8_stream(hidden + t * D + c * 8, v[j]);
+    }
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
             const float f = (float)v[j][k];
             ss = fmaf(f, f, ss);
         }
+    }
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+        const int64_t c = threadIdx.x + j * 256;
+        if (c < nv) st8_stream(hidden + t * D + c * 8, v[j]);
     }
     ss = block_sum(ss, slots);
     const float rrms = rsqrtf(ss / static_cast<float>(D) + eps);

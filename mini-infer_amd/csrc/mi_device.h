@@ -85,6 +85,12 @@ __device__ __forceinline__ void st8_stream(half_t* p, h8 v) {
 __device__ __forceinline__ void st8_stream_wt(half_t* p, h8 v) {
     asm volatile(MI_WT_ASM : : "v"(p), "v"(v) : "memory");
 }
+// A wait for every outstanding vector-memory operation, placed after a
+// store when S: each store then waits for the one before it.
+template <bool S>
+__device__ __forceinline__ void store_gap() {
+    if constexpr (S) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+}
 // Store selected per kernel at compile time.
 template <bool WT>
 __device__ __forceinline__ void st8_out(half_t* p, h8 v) {
