@@ -6,6 +6,7 @@
 #include <cstring>
 #include <stdexcept>
 #include <string>
+#include <utility>
 
 namespace mini_infer {
 
@@ -98,40 +99,37 @@ Tensor::Tensor(const Tensor& other)
     if (nbytes_ > 0 && other.data_) copy_raw(other.data_, data_, nbytes_, other.device_, device_);
 }
 
+// Member-wise exchange: the building block of both assignments below
+// (copy-and-swap), so each has one path that leaves *this either fully old
+// or fully new.
+void Tensor::swap_(Tensor& other) noexcept {
+    using std::swap;
+    swap(shape_, other.shape_);
+    swap(stride_, other.stride_);
+    swap(numel_, other.numel_);
+    swap(nbytes_, other.nbytes_);
+    swap(dtype_, other.dtype_);
+    swap(device_, other.device_);
+    swap(data_, other.data_);
+    swap(owns_data_, other.owns_data_);
+}
+
 Tensor& Tensor::operator=(const Tensor& other) {
     if (this != &other) {
-        Tensor tmp(other);
-        *this = std::move(tmp);
-    }
+        Tensor copy(other);  // allocates and copies first: a failure leaves *this intact
+        swap_(copy);
+    }                        // copy now holds the old buffer and frees it
     return *this;
 }
 
-Tensor::Tensor(Tensor&& other) noexcept
-    : shape_(std::move(other.shape_)), stride_(std::move(other.stride_)), numel_(other.numel_),
-      nbytes_(other.nbytes_), dtype_(other.dtype_), device_(other.device_), data_(other.data_),
-      owns_data_(other.owns_data_) {
-    other.data_ = nullptr;
-    other.owns_data_ = false;
-    other.numel_ = 0;
-    other.nbytes_ = 0;
-}
+// The moved-from tensor is left empty (no shape, no buffer, not owning).
+Tensor::Tensor(Tensor&& other) noexcept { swap_(other); }
 
 Tensor& Tensor::operator=(Tensor&& other) noexcept {
     if (this != &other) {
-        release_();
-        shape_ = std::move(other.shape_);
-        stride_ = std::move(other.stride_);
-        numel_ = other.numel_;
-        nbytes_ = other.nbytes_;
-        dtype_ = other.dtype_;
-        device_ = other.device_;
-        data_ = other.data_;
-        owns_data_ = other.owns_data_;
-        other.data_ = nullptr;
-        other.owns_data_ = false;
-        other.numel_ = 0;
-        other.nbytes_ = 0;
-    }
+        Tensor taken(std::move(other));
+        swap_(taken);
+    }  // taken holds the old buffer and frees it
     return *this;
 }
 

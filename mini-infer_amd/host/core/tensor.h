@@ -90,6 +90,7 @@ public:
 private:
     void allocate_();
     void release_();
+    void swap_(Tensor& other) noexcept;
     void compute_default_stride_();
 
     std::vector<int64_t> shape_;

@@ -100,6 +100,18 @@ void cpu_checks() {
     EXPECT(c.data() != t.data() && std::memcmp(c.data(), t.data(), t.nbytes()) == 0, "deep copy");
     Tensor m = std::move(c);
     EXPECT(c.data() == nullptr && m.numel() == 24, "move leaves the source empty");
+    Tensor a({5}, DType::FP32, Device::cpu());
+    a.fill(2.0f);
+    a = m;  // copy-assign over a tensor of another shape and dtype
+    EXPECT(a.numel() == 24 && a.dtype() == DType::FP16 && a.data() != m.data() &&
+               std::memcmp(a.data(), m.data(), m.nbytes()) == 0,
+           "copy assignment takes shape, dtype and a deep copy");
+    const void* mp = m.data();
+    a = std::move(m);
+    EXPECT(a.data() == mp && m.data() == nullptr && m.numel() == 0 && !m.owns_data(),
+           "move assignment takes the buffer and empties the source");
+    a = std::move(a);  // self-move keeps the tensor
+    EXPECT(a.data() == mp && a.numel() == 24, "self move-assignment is a no-op");
     EXPECT(std::string(mini_infer::dtype_name(DType::INT64)) == "int64", "dtype_name");
     EXPECT(throws([] { Tensor bad({-1}, DType::FP32, Device::cpu()); }), "negative dim throws");
 }
