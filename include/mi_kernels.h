@@ -44,7 +44,7 @@ extern "C" {
 const char* mi_status_string(int status);
 
 /* ABI version of this header; bumped on any incompatible change. */
-#define MI_KERNELS_ABI_VERSION 1
+#define MI_KERNELS_ABI_VERSION 2
 int mi_abi_version(void);
 
 /* RMSNorm: y = x * rsqrt(sum(x^2)/D + eps) * (add_one ? 1 + w : w).
@@ -288,6 +288,12 @@ int mi_greedy_argmax_ws_f16(const void* logits, int64_t B, int64_t V, int32_t* o
  * a one-launch argmax row makes before scanning the row itself; 0 forces
  * that fallback everywhere.  Returns the previous bound. */
 int mi_greedy_argmax_test_poll_limit(int limit);
+
+/* Test hook (no counterpart in the reference): how the one-launch softmax,
+ * argmax and softmax + argmax kernels read their row records.  0 (default):
+ * the copy in the row's XCD L2 first, then the device-scope mirror; 1: the
+ * mirror only.  Returns the previous mode, or MI_ERR_INVALID_ARGUMENT. */
+int mi_exchange_test_mode(int mode);
 
 #ifdef __cplusplus
 }

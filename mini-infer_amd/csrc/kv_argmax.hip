@@ -37,6 +37,7 @@
 #include "argmax_key.h"
 #include "mi_device.h"
 #include "mi_host.h"
+#include "row_exchange.h"
 
 // KV stores: plain non-temporal (1 = write-through "nt sc1"; measured neutral).
 #ifndef MI_WT_KV
@@ -260,8 +261,10 @@ int64_t argmax_splits(int64_t B, int64_t V, int64_t& chunk) {
 // chunk 0 raises the epoch to E + 1 once it has seen every slot; a poll that
 // runs out makes chunk 0 scan the whole row itself and raise it to E + 2).  A key
 // travels as two 64-bit words {tag << 32 | key >> 32}, {tag << 32 | key
-// & 0xffffffff}, each stored and loaded whole at device scope.  The workspace
-// must be zero before its first use.
+// & 0xffffffff}, each stored and loaded whole, into the row's slots in the
+// XCD's L2 and into their device-scope mirror (row_exchange.h; the 1-D grid
+// keeps a row's chunks on one XCD).  The workspace must be zero before its
+// first use.
 // ---------------------------------------------------------------------------
 constexpr int kArgmaxOnePassMaxSplits = 64;
 #ifndef MI_ARGMAX_ONEPASS_U
@@ -269,23 +272,55 @@ constexpr int kArgmaxOnePassMaxSplits = 64;
 #endif
 constexpr int kArgmaxOnePassU = MI_ARGMAX_ONEPASS_U;             // vectors per lane
 constexpr int64_t kArgmaxOnePassChunk = 2048 * kArgmaxOnePassU;  // elements per workgroup
-constexpr int64_t kArgmaxRecordBytes = 16 + kArgmaxOnePassMaxSplits * 16;
+// 128-byte epoch header, the slots, their mirror
+constexpr int64_t kArgmaxRecordBytes = kRecordHeaderBytes + 2 * kArgmaxOnePassMaxSplits * 16;
+constexpr int64_t kArgmaxMirror = 2 * kArgmaxOnePassMaxSplits;  // words from a slot to its mirror
 constexpr int64_t kArgmaxRecordRegion = kArgmaxSplitMaxRows * kArgmaxRecordBytes;
 constexpr int kArgmaxPollLimit = 1 << 16;
 std::atomic<int> g_argmax_poll_limit{kArgmaxPollLimit};  // mi_greedy_argmax_test_poll_limit
 
+// One phase of chunk 0's polls (LOCAL: the L2 copy, else the mirror) of
+// `set` (workgroup-uniform; lane j < splits reads slot j) until every slot
+// carries `tag`, `it` reaches poll_limit or the clock passes t0 + ticks; k:
+// the lane's key.  Returns whether every slot was seen.
+template <bool LOCAL>
+__device__ __forceinline__ bool argmax_poll(const uint64_t* set, int splits, uint32_t tag, int& it,
+                                            int poll_limit, uint64_t t0, uint64_t ticks,
+                                            uint64_t& k) {
+    const int lane = threadIdx.x & (kWave - 1);
+    for (; it < poll_limit; ++it) {
+        if (it > 0 && __builtin_amdgcn_s_memrealtime() - t0 > ticks) return false;
+        bool mine = true;
+        k = 0;
+        if (lane < splits) {
+            uint64_t w[2];
+            load_slot<LOCAL, 2>(set, static_cast<uint32_t>(lane) * 16, w);
+            mine = static_cast<uint32_t>(w[0] >> 32) == tag && static_cast<uint32_t>(w[1] >> 32) == tag;
+            k = (w[0] << 32) | (w[1] & 0xffffffffu);
+        }
+        if (__all(mine)) return true;
+        __builtin_amdgcn_s_sleep(2);
+    }
+    return false;
+}
+
 __global__ __launch_bounds__(256) void argmax_onepass_kernel(const half_t* __restrict__ x,
                                                              int64_t V, unsigned char* ws,
                                                              int32_t* __restrict__ out,
-                                                             int poll_limit) {
+                                                             int poll_limit, int64_t B,
+                                                             int splits, int local) {
     __shared__ uint64_t slots[256 / kWave];
     __shared__ uint64_t epoch_sh;
     __shared__ int fallback_sh;
-    const int split = blockIdx.x, splits = gridDim.x;
-    const int64_t row = blockIdx.y;
+    // 1-D grid of splits x (B rounded up to kXcds): a row's chunks share one
+    // XCD (row_exchange.h); rows past B - 1 do not exist
+    int split, slot_row;
+    chunk_of(blockIdx.x, splits, split, slot_row);
+    const int64_t row = slot_row;
+    if (row >= B) return;  // workgroup-uniform, before any barrier
     unsigned char* rec = ws + row * kArgmaxRecordBytes;
     uint64_t* epoch = reinterpret_cast<uint64_t*>(rec);
-    uint64_t* slot = reinterpret_cast<uint64_t*>(rec + 16);
+    uint64_t* slot = reinterpret_cast<uint64_t*>(rec + kRecordHeaderBytes);
     const half_t* xr = x + row * V;
     const int64_t b = split * kArgmaxOnePassChunk;
     const int64_t e = b + kArgmaxOnePassChunk < V ? b + kArgmaxOnePassChunk : V;
@@ -295,35 +330,26 @@ __global__ __launch_bounds__(256) void argmax_onepass_kernel(const half_t* __res
     const uint64_t E = epoch_sh;
     const uint32_t tag = static_cast<uint32_t>(E + 1);
     if (threadIdx.x == 0) {
-        __hip_atomic_store(&slot[2 * split], (static_cast<uint64_t>(tag) << 32) | (best >> 32),
-                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(&slot[2 * split + 1],
-                           (static_cast<uint64_t>(tag) << 32) | (best & 0xffffffffu),
-                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const uint64_t w0 = (static_cast<uint64_t>(tag) << 32) | (best >> 32);
+        const uint64_t w1 = (static_cast<uint64_t>(tag) << 32) | (best & 0xffffffffu);
+        local_store(&slot[2 * split], w0);
+        local_store(&slot[2 * split + 1], w1);
+        device_store(&slot[kArgmaxMirror + 2 * split], w0);
+        device_store(&slot[kArgmaxMirror + 2 * split + 1], w1);
     }
     if (split != 0) return;  // whole workgroup
     if (threadIdx.x < kWave) {
         const int lane = threadIdx.x;
         uint64_t k = 0;
-        bool all = false;
-        // also bounded by 20000 ticks (200 us) of the 100 MHz constant clock
+        // also bounded by 20000 ticks (200 us) of the 100 MHz constant clock;
+        // the L2 copy for the first kLocalPollTicks, then the mirror
         const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
-        for (int it = 0; it < poll_limit && !all; ++it) {
-            if (it > 0 && __builtin_amdgcn_s_memrealtime() - t0 > 20000) break;
-            bool mine = true;
-            k = 0;
-            if (lane < splits) {
-                const uint64_t w0 = __hip_atomic_load(&slot[2 * lane], __ATOMIC_RELAXED,
-                                                      __HIP_MEMORY_SCOPE_AGENT);
-                const uint64_t w1 = __hip_atomic_load(&slot[2 * lane + 1], __ATOMIC_RELAXED,
-                                                      __HIP_MEMORY_SCOPE_AGENT);
-                mine = static_cast<uint32_t>(w0 >> 32) == tag &&
-                       static_cast<uint32_t>(w1 >> 32) == tag;
-                k = (w0 << 32) | (w1 & 0xffffffffu);
-            }
-            all = __all(mine);
-            if (!all) __builtin_amdgcn_s_sleep(2);
-        }
+        int it = 0;
+        bool all = local != 0 && argmax_poll<true>(slot, splits, tag, it, poll_limit, t0,
+                                                   kLocalPollTicks, k);
+        if (!all)
+            all = argmax_poll<false>(slot + kArgmaxMirror, splits, tag, it, poll_limit, t0, 20000,
+                                     k);
         if (all) {
             k = wave_max_u64(k);
             if (lane == 0) out[row] = key_index(k);
@@ -411,9 +437,10 @@ int argmax(const void* logits, int64_t B, int64_t V, int32_t* out, void* ws, int
     const bool vec = V % 16 == 0 && aligned16(logits);
     if (onepass) {
         const int64_t sp1 = ceil_div(V, kArgmaxOnePassChunk);
-        argmax_onepass_kernel<<<dim3(static_cast<unsigned>(sp1), static_cast<unsigned>(B)),
-                                dim3(256), 0, st>>>(x, V, static_cast<unsigned char*>(ws), out,
-                                                    g_argmax_poll_limit.load());
+        const int64_t rows = ceil_div(B, kXcds) * kXcds;  // <= kArgmaxSplitMaxRows
+        argmax_onepass_kernel<<<dim3(static_cast<unsigned>(sp1 * rows)), dim3(256), 0, st>>>(
+            x, V, static_cast<unsigned char*>(ws), out, g_argmax_poll_limit.load(), B,
+            static_cast<int>(sp1), exchange_test_mode().load() == 0 ? 1 : 0);
         return launch_status();
     }
     auto* w = reinterpret_cast<uint64_t*>(

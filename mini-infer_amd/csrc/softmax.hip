@@ -38,6 +38,7 @@
 #include "argmax_key.h"
 #include "mi_device.h"
 #include "mi_host.h"
+#include "row_exchange.h"
 
 // Softmax stores: plain non-temporal (1 = write-through "nt sc1"; measured neutral).
 #ifndef MI_WT_SM
@@ -383,8 +384,10 @@ __global__ __launch_bounds__(256) void softmax_finish_kernel(const half_t* x, ha
 //
 // Workspace (zero before first use; every call leaves it valid for the
 // next): row slot r owns a fixed record at r * kRowRecordBytes -- a 64-bit
-// epoch word (16-byte header), then two sets of kOnePassMaxSplits slots of
-// two 64-bit words {tag << 32 | bits(max)}, {tag << 32 | bits(sum)}.  A call
+// epoch word (128-byte header), then two sets of kOnePassMaxSplits slots of
+// two 64-bit words {tag << 32 | bits(max)}, {tag << 32 | bits(sum)}, and a
+// mirror of both sets (row_exchange.h: each word is published into the XCD's
+// L2 and through to memory; polls read the L2 copy first).  A call
 // reads the slot's epoch E; round k publishes into set k & 1 with tag = the
 // low 32 bits of E + 1 + k and polls the set until every chunk's pair carries
 // that tag.  Because slots are fixed per (row slot, chunk) whatever the
@@ -409,8 +412,9 @@ __global__ __launch_bounds__(256) void softmax_finish_kernel(const half_t* x, ha
 // A workgroup publishes round k + 2 into a set only after it has seen every
 // chunk's round k + 1 pair, which its row-mates publish after they have read
 // round k: no pair is overwritten before it is read.  Each 64-bit word is
-// stored and loaded whole at device scope (write-through stores, L2-bypassing
-// loads), so a tag always travels with its value.
+// stored and loaded whole, so a tag always travels with its value.
+// The grid is 1-D and places every chunk of a row slot on one XCD
+// (chunk_of), so the L2 copy normally serves the polls.
 // ---------------------------------------------------------------------------
 constexpr int kOnePassMaxSplits = 64;
 #ifndef MI_SOFTMAX_ONEPASS_U
@@ -418,11 +422,11 @@ constexpr int kOnePassMaxSplits = 64;
 #endif
 constexpr int kOnePassU = MI_SOFTMAX_ONEPASS_U;     // vectors per lane
 constexpr int64_t kOnePassChunk = 2048 * kOnePassU;  // elements per workgroup
-// header, then two sets of slots (alternated by round); a slot is the
-// chunk's tagged (max, sum) pair, plus its tagged argmax key (two words) in
-// the fused softmax + argmax pass
-constexpr int64_t kRowRecordBytes = 16 + 2 * kOnePassMaxSplits * 16;
-constexpr int64_t kRowRecordBytesAM = 16 + 2 * kOnePassMaxSplits * 32;
+// header, then two sets of slots (alternated by round) and their mirror; a
+// slot is the chunk's tagged (max, sum) pair, plus its tagged argmax key (two
+// words) in the fused softmax + argmax pass
+constexpr int64_t kRowRecordBytes = kRecordHeaderBytes + 4 * kOnePassMaxSplits * 16;
+constexpr int64_t kRowRecordBytesAM = kRecordHeaderBytes + 4 * kOnePassMaxSplits * 32;
 template <bool AM>
 constexpr int64_t record_bytes() { return AM ? kRowRecordBytesAM : kRowRecordBytes; }
 constexpr int kPollLimit = 1 << 16;
@@ -459,63 +463,89 @@ __device__ __forceinline__ void chunk_lane_stats(const h8 (&a)[U], float& m, flo
     }
 }
 // Thread 0 publishes the chunk's pair (and, AM, its argmax key) into slot
-// `split` of `slots` (SW = 2 or 4 words per slot).
+// `split` of `slots` (SW = 2 or 4 words per slot) and of its mirror
+// (`mirror` words on).
 template <bool AM>
-__device__ __forceinline__ void chunk_publish(uint64_t* slots, int split, uint32_t tag, float m,
-                                              float s, uint64_t key) {
+__device__ __forceinline__ void chunk_publish(uint64_t* slots, int64_t mirror, int split,
+                                              uint32_t tag, float m, float s, uint64_t key) {
     constexpr int SW = AM ? 4 : 2;
     if (threadIdx.x == 0) {
-        uint64_t* p = slots + SW * split;
-        __hip_atomic_store(&p[0], tagged(tag, m), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(&p[1], tagged(tag, s), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        uint64_t w[SW];
+        w[0] = tagged(tag, m);
+        w[1] = tagged(tag, s);
         if constexpr (AM) {
             const uint64_t t = static_cast<uint64_t>(tag) << 32;
-            __hip_atomic_store(&p[2], t | (key >> 32), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(&p[3], t | (key & 0xffffffffu), __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
+            w[2] = t | (key >> 32);
+            w[3] = t | (key & 0xffffffffu);
         }
+        uint64_t* p = slots + SW * split;
+#pragma unroll
+        for (int i = 0; i < SW; ++i) local_store(&p[i], w[i]);
+#pragma unroll
+        for (int i = 0; i < SW; ++i) device_store(&p[mirror + i], w[i]);
     }
 }
 // Wave 0 (the caller calls it there) polls the row's `splits` slots (lane j
-// reads chunk j) until all carry `tag`, at most poll_limit rounds, and leaves
+// reads chunk j) until all carry `tag`, at most poll_limit rounds -- the L2
+// copy (local) for up to kLocalPollTicks, then the mirror `mirror` words on
+// at device scope (row_exchange.h) -- and leaves
 // the row's (M, S) in row_stats[0..1] (AM with want_key: its best key in
 // *row_key, the key words polled too; without, only the pair words, half
 // the bytes per poll: 12.9 -> 12.0 us at [64, 152064]) and row_stats[2] = 0,
 // or row_stats[2] = 1 when polling ran out.  The caller's barrier publishes
 // them.
-template <bool AM>
-__device__ __forceinline__ void row_poll(const uint64_t* slots, int splits, uint32_t tag,
-                                         int poll_limit, float* row_stats, uint64_t* row_key,
-                                         bool want_key) {
+// Polls of one phase (LOCAL: the L2 copy, else the device-scope mirror) of
+// `set` (workgroup-uniform) until every chunk's slot carries `tag`, `it`
+// reaches poll_limit or the clock passes t0 + ticks; lane j < splits reads
+// slot j.  Returns whether every slot was seen.
+template <bool AM, bool LOCAL>
+__device__ __forceinline__ bool poll_phase(const uint64_t* set, int splits, uint32_t tag,
+                                           bool want_key, int& it, int poll_limit, uint64_t t0,
+                                           uint64_t ticks, float& mj, float& sj, uint64_t& kj) {
     constexpr int SW = AM ? 4 : 2;
+    const int lane = threadIdx.x & (kWave - 1);
+    const uint32_t off = static_cast<uint32_t>(lane) * (SW * 8);
+    for (; it < poll_limit; ++it) {
+        if (it > 0 && __builtin_amdgcn_s_memrealtime() - t0 > ticks) return false;
+        bool mine = true;
+        if (lane < splits) {
+            // chunk 0 alone writes the index, so only it reads the key words
+            uint64_t w[SW];
+            if (AM && want_key)
+                load_slot<LOCAL, SW>(set, off, w);
+            else
+                load_slot<LOCAL, 2>(set, off, reinterpret_cast<uint64_t(&)[2]>(w));
+            mine = static_cast<uint32_t>(w[0] >> 32) == tag && static_cast<uint32_t>(w[1] >> 32) == tag;
+            mj = __builtin_bit_cast(float, static_cast<uint32_t>(w[0]));
+            sj = __builtin_bit_cast(float, static_cast<uint32_t>(w[1]));
+            if constexpr (AM) {
+                if (want_key) {
+                    mine = mine && static_cast<uint32_t>(w[2] >> 32) == tag &&
+                           static_cast<uint32_t>(w[3] >> 32) == tag;
+                    kj = (w[2] << 32) | (w[3] & 0xffffffffu);
+                }
+            }
+        }
+        if (__all(mine)) return true;
+        __builtin_amdgcn_s_sleep(2);
+    }
+    return false;
+}
+
+template <bool AM>
+__device__ __forceinline__ void row_poll(const uint64_t* slots, int64_t mirror, bool local,
+                                         int splits, uint32_t tag, int poll_limit,
+                                         float* row_stats, uint64_t* row_key, bool want_key) {
     const int lane = threadIdx.x & (kWave - 1);
     float mj = -INFINITY, sj = 0.0f;
     uint64_t kj = 0;
-    bool all = false;
     const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
-    for (int it = 0; it < poll_limit && !all; ++it) {
-        if (it > 0 && __builtin_amdgcn_s_memrealtime() - t0 > kPollTicks) break;
-        bool mine = true;
-        if (lane < splits) {
-            const uint64_t* p = slots + SW * lane;
-            const uint64_t w0 = __hip_atomic_load(&p[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            const uint64_t w1 = __hip_atomic_load(&p[1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            mine = static_cast<uint32_t>(w0 >> 32) == tag && static_cast<uint32_t>(w1 >> 32) == tag;
-            mj = __builtin_bit_cast(float, static_cast<uint32_t>(w0));
-            sj = __builtin_bit_cast(float, static_cast<uint32_t>(w1));
-            if (AM && want_key) {
-                const uint64_t w2 = __hip_atomic_load(&p[2], __ATOMIC_RELAXED,
-                                                      __HIP_MEMORY_SCOPE_AGENT);
-                const uint64_t w3 = __hip_atomic_load(&p[3], __ATOMIC_RELAXED,
-                                                      __HIP_MEMORY_SCOPE_AGENT);
-                mine = mine && static_cast<uint32_t>(w2 >> 32) == tag &&
-                       static_cast<uint32_t>(w3 >> 32) == tag;
-                kj = (w2 << 32) | (w3 & 0xffffffffu);
-            }
-        }
-        all = __all(mine);
-        if (!all) __builtin_amdgcn_s_sleep(2);
-    }
+    int it = 0;
+    bool all = local && poll_phase<AM, true>(slots, splits, tag, want_key, it, poll_limit, t0,
+                                             kLocalPollTicks, mj, sj, kj);
+    if (!all)
+        all = poll_phase<AM, false>(slots + mirror, splits, tag, want_key, it, poll_limit, t0,
+                                    kPollTicks, mj, sj, kj);
     if (all) {
         if (lane >= splits) {
             mj = -INFINITY;
@@ -591,7 +621,8 @@ __global__ __launch_bounds__(256)
 __attribute__((amdgpu_waves_per_eu(AM ? 5 : 1))) void softmax_stream_kernel(const half_t* x, half_t* y,
                                                              unsigned char* ws, int64_t N,
                                                              int64_t D, int poll_limit,
-                                                             int32_t* out) {
+                                                             int32_t* out, int splits, int R,
+                                                             int local) {
     constexpr int64_t kChunk = 2048 * U;
     constexpr int SW = AM ? 4 : 2;
     __shared__ float slots[256 / kWave];
@@ -599,11 +630,16 @@ __attribute__((amdgpu_waves_per_eu(AM ? 5 : 1))) void softmax_stream_kernel(cons
     __shared__ uint64_t epoch_sh;
     __shared__ uint64_t kslots[AM ? 256 / kWave : 1];  // per-wave keys (AM)
     __shared__ uint64_t row_key;                        // the row's best key (AM)
-    const int split = blockIdx.x, splits = gridDim.x;
-    const int64_t r0 = blockIdx.y, R = gridDim.y;
+    // 1-D grid of splits x R (R a multiple of kXcds): a row slot's chunks
+    // share one XCD (row_exchange.h); slots past N-1 have no rows
+    int split, slot;
+    chunk_of(blockIdx.x, splits, split, slot);
+    const int64_t r0 = slot;
+    if (r0 >= N) return;  // workgroup-uniform, before any barrier
     unsigned char* rec = ws + r0 * record_bytes<AM>();
     uint64_t* epoch = reinterpret_cast<uint64_t*>(rec);
-    uint64_t* sets = reinterpret_cast<uint64_t*>(rec + 16);
+    uint64_t* sets = reinterpret_cast<uint64_t*>(rec + kRecordHeaderBytes);
+    constexpr int64_t kMirror = 2 * SW * kOnePassMaxSplits;  // words from a set to its mirror
     const int64_t K = (N - r0 + R - 1) / R;  // rounds of this row slot (>= 1)
     const int64_t b = split * kChunk;
     const int64_t e = b + kChunk < D ? b + kChunk : D;
@@ -638,13 +674,14 @@ __attribute__((amdgpu_waves_per_eu(AM ? 5 : 1))) void softmax_stream_kernel(cons
         const uint64_t E = epoch_sh;
         const uint32_t tag = static_cast<uint32_t>(E + 1 + k);
         uint64_t* set = sets + (k & 1) * (SW * kOnePassMaxSplits);
-        chunk_publish<AM>(set, split, tag, m, s, key);
+        chunk_publish<AM>(set, kMirror, split, tag, m, s, key);
         if (k + 1 < K) lane_load<U>(x + (row + R) * D, lo, ok, n);
         if (gave_up) {
             if (threadIdx.x == 0) row_stats[2] = 1.0f;
         } else if (threadIdx.x < kWave) {
             // only chunk 0 writes the index, so only it polls the key words
-            row_poll<AM>(set, splits, tag, poll_limit, row_stats, &row_key, split == 0);
+            row_poll<AM>(set, kMirror, local != 0, splits, tag, poll_limit, row_stats, &row_key,
+                         split == 0);
         }
         __syncthreads();
         float M = row_stats[0], S = row_stats[1];
@@ -783,6 +820,24 @@ int64_t onelaunch_rows(int64_t N, int64_t D, bool am = false) {
     return R;
 }
 
+// The one-launch grid: `splits` chunks per row, R row slots (a multiple of
+// kXcds, so that chunk_of keeps each slot's chunks on one XCD; slots past
+// N - 1 exit at once), 1-D.  `local`: whether polls start on the L2 copy.
+struct OneLaunchGrid {
+    int splits, R, local;
+    unsigned blocks() const { return static_cast<unsigned>(splits) * static_cast<unsigned>(R); }
+};
+OneLaunchGrid onelaunch_grid(int64_t N, int64_t D, bool am) {
+    OneLaunchGrid g;
+    g.splits = static_cast<int>(ceil_div(D, 2048 * onelaunch_u(N, D)));
+    const int64_t R = onelaunch_rows(N, D, am);
+    // round down to whole groups while that keeps every row slot resident,
+    // up (idle slots) when there are fewer than kXcds
+    g.R = static_cast<int>(R >= kXcds ? R / kXcds * kXcds : kXcds);
+    g.local = exchange_test_mode().load() == 0 ? 1 : 0;
+    return g;
+}
+
 // Whether [N, D] runs as the one-launch form given row records: a split or
 // kStream shape, aligned rows, y != x (the fallback re-reads x), at most 64
 // chunks per row.
@@ -846,15 +901,14 @@ int softmax_checked(const void* x, void* y, int64_t N, int64_t D, void* ws, int6
     }
     if (onelaunch) {
         const int u = onelaunch_u(N, D);
-        const dim3 g(static_cast<unsigned>(ceil_div(D, 2048 * u)),
-                     static_cast<unsigned>(onelaunch_rows(N, D)));
+        const OneLaunchGrid g = onelaunch_grid(N, D, false);
         auto* rec = static_cast<unsigned char*>(ws);
         if (u == kOnePassU)
-            softmax_stream_kernel<kOnePassU, false><<<g, dim3(256), 0, s>>>(
-                xh, yh, rec, N, D, g_poll_limit.load(), nullptr);
+            softmax_stream_kernel<kOnePassU, false><<<dim3(g.blocks()), dim3(256), 0, s>>>(
+                xh, yh, rec, N, D, g_poll_limit.load(), nullptr, g.splits, g.R, g.local);
         else
-            softmax_stream_kernel<kOnePassU / 2, false><<<g, dim3(256), 0, s>>>(
-                xh, yh, rec, N, D, g_poll_limit.load(), nullptr);
+            softmax_stream_kernel<kOnePassU / 2, false><<<dim3(g.blocks()), dim3(256), 0, s>>>(
+                xh, yh, rec, N, D, g_poll_limit.load(), nullptr, g.splits, g.R, g.local);
         return launch_status();
     }
     auto* part = reinterpret_cast<float*>(static_cast<unsigned char*>(ws) +
@@ -893,7 +947,7 @@ __global__ __launch_bounds__(256) void zero_kernel(uint4* p, int64_t n) {
 }  // namespace
 }  // namespace mi
 
-// 1,318,912 bytes per GPU, held from the library's load until the process
+// 2,424,832 bytes per GPU, held from the library's load until the process
 // ends.  Host code never passes this name to a kernel or a copy: it is a
 // host-side stand-in; the device address comes from hipGetSymbolAddress.
 static __device__ __align__(256) unsigned char scratch[mi::kScratchBytes];
@@ -994,16 +1048,16 @@ extern "C" int mi_softmax_argmax_ws_f16(const void* logits, void* probs, int32_t
     const hipStream_t s = mi::as_stream(stream);
     if (mi::onelaunch_ok(logits, probs, N, V, true)) {
         const int u = mi::onelaunch_u(N, V);
-        const dim3 g(static_cast<unsigned>(mi::ceil_div(V, 2048 * u)),
-                     static_cast<unsigned>(mi::onelaunch_rows(N, V, true)));
+        const mi::OneLaunchGrid g = mi::onelaunch_grid(N, V, true);
         const auto* xh = static_cast<const mi::half_t*>(logits);
         auto* yh = static_cast<mi::half_t*>(probs);
         if (u == mi::kOnePassU)
-            mi::softmax_stream_kernel<mi::kOnePassU, true><<<g, dim3(256), 0, s>>>(
-                xh, yh, ws, N, V, mi::g_poll_limit.load(), out);
+            mi::softmax_stream_kernel<mi::kOnePassU, true><<<dim3(g.blocks()), dim3(256), 0, s>>>(
+                xh, yh, ws, N, V, mi::g_poll_limit.load(), out, g.splits, g.R, g.local);
         else
-            mi::softmax_stream_kernel<mi::kOnePassU / 2, true><<<g, dim3(256), 0, s>>>(
-                xh, yh, ws, N, V, mi::g_poll_limit.load(), out);
+            mi::softmax_stream_kernel<mi::kOnePassU / 2, true>
+                <<<dim3(g.blocks()), dim3(256), 0, s>>>(xh, yh, ws, N, V, mi::g_poll_limit.load(),
+                                                        out, g.splits, g.R, g.local);
         return mi::launch_status();
     }
     // separately: argmax first (in place, softmax would overwrite the logits)

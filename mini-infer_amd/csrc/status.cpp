@@ -1,6 +1,8 @@
 // status.cpp -- status strings and ABI version of libmi_kernels.so.
 #include <hip/hip_runtime.h>
 
+#include <atomic>
+
 #include "mi_kernels.h"
 
 extern "C" const char* mi_status_string(int status) {
@@ -16,3 +18,17 @@ extern "C" const char* mi_status_string(int status) {
 }
 
 extern "C" int mi_abi_version(void) { return MI_KERNELS_ABI_VERSION; }
+
+// The one-launch kernels' exchange mode (row_exchange.h), read at each
+// launch; only the test hook below changes it.
+namespace mi {
+std::atomic<int>& exchange_test_mode() {
+    static std::atomic<int> mode{0};
+    return mode;
+}
+}  // namespace mi
+
+extern "C" int mi_exchange_test_mode(int mode) {
+    if (mode != 0 && mode != 1) return MI_ERR_INVALID_ARGUMENT;
+    return mi::exchange_test_mode().exchange(mode);
+}

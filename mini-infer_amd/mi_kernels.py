@@ -57,6 +57,7 @@ SIGNATURES = {
     "mi_greedy_argmax_ws_f16": [_c_void_p, _i64, _i64, _c_void_p, _c_void_p, _i64, _c_void_p],
     "mi_softmax_test_poll_limit": [_int],
     "mi_greedy_argmax_test_poll_limit": [_int],
+    "mi_exchange_test_mode": [_int],
     "mi_abi_version": [],
 }
 
@@ -435,6 +436,16 @@ def softmax_test_poll_limit(limit: int) -> int:
     prev = int(load_library().mi_softmax_test_poll_limit(int(limit)))
     if prev < 0:
         raise ValueError("limit must be >= 0")
+    return prev
+
+
+def exchange_test_mode(mode: int) -> int:
+    """Test hook: how the one-launch softmax / argmax / softmax + argmax
+    kernels read their row records -- 0 (default) the XCD-local L2 copy first,
+    then the device-scope mirror; 1 the mirror only.  Returns the previous mode."""
+    prev = int(load_library().mi_exchange_test_mode(int(mode)))
+    if prev < 0:
+        raise ValueError("mode must be 0 or 1")
     return prev
 
 

@@ -109,11 +109,12 @@ def test_product_path_has_no_oracle_dependency():
 def test_softmax_workspace_sizes(lib):
     lib.mi_softmax_workspace_bytes.argtypes = [ctypes.c_int64, ctypes.c_int64]
     lib.mi_softmax_workspace_bytes.restype = ctypes.c_int64
-    # Row records: 512 rows x 2064 B (16 B header, two sets of 64 slot pairs).
+    # Row records: 512 rows x 4224 B (128 B header, two sets of 64 slot pairs
+    # and their mirror).
     # 64 rows of 152064: the records, then for the two-launch form chunks of
     # one 4096-element tile (the whole number of tiles nearest 152064 / 32),
     # 38 per row, one (max, sum) pair each
-    rec = 512 * 2064
+    rec = 512 * 4224
     assert lib.mi_softmax_workspace_bytes(64, 152064) == rec + 64 * 38 * 8
     # 512 rows or more (256 or more up to 65536) longer than 32768: the
     # records only (persistent one-launch form; a workgroup per row when a
@@ -133,10 +134,11 @@ def test_softmax_workspace_sizes(lib):
 def test_argmax_workspace_sizes(lib):
     lib.mi_greedy_argmax_workspace_bytes.argtypes = [ctypes.c_int64, ctypes.c_int64]
     lib.mi_greedy_argmax_workspace_bytes.restype = ctypes.c_int64
-    # split rows: the one-launch records (512 rows x 1040 B), then one key per
+    # split rows: the one-launch records (512 rows x 2176 B: 128 B header, 64
+    # slots and their mirror), then one key per
     # chunk for the two-launch form (4096- or 2048-element chunks)
-    assert lib.mi_greedy_argmax_workspace_bytes(64, 152064) == 512 * 1040 + 64 * 38 * 8
-    assert lib.mi_greedy_argmax_workspace_bytes(1, 152064) == 512 * 1040 + 75 * 8
+    assert lib.mi_greedy_argmax_workspace_bytes(64, 152064) == 512 * 2176 + 64 * 38 * 8
+    assert lib.mi_greedy_argmax_workspace_bytes(1, 152064) == 512 * 2176 + 75 * 8
     assert lib.mi_greedy_argmax_workspace_bytes(512, 152064) == 0           # one workgroup per row
     assert lib.mi_greedy_argmax_workspace_bytes(64, 4096) == 0
-    assert 0 < lib.mi_greedy_argmax_workspace_bytes(511, 10**6) <= 512 * 1040 + 256 * 1024
+    assert 0 < lib.mi_greedy_argmax_workspace_bytes(511, 10**6) <= 512 * 2176 + 256 * 1024

@@ -1,0 +1,114 @@
+"""GPU: the one-launch kernels' row exchange (csrc/row_exchange.h).
+
+Softmax, greedy argmax and the fused softmax + argmax over split rows publish
+each chunk's partial result into the row's slots in the XCD's L2 and into a
+device-scope mirror; polls read the L2 copy first.  These tests check that:
+  * the mirror-only mode (mi_exchange_test_mode(1)), the path taken when the
+    L2 copy does not show every chunk, gives bit-identical results to the
+    default mode, on row counts that are and are not multiples of the XCD
+    count, one and several rounds per row slot, with a workspace shared
+    between the modes;
+  * results match the oracle in both modes;
+  * the default mode is served by the L2 copy: a call takes far less than
+    the L2 phase's 20 us bound (a launch that fell through to the mirror
+    would take at least that long).
+"""
+import numpy as np
+import pytest
+
+from helpers import assert_bits_equal, assert_close, normal_f16, to_dev, to_host
+
+pytestmark = pytest.mark.gpu
+
+
+def _case(msg):
+    print(f"[case] {msg}", flush=True)
+
+
+def _run_all(mk, xd, ws_sm, ws_am, ws_fused, N):
+    import torch
+    y = mk.softmax(xd, workspace=ws_sm)
+    idx = mk.greedy_argmax(xd, workspace=ws_am)
+    probs, out = mk.softmax_argmax(xd, ws_fused)
+    torch.cuda.synchronize()
+    return to_host(y), to_host(idx), to_host(probs), to_host(out)
+
+
+@pytest.mark.parametrize("N,D", [(64, 152064), (5, 152064), (13, 100000), (1, 40000),
+                                 (300, 40000), (600, 131072)])
+def test_mirror_mode_matches_default(mk, orc, dev, N, D):
+    import torch
+    _case(f"exchange modes [{N},{D}]")
+    rng = np.random.default_rng(N * 7 + D)
+    x = normal_f16(rng, (N, D), 0, 4)
+    xd = to_dev(x, dev)
+    ws_sm = torch.zeros(max(16, mk.softmax_workspace_bytes(N, D)), dtype=torch.uint8, device=dev)
+    ws_am = torch.zeros(max(16, mk.greedy_argmax_workspace_bytes(N, D)), dtype=torch.uint8,
+                        device=dev)
+    ws_fused = torch.zeros(mk.softmax_argmax_workspace_bytes(N, D), dtype=torch.uint8, device=dev)
+    base = _run_all(mk, xd, ws_sm, ws_am, ws_fused, N)
+    prev = mk.exchange_test_mode(1)
+    try:
+        assert prev == 0
+        mirror = _run_all(mk, xd, ws_sm, ws_am, ws_fused, N)
+    finally:
+        mk.exchange_test_mode(prev)
+    again = _run_all(mk, xd, ws_sm, ws_am, ws_fused, N)  # back on the L2 copy, same workspace
+    for name, a, b, c in zip(("softmax", "argmax", "fused probs", "fused argmax"), base, mirror,
+                             again):
+        assert_bits_equal(b, a, what=f"{name}: mirror vs default")
+        assert_bits_equal(c, a, what=f"{name}: default after mirror")
+    ref = orc.softmax(x, nthreads=8)
+    assert_close(base[0], ref, what="softmax vs oracle")
+    assert_bits_equal(base[2], base[0], what="fused probs vs softmax")
+    want = orc.greedy_argmax(x)
+    np.testing.assert_array_equal(base[1].astype(np.int64), want)
+    np.testing.assert_array_equal(base[3].astype(np.int64), want)
+
+
+def test_default_mode_is_served_by_l2(mk, dev):
+    """Average time per call of the one-launch softmax, argmax and fused pass
+    at [64, 152064], back-to-back launches replayed from a graph and timed
+    with events: all
+    well under the 20 us the L2 phase may last before polls move to the
+    mirror."""
+    import torch
+    _case("exchange: L2 phase serves the default mode")
+    N, D = 64, 152064
+    g = torch.Generator(device=dev)
+    g.manual_seed(3)
+    x = (torch.randn((N, D), generator=g, device=dev) * 4).half()
+    y = torch.empty_like(x)
+    out = torch.empty(N, dtype=torch.int32, device=dev)
+    ws_sm = torch.zeros(mk.softmax_workspace_bytes(N, D), dtype=torch.uint8, device=dev)
+    ws_am = torch.zeros(mk.greedy_argmax_workspace_bytes(N, D), dtype=torch.uint8, device=dev)
+    ws_fused = torch.zeros(mk.softmax_argmax_workspace_bytes(N, D), dtype=torch.uint8, device=dev)
+    calls = {
+        "softmax": lambda: mk.softmax(x, y=y, workspace=ws_sm),
+        "argmax": lambda: mk.greedy_argmax(x, out=out, workspace=ws_am),
+        "softmax+argmax": lambda: mk.softmax_argmax(x, ws_fused, probs=y, out=out),
+    }
+    for name, f in calls.items():
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for _ in range(5):
+                f()
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        n = 50
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for _ in range(n):
+                f()
+        graph.replay()
+        torch.cuda.synchronize()
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0.record()
+        graph.replay()
+        t1.record()
+        torch.cuda.synchronize()
+        del graph
+        us = t0.elapsed_time(t1) * 1e3 / n
+        print(f"[case]   {name}: {us:.1f} us per call", flush=True)
+        assert us < 16.0, f"{name}: {us:.1f} us per call (L2 exchange not taken?)"

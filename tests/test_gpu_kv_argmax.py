@@ -188,9 +188,9 @@ def test_greedy_argmax_onepass_epoch_past_32_bits(mk, orc, dev):
     _case("argmax one-pass epoch past 2^32")
     import torch
     rng = np.random.default_rng(59)
-    B, V, rec = 8, 40000, 1040 // 8
+    B, V, rec = 8, 40000, 2176 // 8  # 2176-byte row records
     ws = torch.zeros(mk.greedy_argmax_workspace_bytes(B, V), dtype=torch.uint8, device=dev)
-    e64 = ws[: 512 * 1040].view(torch.int64)
+    e64 = ws[: 512 * 2176].view(torch.int64)
     start = (1 << 32) - 3
     e64[0:B * rec:rec] = start
     for i in range(5):

@@ -251,9 +251,9 @@ def test_softmax_onepass_epoch_past_32_bits(mk, orc, dev):
     _case("softmax one-pass epoch past 2^32")
     import torch
     rng = np.random.default_rng(58)
-    N, D, rec = 8, 40000, 2064 // 8  # 2064-byte row records
+    N, D, rec = 8, 40000, 4224 // 8  # 4224-byte row records
     ws = torch.zeros(mk.softmax_workspace_bytes(N, D), dtype=torch.uint8, device=dev)
-    e64 = ws[: 512 * 2064].view(torch.int64)
+    e64 = ws[: 512 * 4224].view(torch.int64)
     start = (1 << 32) - 3
     e64[0:N * rec:rec] = start
     for i in range(5):
