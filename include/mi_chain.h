@@ -10,8 +10,11 @@
  *   gather (+ embed scale), copy,     -> mi_embedding_rmsnorm_f16: hidden and `normed`
  *   input_layernorm, copy                in one pass
  *   [QKV GEMMs]                       -> the caller's q, k, v
- *   copies, Q-norm, K-norm, 2x RoPE   -> mi_qk_norm_rope_f16 (or mi_rope_neox_qk_f16)
- *   2x launch_paged_kv_scatter        -> mi_paged_kv_scatter_kv_f16 per segment
+ *   (Qwen2: 3x launch_add_bias)          (folded into the next two steps)
+ *   copies, Q-norm, K-norm, 2x RoPE   -> mi_qk_norm_rope_f16 (or mi_rope_neox_qk_f16;
+ *                                        Qwen2: mi_bias_rope_neox_qk_f16)
+ *   2x launch_paged_kv_scatter        -> mi_paged_kv_scatter_kv_f16 per segment (Qwen2:
+ *                                        mi_paged_kv_scatter_kv_bias_f16, V's bias)
  *   [attention, O GEMM]               -> the caller's attn_out
  *   (Gemma 2/3: post_attn norm of attn_out, in place)
  *   add_inplace, copy, post-attn norm -> mi_fused_add_rmsnorm_f16
@@ -98,13 +101,21 @@ typedef struct mi_chain_desc {
     int32_t* next_tokens; /* [N] greedy argmax */
     void* sample_ws;    /* mi_softmax_argmax_workspace_bytes(N, V) bytes, zero before first use */
     int64_t sample_ws_bytes;
+    /* Qwen2 QKV projection bias (fp16, device): q_bias [Hq * hd], k_bias and
+     * v_bias [Hkv * hd]; all NULL for none, else all set.  q and k are biased
+     * in place with the rotation; v's bias is added on its way into the cache
+     * and v itself is left as it was (the reference's add_bias rewrites its
+     * v scratch buffer, which nothing reads after the scatter). */
+    const void* q_bias;
+    const void* k_bias;
+    const void* v_bias;
 } mi_chain_desc;
 
 /* Stages, in issue order; mi_decoder_chain_run stops after `last_stage`. */
 enum {
     MI_CHAIN_EMBED = 1,          /* hidden = gather(ids) (* sqrt(D)) */
     MI_CHAIN_INPUT_NORM = 2,     /* normed = rmsnorm(hidden) */
-    MI_CHAIN_QK_ROPE = 3,        /* q, k = rope(qk_norm(q, k)) in place */
+    MI_CHAIN_QK_ROPE = 3,        /* q, k = rope(qk_norm(q (+ bias), k (+ bias))) in place */
     MI_CHAIN_KV_SCATTER = 4,     /* k, v -> paged cache */
     MI_CHAIN_POST_ATTN_NORM = 5, /* hidden += attn_out; post_normed = rmsnorm(hidden) */
     MI_CHAIN_ACTIVATION = 6,     /* act_out = act(gate) * up */

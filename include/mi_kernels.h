@@ -100,6 +100,17 @@ int mi_rope_neox_qk_f16(void* q, void* k, const int64_t* positions,
                         const float* inv_freq_host, int64_t T, int64_t Hq,
                         int64_t Hkv, int64_t head_dim, void* stream);
 
+/* mi_rope_neox_qk_f16 with the QKV projection bias added first: q = rope(
+ * half(q + q_bias)), k = rope(half(k + k_bias)), in place; q_bias [Hq * hd],
+ * k_bias [Hkv * hd] (Qwen2's q_proj / k_proj bias).  Equals mi_add_bias_f16 on
+ * q and on k followed by mi_rope_neox_qk_f16, bit for bit, in one pass.
+ * Replaces the Qwen2 sequence at src/layers/attention.cpp:717-780 (two
+ * launch_add_bias calls, src/kernels/model_utils_kernel.cuh:9, two copies and
+ * two RoPE::forward_batched calls). */
+int mi_bias_rope_neox_qk_f16(void* q, void* k, const void* q_bias, const void* k_bias,
+                             const int64_t* positions, const float* inv_freq_host, int64_t T,
+                             int64_t Hq, int64_t Hkv, int64_t head_dim, void* stream);
+
 /* Fused per-head RMSNorm + NeoX RoPE, in place, for Q [T, Hq, hd] and
  * K [T, Hkv, hd]: each head is normalised with its weight (q_weight or
  * k_weight, [hd]; f(w) = w, or 1 + w when add_one), rounded to fp16, then
@@ -140,6 +151,14 @@ int mi_mul_inplace_f16(void* y, const void* x, int64_t n, void* stream);
 /* y = half(y * scale).  Replaces launch_scale_inplace
  * (src/kernels/model_utils_kernel.cuh:23). */
 int mi_scale_inplace_f16(void* y, float scale, int64_t n, void* stream);
+
+/* Broadcast bias add: y[b * batch_stride + m * N + n] = half(y[...] + bias[n])
+ * for b < batch_stride / (M * N), m < M, n < N (the QKV projections' bias).
+ * M == 0 does nothing; batch_stride < M * N is an argument error (the
+ * reference's grid would be empty).  Replaces launch_add_bias
+ * (src/kernels/model_utils_kernel.cuh:9, src/kernels/model_utils_kernel.cu:11-28). */
+int mi_add_bias_f16(void* y, const void* bias, int64_t M, int64_t N, int64_t batch_stride,
+                    void* stream);
 
 /* Row softmax, fp32 math: y = exp(x - max) / sum(exp(x - max)).
  * x, y: [N, D]; y may equal x.  Replaces launch_softmax
@@ -254,6 +273,19 @@ int mi_paged_kv_scatter_kv_f16(const void* k_src, const void* v_src, void* k_cac
                                const int* start_pos, int64_t B, int64_t S, int64_t layer,
                                int64_t num_blocks, int64_t H_kv, int64_t D, int64_t block_size,
                                int64_t max_blocks_per_seq, void* stream);
+
+/* mi_paged_kv_scatter_kv_f16 with a projection bias added on the way:
+ * the caches receive half(k + k_bias) and half(v + v_bias) (bias [H_kv * D];
+ * either may be NULL for none).  Equals mi_add_bias_f16 on k_src / v_src
+ * followed by the scatter, bit for bit, without writing the sources.
+ * Replaces Qwen2's launch_add_bias of V (src/layers/attention.cpp:735-739) and
+ * the two scatters (:823-846) with one launch. */
+int mi_paged_kv_scatter_kv_bias_f16(const void* k_src, const void* v_src, void* k_cache,
+                                    void* v_cache, const void* k_bias, const void* v_bias,
+                                    const int* block_table, const int* seq_len,
+                                    const int* start_pos, int64_t B, int64_t S, int64_t layer,
+                                    int64_t num_blocks, int64_t H_kv, int64_t D,
+                                    int64_t block_size, int64_t max_blocks_per_seq, void* stream);
 
 /* Greedy sampling: out[b] = argmax over logits[b, 0:V) (fp16 [B, V]; out int32
  * [B], DEVICE).  Ties resolve exactly as the reference's 256-thread kernel

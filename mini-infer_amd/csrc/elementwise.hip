@@ -13,6 +13,7 @@
 //   add    : y = half(y + x)   (src/kernels/model_utils_kernel.cu:31-35)
 //   mul    : y = half(y * x)   (:82-86)
 //   scale  : y = half(y * s)   (:68-72)
+//   bias   : y[b, m, n] = half(y[b, m, n] + bias[n])   (:11-20)
 //
 // Design (HBM-bound; 6 bytes/element for the binary ops, 4 for unary): each
 // 256-lane workgroup owns a contiguous tile of kUnroll x 256 16-byte vectors
@@ -130,8 +131,69 @@ int ew_launch(const void* av, const void* bv, void* outv, int64_t n, float scale
     return launch_status();
 }
 
+// Broadcast bias add over rows of N: one 16-byte vector per lane, the
+// batch on grid.y; bias vector = (vector index within the batch) mod (N / 8),
+// read through the caches (the bias is a few KB that every row re-reads).
+__global__ __launch_bounds__(kThreads) void bias_vec_kernel(half_t* y, const half_t* __restrict__ bias,
+                                                            uint32_t row_vec, int64_t batch_vec,
+                                                            int64_t batch_stride) {
+    const int64_t v = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+    if (v >= batch_vec) return;
+    half_t* p = y + static_cast<int64_t>(blockIdx.y) * batch_stride + v * 8;
+    const h8 a = ld8_stream(p);
+    const h8 b = ld8(bias + (static_cast<uint32_t>(v) % row_vec) * 8);
+    h8 o;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) o[k] = to_half((float)a[k] + (float)b[k]);
+    st8_stream(p, o);
+}
+
+__global__ __launch_bounds__(kThreads) void bias_scalar_kernel(half_t* y, const half_t* bias,
+                                                               int64_t N, int64_t batch_elems,
+                                                               int64_t batch_stride) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+    if (i >= batch_elems) return;
+    half_t* p = y + static_cast<int64_t>(blockIdx.y) * batch_stride + i;
+    *p = to_half((float)*p + (float)bias[i % N]);
+}
+
+// y [batches, M, N] (batches = batch_stride / (M * N), batch b at
+// b * batch_stride) += bias [N], broadcast over rows.
+int add_bias(void* yv, const void* biasv, int64_t M, int64_t N, int64_t batch_stride,
+             void* stream) {
+    if (M < 0 || N < 0 || batch_stride < 0) return MI_ERR_INVALID_ARGUMENT;
+    if (M == 0) return MI_OK;  // the reference returns before launching
+    if (N == 0 || !yv || !biasv) return MI_ERR_INVALID_ARGUMENT;
+    const int64_t per = M * N;
+    const int64_t batches = batch_stride / per;
+    if (batches < 1) return MI_ERR_INVALID_ARGUMENT;  // a grid with no batch: no launch
+    if (batches > 65535) return MI_ERR_UNSUPPORTED;   // grid.y
+    const int64_t span = (batches - 1) * batch_stride + per;
+    if (overlaps(biasv, N * 2, yv, span * 2)) return MI_ERR_ALIASING;
+    auto* y = static_cast<half_t*>(yv);
+    const auto* bias = static_cast<const half_t*>(biasv);
+    const hipStream_t s = as_stream(stream);
+    const bool vec = N % 8 == 0 && batch_stride % 8 == 0 && aligned16(y) && aligned16(bias) &&
+                     per / 8 <= 0xffffffffll;
+    const int64_t items = vec ? per / 8 : per;
+    const int64_t grid = ceil_div(items, kThreads);
+    if (grid > kMaxGridX) return MI_ERR_UNSUPPORTED;
+    const dim3 g(static_cast<unsigned>(grid), static_cast<unsigned>(batches));
+    if (vec)
+        bias_vec_kernel<<<g, dim3(kThreads), 0, s>>>(y, bias, static_cast<uint32_t>(N / 8), items,
+                                                     batch_stride);
+    else
+        bias_scalar_kernel<<<g, dim3(kThreads), 0, s>>>(y, bias, N, items, batch_stride);
+    return launch_status();
+}
+
 }  // namespace
 }  // namespace mi
+
+extern "C" int mi_add_bias_f16(void* y, const void* bias, int64_t M, int64_t N,
+                               int64_t batch_stride, void* stream) {
+    return mi::add_bias(y, bias, M, N, batch_stride, stream);
+}
 
 extern "C" int mi_swiglu_f16(const void* gate, const void* up, void* out, int64_t n,
                              void* stream) {

@@ -81,9 +81,26 @@ struct HVecKv<1> {
     __device__ static void store(half_t* p, T v) { *p = v; }
 };
 
+// half(x + b) per element; the bias is a few KB every token re-reads, so
+// plain loads.
+template <int VEC>
+__device__ __forceinline__ typename HVecKv<VEC>::T add_bias_vec(typename HVecKv<VEC>::T x,
+                                                              const half_t* b) {
+    if constexpr (VEC == 8) {
+        const h8 bv = ld8(b);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) x[k] = to_half((float)x[k] + (float)bv[k]);
+        return x;
+    } else {
+        return to_half((float)x + (float)*b);
+    }
+}
+
 // L lanes per token (64, or 32 / 16 / 8 when a token has that few vectors,
 // so a wave moves 2 / 4 / 8 tokens: one KV head of 128 is 16 vectors),
-// 256 / L tokens per workgroup.
+// 256 / L tokens per workgroup.  bias0 / bias1 ([H_kv * D], or null): a
+// projection bias added to each source element, rounded to fp16 as the
+// reference's launch_add_bias stores it (model_utils_kernel.cu:19).
 template <int VEC, int L>
 __global__ __launch_bounds__(256) void kv_scatter_kernel(const half_t* __restrict__ src0,
                                                          half_t* __restrict__ cache0,
@@ -92,7 +109,9 @@ __global__ __launch_bounds__(256) void kv_scatter_kernel(const half_t* __restric
                                                          const int* __restrict__ block_table,
                                                          const int* __restrict__ seq_len,
                                                          const int* __restrict__ start_pos,
-                                                         KvGeometry g) {
+                                                         KvGeometry g,
+                                                         const half_t* __restrict__ bias0,
+                                                         const half_t* __restrict__ bias1) {
     int tl = threadIdx.x / L;  // token within the workgroup
     if constexpr (L == kWave) tl = __builtin_amdgcn_readfirstlane(tl);  // wave-uniform
     const int lane = threadIdx.x & (L - 1);
@@ -135,6 +154,8 @@ __global__ __launch_bounds__(256) void kv_scatter_kernel(const half_t* __restric
             a0 = HVecKv<VEC>::load(s0 + v * VEC);
             if (s1) c0 = HVecKv<VEC>::load(s1 + v * VEC);
         }
+        if (bias0) a0 = add_bias_vec<VEC>(a0, bias0 + v * VEC);
+        if (bias1) c0 = add_bias_vec<VEC>(c0, bias1 + v * VEC);
         HVecKv<VEC>::store(cache0 + dst, a0);
         if (s1) HVecKv<VEC>::store(cache1 + dst, c0);
     }
@@ -143,7 +164,8 @@ __global__ __launch_bounds__(256) void kv_scatter_kernel(const half_t* __restric
 int kv_scatter(const void* src0, void* cache0, const void* src1, void* cache1,
                const int* block_table, const int* seq_len, const int* start_pos, int64_t B,
                int64_t S, int64_t layer, int64_t num_blocks, int64_t H_kv, int64_t D,
-               int64_t block_size, int64_t max_blocks_per_seq, void* stream) {
+               int64_t block_size, int64_t max_blocks_per_seq, void* stream,
+               const void* bias0v = nullptr, const void* bias1v = nullptr) {
     if (B < 0 || S < 0 || layer < 0 || num_blocks < 0 || H_kv < 0 || D < 0 || block_size <= 0 ||
         max_blocks_per_seq < 0)
         return MI_ERR_INVALID_ARGUMENT;
@@ -151,9 +173,11 @@ int kv_scatter(const void* src0, void* cache0, const void* src1, void* cache1,
         return MI_OK;
     if (!src0 || !cache0 || !block_table || !seq_len || !start_pos) return MI_ERR_INVALID_ARGUMENT;
     if ((src1 == nullptr) != (cache1 == nullptr)) return MI_ERR_INVALID_ARGUMENT;
+    if (bias1v && !src1) return MI_ERR_INVALID_ARGUMENT;
     const int64_t tokens = B * S;
     const bool vec = D % 8 == 0 && aligned16(src0) && aligned16(cache0) &&
-                     (!src1 || (aligned16(src1) && aligned16(cache1)));
+                     (!src1 || (aligned16(src1) && aligned16(cache1))) &&
+                     (!bias0v || aligned16(bias0v)) && (!bias1v || aligned16(bias1v));
     const int64_t nv = H_kv * D / (vec ? 8 : 1);  // vectors per token
     const int L = nv > 32 ? 64 : nv > 16 ? 32 : nv > 8 ? 16 : 8;
     const int64_t grid = ceil_div(tokens, 256 / L);
@@ -165,6 +189,13 @@ int kv_scatter(const void* src0, void* cache0, const void* src1, void* cache1,
     if (src1 && (overlaps(src1, src_bytes, cache1, cache_bytes) ||
                  overlaps(cache0, cache_bytes, cache1, cache_bytes)))
         return MI_ERR_ALIASING;
+    const int64_t bias_bytes = H_kv * D * 2;
+    for (const void* bz : {bias0v, bias1v})
+        if (bz && (overlaps(bz, bias_bytes, cache0, cache_bytes) ||
+                   (cache1 && overlaps(bz, bias_bytes, cache1, cache_bytes))))
+            return MI_ERR_ALIASING;
+    const auto* bias0 = static_cast<const half_t*>(bias0v);
+    const auto* bias1 = static_cast<const half_t*>(bias1v);
     const KvGeometry g{B, S, layer, num_blocks, H_kv, D, block_size, max_blocks_per_seq};
     const hipStream_t st = as_stream(stream);
     const auto* s0 = static_cast<const half_t*>(src0);
@@ -173,7 +204,8 @@ int kv_scatter(const void* src0, void* cache0, const void* src1, void* cache1,
     auto* c1 = static_cast<half_t*>(cache1);
     const dim3 gr(static_cast<unsigned>(grid)), b(256);
 #define MI_KV_CASE(V, LL)                                                                      \
-    kv_scatter_kernel<V, LL><<<gr, b, 0, st>>>(s0, c0, s1, c1, block_table, seq_len, start_pos, g)
+    kv_scatter_kernel<V, LL><<<gr, b, 0, st>>>(s0, c0, s1, c1, block_table, seq_len, start_pos, g, \
+                                               bias0, bias1)
     if (vec) {
         if (L == 64) MI_KV_CASE(8, 64);
         else if (L == 32) MI_KV_CASE(8, 32);
@@ -487,6 +519,20 @@ extern "C" int mi_paged_kv_scatter_kv_f16(const void* k_src, const void* v_src, 
     if (!v_src || !v_cache) return MI_ERR_INVALID_ARGUMENT;
     return mi::kv_scatter(k_src, k_cache, v_src, v_cache, block_table, seq_len, start_pos, B, S,
                           layer, num_blocks, H_kv, D, block_size, max_blocks_per_seq, stream);
+}
+
+extern "C" int mi_paged_kv_scatter_kv_bias_f16(const void* k_src, const void* v_src,
+                                               void* k_cache, void* v_cache, const void* k_bias,
+                                               const void* v_bias, const int* block_table,
+                                               const int* seq_len, const int* start_pos,
+                                               int64_t B, int64_t S, int64_t layer,
+                                               int64_t num_blocks, int64_t H_kv, int64_t D,
+                                               int64_t block_size, int64_t max_blocks_per_seq,
+                                               void* stream) {
+    if (!v_src || !v_cache) return MI_ERR_INVALID_ARGUMENT;
+    return mi::kv_scatter(k_src, k_cache, v_src, v_cache, block_table, seq_len, start_pos, B, S,
+                          layer, num_blocks, H_kv, D, block_size, max_blocks_per_seq, stream,
+                          k_bias, v_bias);
 }
 
 extern "C" int64_t mi_greedy_argmax_workspace_bytes(int64_t B, int64_t V) {

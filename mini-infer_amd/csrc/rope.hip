@@ -117,17 +117,22 @@ __device__ __forceinline__ void set_elem(typename HVec<VEC>::T& v, int k, float 
 // TPW tokens per 256-lane workgroup.  Sources q_in/k_in, destinations
 // q_out/k_out (may equal the sources).  FROM_POS: cos/sin from positions +
 // inv_freq, else from fp16 tables [T, half].  A unit is one (token, head,
-// VEC-element slice) pair: x[i..i+VEC) and x[h+i..h+i+VEC).
+// VEC-element slice) pair: x[i..i+VEC) and x[h+i..h+i+VEC).  BIAS: the
+// projection bias bq [Hq * hd] / bk [Hkv * hd] is added first, rounded to
+// fp16 as the reference's launch_add_bias stores it
+// (src/kernels/model_utils_kernel.cu:19), and the sum rotated.
 // (8 tokens: held to 128 VGPRs, 4 waves per SIMD; the compiler otherwise
 // settles at 130 and the residency drops to 3)
-template <int VEC, bool FROM_POS, int TPW>
+template <int VEC, bool FROM_POS, int TPW, bool BIAS = false>
 __global__ __launch_bounds__(256)
 __attribute__((amdgpu_waves_per_eu(TPW == 8 ? 4 : 1))) void rope_kernel(const half_t* q_in, half_t* q_out, int Hq,
                                                    const half_t* k_in, half_t* k_out, int Hkv,
                                                    const int64_t* __restrict__ positions,
                                                    const half_t* __restrict__ cos_t,
                                                    const half_t* __restrict__ sin_t, int64_t T,
-                                                   int hd, InvFreq inv) {
+                                                   int hd, InvFreq inv,
+                                                   const half_t* __restrict__ bq = nullptr,
+                                                   const half_t* __restrict__ bk = nullptr) {
     typedef HVec<VEC> V;
     __shared__ float cs[TPW][2 * kMaxHalf];
     const int64_t tok0 = static_cast<int64_t>(blockIdx.x) * TPW;
@@ -140,7 +145,7 @@ __attribute__((amdgpu_waves_per_eu(TPW == 8 ? 4 : 1))) void rope_kernel(const ha
     const float inv_upt = 1.0f / static_cast<float>(upt);
     const float inv_cph = 1.0f / static_cast<float>(cph);
     // units < 2^22 (checked at launch), so small_div is exact
-    auto locate = [&](int u, const half_t*& src, half_t*& dst) {
+    auto locate = [&](int u, const half_t*& src, half_t*& dst, const half_t** bias = nullptr) {
         const int t = small_div(u, inv_upt);
         const int rem = u - t * upt;
         const int h = small_div(rem, inv_cph);
@@ -150,10 +155,12 @@ __attribute__((amdgpu_waves_per_eu(TPW == 8 ? 4 : 1))) void rope_kernel(const ha
             const int64_t base = (tok * Hq + h) * static_cast<int64_t>(hd) + c * VEC;
             src = q_in + base;
             dst = q_out + base;
+            if (BIAS && bias) *bias = bq + h * hd + c * VEC;
         } else {
             const int64_t base = (tok * Hkv + (h - Hq)) * static_cast<int64_t>(hd) + c * VEC;
             src = k_in + base;
             dst = k_out + base;
+            if (BIAS && bias) *bias = bk + (h - Hq) * hd + c * VEC;
         }
         // offset of this unit's first cos entry in cs (quad_split layout for VEC = 8)
         return t * (2 * kMaxHalf) + (VEC == 8 ? c * 4 : c * VEC);
@@ -162,19 +169,25 @@ __attribute__((amdgpu_waves_per_eu(TPW == 8 ? 4 : 1))) void rope_kernel(const ha
     // 1. issue up to TPW units' loads per lane before the table work,
     //    so HBM latency overlaps the sincos evaluation
     typename V::T x1[TPW], x2[TPW];
+    typename V::T b1[BIAS ? TPW : 1], b2[BIAS ? TPW : 1];  // bias slices (BIAS)
 #pragma unroll
     for (int p = 0; p < TPW; ++p) {
         const int u = threadIdx.x + p * 256;
         if (u < units) {
             const half_t* src;
             half_t* dst;
-            locate(u, src, dst);
+            const half_t* bp = nullptr;
+            locate(u, src, dst, &bp);
             if constexpr (VEC == 8) {
                 x1[p] = ld8_stream(src);
                 x2[p] = ld8_stream(src + half);
             } else {
                 x1[p] = V::load(src);
                 x2[p] = V::load(src + half);
+            }
+            if constexpr (BIAS) {  // a few KB every token re-reads: plain loads
+                b1[p] = V::load(bp);
+                b2[p] = V::load(bp + half);
             }
         }
     }
@@ -200,7 +213,8 @@ __attribute__((amdgpu_waves_per_eu(TPW == 8 ? 4 : 1))) void rope_kernel(const ha
 
     // 3. rotate: y1 = x1 c - x2 s, y2 = x2 c + x1 s
     const float* csf = &cs[0][0];
-    auto rotate = [&](int u, const typename V::T& a1, const typename V::T& a2) {
+    auto rotate = [&](int u, const typename V::T& a1, const typename V::T& a2,
+                      const typename V::T* c1, const typename V::T* c2) {
         const half_t* src;
         half_t* dst;
         const int off = locate(u, src, dst);
@@ -211,7 +225,11 @@ __attribute__((amdgpu_waves_per_eu(TPW == 8 ? 4 : 1))) void rope_kernel(const ha
             const int kk = (VEC == 8 && (k & 4)) ? ((half >> 3) << 2) + (k & 3) : k;
             const float cv = csf[off + kk];
             const float sv = csf[off + kMaxHalf + kk];
-            const float a = elem<VEC>(a1, k), b = elem<VEC>(a2, k);
+            float a = elem<VEC>(a1, k), b = elem<VEC>(a2, k);
+            if constexpr (BIAS) {
+                a = (float)to_half(a + elem<VEC>(*c1, k));
+                b = (float)to_half(b + elem<VEC>(*c2, k));
+            }
             set_elem<VEC>(y1, k, fp32_rounded(a * cv - b * sv));
             set_elem<VEC>(y2, k, fp32_rounded(b * cv + a * sv));
         }
@@ -226,13 +244,19 @@ __attribute__((amdgpu_waves_per_eu(TPW == 8 ? 4 : 1))) void rope_kernel(const ha
 #pragma unroll
     for (int p = 0; p < TPW; ++p) {
         const int u = threadIdx.x + p * 256;
-        if (u < units) rotate(u, x1[p], x2[p]);
+        if (u < units) rotate(u, x1[p], x2[p], &b1[BIAS ? p : 0], &b2[BIAS ? p : 0]);
     }
     for (int u = threadIdx.x + TPW * 256; u < units; u += 256) {
         const half_t* src;
         half_t* dst;
-        locate(u, src, dst);
-        rotate(u, V::load(src), V::load(src + half));
+        const half_t* bp = nullptr;
+        locate(u, src, dst, &bp);
+        typename V::T c1{}, c2{};
+        if constexpr (BIAS) {
+            c1 = V::load(bp);
+            c2 = V::load(bp + half);
+        }
+        rotate(u, V::load(src), V::load(src + half), &c1, &c2);
     }
 }
 
@@ -574,10 +598,11 @@ int pick_tokens_per_wg(int64_t T, K1 k1, K2 k2, K4 k4, K8 k8) {
     return best;
 }
 
-template <int VEC, bool FROM_POS>
+template <int VEC, bool FROM_POS, bool BIAS = false>
 int launch_rope_t(const half_t* q_in, half_t* q_out, int hq, const half_t* k_in, half_t* k_out,
                   int hk, const int64_t* positions, const half_t* cos_t, const half_t* sin_t,
-                  int64_t T, int d, const InvFreq& inv, hipStream_t s) {
+                  int64_t T, int d, const InvFreq& inv, hipStream_t s,
+                  const half_t* bq = nullptr, const half_t* bk = nullptr) {
     const int tpw = fill_tokens_per_wg((hq + hk) * (d / 2 / VEC));
     const int64_t grid = ceil_div(T, tpw);
     if (grid > kMaxGridX) return MI_ERR_UNSUPPORTED;
@@ -587,8 +612,9 @@ int launch_rope_t(const half_t* q_in, half_t* q_out, int hq, const half_t* k_in,
     switch (tpw) {
 #define MI_ROPE_CASE(P)                                                                        \
     case P:                                                                                    \
-        rope_kernel<VEC, FROM_POS, P><<<g, b, 0, s>>>(q_in, q_out, hq, k_in, k_out, hk,        \
-                                                      positions, cos_t, sin_t, T, d, inv);     \
+        rope_kernel<VEC, FROM_POS, P, BIAS><<<g, b, 0, s>>>(q_in, q_out, hq, k_in, k_out, hk,  \
+                                                            positions, cos_t, sin_t, T, d, inv, \
+                                                            bq, bk);                            \
         break;
         MI_ROPE_CASE(1)
         MI_ROPE_CASE(2)
@@ -602,11 +628,20 @@ int launch_rope_t(const half_t* q_in, half_t* q_out, int hq, const half_t* k_in,
 
 int launch_rope(const half_t* q_in, half_t* q_out, int64_t Hq, const half_t* k_in, half_t* k_out,
                 int64_t Hkv, const int64_t* positions, const half_t* cos_t, const half_t* sin_t,
-                int64_t T, int64_t hd, const InvFreq& inv, hipStream_t s) {
+                int64_t T, int64_t hd, const InvFreq& inv, hipStream_t s,
+                const half_t* bq = nullptr, const half_t* bk = nullptr) {
     const int64_t half = hd / 2;
     bool vec = (half % 8 == 0) && aligned16(q_in) && aligned16(q_out);
     if (Hkv > 0) vec = vec && aligned16(k_in) && aligned16(k_out);
     const int hq = static_cast<int>(Hq), hk = static_cast<int>(Hkv), d = static_cast<int>(hd);
+    if (bq) {  // positions, in place, with the projection bias
+        vec = vec && aligned16(bq) && (Hkv == 0 || aligned16(bk));
+        if (vec)
+            return launch_rope_t<8, true, true>(q_in, q_out, hq, k_in, k_out, hk, positions,
+                                                nullptr, nullptr, T, d, inv, s, bq, bk);
+        return launch_rope_t<1, true, true>(q_in, q_out, hq, k_in, k_out, hk, positions, nullptr,
+                                            nullptr, T, d, inv, s, bq, bk);
+    }
     if (positions) {
         if (vec)
             return launch_rope_t<8, true>(q_in, q_out, hq, k_in, k_out, hk, positions, nullptr,
@@ -772,6 +807,39 @@ extern "C" int mi_rope_neox_qk_f16(void* q, void* k, const int64_t* positions,
                            static_cast<const half_t*>(k), static_cast<half_t*>(k), Hkv,
                            positions, nullptr, nullptr, T, head_dim, inv,
                            mi::as_stream(stream));
+}
+
+extern "C" int mi_bias_rope_neox_qk_f16(void* q, void* k, const void* q_bias, const void* k_bias,
+                                        const int64_t* positions, const float* inv_freq_host,
+                                        int64_t T, int64_t Hq, int64_t Hkv, int64_t head_dim,
+                                        void* stream) {
+    if (T < 0 || Hq < 0 || Hkv < 0 || head_dim < 0) return MI_ERR_INVALID_ARGUMENT;
+    if (T == 0 || Hq + Hkv == 0) return MI_OK;
+    if (!positions || (Hq > 0 && (!q || !q_bias)) || (Hkv > 0 && (!k || !k_bias)))
+        return MI_ERR_INVALID_ARGUMENT;
+    if (!mi::heads_ok(Hq, Hkv, head_dim)) return MI_ERR_UNSUPPORTED;
+    const int64_t qb = T * Hq * head_dim * 2, kb = T * Hkv * head_dim * 2;
+    if (Hq > 0 && Hkv > 0 && mi::overlaps(q, qb, k, kb)) return MI_ERR_ALIASING;
+    if ((Hq > 0 && (mi::overlaps(q_bias, Hq * head_dim * 2, q, qb) ||
+                    (Hkv > 0 && mi::overlaps(q_bias, Hq * head_dim * 2, k, kb)))) ||
+        (Hkv > 0 && (mi::overlaps(k_bias, Hkv * head_dim * 2, k, kb) ||
+                     (Hq > 0 && mi::overlaps(k_bias, Hkv * head_dim * 2, q, qb)))))
+        return MI_ERR_ALIASING;
+    mi::InvFreq inv;
+    if (!mi::load_inv_freq(inv_freq_host, head_dim / 2, inv)) return MI_ERR_INVALID_ARGUMENT;
+    // With no Q heads, run K through the Q slot (the kernel has one code path).
+    if (Hq == 0) {
+        q = k;
+        q_bias = k_bias;
+        Hq = Hkv;
+        k = nullptr;
+        k_bias = nullptr;
+        Hkv = 0;
+    }
+    return mi::launch_rope(static_cast<const half_t*>(q), static_cast<half_t*>(q), Hq,
+                           static_cast<const half_t*>(k), static_cast<half_t*>(k), Hkv,
+                           positions, nullptr, nullptr, T, head_dim, inv, mi::as_stream(stream),
+                           static_cast<const half_t*>(q_bias), static_cast<const half_t*>(k_bias));
 }
 
 extern "C" int mi_qk_norm_rope_f16(void* q, void* k, const void* q_weight, const void* k_weight,

@@ -152,6 +152,14 @@ void launch_rope_qk(__half* q, __half* k, const int64_t* positions_d, const floa
           "launch_rope_qk");
 }
 
+void launch_bias_rope_qk(__half* q, __half* k, const __half* q_bias, const __half* k_bias,
+                         const int64_t* positions_d, const float* inv_freq_h, int T, int Hq,
+                         int Hkv, int head_dim, hipStream_t stream) {
+    check(mi_bias_rope_neox_qk_f16(q, k, q_bias, k_bias, positions_d, inv_freq_h, T, Hq, Hkv,
+                                   head_dim, sv(stream)),
+          "launch_bias_rope_qk");
+}
+
 void launch_qk_norm_rope(__half* q, __half* k, const __half* q_weight, const __half* k_weight,
                          const int64_t* positions_d, const float* inv_freq_h, int T, int Hq,
                          int Hkv, int head_dim, float eps, int add_one, hipStream_t stream) {
@@ -175,6 +183,11 @@ void launch_geglu(const __half* gate, const __half* up, __half* out, int64_t n,
 
 void launch_softmax(const __half* x, __half* y, int N, int D, hipStream_t stream) {
     check(mi_softmax_f16(x, y, N, D, sv(stream)), "launch_softmax");
+}
+
+void launch_add_bias(__half* y, const __half* bias, int M, int N, int batch_stride,
+                     hipStream_t stream) {
+    check(mi_add_bias_f16(y, bias, M, N, batch_stride, sv(stream)), "launch_add_bias");
 }
 
 void launch_add_inplace(__half* y, const __half* x, int64_t n, hipStream_t s) {
@@ -214,6 +227,19 @@ void launch_paged_kv_scatter_kv(const __half* k_src, const __half* v_src, __half
                                      start_pos, B, S, layer, num_blocks, H_kv, D, block_size,
                                      max_blocks_per_seq, sv(stream)),
           "launch_paged_kv_scatter_kv");
+}
+
+void launch_paged_kv_scatter_kv_bias(const __half* k_src, const __half* v_src, __half* k_cache,
+                                     __half* v_cache, const __half* k_bias, const __half* v_bias,
+                                     const int* block_table, const int* seq_len,
+                                     const int* start_pos, int B, int S, int layer,
+                                     int num_blocks, int H_kv, int D, int block_size,
+                                     int max_blocks_per_seq, hipStream_t stream) {
+    check(mi_paged_kv_scatter_kv_bias_f16(k_src, v_src, k_cache, v_cache, k_bias, v_bias,
+                                          block_table, seq_len, start_pos, B, S, layer,
+                                          num_blocks, H_kv, D, block_size, max_blocks_per_seq,
+                                          sv(stream)),
+          "launch_paged_kv_scatter_kv_bias");
 }
 
 void launch_greedy_sample(const __half* logits, int vocab, int* out, hipStream_t stream) {

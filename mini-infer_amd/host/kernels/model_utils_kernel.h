@@ -1,7 +1,5 @@
 // model_utils_kernel.h -- the model-chain utility launchers on the hot path,
-// with the reference's signatures (src/kernels/model_utils_kernel.cuh:12-67).
-// launch_add_bias belongs to the QKV projection and is not part of this
-// library.
+// with the reference's signatures (src/kernels/model_utils_kernel.cuh:9-67).
 #pragma once
 
 #include <cstdint>
@@ -11,6 +9,11 @@
 
 namespace mini_infer {
 namespace kernels {
+
+// y[b * batch_stride + m * N + n] = half(y[...] + bias[n]) for
+// b < batch_stride / (M * N): the QKV projections' bias, broadcast over rows.
+void launch_add_bias(__half* y, const __half* bias, int M, int N, int batch_stride,
+                     hipStream_t stream);
 
 // y[i] = half(y[i] + x[i])
 void launch_add_inplace(__half* y, const __half* x, int64_t n, hipStream_t s);
@@ -42,6 +45,16 @@ void launch_paged_kv_scatter_kv(const __half* k_src, const __half* v_src, __half
                                 const int* start_pos, int B, int S, int layer, int num_blocks,
                                 int H_kv, int D, int block_size, int max_blocks_per_seq,
                                 hipStream_t stream);
+
+// launch_paged_kv_scatter_kv with a projection bias added on the way: the
+// caches receive half(k + k_bias), half(v + v_bias) (bias [H_kv * D], either
+// may be null).  Replaces Qwen2's launch_add_bias of V and the two scatters.
+void launch_paged_kv_scatter_kv_bias(const __half* k_src, const __half* v_src, __half* k_cache,
+                                     __half* v_cache, const __half* k_bias, const __half* v_bias,
+                                     const int* block_table, const int* seq_len,
+                                     const int* start_pos, int B, int S, int layer,
+                                     int num_blocks, int H_kv, int D, int block_size,
+                                     int max_blocks_per_seq, hipStream_t stream);
 
 }  // namespace kernels
 }  // namespace mini_infer

@@ -31,6 +31,13 @@ void launch_rope_precompute_batched(const float* inv_freq_h, const int64_t* posi
 void launch_rope_qk(__half* q, __half* k, const int64_t* positions_d, const float* inv_freq_h,
                     int T, int Hq, int Hkv, int head_dim, hipStream_t stream);
 
+// launch_rope_qk with the QKV projection bias added first (Qwen2):
+// q = rope(half(q + q_bias)), k = rope(half(k + k_bias)); q_bias [Hq * hd],
+// k_bias [Hkv * hd].  Replaces two launch_add_bias calls and the RoPE pair.
+void launch_bias_rope_qk(__half* q, __half* k, const __half* q_bias, const __half* k_bias,
+                         const int64_t* positions_d, const float* inv_freq_h, int T, int Hq,
+                         int Hkv, int head_dim, hipStream_t stream);
+
 // In place: per-head RMSNorm of q / k with q_weight / k_weight [head_dim]
 // (f(w) = w, or 1 + w when add_one), rounded to fp16, then the NeoX rotation
 // of launch_rope_qk -- the Q/K-norm + RoPE sequence in one pass.

@@ -57,6 +57,9 @@ void DecoderChain::validate_() const {
     const int L = last_;
     need(d.ids && d.embed && d.hidden, "embed stage needs ids, embed, hidden");
     if (L >= MI_CHAIN_INPUT_NORM) need(d.input_norm && d.normed, "input norm needs input_norm, normed");
+    const bool bias = d.q_bias || d.k_bias || d.v_bias;
+    need(!bias || ((d.num_heads == 0 || d.q_bias) && (d.num_kv_heads == 0 || (d.k_bias && d.v_bias))),
+         "qkv bias: set q_bias, k_bias and v_bias together");
     if (L >= MI_CHAIN_QK_ROPE) {
         need(d.positions && (d.num_heads == 0 || d.q) && (d.num_kv_heads == 0 || d.k),
              "rope needs positions, q, k");
@@ -120,9 +123,23 @@ void DecoderChain::run(hipStream_t s, DecoderChainHooks* hooks) const {
     if (last_ == MI_CHAIN_INPUT_NORM) return;
 
     // 3. QKV GEMMs, then Q/K-norm + RoPE in one in-place pass
-    //    (attention.cpp:743-780: two copies, two norms, two RoPE forwards)
+    //    (attention.cpp:717-780: Qwen2's bias adds, two copies, two norms,
+    //    two RoPE forwards); with the bias and no Q/K norm (Qwen2) the bias
+    //    add rides in the rotation pass
     h.qkv(d, s);
-    if (d.use_qk_norm)
+    const bool bias = d.q_bias != nullptr || d.k_bias != nullptr;
+    if (bias && d.use_qk_norm) {  // bias, then norm: no model has both; kept unfused
+        const int64_t qn = d.num_heads * d.head_dim, kn = d.num_kv_heads * d.head_dim;
+        if (d.num_heads > 0)
+            check(mi_add_bias_f16(d.q, d.q_bias, T, qn, T * qn, sv(s)), "q bias");
+        if (d.num_kv_heads > 0)
+            check(mi_add_bias_f16(d.k, d.k_bias, T, kn, T * kn, sv(s)), "k bias");
+    }
+    if (bias && !d.use_qk_norm)
+        check(mi_bias_rope_neox_qk_f16(d.q, d.k, d.q_bias, d.k_bias, d.positions, inv_freq_.data(),
+                                       T, d.num_heads, d.num_kv_heads, d.head_dim, sv(s)),
+              "bias + rope");
+    else if (d.use_qk_norm)
         check(mi_qk_norm_rope_f16(d.q, d.k, d.q_norm, d.k_norm, d.positions, inv_freq_.data(), T,
                                   d.num_heads, d.num_kv_heads, d.head_dim, d.qk_norm_eps,
                                   /*add_one=*/0, sv(s)),
@@ -134,17 +151,26 @@ void DecoderChain::run(hipStream_t s, DecoderChainHooks* hooks) const {
     if (last_ == MI_CHAIN_QK_ROPE) return;
 
     // 4. K and V into the paged cache, one launch per segment
-    //    (attention.cpp:819-846: one scatter for K, one for V)
+    //    (attention.cpp:819-846: one scatter for K, one for V; Qwen2's V bias
+    //    added on the way, attention.cpp:735-739)
     const int64_t kv_row = d.num_kv_heads * d.head_dim;
     for (const mi_chain_kv_segment& g : segs_) {
         if (g.B * g.S == 0) continue;
         const auto* ks = static_cast<const uint16_t*>(d.k) + g.token_offset * kv_row;
         const auto* vs = static_cast<const uint16_t*>(d.v) + g.token_offset * kv_row;
-        check(mi_paged_kv_scatter_kv_f16(ks, vs, d.k_cache, d.v_cache, g.block_table, g.seq_len,
-                                         g.start_pos, g.B, g.S, d.layer, d.num_blocks,
-                                         d.num_kv_heads, d.head_dim, d.block_size,
-                                         g.max_blocks_per_seq, sv(s)),
-              "kv scatter");
+        if (d.v_bias)
+            check(mi_paged_kv_scatter_kv_bias_f16(ks, vs, d.k_cache, d.v_cache, nullptr, d.v_bias,
+                                                  g.block_table, g.seq_len, g.start_pos, g.B, g.S,
+                                                  d.layer, d.num_blocks, d.num_kv_heads,
+                                                  d.head_dim, d.block_size, g.max_blocks_per_seq,
+                                                  sv(s)),
+                  "kv scatter + v bias");
+        else
+            check(mi_paged_kv_scatter_kv_f16(ks, vs, d.k_cache, d.v_cache, g.block_table,
+                                             g.seq_len, g.start_pos, g.B, g.S, d.layer,
+                                             d.num_blocks, d.num_kv_heads, d.head_dim,
+                                             d.block_size, g.max_blocks_per_seq, sv(s)),
+                  "kv scatter");
     }
     if (last_ == MI_CHAIN_KV_SCATTER) return;
 

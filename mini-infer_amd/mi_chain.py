@@ -38,6 +38,7 @@ class KvSegment(ctypes.Structure):
 
 _PTRS = ["embed", "input_norm", "post_attn_norm", "pre_ff_norm", "post_ff_norm", "final_norm",
          "q_norm", "k_norm", "ids", "positions"]
+_BIAS = ["q_bias", "k_bias", "v_bias"]
 _BUFS = ["hidden", "normed", "q", "k", "v", "k_cache", "v_cache", "attn_out", "post_normed",
          "gate", "up", "act_out", "mlp_out", "final_normed", "logits", "probs", "next_tokens"]
 
@@ -52,7 +53,8 @@ class ChainDesc(ctypes.Structure):
                 + [(n, _vp) for n in _PTRS]
                 + [("num_kv_segments", _int), ("kv_segments", ctypes.POINTER(KvSegment))]
                 + [(n, _vp) for n in _BUFS]
-                + [("sample_ws", _vp), ("sample_ws_bytes", _i64)])
+                + [("sample_ws", _vp), ("sample_ws_bytes", _i64)]
+                + [(n, _vp) for n in _BIAS])
 
 
 _lib = None
@@ -83,7 +85,7 @@ def make_desc(shapes: dict, tensors: dict, segments) -> tuple:
     for name, _ in ChainDesc._fields_:
         if name in shapes:
             setattr(d, name, shapes[name])
-    for name in _PTRS + _BUFS + ["sample_ws"]:
+    for name in _PTRS + _BUFS + ["sample_ws"] + _BIAS:
         t = tensors.get(name)
         setattr(d, name, t.data_ptr() if t is not None else None)
     t = tensors.get("sample_ws")
@@ -118,7 +120,8 @@ def run(desc: ChainDesc, last_stage: int = Stage.SAMPLE, stream=None) -> None:
 
 QWEN25_7B = dict(hidden_size=3584, intermediate_size=18944, num_heads=28, num_kv_heads=4,
                  head_dim=128, vocab=152064, rms_eps=1e-6, qk_norm_eps=1e-6, rope_theta=1e6,
-                 norm_add_one=0, use_qk_norm=1, embed_scale=0, double_norm=0, act=0)
+                 norm_add_one=0, use_qk_norm=1, embed_scale=0, double_norm=0, act=0,
+                 qkv_bias=0)
 
 
 def batch_layout(rng, n_decode, prefills, max_start=28000, block_size=16):
@@ -168,7 +171,7 @@ class Workload:
 
     INPUTS = ("ids", "positions", "embed", "input_norm", "post_attn_norm", "pre_ff_norm",
               "post_ff_norm", "final_norm", "q_norm", "k_norm", "q", "k", "v", "attn_out",
-              "gate", "up", "mlp_out", "logits")
+              "gate", "up", "mlp_out", "logits", "q_bias", "k_bias", "v_bias")
 
     def __init__(self, dev, seed=0, n_decode=64, prefills=(3000, 3000), logit_rows=64,
                  num_layers=2, layer=1, block_size=16, host=True, **overrides):
@@ -195,6 +198,9 @@ class Workload:
             "gate": ((T, I), 0.0, 1.0), "up": ((T, I), 0.0, 1.0), "mlp_out": ((T, D), 0.0, 1.0),
             "logits": ((logit_rows, V), 0.0, 4.0),
         }
+        if cfg["qkv_bias"]:  # Qwen2 q/k/v_proj bias
+            spec.update({"q_bias": ((Hq * hd,), 0.0, 0.5), "k_bias": ((Hkv * hd,), 0.0, 0.5),
+                         "v_bias": ((Hkv * hd,), 0.0, 0.5)})
         self.host = {}
         t = {}
         ids = rng.integers(0, V, T).astype(np.int64)

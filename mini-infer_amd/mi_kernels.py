@@ -43,6 +43,9 @@ SIGNATURES = {
     "mi_add_inplace_f16": [_c_void_p, _c_void_p, _i64, _c_void_p],
     "mi_mul_inplace_f16": [_c_void_p, _c_void_p, _i64, _c_void_p],
     "mi_scale_inplace_f16": [_c_void_p, _f32, _i64, _c_void_p],
+    "mi_add_bias_f16": [_c_void_p, _c_void_p, _i64, _i64, _i64, _c_void_p],
+    "mi_bias_rope_neox_qk_f16": [_c_void_p] * 5 + [_c_void_p, _i64, _i64, _i64, _i64, _c_void_p],
+    "mi_paged_kv_scatter_kv_bias_f16": [_c_void_p] * 9 + [_i64] * 8 + [_c_void_p],
     "mi_softmax_f16": [_c_void_p, _c_void_p, _i64, _i64, _c_void_p],
     "mi_embedding_gather_f16": [_c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64, _c_void_p],
     "mi_embedding_rmsnorm_f16": [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64,
@@ -254,6 +257,37 @@ def rope_neox_qk(q, k, positions, inv_freq, stream=None):
     return q, k
 
 
+def bias_rope_neox_qk(q, k, q_bias, k_bias, positions, inv_freq, stream=None):
+    """In place: q = rope(half(q + q_bias)), k = rope(half(k + k_bias)) for
+    q [T, Hq, hd], k [T, Hkv, hd] (k may be None), biases [Hq * hd] / [Hkv * hd]."""
+    torch = _torch()
+    _need(q, _f16(), "q"); _need(q_bias, _f16(), "q_bias"); _need(positions, torch.int64, "positions")
+    if q.dim() != 3:
+        raise ValueError("q must be 3-D [T, Hq, hd]")
+    T, Hq, hd = q.shape
+    if q_bias.numel() != Hq * hd:
+        raise ValueError("q_bias must hold Hq * hd entries")
+    Hkv = 0
+    if k is not None:
+        _need(k, _f16(), "k"); _need(k_bias, _f16(), "k_bias")
+        if k.dim() != 3 or k.shape[0] != T or k.shape[2] != hd:
+            raise ValueError("k must be [T, Hkv, hd]")
+        Hkv = k.shape[1]
+        if k_bias.numel() != Hkv * hd:
+            raise ValueError("k_bias must hold Hkv * hd entries")
+    if positions.numel() != T:
+        raise ValueError("positions must hold T entries")
+    arr, p = _inv_freq_buffer(inv_freq)
+    if arr.size != hd // 2:
+        raise ValueError("inv_freq must hold head_dim/2 entries")
+    null = ctypes.c_void_p(0)
+    _check(load_library().mi_bias_rope_neox_qk_f16(
+        _ptr(q), _ptr(k) if k is not None else null, _ptr(q_bias),
+        _ptr(k_bias) if k is not None else null, _ptr(positions), p, T, Hq, Hkv, hd,
+        _stream(stream)), "mi_bias_rope_neox_qk_f16")
+    return q, k
+
+
 def qk_norm_rope(q, k, q_weight, k_weight, positions, inv_freq, eps: float = 1e-6,
                  add_one: bool = False, stream=None):
     """In place: per-head RMSNorm of q [T, Hq, hd] / k [T, Hkv, hd] (k may be
@@ -330,6 +364,21 @@ def add_inplace(y, x, stream=None):
         raise ValueError("size mismatch")
     _check(load_library().mi_add_inplace_f16(_ptr(y), _ptr(x), y.numel(), _stream(stream)),
            "mi_add_inplace_f16")
+    return y
+
+
+def add_bias(y, bias, M: int, N: int, batch_stride: int, stream=None):
+    """y[b * batch_stride + m * N + n] += bias[n] (fp16 rounding) for
+    b < batch_stride // (M * N), m < M, n < N; y is any fp16 GPU tensor."""
+    _need(y, _f16(), "y"); _need(bias, _f16(), "bias")
+    if bias.numel() < N:
+        raise ValueError("bias must hold N entries")
+    if M > 0 and N > 0 and batch_stride >= M * N:
+        batches = batch_stride // (M * N)
+        if y.numel() < (batches - 1) * batch_stride + M * N:
+            raise ValueError("y is smaller than the batches it names")
+    _check(load_library().mi_add_bias_f16(_ptr(y), _ptr(bias), M, N, batch_stride,
+                                          _stream(stream)), "mi_add_bias_f16")
     return y
 
 
@@ -505,9 +554,10 @@ def embedding_rmsnorm(ids, table, weight, hidden=None, y=None, scale: float = 1.
 # ---------------------------------------------------------------------------
 
 def paged_kv_scatter(src, cache, block_table, seq_len, start_pos, layer: int, block_size: int,
-                     v_src=None, v_cache=None, stream=None):
+                     v_src=None, v_cache=None, stream=None, k_bias=None, v_bias=None):
     """Scatter src [B, S, H_kv, D] into cache [L, num_blocks, H_kv, bs, D] (and
-    v_src into v_cache in the same launch when given)."""
+    v_src into v_cache in the same launch when given).  k_bias / v_bias
+    ([H_kv * D], with v_src): the caches receive half(src + bias)."""
     torch = _torch()
     _need(src, _f16(), "src"); _need(cache, _f16(), "cache")
     for t, n in ((block_table, "block_table"), (seq_len, "seq_len"), (start_pos, "start_pos")):
@@ -527,6 +577,22 @@ def paged_kv_scatter(src, cache, block_table, seq_len, start_pos, layer: int, bl
         _check(lib.mi_paged_kv_scatter_f16(_ptr(src), _ptr(cache), _ptr(block_table), _ptr(seq_len),
                                            _ptr(start_pos), B, S, layer, NB, H, D, block_size, mb,
                                            _stream(stream)), "mi_paged_kv_scatter_f16")
+    elif k_bias is not None or v_bias is not None:
+        _need(v_src, _f16(), "v_src"); _need(v_cache, _f16(), "v_cache")
+        if v_src.shape != src.shape or v_cache.shape != cache.shape:
+            raise ValueError("v_src / v_cache must match src / cache")
+        for bz, n in ((k_bias, "k_bias"), (v_bias, "v_bias")):
+            if bz is not None:
+                _need(bz, _f16(), n)
+                if bz.numel() != H * D:
+                    raise ValueError(f"{n} must hold H_kv * D entries")
+        null = ctypes.c_void_p(0)
+        _check(lib.mi_paged_kv_scatter_kv_bias_f16(
+            _ptr(src), _ptr(v_src), _ptr(cache), _ptr(v_cache),
+            _ptr(k_bias) if k_bias is not None else null,
+            _ptr(v_bias) if v_bias is not None else null, _ptr(block_table), _ptr(seq_len),
+            _ptr(start_pos), B, S, layer, NB, H, D, block_size, mb, _stream(stream)),
+            "mi_paged_kv_scatter_kv_bias_f16")
     else:
         _need(v_src, _f16(), "v_src"); _need(v_cache, _f16(), "v_cache")
         if v_src.shape != src.shape or v_cache.shape != cache.shape:

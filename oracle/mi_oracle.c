@@ -345,6 +345,18 @@ void mio_add_inplace(uint16_t* y, const uint16_t* x, int64_t n) {
         y[i] = mio_f32_to_f16(mio_f16_to_f32(y[i]) + mio_f16_to_f32(x[i]));
 }
 
+void mio_add_bias(uint16_t* y, const uint16_t* bias, int64_t M, int64_t N,
+                  int64_t batch_stride) {
+    if (M <= 0 || N <= 0) return;
+    const int64_t batches = batch_stride / (M * N);
+    for (int64_t b = 0; b < batches; ++b)
+        for (int64_t m = 0; m < M; ++m)
+            for (int64_t n = 0; n < N; ++n) {
+                uint16_t* p = y + b * batch_stride + m * N + n;
+                *p = mio_f32_to_f16(mio_f16_to_f32(*p) + mio_f16_to_f32(bias[n]));
+            }
+}
+
 void mio_mul_inplace(uint16_t* y, const uint16_t* x, int64_t n) {
     for (int64_t i = 0; i < n; ++i)
         y[i] = mio_f32_to_f16(mio_f16_to_f32(y[i]) * mio_f16_to_f32(x[i]));

@@ -104,6 +104,13 @@ void mio_add_inplace(uint16_t* y, const uint16_t* x, int64_t n);
 void mio_mul_inplace(uint16_t* y, const uint16_t* x, int64_t n);
 void mio_scale_inplace(uint16_t* y, float scale, int64_t n);
 
+/* Broadcast bias add (src/kernels/model_utils_kernel.cu:11-28): for
+ * b < batch_stride / (M * N), m < M, n < N,
+ * y[b * batch_stride + m * N + n] = half(y[...] + bias[n]); M == 0 or an empty
+ * batch count does nothing. */
+void mio_add_bias(uint16_t* y, const uint16_t* bias, int64_t M, int64_t N,
+                  int64_t batch_stride);
+
 /* Row softmax, fp32 result (tests/verify/verify.py:69-73 torch.softmax;
  * src/kernels/softmax_kernel.cu:26-58).  Max-shifted, sums in double. */
 void mio_softmax(const uint16_t* x, float* y, int64_t N, int64_t D,

@@ -54,6 +54,7 @@ def lib() -> ctypes.CDLL:
             "mio_geglu": ([P, P, P, I64, I], None),
             "mio_geglu_composed": ([P, P, P, I64], None),
             "mio_add_inplace": ([P, P, I64], None),
+            "mio_add_bias": ([P, P, I64, I64, I64], None),
             "mio_mul_inplace": ([P, P, I64], None),
             "mio_scale_inplace": ([P, F, I64], None),
             "mio_softmax": ([P, P, I64, I64, I], None),
@@ -198,6 +199,14 @@ def geglu_composed(g, u) -> np.ndarray:
 def add(y, x) -> np.ndarray:
     y = _h(y).copy(); x = _h(x)
     lib().mio_add_inplace(_p(y), _p(x), y.size)
+    return y
+
+
+def add_bias(y, bias, M: int, N: int, batch_stride: int) -> np.ndarray:
+    """y (flat fp16, at least (batches - 1) * batch_stride + M * N elements)
+    with bias [N] added to each of the M rows of every batch."""
+    y = _h(y).copy(); bias = _h(bias)
+    lib().mio_add_bias(_p(y), _p(bias), M, N, batch_stride)
     return y
 
 

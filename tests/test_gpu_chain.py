@@ -46,16 +46,29 @@ def cfg5(chain_mod, dev):
     return chain_mod.Workload(dev, seed=5)
 
 
+def _biased(orc, w, name):
+    """The GEMM stand-in `name` (q, k or v) as the reference's add_bias leaves
+    it (model_utils_kernel.cu:11-28), or as it is without a QKV bias."""
+    h, s = w.host, w.shapes
+    if not s.get("qkv_bias"):
+        return h[name]
+    x = h[name]
+    n = x.shape[1] * x.shape[2]
+    T = x.shape[0]
+    return orc.add_bias(x.reshape(-1), h[name + "_bias"], T, n, T * n).reshape(x.shape)
+
+
 def _check_kv(orc, w, k_src, what):
     """K and V caches against the oracle's scatter of (k_src, v) per segment."""
     s = w.shapes
+    v_src = _biased(orc, w, "v")
     kc = np.zeros((s["num_layers"], s["num_blocks"], s["num_kv_heads"], s["block_size"],
                    s["head_dim"]), np.float16)
     vc = kc.copy()
     for g in w.groups:
         o, B, S = g["token_offset"], g["B"], g["S"]
         ks = k_src[o:o + B * S].reshape(B, S, s["num_kv_heads"], s["head_dim"])
-        vs = w.host["v"][o:o + B * S].reshape(B, S, s["num_kv_heads"], s["head_dim"])
+        vs = v_src[o:o + B * S].reshape(B, S, s["num_kv_heads"], s["head_dim"])
         kc = orc.paged_kv_scatter(ks, kc, g["block_table"], g["seq_len"], g["start_pos"],
                                   s["layer"], s["block_size"])
         vc = orc.paged_kv_scatter(vs, vc, g["block_table"], g["seq_len"], g["start_pos"],
@@ -87,15 +100,18 @@ def _check_chain(chain_mod, orc, w, what):
     inv = orc.rope_inv_freq(s["head_dim"], s["rope_theta"])
     pos = h["positions"]
     q_out, k_out = to_host(w.t["q"]), to_host(w.t["k"])
+    qk_in = {n: _biased(orc, w, n) for n in ("q", "k")}
     if s["use_qk_norm"]:
         for name, got, wt in (("q", q_out, h["q_norm"]), ("k", k_out, h["k_norm"])):
-            ref, n16 = qk_norm_rope_ref(orc, h[name], wt, pos, inv, s["qk_norm_eps"])
+            ref, n16 = qk_norm_rope_ref(orc, qk_in[name], wt, pos, inv, s["qk_norm_eps"])
             assert_norm_rope_close(got, ref, n16, what=f"{what}: qk-norm + rope {name}")
     else:
         c, sn = orc.rope_tables(inv, pos)
         for name, got in (("q", q_out), ("k", k_out)):
-            assert_bits_equal(got, orc.rope_neox(h[name], c, sn, nthreads=8).astype(np.float16),
+            assert_bits_equal(got, orc.rope_neox(qk_in[name], c, sn, nthreads=8).astype(np.float16),
                               what=f"{what}: rope {name}")
+    if s.get("qkv_bias"):  # v is read, not rewritten
+        assert_bits_equal(to_host(w.t["v"]), h["v"], what=f"{what}: v left as it was")
     _check_kv(orc, w, k_out, what)
     attn = h["attn_out"]
     if s["double_norm"]:
@@ -159,6 +175,41 @@ def test_chain_config5_plain_rope(chain_mod, orc, cfg5):
     assert_bits_equal(k_out, orc.rope_neox(h["k"], c, sn, nthreads=8).astype(np.float16),
                       what="rope k")
     _check_kv(orc, w, k_out, "plain rope")
+
+
+def test_chain_config5_qwen2_bias(chain_mod, orc, dev, cfg5):
+    """Qwen2.5 proper: the QKV projection bias and no Q/K norm, at config 5
+    (T = 6064): Q/K biased and rotated in one pass (bit-exact against
+    add_bias then RoPE), V's bias added on its way into the cache
+    (bit-exact), then the rest of the step."""
+    _case("chain config 5, Qwen2 QKV bias, no qk-norm")
+    import copy
+    import torch
+    w = copy.copy(cfg5)
+    rng = np.random.default_rng(55)
+    s = cfg5.shapes
+    qn, kn = s["num_heads"] * s["head_dim"], s["num_kv_heads"] * s["head_dim"]
+    w.host = dict(cfg5.host)
+    w.t = dict(cfg5.t)
+    for name, n in (("q_bias", qn), ("k_bias", kn), ("v_bias", kn)):
+        w.host[name] = (rng.standard_normal(n, dtype=np.float32) * np.float32(0.5)).astype(np.float16)
+        w.t[name] = torch.from_numpy(w.host[name]).to(dev)
+    w.t["k_cache"].zero_()
+    w.t["v_cache"].zero_()
+    w.shapes = dict(s, use_qk_norm=0, qkv_bias=1)
+    w.desc, w._keep = chain_mod.make_desc(w.shapes, w.t, cfg5.segments)
+    _check_chain(chain_mod, orc, w, "qwen2 bias")
+
+
+def test_chain_bias_with_qk_norm(chain_mod, orc, dev):
+    """QKV bias together with Q/K norm (the reference adds the bias, then
+    normalises): the chain's unfused bias launches ahead of the fused
+    Q/K-norm + RoPE, on a small batch."""
+    _case("chain bias + qk-norm, small batch")
+    w = chain_mod.Workload(dev, seed=41, n_decode=5, prefills=(29, 29), logit_rows=5,
+                           hidden_size=256, intermediate_size=512, num_heads=4, num_kv_heads=2,
+                           head_dim=64, vocab=777, use_qk_norm=1, qkv_bias=1)
+    _check_chain(chain_mod, orc, w, "bias + qk-norm")
 
 
 @pytest.mark.parametrize("act", [0, 1])

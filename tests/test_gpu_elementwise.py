@@ -138,3 +138,39 @@ def test_in_place_activation(mk, orc, dev):
     gd = to_dev(g, dev)
     mk.swiglu(gd, to_dev(u, dev), out=gd)
     assert_close(to_host(gd), orc.swiglu(g, u), what="in place")
+
+
+@pytest.mark.parametrize("M,N,batches,gap,offset", [
+    (6064, 3584, 1, 0, 0),    # Qwen2.5 q_proj bias at T = 6064 (vector path)
+    (6064, 512, 1, 0, 0),     # k_proj / v_proj
+    (37, 24, 3, 16, 0),       # three batches with gaps between them
+    (5, 7, 2, 3, 0),          # N % 8 != 0: scalar path
+    (33, 64, 1, 0, 1),        # unaligned y: scalar path
+])
+def test_add_bias_bit_exact(mk, orc, dev, M, N, batches, gap, offset):
+    """launch_add_bias (model_utils_kernel.cu:11-28): every batch of M rows
+    gets bias [N] added with one fp16 rounding; elements between batches are
+    left alone."""
+    _case(f"add_bias M={M} N={N} batches={batches} gap={gap} offset={offset}")
+    import torch
+    rng = np.random.default_rng(M * 7 + N + batches)
+    stride = M * N + gap
+    total = (batches - 1) * stride + M * N
+    y = normal_f16(rng, (total,), 0, 30)
+    bias = normal_f16(rng, (N,), 0, 30)
+    buf = torch.empty(total + offset, dtype=torch.float16, device=dev)
+    yd = buf[offset:]
+    yd.copy_(to_dev(y, dev))
+    mk.add_bias(yd, to_dev(bias, dev), M, N, stride)
+    assert_bits_equal(to_host(yd), orc.add_bias(y, bias, M, N, stride), what="add_bias")
+
+
+def test_add_bias_argument_errors(mk, dev):
+    import torch
+    y = torch.zeros(64, dtype=torch.float16, device=dev)
+    b = torch.zeros(8, dtype=torch.float16, device=dev)
+    mk.add_bias(y, b, 0, 8, 0)  # M == 0: nothing to do, as in the reference
+    with pytest.raises(RuntimeError):
+        mk.add_bias(y, b, 8, 8, 63)  # no whole batch
+    with pytest.raises(RuntimeError):
+        mk.add_bias(y, y[:8], 8, 8, 64)  # bias inside y

@@ -58,6 +58,39 @@ def test_kv_scatter_pair_and_bad_blocks(mk, orc, dev):
     assert_bits_equal(to_host(vcd), orc.paged_kv_scatter(v, vc, bt, sl, sp, 2, bs), what="v")
 
 
+@pytest.mark.parametrize("D", [128, 6])
+def test_kv_scatter_with_bias(mk, orc, dev, D):
+    """Qwen2's V bias (and a K bias) added on the way into the cache:
+    bit-exact against launch_add_bias then the scatter
+    (attention.cpp:735-739, :823-846); the sources are not written.  D = 6
+    takes the scalar path."""
+    _case(f"kv scatter K+V with bias, D={D}")
+    rng = np.random.default_rng(90 + D)
+    B, S, H, bs, L = 3, 37, 4, 16, 2
+    NB = 20
+    starts, seqs = [0, 9, 30], [37, 46, 60]
+    k, kc, bt, sl, sp = _paged_setup(rng, B, S, H, D, bs, L, NB, starts, seqs)
+    v = normal_f16(rng, k.shape)
+    vc = normal_f16(rng, kc.shape)
+    kb = normal_f16(rng, (H * D,), 0, 0.5)
+    vb = normal_f16(rng, (H * D,), 0, 0.5)
+    args = (to_dev(bt, dev), to_dev(sl, dev), to_dev(sp, dev))
+    for use_k in (False, True):
+        kcd, vcd = to_dev(kc, dev), to_dev(vc, dev)
+        kd, vd = to_dev(k, dev), to_dev(v, dev)
+        mk.paged_kv_scatter(kd, kcd, *args, layer=1, block_size=bs, v_src=vd, v_cache=vcd,
+                            k_bias=to_dev(kb, dev) if use_k else None, v_bias=to_dev(vb, dev))
+        n = B * S
+        vbias = orc.add_bias(v.reshape(-1), vb, n, H * D, n * H * D).reshape(v.shape)
+        kbias = orc.add_bias(k.reshape(-1), kb, n, H * D, n * H * D).reshape(k.shape) if use_k else k
+        assert_bits_equal(to_host(kcd), orc.paged_kv_scatter(kbias, kc, bt, sl, sp, 1, bs),
+                          what=f"k (k bias {use_k})")
+        assert_bits_equal(to_host(vcd), orc.paged_kv_scatter(vbias, vc, bt, sl, sp, 1, bs),
+                          what=f"v (k bias {use_k})")
+        assert_bits_equal(to_host(vd), v, what="v source untouched")
+        assert_bits_equal(to_host(kd), k, what="k source untouched")
+
+
 def test_kv_scatter_odd_head_dim(mk, orc, dev):
     _case("kv scatter D=6 (scalar path)")
     rng = np.random.default_rng(8)

@@ -223,3 +223,64 @@ def test_qk_norm_rope_vs_two_launches(mk, orc, dev):
     a, b = to_host(q1), to_host(q2)
     assert_close(a, b.astype(np.float32), what="q vs two launches")
     assert (a.view(np.uint16) == b.view(np.uint16)).mean() > 0.99
+
+
+def _bias_ref(orc, x, bias):
+    T = x.shape[0]
+    n = x.shape[1] * x.shape[2]
+    return orc.add_bias(x.reshape(-1), bias, T, n, T * n).reshape(x.shape)
+
+
+@pytest.mark.parametrize("T,Hq,Hkv,hd,chain", [(6064, 28, 4, 128, True), (4096, 28, 4, 128, False),
+                                               (7, 3, 1, 6, False), (5, 0, 2, 64, False),
+                                               (3, 8, 1, 256, False)])
+def test_bias_rope(mk, orc, dev, T, Hq, Hkv, hd, chain):
+    """Qwen2's q_proj / k_proj bias with the rotation in one pass, bit-exact
+    against launch_add_bias followed by RoPE (attention.cpp:717-780): at the
+    chain's tokens and positions, config 3's, a head_dim of 6 (scalar path)
+    and K-only."""
+    _case(f"bias + rope T={T} Hq={Hq} Hkv={Hkv} hd={hd}")
+    rng = np.random.default_rng(T + Hq * 10 + hd)
+    q = normal_f16(rng, (T, Hq, hd))
+    k = normal_f16(rng, (T, Hkv, hd))
+    bq = normal_f16(rng, (Hq * hd,), 0, 0.5)
+    bk = normal_f16(rng, (Hkv * hd,), 0, 0.5)
+    if chain:
+        dec = rng.integers(0, 28000, 64)
+        pos = np.concatenate([dec, 100 + np.arange(3000), 9000 + np.arange(3000)]).astype(np.int64)
+    elif T == 4096:
+        pos = config3_positions(rng)
+    else:
+        pos = rng.integers(0, 32000, T).astype(np.int64)
+    inv = orc.rope_inv_freq(hd, 1e6)
+    qd, kd = to_dev(q, dev), to_dev(k, dev)
+    mk.bias_rope_neox_qk(qd, kd if Hkv else None, to_dev(bq, dev), to_dev(bk, dev) if Hkv else None,
+                         to_dev(pos, dev), inv)
+    c, s = orc.rope_tables(inv, pos)
+    if Hq:
+        want = orc.rope_neox(_bias_ref(orc, q, bq), c, s, nthreads=8).astype(np.float16)
+        assert_bits_equal(to_host(qd), want, what="q")
+    if Hkv:
+        want = orc.rope_neox(_bias_ref(orc, k, bk), c, s, nthreads=8).astype(np.float16)
+        assert_bits_equal(to_host(kd), want, what="k")
+
+
+def test_bias_rope_equals_two_launches(mk, orc, dev):
+    """The fused pass against this library's own add_bias + rope_neox_qk."""
+    _case("bias + rope == add_bias + rope_neox_qk")
+    rng = np.random.default_rng(77)
+    T, Hq, Hkv, hd = 500, 28, 4, 128
+    q = normal_f16(rng, (T, Hq, hd))
+    k = normal_f16(rng, (T, Hkv, hd))
+    bq = normal_f16(rng, (Hq * hd,), 0, 2)
+    bk = normal_f16(rng, (Hkv * hd,), 0, 2)
+    pos = to_dev(rng.integers(0, 1 << 20, T).astype(np.int64), dev)
+    inv = orc.rope_inv_freq(hd, 1e6)
+    qa, ka = to_dev(q, dev), to_dev(k, dev)
+    mk.add_bias(qa, to_dev(bq, dev), T, Hq * hd, T * Hq * hd)
+    mk.add_bias(ka, to_dev(bk, dev), T, Hkv * hd, T * Hkv * hd)
+    mk.rope_neox_qk(qa, ka, pos, inv)
+    qb, kb = to_dev(q, dev), to_dev(k, dev)
+    mk.bias_rope_neox_qk(qb, kb, to_dev(bq, dev), to_dev(bk, dev), pos, inv)
+    assert_bits_equal(to_host(qb), to_host(qa), what="q")
+    assert_bits_equal(to_host(kb), to_host(ka), what="k")

@@ -262,6 +262,38 @@ def test_elementwise_bit_exact_vs_numpy():
                 (a.astype(np.float32) * s).astype(np.float16).view(np.uint16)).all()
 
 
+def test_add_bias_brute_force_and_numpy_broadcast():
+    """mio_add_bias (model_utils_kernel.cu:11-28): numpy's broadcast add with an
+    IEEE cast on a whole-batch layout; a strided layout (batch_stride > M*N)
+    leaves the gaps untouched; batch_stride below M*N (no batch) and M == 0 do
+    nothing; a bias of -0 keeps every bit."""
+    rng = np.random.default_rng(17)
+    M, N = 37, 24
+    y = normal_f16(rng, (3, M, N), 0, 50)
+    bias = normal_f16(rng, (N,), 0, 50)
+    want = (y.astype(np.float32) + bias.astype(np.float32)).astype(np.float16)
+    got = O.add_bias(y.reshape(-1), bias, M, N, M * N)
+    assert (got[: M * N] == want[0].reshape(-1)).all()
+    assert (got[M * N:] == y.reshape(-1)[M * N:]).all()  # batch_stride = M*N: one batch
+    got3 = O.add_bias(y.reshape(-1), bias, M, N // 2, M * (N // 2) * 2)  # 2 batches of half rows
+    flat = y.reshape(-1).astype(np.float32)
+    exp3 = flat.copy()
+    for b in range(2):
+        for m in range(M):
+            for n in range(N // 2):
+                i = b * M * (N // 2) * 2 + m * (N // 2) + n
+                exp3[i] = flat[i] + np.float32(bias[n])
+    exp3 = np.where(np.isin(np.arange(flat.size), [b * M * N + m * (N // 2) + n for b in range(2)
+                                                   for m in range(M) for n in range(N // 2)]),
+                    exp3.astype(np.float16), y.reshape(-1))
+    assert (got3.view(np.uint16) == exp3.astype(np.float16).view(np.uint16)).all()
+    assert (O.add_bias(y.reshape(-1), bias, M, N, M * N - 1) == y.reshape(-1)).all()
+    assert (O.add_bias(y.reshape(-1), bias, 0, N, 0) == y.reshape(-1)).all()
+    z = np.full(N, -0.0, dtype=np.float16)
+    assert (O.add_bias(y.reshape(-1), z, M, N, M * N).view(np.uint16)[: M * N] ==
+            y.reshape(-1).view(np.uint16)[: M * N]).all()
+
+
 def test_softmax_vs_torch_and_invariants():
     rng = np.random.default_rng(8)
     x = normal_f16(rng, (4, 5000), 0, 4)
