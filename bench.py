@@ -410,6 +410,14 @@ def all_kernels(mk, dev, iters, warmup):
     sec = time_launches(lambda i: mk.qk_norm_rope(qs[i].view(T, 28, 128), ks[i].view(T, 4, 128),
                                                   wq, wk, pos, inv), ns, iters, warmup)
     out.append(report("qk_norm_rope", "chain Q[6064,28,128]+K[6064,4,128]", nb, sec, T, "inplace"))
+    # 5d'. Qwen2.5 proper: the q_proj / k_proj bias added and the rotation in
+    # one pass (replaces launch_add_bias on Q and on K, then RoPE)
+    bq, bk = randn16((28 * 128,), gen, dev, 0.0, 0.5), randn16((4 * 128,), gen, dev, 0.0, 0.5)
+    nb = 2 * T * 32 * 128 * 2 + T * 8 + 32 * 128 * 2
+    sec = time_launches(lambda i: mk.bias_rope_neox_qk(qs[i].view(T, 28, 128), ks[i].view(T, 4, 128),
+                                                       bq, bk, pos, inv), ns, iters, warmup)
+    out.append(report("bias_rope_neox_qk", "chain Q[6064,28,128]+K[6064,4,128]", nb, sec, T,
+                      "inplace"))
     del qs, ks
     # 5e. SwiGLU [6064, 18944]
     nb = 3 * T * I * 2
@@ -464,6 +472,14 @@ def all_kernels(mk, dev, iters, warmup):
                                                       v_src=kv[i][1], v_cache=kv[i][3]),
                         ns, iters, warmup)
     out.append(report("paged_kv_scatter_kv", "chain K+V [6064,4,128] bs=16", nb, sec, T))
+    # 5h'. the same with Qwen2's V bias added on the way into the cache
+    vb = randn16((H * hd,), gen, dev, 0.0, 0.5)
+    sec = time_launches(lambda i: mk.paged_kv_scatter(kv[i][0], kv[i][2], bt, sl, sp, 0, bs,
+                                                      v_src=kv[i][1], v_cache=kv[i][3],
+                                                      v_bias=vb),
+                        ns, iters, warmup)
+    out.append(report("paged_kv_scatter_kv_bias", "chain K+V [6064,4,128] bs=16, V bias",
+                      nb + H * hd * 2, sec, T))
     del kv
     torch.cuda.synchronize()
     for r in out:
@@ -609,6 +625,16 @@ def cpu_kernel_table(budget_s=1.0):
                     oracle.rope_neox(n16.reshape(t.shape), c, sn, nthreads=cores)
             add("qk_norm_rope", cfg, 2 * T * 32 * 128 * 2 + T * 8 + 512, T, qk_norm_rope,
                 "norm, fp16 rounding, then rotation (the reference's composition)")
+            bq, bk = h((28 * 128,), 0.0, 0.5), h((4 * 128,), 0.0, 0.5)
+
+            def bias_rope():
+                c, sn = oracle.rope_tables(inv, pos)
+                for t, bz in ((q, bq), (k, bk)):
+                    n = t.shape[1] * 128
+                    b16 = oracle.add_bias(t.reshape(-1), bz, T, n, T * n)
+                    oracle.rope_neox(b16.reshape(t.shape), c, sn, nthreads=cores)
+            add("bias_rope_neox_qk", cfg, 2 * T * 32 * 128 * 2 + T * 8 + 32 * 128 * 2, T,
+                bias_rope, "bias add (fp16 rounding), then rotation (the reference's composition)")
     for name, fn, T, I_, cfg in (("swiglu", oracle.swiglu, 4096, I, "[4096,18944]"),
                                  ("geglu", oracle.geglu, 4096, 14336, "[4096,14336]"),
                                  ("swiglu", oracle.swiglu, 6064, I, "chain [6064,18944]")):
@@ -643,15 +669,17 @@ def chain_bytes(s, segments_tokens):
     output written once), from the workload's shapes."""
     T, D, I, V, N = s["T"], s["hidden_size"], s["intermediate_size"], s["vocab"], s["logit_rows"]
     Hq, Hkv, hd = s["num_heads"], s["num_kv_heads"], s["head_dim"]
+    weights = (2 * hd * 2 if s["use_qk_norm"] else 0) + \
+        ((Hq + 2 * Hkv) * hd * 2 if s.get("qkv_bias") else 0)       # q/k norm weights, qkv bias
     return ((T * 8 + 3 * T * D * 2 + D * 2)                           # gather + input norm
-            + (2 * T * (Hq + Hkv) * hd * 2 + T * 8 + 2 * hd * 2)      # qk-norm + rope
+            + (2 * T * (Hq + Hkv) * hd * 2 + T * 8 + weights)         # (bias,) (qk-norm,) rope
             + (2 * 2 * segments_tokens * Hkv * hd * 2)                # K + V scatter
             + 2 * (4 * T * D * 2 + D * 2)                             # 2x residual add + norm
             + 3 * T * I * 2                                           # SwiGLU
             + (2 * N * V * 2 + N * 4))                                # softmax + argmax
 
 
-def decoder_chain(mk, dev, iters, warmup):
+def decoder_chain(mk, dev, iters, warmup, qwen2=False):
     """BASELINE config 5 as one step: the C++ decoder chain (include/mi_chain.h)
     over one non-GEMM decoder layer at T = 6064 (64 decode tokens at random
     positions + two 3000-token prefills), then the sampling step:
@@ -666,10 +694,19 @@ def decoder_chain(mk, dev, iters, warmup):
     for V per segment, add in place + copy + RMSNorm twice.  Both run this
     library's kernels, so the difference is the fusion alone.  Bytes are the
     fused step's algorithmic bytes.  Two workloads alternate, so consecutive
-    steps stream from HBM rather than the Infinity Cache."""
+    steps stream from HBM rather than the Infinity Cache.
+
+    qwen2: Qwen2.5-7B's own attention pre-processing instead of config 5's
+    Gemma-3-style Q/K norm -- the q/k/v_proj bias and no Q/K norm
+    (attention.cpp:717-780): the chain adds the Q/K bias in the rotation pass
+    and V's on its way into the cache; the unfused composition runs
+    launch_add_bias on Q, K and V, the tables and two RoPE launches, then the
+    two scatters (like the config-5 composition, without the reference's
+    Q/K device copies)."""
     import torch
     import mi_chain
-    ws = [mi_chain.Workload(dev, seed=5 + i, host=False) for i in range(2)]
+    extra = dict(use_qk_norm=0, qkv_bias=1) if qwen2 else {}
+    ws = [mi_chain.Workload(dev, seed=5 + i, host=False, **extra) for i in range(2)]
     s = ws[0].shapes
     T, D, V, N = s["T"], s["hidden_size"], s["vocab"], s["logit_rows"]
     Hq, Hkv, hd = s["num_heads"], s["num_kv_heads"], s["head_dim"]
@@ -690,9 +727,13 @@ def decoder_chain(mk, dev, iters, warmup):
         mk.embedding_gather(t["ids"], t["embed"], out=t["hidden"])
         tmp.copy_(t["hidden"])
         mk.rmsnorm(tmp, t["input_norm"], y=t["normed"])
-        q2, k2 = t["q"].view(T * Hq, hd), t["k"].view(T * Hkv, hd)
-        mk.rmsnorm(q2, t["q_norm"], y=q2)
-        mk.rmsnorm(k2, t["k_norm"], y=k2)
+        if qwen2:
+            for name, n in (("q", Hq), ("k", Hkv), ("v", Hkv)):
+                mk.add_bias(t[name], t[name + "_bias"], T, n * hd, T * n * hd)
+        else:
+            q2, k2 = t["q"].view(T * Hq, hd), t["k"].view(T * Hkv, hd)
+            mk.rmsnorm(q2, t["q_norm"], y=q2)
+            mk.rmsnorm(k2, t["k_norm"], y=k2)
         mk.rope_tables(inv, t["positions"], cos_t=cos_t, sin_t=sin_t)
         q4, k4 = t["q"].view(1, T, Hq, hd), t["k"].view(1, T, Hkv, hd)
         mk.rope_neox(q4, cos_t, sin_t, y=q4)
@@ -715,8 +756,13 @@ def decoder_chain(mk, dev, iters, warmup):
     nb = chain_bytes(s, sum(g["B"] * g["S"] for g in ws[0].segments))
     cfg = ("gather&norm+qk-norm&rope+kv+add&norm+swiglu+add&norm+softmax&argmax "
            f"T={T} (64 decode + 2x3000 prefill)")
+    if qwen2:
+        cfg = ("gather&norm+qkv-bias&rope+kv(v-bias)+add&norm+swiglu+add&norm+softmax&argmax "
+               f"T={T} (64 decode + 2x3000 prefill)")
     rows = []
-    for name, fn in (("decoder_chain", fused), ("decoder_chain_unfused", unfused)):
+    suffix = "_qwen2" if qwen2 else ""
+    for name, fn in (("decoder_chain" + suffix, fused), ("decoder_chain" + suffix + "_unfused",
+                                                          unfused)):
         sec = time_launches(fn, len(ws), iters, warmup)
         rows.append(report(name, cfg, nb, sec, T))
     rows[0]["speedup_over_unfused"] = round(rows[1]["us"] / rows[0]["us"], 3)
@@ -864,6 +910,8 @@ def main():
         kernels = all_kernels(mk, dev, max(20, args.steps // 2), max(5, args.warmup // 2))
         if not args.no_chain:
             kernels += decoder_chain(mk, dev, max(10, args.steps // 8), max(3, args.warmup // 4))
+            kernels += decoder_chain(mk, dev, max(10, args.steps // 8), max(3, args.warmup // 4),
+                                     qwen2=True)
         for k in kernels:
             floor = ""
             if "frac_of_floor" in k:
