@@ -385,7 +385,7 @@ def all_kernels(mk, dev, iters, warmup):
                         ns, iters, warmup)
     out.append(report("fused_add_rmsnorm", "chain [6064,3584]", nb, sec, T))
     del sets
-    # 5c. Q/K RMSNorm, head_dim 128, in place (two launches: Q rows, K rows)
+    # 5c. Q/K RMSNorm, head_dim 128, in place (Q rows and K rows in one launch)
     nb = 2 * (T * 32 * 128) * 2 + 2 * 128 * 2
     ns = rotations(T * 32 * 128 * 2)
     wq = randn16((128,), gen, dev, 1.0, 0.1)
@@ -393,9 +393,8 @@ def all_kernels(mk, dev, iters, warmup):
     qs = [randn16((T * 28, 128), gen, dev) for _ in range(ns)]
     ks = [randn16((T * 4, 128), gen, dev) for _ in range(ns)]
 
-    def qk(i):
-        mk.rmsnorm(qs[i], wq, y=qs[i])
-        mk.rmsnorm(ks[i], wk, y=ks[i])
+    def qk(i):  # Q-norm and K-norm in one launch (mi_qk_rmsnorm_f16)
+        mk.qk_rmsnorm(qs[i].view(T, 28, 128), ks[i].view(T, 4, 128), wq, wk)
     sec = time_launches(qk, ns, iters, warmup)
     out.append(report("qk_rmsnorm", "chain Q[6064*28,128]+K[6064*4,128]", nb, sec, T, "inplace"))
     # 5d. RoPE on the same Q/K (fused Q+K launch)

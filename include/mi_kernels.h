@@ -111,6 +111,16 @@ int mi_bias_rope_neox_qk_f16(void* q, void* k, const void* q_bias, const void* k
                              const int64_t* positions, const float* inv_freq_host, int64_t T,
                              int64_t Hq, int64_t Hkv, int64_t head_dim, void* stream);
 
+/* Per-head RMSNorm of Q [T, Hq, hd] and K [T, Hkv, hd] in place, one launch:
+ * each head normalised with its weight (q_weight / k_weight [hd]; f(w) = w,
+ * or 1 + w when add_one).  Equals mi_rmsnorm_f16 on the T*Hq Q rows and on
+ * the T*Hkv K rows (k may be NULL when Hkv == 0).  Replaces the Gemma-3 pair
+ * of launch_rmsnorm calls at src/layers/attention.cpp:757-768
+ * (src/kernels/rmsnorm_kernel.cuh:19). */
+int mi_qk_rmsnorm_f16(void* q, void* k, const void* q_weight, const void* k_weight, int64_t T,
+                      int64_t Hq, int64_t Hkv, int64_t head_dim, float eps, int add_one,
+                      void* stream);
+
 /* Fused per-head RMSNorm + NeoX RoPE, in place, for Q [T, Hq, hd] and
  * K [T, Hkv, hd]: each head is normalised with its weight (q_weight or
  * k_weight, [hd]; f(w) = w, or 1 + w when add_one), rounded to fp16, then

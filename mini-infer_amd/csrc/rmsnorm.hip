@@ -181,6 +181,55 @@ __global__ __launch_bounds__(256) void rms_small_kernel(const half_t* x, half_t*
 }
 
 // ---------------------------------------------------------------------------
+// Q and K heads in one launch (in place): the short-row kernel over the
+// Nq + Nk rows of both tensors, row r < Nq from q with wq, the rest from k
+// with wk -- the reference's two launch_rmsnorm calls
+// (src/layers/attention.cpp:757-768) as one, saving a launch and its ramp.
+// ---------------------------------------------------------------------------
+template <int G, int RPG>
+__global__ __launch_bounds__(256) void rms_pair_kernel(half_t* q, const half_t* __restrict__ wq,
+                                                       int64_t Nq, half_t* k,
+                                                       const half_t* __restrict__ wk, int64_t Nk,
+                                                       int D, float eps, float w_bias) {
+    constexpr int kGroups = 256 / G;
+    const int lane = threadIdx.x & (G - 1);
+    const int64_t base = static_cast<int64_t>(blockIdx.x) * (kGroups * RPG) + threadIdx.x / G;
+    const int chunks = D >> 3;
+    const bool lane_ok = lane < chunks;
+    const int64_t N = Nq + Nk;
+    auto row_ptr = [&](int64_t row) { return row < Nq ? q + row * D : k + (row - Nq) * D; };
+
+    h8 a[RPG];
+#pragma unroll
+    for (int j = 0; j < RPG; ++j) {
+        const int64_t row = base + j * kGroups;
+        a[j] = (lane_ok && row < N) ? ld8_stream(row_ptr(row) + lane * 8) : h8(0);
+    }
+    const h8 wqv = lane_ok ? ld8(wq + lane * 8) : h8(0);
+    const h8 wkv = lane_ok && Nk > 0 ? ld8(wk + lane * 8) : h8(0);
+#pragma unroll
+    for (int j = 0; j < RPG; ++j) {
+        const int64_t row = base + j * kGroups;
+        const bool ok = lane_ok && row < N;
+        float ss = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const float f = (float)a[j][e];
+            ss = fmaf(f, f, ss);
+        }
+        ss = group_sum<G>(ss);  // every lane takes part (no lane has exited)
+        const float rrms = rsqrtf(ss / static_cast<float>(D) + eps);
+        if (ok) {
+            const h8 wv = row < Nq ? wqv : wkv;
+            h8 o;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) o[e] = to_half((float)a[j][e] * rrms * ((float)wv[e] + w_bias));
+            st8_out<MI_WT_RMSS>(row_ptr(row) + lane * 8, o);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Scalar fallback: one 256-lane workgroup per row, two passes.  Each lane
 // revisits only the elements it produced in pass 1, so in-place use is safe.
 // ---------------------------------------------------------------------------
@@ -315,8 +364,64 @@ int rmsnorm_dispatch(const void* xv, void* rv, const void* wv, void* yv, int64_t
     return launch_status();
 }
 
+int qk_rmsnorm(void* qv, void* kv, const void* wqv, const void* wkv, int64_t T, int64_t Hq,
+               int64_t Hkv, int64_t D, float eps, int add_one, void* stream) {
+    if (T < 0 || Hq < 0 || Hkv < 0 || D < 0) return MI_ERR_INVALID_ARGUMENT;
+    if (T == 0 || Hq + Hkv == 0 || D == 0) return MI_OK;
+    if ((Hq > 0 && (!qv || !wqv)) || (Hkv > 0 && (!kv || !wkv))) return MI_ERR_INVALID_ARGUMENT;
+    const int64_t Nq = T * Hq, Nk = T * Hkv;
+    if (Hq > 0 && Hkv > 0 && overlaps(qv, Nq * D * 2, kv, Nk * D * 2)) return MI_ERR_ALIASING;
+    const bool vec = D % 8 == 0 && D <= 512 && (Hq == 0 || (aligned16(qv) && aligned16(wqv))) &&
+                     (Hkv == 0 || (aligned16(kv) && aligned16(wkv)));
+    if (!vec) {  // the general kernels, one launch per tensor
+        if (Hq > 0) {
+            const int st = rmsnorm_dispatch<false>(qv, nullptr, wqv, qv, Nq, D, eps, add_one, stream);
+            if (st != MI_OK) return st;
+        }
+        return Hkv > 0 ? rmsnorm_dispatch<false>(kv, nullptr, wkv, kv, Nk, D, eps, add_one, stream)
+                       : MI_OK;
+    }
+    // with no Q heads, K takes the Q slot
+    auto* q = static_cast<half_t*>(Hq > 0 ? qv : kv);
+    const auto* wq = static_cast<const half_t*>(Hq > 0 ? wqv : wkv);
+    auto* k = static_cast<half_t*>(Hq > 0 ? kv : nullptr);
+    const auto* wk = static_cast<const half_t*>(Hq > 0 ? wkv : nullptr);
+    const int64_t n1 = Hq > 0 ? Nq : Nk, n2 = Hq > 0 ? Nk : 0;
+    const int chunks = static_cast<int>(D >> 3);
+    int G = 1;
+    while (G < chunks) G <<= 1;
+    const int64_t grid = ceil_div(n1 + n2, (256 / G) * kRowsPerGroup);
+    if (grid > kMaxGridX) return MI_ERR_UNSUPPORTED;
+    const float bias = add_one ? 1.0f : -0.0f;  // -0: w + bias == w, signed zeros kept
+    const dim3 g(static_cast<unsigned>(grid)), b(256);
+    const hipStream_t s = as_stream(stream);
+    const int d = static_cast<int>(D);
+    switch (G) {
+#define MI_PAIR_CASE(GG)                                                                         \
+    case GG:                                                                                     \
+        rms_pair_kernel<GG, kRowsPerGroup><<<g, b, 0, s>>>(q, wq, n1, k, wk, n2, d, eps, bias);  \
+        break;
+        MI_PAIR_CASE(1)
+        MI_PAIR_CASE(2)
+        MI_PAIR_CASE(4)
+        MI_PAIR_CASE(8)
+        MI_PAIR_CASE(16)
+        MI_PAIR_CASE(32)
+        MI_PAIR_CASE(64)
+#undef MI_PAIR_CASE
+        default: return MI_ERR_UNSUPPORTED;
+    }
+    return launch_status();
+}
+
 }  // namespace
 }  // namespace mi
+
+extern "C" int mi_qk_rmsnorm_f16(void* q, void* k, const void* q_weight, const void* k_weight,
+                                 int64_t T, int64_t Hq, int64_t Hkv, int64_t head_dim, float eps,
+                                 int add_one, void* stream) {
+    return mi::qk_rmsnorm(q, k, q_weight, k_weight, T, Hq, Hkv, head_dim, eps, add_one, stream);
+}
 
 extern "C" int mi_rmsnorm_f16(const void* x, const void* weight, void* y, int64_t N, int64_t D,
                               float eps, int add_one, void* stream) {

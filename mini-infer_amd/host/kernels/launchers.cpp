@@ -112,6 +112,14 @@ void launch_fused_add_rmsnorm(const __half* x, __half* residual, const __half* w
           "launch_fused_add_rmsnorm");
 }
 
+void launch_qk_rmsnorm(__half* q, __half* k, const __half* q_weight, const __half* k_weight,
+                       int T, int Hq, int Hkv, int head_dim, float eps, int add_one,
+                       hipStream_t stream) {
+    check(mi_qk_rmsnorm_f16(q, k, q_weight, k_weight, T, Hq, Hkv, head_dim, eps, add_one,
+                            sv(stream)),
+          "launch_qk_rmsnorm");
+}
+
 void launch_rope(const __half* x, const __half* cos_t, const __half* sin_t, __half* y, int B,
                  int S, int H, int D, hipStream_t stream) {
     check(mi_rope_neox_f16(x, cos_t, sin_t, y, B, S, H, D, sv(stream)), "launch_rope");

@@ -21,5 +21,12 @@ void launch_rmsnorm(const __half* x, const __half* weight, __half* y, int N, int
 void launch_fused_add_rmsnorm(const __half* x, __half* residual, const __half* weight, __half* y,
                               int N, int D, float eps, int add_one, hipStream_t stream);
 
+// Per-head RMSNorm of q [T, Hq, hd] and k [T, Hkv, hd] in place, one launch
+// replacing the Q-norm and K-norm launch_rmsnorm pair (Gemma 3); k may be
+// null when Hkv == 0.
+void launch_qk_rmsnorm(__half* q, __half* k, const __half* q_weight, const __half* k_weight,
+                       int T, int Hq, int Hkv, int head_dim, float eps, int add_one,
+                       hipStream_t stream);
+
 }  // namespace kernels
 }  // namespace mini_infer

@@ -35,6 +35,7 @@ SIGNATURES = {
     "mi_rope_tables_f16": [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _c_void_p],
     "mi_rope_neox_qk_f16": [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64, _i64,
                             _c_void_p],
+    "mi_qk_rmsnorm_f16": [_c_void_p] * 4 + [_i64] * 4 + [_f32, _int, _c_void_p],
     "mi_qk_norm_rope_f16": [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
                             _i64, _i64, _i64, _i64, _f32, _int, _c_void_p],
     "mi_swiglu_f16": [_c_void_p, _c_void_p, _c_void_p, _i64, _c_void_p],
@@ -285,6 +286,29 @@ def bias_rope_neox_qk(q, k, q_bias, k_bias, positions, inv_freq, stream=None):
         _ptr(q), _ptr(k) if k is not None else null, _ptr(q_bias),
         _ptr(k_bias) if k is not None else null, _ptr(positions), p, T, Hq, Hkv, hd,
         _stream(stream)), "mi_bias_rope_neox_qk_f16")
+    return q, k
+
+
+def qk_rmsnorm(q, k, q_weight, k_weight, eps: float = 1e-6, add_one: bool = False, stream=None):
+    """In place, one launch: per-head RMSNorm of q [T, Hq, hd] with q_weight
+    and of k [T, Hkv, hd] (may be None) with k_weight [hd]."""
+    _need(q, _f16(), "q"); _need(q_weight, _f16(), "q_weight")
+    if q.dim() != 3:
+        raise ValueError("q must be 3-D [T, Hq, hd]")
+    T, Hq, hd = q.shape
+    Hkv = 0
+    if k is not None:
+        _need(k, _f16(), "k"); _need(k_weight, _f16(), "k_weight")
+        if k.dim() != 3 or k.shape[0] != T or k.shape[2] != hd:
+            raise ValueError("k must be [T, Hkv, hd]")
+        Hkv = k.shape[1]
+    if q_weight.numel() != hd or (k is not None and k_weight.numel() != hd):
+        raise ValueError("weights must hold head_dim entries")
+    null = ctypes.c_void_p(0)
+    _check(load_library().mi_qk_rmsnorm_f16(
+        _ptr(q), _ptr(k) if k is not None else null, _ptr(q_weight),
+        _ptr(k_weight) if k is not None else null, T, Hq, Hkv, hd, float(eps), int(add_one),
+        _stream(stream)), "mi_qk_rmsnorm_f16")
     return q, k
 
 

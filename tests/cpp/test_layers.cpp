@@ -323,6 +323,26 @@ void gpu_checks() {
                                                   0);
         EXPECT(bit_equal(ad, rsc.data(), "launch_scale_inplace"), "scale");
 
+        // Qwen2's QKV bias at the reference's call shape (attention.cpp:717-721:
+        // M = tokens, N = Hq * hd, batch_stride = M * N)
+        {
+            const int M = 70, N = 3584;
+            Tensor y = reftest_f16({M, N}, 4.0f, 31), bias = reftest_f16({N}, 1.0f, 32);
+            std::vector<uint16_t> ry(bits(y), bits(y) + static_cast<size_t>(M) * N);
+            mio_add_bias(ry.data(), bits(bias), M, N, static_cast<int64_t>(M) * N);
+            Tensor yd = y.to(Device::cuda(0)), bd2 = bias.to(Device::cuda(0));
+            mini_infer::kernels::launch_add_bias(static_cast<__half*>(yd.data()),
+                                                 static_cast<const __half*>(bd2.data()), M, N,
+                                                 M * N, 0);
+            EXPECT(bit_equal(yd, ry.data(), "launch_add_bias [70,3584]"), "add_bias");
+            EXPECT(throws([&] {
+                       mini_infer::kernels::launch_add_bias(
+                           static_cast<__half*>(yd.data()), static_cast<const __half*>(bd2.data()),
+                           M, N, M * N - 1, 0);
+                   }),
+                   "launch_add_bias with no whole batch throws");
+        }
+
         const int V = 500, Hd = 3584, B = 2, S = 33;
         Tensor table = reftest_f16({V, Hd}, 0.02f, 9);
         std::vector<int64_t> ids(B * S);

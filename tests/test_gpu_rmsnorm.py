@@ -158,3 +158,43 @@ def test_signed_zero_weights(mk, orc, dev, N, D):
     yf = to_host(mk.fused_add_rmsnorm(to_dev(x, dev), to_dev(r, dev), to_dev(w, dev)))
     reff = orc.f32_to_f16(orc.fused_add_rmsnorm(x, r, w)[1])
     assert_bits_equal(yf[zero], reff[zero], what="signed zeros, fused")
+
+
+@pytest.mark.parametrize("T,Hq,Hkv,hd,add_one,offset", [
+    (6064, 28, 4, 128, False, 0),   # the chain config, one launch for Q and K
+    (333, 8, 2, 64, True, 0),       # Gemma (1 + w), rows straddling workgroups at the Q/K seam
+    (17, 4, 1, 256, False, 0),
+    (9, 0, 3, 128, False, 0),       # K only
+    (11, 5, 0, 128, False, 0),      # Q only
+    (7, 3, 2, 128, False, 1),       # unaligned: two general launches
+])
+def test_qk_rmsnorm_one_launch(mk, orc, dev, T, Hq, Hkv, hd, add_one, offset):
+    """mi_qk_rmsnorm_f16: the Gemma-3 Q-norm and K-norm pair in one launch,
+    against the oracle (1e-3) and bit for bit against two mi_rmsnorm_f16 calls."""
+    _case(f"qk rmsnorm one launch T={T} Hq={Hq} Hkv={Hkv} hd={hd}")
+    import torch
+    rng = np.random.default_rng(T + Hq + 7 * Hkv + hd)
+    q = normal_f16(rng, (T, Hq, hd))
+    k = normal_f16(rng, (T, Hkv, hd))
+    wq, wk = normal_f16(rng, (hd,), 1.0, 0.1), normal_f16(rng, (hd,), 0.0 if add_one else 1.0, 0.1)
+
+    def dev_buf(a):
+        buf = torch.empty(a.size + offset, dtype=torch.float16, device=dev)
+        t = buf[offset:].view(a.shape)
+        t.copy_(to_dev(a, dev))
+        return t
+    qd, kd = dev_buf(q), dev_buf(k)
+    mk.qk_rmsnorm(qd if Hq else kd, (kd if Hkv else None) if Hq else None,
+                  to_dev(wq if Hq else wk, dev), to_dev(wk, dev) if Hq and Hkv else None,
+                  eps=1e-6, add_one=add_one)
+    for name, x, w, got in (("q", q, wq, qd), ("k", k, wk, kd)):
+        if x.shape[1] == 0:
+            continue
+        rows = x.reshape(-1, hd)
+        assert_close(to_host(got).reshape(-1, hd), orc.rmsnorm(rows, w, 1e-6, add_one, nthreads=8),
+                     what=f"{name} vs oracle")
+        if offset == 0:  # the same kernel arithmetic as one aligned mi_rmsnorm_f16 call
+            two = to_dev(rows, dev)
+            mk.rmsnorm(two, to_dev(w, dev), y=two, eps=1e-6, add_one=add_one)
+            assert_bits_equal(to_host(got).reshape(-1, hd), to_host(two),
+                              what=f"{name} vs mi_rmsnorm_f16")
