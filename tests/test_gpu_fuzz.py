@@ -222,3 +222,61 @@ def test_fuzz_kv_scatter(mk, orc, dev, seed):
                         _dev_array(sp, dev), layer=layer, block_size=bs)
     assert_bits_equal(to_host(cd), orc.paged_kv_scatter(src, cache, bt, sl, sp, layer, bs),
                       what="cache")
+
+
+@pytest.mark.parametrize("seed", range(CASES))
+def test_fuzz_bias_paths(mk, orc, dev, seed):
+    """Qwen2's QKV bias: the bias add alone (batches, gaps, misaligned y), fused
+    into RoPE (bit-exact against add_bias + rope), and the Q/K norm pair in one
+    launch against the oracle."""
+    rng = np.random.default_rng(11000 + seed)
+    # add_bias
+    M, N = int(rng.integers(1, 200)), int(rng.choice([int(rng.integers(1, 100)), 8 * int(rng.integers(1, 600))]))
+    batches, gap = int(rng.integers(1, 4)), int(rng.choice([0, 0, int(rng.integers(1, 40))]))
+    mis = bool(rng.integers(0, 4) == 0)
+    stride = M * N + gap
+    _case(f"bias seed={seed} add_bias M={M} N={N} batches={batches} gap={gap} misaligned={mis}")
+    y = normal_f16(rng, ((batches - 1) * stride + M * N,), 0, 20)
+    b = normal_f16(rng, (N,), 0, 20)
+    yd = _dev_array(y, dev, mis)
+    mk.add_bias(yd, _dev_array(b, dev), M, N, stride)
+    assert_bits_equal(to_host(yd), orc.add_bias(y, b, M, N, stride), what="add_bias")
+    # bias + rope
+    T = int(rng.integers(1, 300))
+    hd = int(rng.choice([2, 6, 16, 64, 128, 256]))
+    Hq, Hkv = int(rng.integers(0, 30)), int(rng.integers(0, 6))
+    if Hq + Hkv == 0:
+        Hq = 1
+    _case(f"bias seed={seed} bias_rope T={T} Hq={Hq} Hkv={Hkv} hd={hd}")
+    q, k = normal_f16(rng, (T, Hq, hd)), normal_f16(rng, (T, Hkv, hd))
+    bq, bk = normal_f16(rng, (Hq * hd,), 0, 1), normal_f16(rng, (Hkv * hd,), 0, 1)
+    pos = rng.integers(0, 1 << int(rng.integers(4, 22)), T).astype(np.int64)
+    inv = orc.rope_inv_freq(hd, 1e6)
+    qd, kd = _dev_array(q, dev), _dev_array(k, dev)
+    if Hq:
+        mk.bias_rope_neox_qk(qd, kd if Hkv else None, _dev_array(bq, dev),
+                             _dev_array(bk, dev) if Hkv else None, _dev_array(pos, dev), inv)
+    else:  # K alone goes in the Q slot of the binding
+        mk.bias_rope_neox_qk(kd, None, _dev_array(bk, dev), None, _dev_array(pos, dev), inv)
+    c, s = orc.rope_tables(inv, pos)
+    for name, x, bz, got in (("q", q, bq, qd), ("k", k, bk, kd)):
+        if x.shape[1] == 0:
+            continue
+        n = x.shape[1] * hd
+        xb = orc.add_bias(x.reshape(-1), bz, T, n, T * n).reshape(x.shape)
+        assert_bits_equal(to_host(got), orc.rope_neox(xb, c, s).astype(np.float16), what=name)
+    # Q/K norm in one launch
+    hd2 = int(rng.choice([8, 16, 64, 128, 256, 512, 40]))
+    T2, Hq2, Hkv2 = int(rng.integers(1, 200)), int(rng.integers(1, 30)), int(rng.integers(0, 6))
+    add_one = bool(rng.integers(0, 2))
+    _case(f"bias seed={seed} qk_rmsnorm T={T2} Hq={Hq2} Hkv={Hkv2} hd={hd2} add_one={add_one}")
+    q2, k2 = normal_f16(rng, (T2, Hq2, hd2)), normal_f16(rng, (T2, Hkv2, hd2))
+    wq, wk = normal_f16(rng, (hd2,), 1.0, 0.1), normal_f16(rng, (hd2,), 1.0, 0.1)
+    qd2, kd2 = _dev_array(q2, dev), _dev_array(k2, dev)
+    mk.qk_rmsnorm(qd2, kd2 if Hkv2 else None, _dev_array(wq, dev),
+                  _dev_array(wk, dev) if Hkv2 else None, add_one=add_one)
+    assert_close(to_host(qd2).reshape(-1, hd2), orc.rmsnorm(q2.reshape(-1, hd2), wq, add_one=add_one),
+                 what="q norm")
+    if Hkv2:
+        assert_close(to_host(kd2).reshape(-1, hd2),
+                     orc.rmsnorm(k2.reshape(-1, hd2), wk, add_one=add_one), what="k norm")
