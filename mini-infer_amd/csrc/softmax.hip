@@ -829,11 +829,17 @@ struct OneLaunchGrid {
 };
 OneLaunchGrid onelaunch_grid(int64_t N, int64_t D, bool am) {
     OneLaunchGrid g;
-    g.splits = static_cast<int>(ceil_div(D, 2048 * onelaunch_u(N, D)));
-    const int64_t R = onelaunch_rows(N, D, am);
-    // round down to whole groups while that keeps every row slot resident,
-    // up (idle slots) when there are fewer than kXcds
-    g.R = static_cast<int>(R >= kXcds ? R / kXcds * kXcds : kXcds);
+    const int u = onelaunch_u(N, D);
+    g.splits = static_cast<int>(ceil_div(D, 2048 * u));
+    // row slots that stay resident next to each other (at most the records;
+    // at least 20 = 1280 resident workgroups / 64 chunks)
+    int64_t cap = resident_workgroups(onelaunch_kernel(u, am), 256) / g.splits;
+    if (cap > kSplitMaxRows) cap = kSplitMaxRows;
+    // every row in one round when a whole number of groups of that many
+    // slots fits (slots past N - 1 idle), else the largest whole number of
+    // groups that does (rows in rounds)
+    const int64_t up = ceil_div(N < cap ? N : cap, kXcds) * kXcds;
+    g.R = static_cast<int>(up <= cap ? up : cap / kXcds * kXcds);
     g.local = exchange_test_mode().load() == 0 ? 1 : 0;
     return g;
 }
