@@ -91,3 +91,11 @@ def test_refuses_missing_buffers_on_host(lib):
     assert run(ctypes.byref(d3), 1, None) == -1
     d4 = _desc(hidden_size=0)
     assert run(ctypes.byref(d4), 1, None) == -1
+
+
+def test_refuses_partial_qkv_bias(lib):
+    """Qwen2's QKV bias comes as q_bias, k_bias and v_bias together."""
+    d = _desc()
+    d.q_bias = 0x200000
+    assert lib.mi_decoder_chain_run(ctypes.byref(d), 1, None) == -1
+    assert b"qkv bias" in lib.mi_decoder_chain_last_error(), lib.mi_decoder_chain_last_error()
