@@ -480,6 +480,60 @@ def all_kernels(mk, dev, iters, warmup):
     out.append(report("paged_kv_scatter_kv_bias", "chain K+V [6064,4,128] bs=16, V bias",
                       nb + H * hd * 2, sec, T))
     del kv
+    # 5i. Qwen2.5 attention pre-processing in one launch: RoPE of Q/K in place
+    # and the rotated K and the V rows into the paged cache (5d + 5h), with
+    # and without the q/k/v bias, for the chain's continuous batch: 64 decode
+    # tokens of 64 sequences, then two 3000-token prefills
+    dec_start = rng.integers(0, 6000, 64)
+    spans = [(0, 64, 1, dec_start), (64, 1, 3000, [0]), (3064, 1, 3000, [9000])]
+    perm = rng.permutation(64 * 376 + 188 + 751)
+    segs, nxt = [], 0
+    for off, B, S, st in spans:
+        sl = [int(x) + S for x in st]
+        mbs = -(-max(sl) // bs)
+        btab = perm[nxt:nxt + B * mbs].reshape(B, mbs).astype(np.int32)
+        nxt += B * mbs
+        segs.append(dict(token_offset=off, S=S, block_table=torch.from_numpy(btab).to(dev),
+                         seq_len=torch.tensor(sl, dtype=torch.int32, device=dev),
+                         start_pos=torch.tensor([int(x) for x in st], dtype=torch.int32,
+                                                device=dev)))
+    NBc = nxt
+    nb = 2 * T * 32 * 128 * 2 + T * H * hd * 2 + 2 * T * H * hd * 2 + T * 8
+    ns = rotations(nb, max_sets=32)
+    sets = [(randn16((T, 28, 128), gen, dev), randn16((T, H, hd), gen, dev),
+             randn16((T, H, hd), gen, dev)) for _ in range(ns)]
+    kcache = torch.empty((1, NBc, H, bs, hd), dtype=f16, device=dev)
+    vcache = torch.empty_like(kcache)
+    bv = randn16((H * hd,), gen, dev, 0.0, 0.5)
+    for tag, extra in (("", ()), ("_bias", (bq, bk, bv))):
+        sec = time_launches(lambda i: mk.rope_kv_scatter(sets[i][0], sets[i][1], sets[i][2], pos,
+                                                         inv, kcache, vcache, 0, bs, segs, *extra),
+                            ns, iters, warmup)
+        out.append(report("rope_kv_scatter" + tag,
+                          "chain Q[6064,28,128]+K,V[6064,4,128] -> cache bs=16"
+                          + (", q/k/v bias" if extra else ""),
+                          nb + (len(extra) and 36 * 128 * 2), sec, T))
+    # the same work as the reference composes it: RoPE (or bias + RoPE), then
+    # one K+V scatter per segment (V bias on the way)
+
+    def unfused(i, extra):
+        qx, kx, vx = sets[i]
+        if extra:
+            mk.bias_rope_neox_qk(qx, kx, bq, bk, pos, inv)
+        else:
+            mk.rope_neox_qk(qx, kx, pos, inv)
+        for g in segs:
+            B, S, o = g["block_table"].shape[0], g["S"], g["token_offset"]
+            mk.paged_kv_scatter(kx[o:o + B * S].view(B, S, H, hd), kcache, g["block_table"],
+                                g["seq_len"], g["start_pos"], 0, bs,
+                                v_src=vx[o:o + B * S].view(B, S, H, hd), v_cache=vcache,
+                                v_bias=bv if extra else None)
+    for tag, extra in (("", ()), ("_bias", (bq, bk, bv))):
+        sec = time_launches(lambda i: unfused(i, extra), ns, iters, warmup)
+        out.append(report("rope_kv_scatter" + tag + "_unfused",
+                          "RoPE launch + 3 per-segment K+V scatters" + (", bias" if extra else ""),
+                          nb + (len(extra) and 36 * 128 * 2), sec, T))
+    del sets, kcache, vcache
     torch.cuda.synchronize()
     for r in out:
         if r["bytes"] >= 8 << 20:

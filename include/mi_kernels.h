@@ -121,6 +121,41 @@ int mi_qk_rmsnorm_f16(void* q, void* k, const void* q_weight, const void* k_weig
                       int64_t Hq, int64_t Hkv, int64_t head_dim, float eps, int add_one,
                       void* stream);
 
+/* One group of sequences in the reference's [B, S] KV-scatter layout
+ * (launch_paged_kv_scatter, src/kernels/model_utils_kernel.cuh:53-63):
+ * tokens [token_offset, token_offset + B*S) of the step, with int32 DEVICE
+ * block_table [B, max_blocks_per_seq], seq_len [B] and start_pos [B].  (The
+ * same layout as mi_chain_kv_segment in mi_chain.h.) */
+typedef struct mi_kv_segment {
+    int64_t token_offset;
+    int64_t B, S;
+    const int* block_table;
+    const int* seq_len;
+    const int* start_pos;
+    int64_t max_blocks_per_seq;
+} mi_kv_segment;
+
+/* Attention pre-processing without Q/K norm, one launch: NeoX RoPE of
+ * q [T, Hq, hd] and k [T, Hkv, hd] in place (cos/sin from DEVICE positions and
+ * HOST inv_freq, as mi_rope_neox_qk_f16), and the rotated K rows and the V
+ * rows [T, Hkv, hd] written into the paged caches [>= layer + 1, num_blocks,
+ * Hkv, block_size, hd] for the tokens of each segment (placement and skip
+ * rules of mi_paged_kv_scatter_f16).  With q_bias / k_bias / v_bias (Qwen2;
+ * all three or none) each tensor gets its bias added first, rounded to fp16
+ * (v itself is not written).  Equals mi_rope_neox_qk_f16 (or
+ * mi_bias_rope_neox_qk_f16) followed by mi_paged_kv_scatter_kv_f16 (or its
+ * bias form) per segment, bit for bit.  hd a multiple of 16 (<= 512),
+ * (Hq + Hkv) * hd / 16 <= 256, Hkv * hd <= 6144, at most 8 segments,
+ * 16-byte-aligned buffers; otherwise MI_ERR_UNSUPPORTED (use the separate
+ * entry points).  Replaces src/layers/attention.cpp:717-780 (bias adds,
+ * copies, RoPE pair) and :823-846 (the two scatters). */
+int mi_rope_kv_scatter_f16(void* q, void* k, const void* v, const void* q_bias,
+                           const void* k_bias, const void* v_bias, const int64_t* positions,
+                           const float* inv_freq_host, int64_t T, int64_t Hq, int64_t Hkv,
+                           int64_t head_dim, void* k_cache, void* v_cache, int64_t layer,
+                           int64_t num_blocks, int64_t block_size,
+                           const mi_kv_segment* segments, int num_segments, void* stream);
+
 /* Fused per-head RMSNorm + NeoX RoPE, in place, for Q [T, Hq, hd] and
  * K [T, Hkv, hd]: each head is normalised with its weight (q_weight or
  * k_weight, [hd]; f(w) = w, or 1 + w when add_one), rounded to fp16, then

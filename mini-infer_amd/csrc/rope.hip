@@ -737,6 +737,132 @@ int launch_qk_norm_rope(half_t* q, int64_t Hq, half_t* k, int64_t Hkv, const hal
     }
 }
 
+// ---------------------------------------------------------------------------
+// RoPE of Q and K in place, with K's rotated rows and V's rows also written
+// into the paged KV cache, one workgroup per token: the attention
+// pre-processing of a model without Q/K norm (Qwen2: with the q/k/v_proj
+// bias) -- the reference's RoPE pair and two launch_paged_kv_scatter calls
+// per sequence group (src/layers/attention.cpp:779-780, :823-846) in one
+// launch.  K is not re-read for the scatter.  Lanes 0..255 take the
+// (head, slice) units of the token as rope_kernel does; the lanes after them
+// carry V's 16-byte vectors.  The token's cache slot comes from the segment
+// holding it (workgroup-uniform scalar lookups issued with the data loads).
+// ---------------------------------------------------------------------------
+constexpr int kMaxKvSegs = 8;
+struct KvSegs {
+    int n;
+    int64_t off[kMaxKvSegs], B[kMaxKvSegs], S[kMaxKvSegs], mb[kMaxKvSegs];
+    const int* bt[kMaxKvSegs];
+    const int* sl[kMaxKvSegs];
+    const int* sp[kMaxKvSegs];
+};
+
+template <bool BIAS>
+__global__ __launch_bounds__(1024) void rope_kv_kernel(half_t* q, half_t* k, const half_t* v,
+                                                       int Hq, int Hkv, int hd,
+                                                       const int64_t* __restrict__ positions,
+                                                       InvFreq inv, const half_t* __restrict__ bq,
+                                                       const half_t* __restrict__ bk,
+                                                       const half_t* __restrict__ bv,
+                                                       half_t* k_cache, half_t* v_cache, KvSegs sg,
+                                                       int64_t layer, int64_t num_blocks,
+                                                       int64_t bs) {
+    __shared__ float cs[2 * kMaxHalf];
+    const int64_t tok = blockIdx.x;
+    const int half = hd >> 1;
+    const int cph = half >> 3;  // 16-byte slices per half head
+    const int units = (Hq + Hkv) * cph;
+    const int tid = threadIdx.x;
+
+    h8 x1 = h8(0), x2 = h8(0), b1 = h8(0), b2 = h8(0);
+    half_t* hp = nullptr;
+    int h = 0, c = 0;
+    if (tid < units) {
+        h = small_div(tid, 1.0f / static_cast<float>(cph));  // units < 2^22: exact
+        c = tid - h * cph;
+        hp = h < Hq ? q + (tok * Hq + h) * hd : k + (tok * Hkv + (h - Hq)) * hd;
+        x1 = ld8_stream(hp + c * 8);
+        x2 = ld8_stream(hp + half + c * 8);
+        if constexpr (BIAS) {  // a few KB every token re-reads: plain loads
+            const half_t* bp = h < Hq ? bq + h * hd : bk + (h - Hq) * hd;
+            b1 = ld8(bp + c * 8);
+            b2 = ld8(bp + half + c * 8);
+        }
+    }
+    const int vj = tid - 256;  // V vector of this lane
+    const bool vlane = vj >= 0 && vj < Hkv * (hd >> 3);
+    h8 vv = h8(0), vb = h8(0);
+    if (vlane) {
+        vv = ld8_stream(v + tok * Hkv * hd + vj * 8);
+        if constexpr (BIAS) vb = ld8(bv + vj * 8);
+    }
+    const float fpos = static_cast<float>(positions[tok]);
+    // the token's cache row (-1: not scattered), as launch_paged_kv_scatter
+    // places it (src/kernels/model_utils_kernel.cu:108-164); looked up after
+    // the data loads are issued, so its dependent scalar loads overlap them
+    // (token indices and segment sizes fit 32 bits: T <= kMaxGridX)
+    int64_t dst_base = -1;
+    const int itok = static_cast<int>(tok);
+    for (int i = 0; i < sg.n; ++i) {
+        const int r = itok - static_cast<int>(sg.off[i]);
+        const int S = static_cast<int>(sg.S[i]);
+        if (r < 0 || r >= static_cast<int>(sg.B[i]) * S) continue;
+        const int b = static_cast<int>(static_cast<uint32_t>(r) / static_cast<uint32_t>(S));
+        const int64_t pos = static_cast<int64_t>(sg.sp[i][b]) + (r - b * S);
+        const int len = sg.sl[i][b];
+        if (pos < 0 || pos >= len) break;
+        // 0 <= pos < len and bs < 2^31: 32-bit division
+        const int blk = static_cast<int>(static_cast<uint32_t>(pos) / static_cast<uint32_t>(bs));
+        if (blk >= sg.mb[i]) break;
+        const int64_t phys = sg.bt[i][b * sg.mb[i] + blk];
+        if (phys >= 0 && phys < num_blocks)
+            dst_base = (layer * num_blocks + phys) * Hkv * bs * hd + (pos - blk * bs) * hd;
+        break;
+    }
+    if (tid < half) {
+        half_t hc, hs;
+        cos_sin_half(fpos * inv.v[tid], hc, hs);
+        const int li = quad_split(tid, half);
+        cs[li] = (float)hc;
+        cs[kMaxHalf + li] = (float)hs;
+    }
+    __syncthreads();
+
+    if (tid < units) {
+        h8 y1, y2;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            // quad_split layout: entry e of slice c at c*4 + (e & 3), + half/2 for e >= 4
+            const int le = ((e & 4) ? (half >> 1) : 0) + c * 4 + (e & 3);
+            const float cv = cs[le], sv = cs[kMaxHalf + le];
+            float a = (float)x1[e], bb = (float)x2[e];
+            if constexpr (BIAS) {
+                a = (float)to_half(a + (float)b1[e]);
+                bb = (float)to_half(bb + (float)b2[e]);
+            }
+            y1[e] = to_half(fp32_rounded(a * cv - bb * sv));
+            y2[e] = to_half(fp32_rounded(bb * cv + a * sv));
+        }
+        st8_out<MI_WT_ROPE>(hp + c * 8, y1);
+        st8_out<MI_WT_ROPE>(hp + half + c * 8, y2);
+        if (h >= Hq && dst_base >= 0) {
+            half_t* kd = k_cache + dst_base + static_cast<int64_t>(h - Hq) * bs * hd;
+            st8_stream(kd + c * 8, y1);
+            st8_stream(kd + half + c * 8, y2);
+        }
+    }
+    if (vlane && dst_base >= 0) {
+        if constexpr (BIAS) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) vv[e] = to_half((float)vv[e] + (float)vb[e]);
+        }
+        const int per_head = hd >> 3;
+        const int vh = small_div(vj, 1.0f / static_cast<float>(per_head));
+        const int vd = (vj - vh * per_head) * 8;
+        st8_stream(v_cache + dst_base + static_cast<int64_t>(vh) * bs * hd + vd, vv);
+    }
+}
+
 // (Hq + Hkv) * hd/2 must fit the int lane arithmetic of rope_kernel.
 bool heads_ok(int64_t Hq, int64_t Hkv, int64_t hd) {
     return Hq >= 0 && Hkv >= 0 && hd > 0 && hd % 2 == 0 && hd / 2 <= kMaxHalf &&
@@ -840,6 +966,82 @@ extern "C" int mi_bias_rope_neox_qk_f16(void* q, void* k, const void* q_bias, co
                            static_cast<const half_t*>(k), static_cast<half_t*>(k), Hkv,
                            positions, nullptr, nullptr, T, head_dim, inv, mi::as_stream(stream),
                            static_cast<const half_t*>(q_bias), static_cast<const half_t*>(k_bias));
+}
+
+extern "C" int mi_rope_kv_scatter_f16(void* q, void* k, const void* v, const void* q_bias,
+                                      const void* k_bias, const void* v_bias,
+                                      const int64_t* positions, const float* inv_freq_host,
+                                      int64_t T, int64_t Hq, int64_t Hkv, int64_t head_dim,
+                                      void* k_cache, void* v_cache, int64_t layer,
+                                      int64_t num_blocks, int64_t block_size,
+                                      const mi_kv_segment* segments, int num_segments,
+                                      void* stream) {
+    if (T < 0 || Hq < 0 || Hkv < 0 || head_dim < 0 || layer < 0 || num_blocks < 0 ||
+        block_size <= 0 || num_segments < 0)
+        return MI_ERR_INVALID_ARGUMENT;
+    if (T == 0) return MI_OK;
+    const bool bias = q_bias || k_bias || v_bias;
+    if (!q || !k || !v || !positions || !k_cache || !v_cache || Hq < 1 || Hkv < 1 ||
+        (num_segments > 0 && !segments) ||
+        (bias && (!q_bias || !k_bias || !v_bias)))
+        return MI_ERR_INVALID_ARGUMENT;
+    // one workgroup per token: lanes for the token's Q/K slices (<= 256) and
+    // V's vectors (<= 768), 16-byte vectors, few segments
+    if (head_dim % 16 != 0 || head_dim / 2 > mi::kMaxHalf || (Hq + Hkv) * (head_dim / 16) > 256 ||
+        Hkv * head_dim / 8 > 768 || num_segments > mi::kMaxKvSegs || T > mi::kMaxGridX ||
+        block_size > INT32_MAX)
+        return MI_ERR_UNSUPPORTED;
+    for (const void* p : {static_cast<const void*>(q), static_cast<const void*>(k), v,
+                          static_cast<const void*>(k_cache), static_cast<const void*>(v_cache)})
+        if (!mi::aligned16(p)) return MI_ERR_UNSUPPORTED;
+    if (bias && !(mi::aligned16(q_bias) && mi::aligned16(k_bias) && mi::aligned16(v_bias)))
+        return MI_ERR_UNSUPPORTED;
+    const int64_t qb = T * Hq * head_dim * 2, kb = T * Hkv * head_dim * 2;
+    const int64_t cb = (layer + 1) * num_blocks * Hkv * block_size * head_dim * 2;
+    const void* bufs[5] = {q, k, v, k_cache, v_cache};
+    const int64_t lens[5] = {qb, kb, kb, cb, cb};
+    for (int i = 0; i < 5; ++i)
+        for (int j = i + 1; j < 5; ++j)
+            if (mi::overlaps(bufs[i], lens[i], bufs[j], lens[j])) return MI_ERR_ALIASING;
+    mi::KvSegs sg{};
+    sg.n = num_segments;
+    for (int i = 0; i < num_segments; ++i) {
+        const mi_kv_segment& g = segments[i];
+        if (g.token_offset < 0 || g.B < 0 || g.S < 0 || g.token_offset + g.B * g.S > T)
+            return MI_ERR_INVALID_ARGUMENT;
+        if (g.B * g.S > 0 && (!g.block_table || !g.seq_len || !g.start_pos ||
+                              g.max_blocks_per_seq <= 0))
+            return MI_ERR_INVALID_ARGUMENT;
+        sg.off[i] = g.token_offset;
+        sg.B[i] = g.B;
+        sg.S[i] = g.S;
+        sg.mb[i] = g.max_blocks_per_seq;
+        sg.bt[i] = g.block_table;
+        sg.sl[i] = g.seq_len;
+        sg.sp[i] = g.start_pos;
+    }
+    mi::InvFreq inv;
+    if (!mi::load_inv_freq(inv_freq_host, head_dim / 2, inv)) return MI_ERR_INVALID_ARGUMENT;
+    const int vlanes = static_cast<int>(mi::ceil_div(Hkv * head_dim / 8, mi::kWave)) * mi::kWave;
+    const dim3 g(static_cast<unsigned>(T)), b(256 + vlanes);
+    auto* qh = static_cast<half_t*>(q);
+    auto* kh = static_cast<half_t*>(k);
+    const auto* vh = static_cast<const half_t*>(v);
+    auto* kc = static_cast<half_t*>(k_cache);
+    auto* vc = static_cast<half_t*>(v_cache);
+    const hipStream_t s = mi::as_stream(stream);
+    const int hq = static_cast<int>(Hq), hk = static_cast<int>(Hkv), d = static_cast<int>(head_dim);
+    if (bias)
+        mi::rope_kv_kernel<true><<<g, b, 0, s>>>(qh, kh, vh, hq, hk, d, positions, inv,
+                                                 static_cast<const half_t*>(q_bias),
+                                                 static_cast<const half_t*>(k_bias),
+                                                 static_cast<const half_t*>(v_bias), kc, vc, sg,
+                                                 layer, num_blocks, block_size);
+    else
+        mi::rope_kv_kernel<false><<<g, b, 0, s>>>(qh, kh, vh, hq, hk, d, positions, inv, nullptr,
+                                                  nullptr, nullptr, kc, vc, sg, layer, num_blocks,
+                                                  block_size);
+    return mi::launch_status();
 }
 
 extern "C" int mi_qk_norm_rope_f16(void* q, void* k, const void* q_weight, const void* k_weight,

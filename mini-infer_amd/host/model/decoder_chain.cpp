@@ -97,6 +97,30 @@ void DecoderChain::validate_() const {
     }
 }
 
+// Steps 3 and 4 in one launch when the model has no Q/K norm: the rotation
+// pass also writes the rotated K rows and the V rows (+ V bias) into the
+// paged cache, so K is not re-read.  False (nothing launched) for shapes the
+// one-launch kernel does not take; the caller then runs the two steps.
+bool DecoderChain::rope_kv_fused(hipStream_t s) const {
+    const mi_chain_desc& d = d_;
+    if (d.use_qk_norm || d.num_heads <= 0 || d.num_kv_heads <= 0) return false;
+    mi_kv_segment fs[8];
+    int n = 0;
+    for (const mi_chain_kv_segment& g : segs_) {
+        if (g.B * g.S == 0) continue;
+        if (n == 8) return false;
+        fs[n++] = mi_kv_segment{g.token_offset, g.B, g.S, g.block_table, g.seq_len,
+                                g.start_pos, g.max_blocks_per_seq};
+    }
+    const int st = mi_rope_kv_scatter_f16(d.q, d.k, d.v, d.q_bias, d.k_bias, d.v_bias,
+                                          d.positions, inv_freq_.data(), d.T, d.num_heads,
+                                          d.num_kv_heads, d.head_dim, d.k_cache, d.v_cache,
+                                          d.layer, d.num_blocks, d.block_size, fs, n, sv(s));
+    if (st == MI_ERR_UNSUPPORTED) return false;
+    check(st, d.q_bias ? "bias + rope + kv scatter" : "rope + kv scatter");
+    return true;
+}
+
 void DecoderChain::run(hipStream_t s, DecoderChainHooks* hooks) const {
     DecoderChainHooks none;
     DecoderChainHooks& h = hooks ? *hooks : none;
@@ -125,54 +149,59 @@ void DecoderChain::run(hipStream_t s, DecoderChainHooks* hooks) const {
     // 3. QKV GEMMs, then Q/K-norm + RoPE in one in-place pass
     //    (attention.cpp:717-780: Qwen2's bias adds, two copies, two norms,
     //    two RoPE forwards); with the bias and no Q/K norm (Qwen2) the bias
-    //    add rides in the rotation pass
+    //    add rides in the rotation pass, and without Q/K norm a chain that
+    //    runs to the KV scatter does steps 3 and 4 in one launch
     h.qkv(d, s);
     const bool bias = d.q_bias != nullptr || d.k_bias != nullptr;
-    if (bias && d.use_qk_norm) {  // bias, then norm: no model has both; kept unfused
-        const int64_t qn = d.num_heads * d.head_dim, kn = d.num_kv_heads * d.head_dim;
-        if (d.num_heads > 0)
-            check(mi_add_bias_f16(d.q, d.q_bias, T, qn, T * qn, sv(s)), "q bias");
-        if (d.num_kv_heads > 0)
-            check(mi_add_bias_f16(d.k, d.k_bias, T, kn, T * kn, sv(s)), "k bias");
-    }
-    if (bias && !d.use_qk_norm)
-        check(mi_bias_rope_neox_qk_f16(d.q, d.k, d.q_bias, d.k_bias, d.positions, inv_freq_.data(),
-                                       T, d.num_heads, d.num_kv_heads, d.head_dim, sv(s)),
-              "bias + rope");
-    else if (d.use_qk_norm)
-        check(mi_qk_norm_rope_f16(d.q, d.k, d.q_norm, d.k_norm, d.positions, inv_freq_.data(), T,
-                                  d.num_heads, d.num_kv_heads, d.head_dim, d.qk_norm_eps,
-                                  /*add_one=*/0, sv(s)),
-              "qk norm + rope");
-    else
-        check(mi_rope_neox_qk_f16(d.q, d.k, d.positions, inv_freq_.data(), T, d.num_heads,
-                                  d.num_kv_heads, d.head_dim, sv(s)),
-              "rope");
-    if (last_ == MI_CHAIN_QK_ROPE) return;
-
-    // 4. K and V into the paged cache, one launch per segment
-    //    (attention.cpp:819-846: one scatter for K, one for V; Qwen2's V bias
-    //    added on the way, attention.cpp:735-739)
-    const int64_t kv_row = d.num_kv_heads * d.head_dim;
-    for (const mi_chain_kv_segment& g : segs_) {
-        if (g.B * g.S == 0) continue;
-        const auto* ks = static_cast<const uint16_t*>(d.k) + g.token_offset * kv_row;
-        const auto* vs = static_cast<const uint16_t*>(d.v) + g.token_offset * kv_row;
-        if (d.v_bias)
-            check(mi_paged_kv_scatter_kv_bias_f16(ks, vs, d.k_cache, d.v_cache, nullptr, d.v_bias,
-                                                  g.block_table, g.seq_len, g.start_pos, g.B, g.S,
-                                                  d.layer, d.num_blocks, d.num_kv_heads,
-                                                  d.head_dim, d.block_size, g.max_blocks_per_seq,
-                                                  sv(s)),
-                  "kv scatter + v bias");
+    if (last_ >= MI_CHAIN_KV_SCATTER && rope_kv_fused(s)) {
+        if (last_ == MI_CHAIN_KV_SCATTER) return;
+    } else {
+        if (bias && d.use_qk_norm) {  // bias, then norm: no model has both; kept unfused
+            const int64_t qn = d.num_heads * d.head_dim, kn = d.num_kv_heads * d.head_dim;
+            if (d.num_heads > 0)
+                check(mi_add_bias_f16(d.q, d.q_bias, T, qn, T * qn, sv(s)), "q bias");
+            if (d.num_kv_heads > 0)
+                check(mi_add_bias_f16(d.k, d.k_bias, T, kn, T * kn, sv(s)), "k bias");
+        }
+        if (bias && !d.use_qk_norm)
+            check(mi_bias_rope_neox_qk_f16(d.q, d.k, d.q_bias, d.k_bias, d.positions,
+                                           inv_freq_.data(), T, d.num_heads, d.num_kv_heads,
+                                           d.head_dim, sv(s)),
+                  "bias + rope");
+        else if (d.use_qk_norm)
+            check(mi_qk_norm_rope_f16(d.q, d.k, d.q_norm, d.k_norm, d.positions,
+                                      inv_freq_.data(), T, d.num_heads, d.num_kv_heads,
+                                      d.head_dim, d.qk_norm_eps, /*add_one=*/0, sv(s)),
+                  "qk norm + rope");
         else
-            check(mi_paged_kv_scatter_kv_f16(ks, vs, d.k_cache, d.v_cache, g.block_table,
-                                             g.seq_len, g.start_pos, g.B, g.S, d.layer,
-                                             d.num_blocks, d.num_kv_heads, d.head_dim,
-                                             d.block_size, g.max_blocks_per_seq, sv(s)),
-                  "kv scatter");
+            check(mi_rope_neox_qk_f16(d.q, d.k, d.positions, inv_freq_.data(), T, d.num_heads,
+                                      d.num_kv_heads, d.head_dim, sv(s)),
+                  "rope");
+        if (last_ == MI_CHAIN_QK_ROPE) return;
+
+        // 4. K and V into the paged cache, one launch per segment
+        //    (attention.cpp:819-846: one scatter for K, one for V; Qwen2's V bias
+        //    added on the way, attention.cpp:735-739)
+        const int64_t kv_row = d.num_kv_heads * d.head_dim;
+        for (const mi_chain_kv_segment& g : segs_) {
+            if (g.B * g.S == 0) continue;
+            const auto* ks = static_cast<const uint16_t*>(d.k) + g.token_offset * kv_row;
+            const auto* vs = static_cast<const uint16_t*>(d.v) + g.token_offset * kv_row;
+            if (d.v_bias)
+                check(mi_paged_kv_scatter_kv_bias_f16(
+                          ks, vs, d.k_cache, d.v_cache, nullptr, d.v_bias, g.block_table,
+                          g.seq_len, g.start_pos, g.B, g.S, d.layer, d.num_blocks,
+                          d.num_kv_heads, d.head_dim, d.block_size, g.max_blocks_per_seq, sv(s)),
+                      "kv scatter + v bias");
+            else
+                check(mi_paged_kv_scatter_kv_f16(ks, vs, d.k_cache, d.v_cache, g.block_table,
+                                                 g.seq_len, g.start_pos, g.B, g.S, d.layer,
+                                                 d.num_blocks, d.num_kv_heads, d.head_dim,
+                                                 d.block_size, g.max_blocks_per_seq, sv(s)),
+                      "kv scatter");
+        }
+        if (last_ == MI_CHAIN_KV_SCATTER) return;
     }
-    if (last_ == MI_CHAIN_KV_SCATTER) return;
 
     // 5. attention + O GEMM, then residual add fused with the post-attention
     //    norm (transformer_model.cpp:591-603, 605-625)

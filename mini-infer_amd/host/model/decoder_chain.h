@@ -47,6 +47,7 @@ public:
 
 private:
     void validate_() const;
+    bool rope_kv_fused(hipStream_t stream) const;
 
     mi_chain_desc d_;
     int last_;

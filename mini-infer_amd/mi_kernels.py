@@ -47,6 +47,8 @@ SIGNATURES = {
     "mi_add_bias_f16": [_c_void_p, _c_void_p, _i64, _i64, _i64, _c_void_p],
     "mi_bias_rope_neox_qk_f16": [_c_void_p] * 5 + [_c_void_p, _i64, _i64, _i64, _i64, _c_void_p],
     "mi_paged_kv_scatter_kv_bias_f16": [_c_void_p] * 9 + [_i64] * 8 + [_c_void_p],
+    "mi_rope_kv_scatter_f16": [_c_void_p] * 8 + [_i64] * 4 + [_c_void_p, _c_void_p] + [_i64] * 3
+                              + [_c_void_p, _int, _c_void_p],
     "mi_softmax_f16": [_c_void_p, _c_void_p, _i64, _i64, _c_void_p],
     "mi_embedding_gather_f16": [_c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64, _c_void_p],
     "mi_embedding_rmsnorm_f16": [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64,
@@ -286,6 +288,72 @@ def bias_rope_neox_qk(q, k, q_bias, k_bias, positions, inv_freq, stream=None):
         _ptr(q), _ptr(k) if k is not None else null, _ptr(q_bias),
         _ptr(k_bias) if k is not None else null, _ptr(positions), p, T, Hq, Hkv, hd,
         _stream(stream)), "mi_bias_rope_neox_qk_f16")
+    return q, k
+
+
+class KvSegment(ctypes.Structure):
+    """mi_kv_segment: tokens [token_offset, token_offset + B*S) of a step in
+    the [B, S] scatter layout, with int32 device block_table / seq_len /
+    start_pos."""
+    _fields_ = [("token_offset", _i64), ("B", _i64), ("S", _i64), ("block_table", _c_void_p),
+                ("seq_len", _c_void_p), ("start_pos", _c_void_p), ("max_blocks_per_seq", _i64)]
+
+
+def rope_kv_scatter(q, k, v, positions, inv_freq, k_cache, v_cache, layer: int, block_size: int,
+                    segments, q_bias=None, k_bias=None, v_bias=None, stream=None):
+    """One launch: NeoX RoPE of q [T, Hq, hd] and k [T, Hkv, hd] in place and
+    the rotated K and V [T, Hkv, hd] rows written into k_cache / v_cache
+    [L, num_blocks, Hkv, bs, hd] for the tokens of `segments` (dicts with
+    token_offset, S, block_table [B, max_blocks], seq_len [B], start_pos [B]).
+    With q_bias / k_bias / v_bias (all three) the biases are added first."""
+    torch = _torch()
+    _need(q, _f16(), "q"); _need(k, _f16(), "k"); _need(v, _f16(), "v")
+    _need(positions, torch.int64, "positions")
+    _need(k_cache, _f16(), "k_cache"); _need(v_cache, _f16(), "v_cache")
+    if q.dim() != 3 or k.dim() != 3 or v.shape != k.shape:
+        raise ValueError("q must be [T, Hq, hd], k and v [T, Hkv, hd]")
+    T, Hq, hd = q.shape
+    Hkv = k.shape[1]
+    if k.shape[0] != T or k.shape[2] != hd or positions.numel() != T:
+        raise ValueError("k / positions do not match q")
+    if k_cache.dim() != 5 or v_cache.shape != k_cache.shape:
+        raise ValueError("caches must be [L, num_blocks, Hkv, bs, hd], equal shapes")
+    L, NB, Hc, bs, Dc = k_cache.shape
+    if Hc != Hkv or Dc != hd or bs != block_size or not 0 <= layer < L:
+        raise ValueError("cache shape does not match k / block_size / layer")
+    biases = (q_bias, k_bias, v_bias)
+    if any(b is not None for b in biases):
+        for b, n, h in zip(biases, ("q_bias", "k_bias", "v_bias"), (Hq, Hkv, Hkv)):
+            if b is None:
+                raise ValueError("set q_bias, k_bias and v_bias together")
+            _need(b, _f16(), n)
+            if b.numel() != h * hd:
+                raise ValueError(f"{n} must hold {h} * head_dim entries")
+    segs = (KvSegment * max(1, len(segments)))()
+    for i, g in enumerate(segments):
+        bt = g["block_table"]
+        for t, n in ((bt, "block_table"), (g["seq_len"], "seq_len"),
+                     (g["start_pos"], "start_pos")):
+            _need(t, torch.int32, n)
+        if bt.dim() != 2 or g["seq_len"].numel() != bt.shape[0] or \
+                g["start_pos"].numel() != bt.shape[0]:
+            raise ValueError("segment: block_table [B, max_blocks], seq_len and start_pos [B]")
+        segs[i].token_offset = g["token_offset"]
+        segs[i].B = bt.shape[0]
+        segs[i].S = g["S"]
+        segs[i].block_table = _ptr(bt).value
+        segs[i].seq_len = _ptr(g["seq_len"]).value
+        segs[i].start_pos = _ptr(g["start_pos"]).value
+        segs[i].max_blocks_per_seq = bt.shape[1]
+    arr, p = _inv_freq_buffer(inv_freq)
+    if arr.size != hd // 2:
+        raise ValueError("inv_freq must hold head_dim/2 entries")
+    null = ctypes.c_void_p(0)
+    bp = [_ptr(b) if b is not None else null for b in biases]
+    _check(load_library().mi_rope_kv_scatter_f16(
+        _ptr(q), _ptr(k), _ptr(v), bp[0], bp[1], bp[2], _ptr(positions), p, T, Hq, Hkv, hd,
+        _ptr(k_cache), _ptr(v_cache), layer, NB, block_size, segs, len(segments),
+        _stream(stream)), "mi_rope_kv_scatter_f16")
     return q, k
 
 
