@@ -38,6 +38,21 @@ void launch_bias_rope_qk(__half* q, __half* k, const __half* q_bias, const __hal
                          const int64_t* positions_d, const float* inv_freq_h, int T, int Hq,
                          int Hkv, int head_dim, hipStream_t stream);
 
+// Attention pre-processing of one [B, S] batch without Q/K norm, in one
+// launch where the shape allows: launch_rope_qk (launch_bias_rope_qk when the
+// biases are given: all three or none) on q [B*S, Hq, hd] and k [B*S, Hkv, hd],
+// then the rotated k and v (+ v_bias) into k_cache / v_cache as
+// launch_paged_kv_scatter_kv places them (block_table [B, max_blocks_per_seq],
+// seq_len [B], start_pos [B], device).  Shapes the one-launch kernel does not
+// take run as those separate launches; results are the same bit for bit.
+void launch_rope_kv_scatter(__half* q, __half* k, const __half* v, const __half* q_bias,
+                            const __half* k_bias, const __half* v_bias,
+                            const int64_t* positions_d, const float* inv_freq_h, int B, int S,
+                            int Hq, int Hkv, int head_dim, __half* k_cache, __half* v_cache,
+                            const int* block_table, const int* seq_len, const int* start_pos,
+                            int layer, int num_blocks, int block_size, int max_blocks_per_seq,
+                            hipStream_t stream);
+
 // In place: per-head RMSNorm of q / k with q_weight / k_weight [head_dim]
 // (f(w) = w, or 1 + w when add_one), rounded to fp16, then the NeoX rotation
 // of launch_rope_qk -- the Q/K-norm + RoPE sequence in one pass.

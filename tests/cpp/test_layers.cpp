@@ -110,7 +110,8 @@ void cpu_checks() {
     a = std::move(m);
     EXPECT(a.data() == mp && m.data() == nullptr && m.numel() == 0 && !m.owns_data(),
            "move assignment takes the buffer and empties the source");
-    a = std::move(a);  // self-move keeps the tensor
+    Tensor& alias = a;
+    a = std::move(alias);  // self-move keeps the tensor
     EXPECT(a.data() == mp && a.numel() == 24, "self move-assignment is a no-op");
     EXPECT(std::string(mini_infer::dtype_name(DType::INT64)) == "int64", "dtype_name");
     EXPECT(throws([] { Tensor bad({-1}, DType::FP32, Device::cpu()); }), "negative dim throws");
@@ -407,6 +408,47 @@ void gpu_checks() {
             static_cast<const int*>(spd.data()), B, S, 0, NB, Hk, D, BS, MB, 0);
         EXPECT(bit_equal(kcd, kref.data(), "launch_paged_kv_scatter_kv (K)"), "kv scatter K");
         EXPECT(bit_equal(vcd, vref.data(), "launch_paged_kv_scatter_kv (V)"), "kv scatter V");
+
+        // RoPE + K/V scatter in one call, against launch_rope_qk then
+        // launch_paged_kv_scatter_kv: Hq = 8 takes the one-launch kernel,
+        // Hq = 40 (44 heads x 8 slices > 256 lanes) the separate launches
+        for (int Hq : {8, 40}) {
+            const int T = B * S;
+            Tensor q = reftest_f16({T, Hq, D}, 1.0f, 46 + Hq);
+            std::vector<float> inv(D / 2);
+            mio_rope_inv_freq(inv.data(), D, 1e6f);
+            std::vector<int64_t> pos(T);
+            mio_fill_uniform_int64(pos.data(), T, 47, 0, 30000);
+            Tensor pt(std::vector<int64_t>{T}, DType::INT64, Device::cpu());
+            std::memcpy(pt.data(), pos.data(), pos.size() * 8);
+            Tensor pd = pt.to(Device::cuda(0));
+            const auto* pp = static_cast<const int64_t*>(pd.data());
+            Tensor qa = q.to(Device::cuda(0)), ka = src.to(Device::cuda(0));
+            Tensor kca = cache.to(Device::cuda(0)), vca = vcache.to(Device::cuda(0));
+            mini_infer::kernels::launch_rope_qk(static_cast<__half*>(qa.data()),
+                                                static_cast<__half*>(ka.data()), pp, inv.data(),
+                                                T, Hq, Hk, D, 0);
+            mini_infer::kernels::launch_paged_kv_scatter_kv(
+                static_cast<const __half*>(ka.data()), static_cast<const __half*>(vsd.data()),
+                static_cast<__half*>(kca.data()), static_cast<__half*>(vca.data()),
+                static_cast<const int*>(btd.data()), static_cast<const int*>(sld.data()),
+                static_cast<const int*>(spd.data()), B, S, 1, NB, Hk, D, BS, MB, 0);
+            Tensor qb = q.to(Device::cuda(0)), kb = src.to(Device::cuda(0));
+            Tensor kcb = cache.to(Device::cuda(0)), vcb = vcache.to(Device::cuda(0));
+            mini_infer::kernels::launch_rope_kv_scatter(
+                static_cast<__half*>(qb.data()), static_cast<__half*>(kb.data()),
+                static_cast<const __half*>(vsd.data()), nullptr, nullptr, nullptr, pp, inv.data(),
+                B, S, Hq, Hk, D, static_cast<__half*>(kcb.data()), static_cast<__half*>(vcb.data()),
+                static_cast<const int*>(btd.data()), static_cast<const int*>(sld.data()),
+                static_cast<const int*>(spd.data()), 1, NB, BS, MB, 0);
+            Tensor qah = qa.to(Device::cpu()), kah = ka.to(Device::cpu());
+            Tensor kcah = kca.to(Device::cpu()), vcah = vca.to(Device::cpu());
+            const bool ok = bit_equal(qb, bits(qah), "launch_rope_kv_scatter (Q)") &&
+                            bit_equal(kb, bits(kah), "launch_rope_kv_scatter (K)") &&
+                            bit_equal(kcb, bits(kcah), "launch_rope_kv_scatter (K cache)") &&
+                            bit_equal(vcb, bits(vcah), "launch_rope_kv_scatter (V cache)");
+            EXPECT(ok, Hq == 8 ? "rope + kv scatter, one launch" : "rope + kv scatter, fallback");
+        }
 
         const int R = 3, V = 152064;
         Tensor lg = reftest_f16({R, V}, 8.0f, 43);
