@@ -743,9 +743,12 @@ int launch_qk_norm_rope(half_t* q, int64_t Hq, half_t* k, int64_t Hkv, const hal
 // pre-processing of a model without Q/K norm (Qwen2: with the q/k/v_proj
 // bias) -- the reference's RoPE pair and two launch_paged_kv_scatter calls
 // per sequence group (src/layers/attention.cpp:779-780, :823-846) in one
-// launch.  K is not re-read for the scatter.  Lanes 0..255 take the
-// (head, slice) units of the token as rope_kernel does; the lanes after them
-// carry V's 16-byte vectors.  The token's cache slot comes from the segment
+// launch.  K is not re-read for the scatter.  256 lanes take the (head,
+// slice) units of the token as rope_kernel does, and lane j also carries V's
+// 16-byte vector j (a 256-lane workgroup keeps rope_kernel's residency of
+// 8 workgroups per CU; 64 extra V lanes made it 6: 0.4-0.9 us slower at
+// Qwen2.5's shape, T = 6064).  Cache rows are written through to memory ("nt sc1"), as the
+// scatter kernel writes them.  The token's cache slot comes from the segment
 // holding it (workgroup-uniform scalar lookups issued with the data loads).
 // ---------------------------------------------------------------------------
 constexpr int kMaxKvSegs = 8;
@@ -758,7 +761,7 @@ struct KvSegs {
 };
 
 template <bool BIAS>
-__global__ __launch_bounds__(1024) void rope_kv_kernel(half_t* q, half_t* k, const half_t* v,
+__global__ __launch_bounds__(256) void rope_kv_kernel(half_t* q, half_t* k, const half_t* v,
                                                        int Hq, int Hkv, int hd,
                                                        const int64_t* __restrict__ positions,
                                                        InvFreq inv, const half_t* __restrict__ bq,
@@ -789,8 +792,8 @@ __global__ __launch_bounds__(1024) void rope_kv_kernel(half_t* q, half_t* k, con
             b2 = ld8(bp + half + c * 8);
         }
     }
-    const int vj = tid - 256;  // V vector of this lane
-    const bool vlane = vj >= 0 && vj < Hkv * (hd >> 3);
+    const int vj = tid;  // V vector of this lane (Hkv * hd / 8 <= 256)
+    const bool vlane = vj < Hkv * (hd >> 3);
     h8 vv = h8(0), vb = h8(0);
     if (vlane) {
         vv = ld8_stream(v + tok * Hkv * hd + vj * 8);
@@ -847,8 +850,8 @@ __global__ __launch_bounds__(1024) void rope_kv_kernel(half_t* q, half_t* k, con
         st8_out<MI_WT_ROPE>(hp + half + c * 8, y2);
         if (h >= Hq && dst_base >= 0) {
             half_t* kd = k_cache + dst_base + static_cast<int64_t>(h - Hq) * bs * hd;
-            st8_stream(kd + c * 8, y1);
-            st8_stream(kd + half + c * 8, y2);
+            st8_stream_wt(kd + c * 8, y1);
+            st8_stream_wt(kd + half + c * 8, y2);
         }
     }
     if (vlane && dst_base >= 0) {
@@ -859,7 +862,7 @@ __global__ __launch_bounds__(1024) void rope_kv_kernel(half_t* q, half_t* k, con
         const int per_head = hd >> 3;
         const int vh = small_div(vj, 1.0f / static_cast<float>(per_head));
         const int vd = (vj - vh * per_head) * 8;
-        st8_stream(v_cache + dst_base + static_cast<int64_t>(vh) * bs * hd + vd, vv);
+        st8_stream_wt(v_cache + dst_base + static_cast<int64_t>(vh) * bs * hd + vd, vv);
     }
 }
 
@@ -985,10 +988,10 @@ extern "C" int mi_rope_kv_scatter_f16(void* q, void* k, const void* v, const voi
         (num_segments > 0 && !segments) ||
         (bias && (!q_bias || !k_bias || !v_bias)))
         return MI_ERR_INVALID_ARGUMENT;
-    // one workgroup per token: lanes for the token's Q/K slices (<= 256) and
-    // V's vectors (<= 768), 16-byte vectors, few segments
+    // one 256-lane workgroup per token: its Q/K slices and V's vectors one
+    // per lane (both <= 256), 16-byte vectors, few segments
     if (head_dim % 16 != 0 || head_dim / 2 > mi::kMaxHalf || (Hq + Hkv) * (head_dim / 16) > 256 ||
-        Hkv * head_dim / 8 > 768 || num_segments > mi::kMaxKvSegs || T > mi::kMaxGridX ||
+        Hkv * head_dim / 8 > 256 || num_segments > mi::kMaxKvSegs || T > mi::kMaxGridX ||
         block_size > INT32_MAX)
         return MI_ERR_UNSUPPORTED;
     for (const void* p : {static_cast<const void*>(q), static_cast<const void*>(k), v,
@@ -1022,8 +1025,7 @@ extern "C" int mi_rope_kv_scatter_f16(void* q, void* k, const void* v, const voi
     }
     mi::InvFreq inv;
     if (!mi::load_inv_freq(inv_freq_host, head_dim / 2, inv)) return MI_ERR_INVALID_ARGUMENT;
-    const int vlanes = static_cast<int>(mi::ceil_div(Hkv * head_dim / 8, mi::kWave)) * mi::kWave;
-    const dim3 g(static_cast<unsigned>(T)), b(256 + vlanes);
+    const dim3 g(static_cast<unsigned>(T)), b(256);
     auto* qh = static_cast<half_t*>(q);
     auto* kh = static_cast<half_t*>(k);
     const auto* vh = static_cast<const half_t*>(v);

@@ -87,6 +87,7 @@ def _dev_segs(segs, dev):
     (48, 8, 4, 256, "ragged"),
     (48, 4, 2, 16, "ragged"),
     (48, 15, 1, 32, "ragged"),     # 16 units per token: Q/K lanes < 256, 4 V lanes
+    (48, 16, 16, 128, "ragged"),   # MHA at the limit: 256 Q/K units and 256 V vectors
     (20, 8, 8, 128, "none"),       # no segment: RoPE only
 ])
 @pytest.mark.parametrize("bias", [False, True])
