@@ -533,6 +533,26 @@ def all_kernels(mk, dev, iters, warmup):
         out.append(report("rope_kv_scatter" + tag + "_unfused",
                           "RoPE launch + 3 per-segment K+V scatters" + (", bias" if extra else ""),
                           nb + (len(extra) and 36 * 128 * 2), sec, T))
+    # 5j. config 5's form: Q/K RMSNorm + RoPE + K/V scatter in one launch,
+    # against qk_norm_rope then the three per-segment scatters
+    nbn = nb + 2 * 128 * 2
+    sec = time_launches(lambda i: mk.qk_norm_rope_kv_scatter(sets[i][0], sets[i][1], sets[i][2],
+                                                             wq, wk, pos, inv, kcache, vcache, 0,
+                                                             bs, segs), ns, iters, warmup)
+    out.append(report("qk_norm_rope_kv_scatter",
+                      "chain Q[6064,28,128]+K,V[6064,4,128] -> cache bs=16, Q/K norm", nbn, sec, T))
+
+    def unfused_norm(i):
+        qx, kx, vx = sets[i]
+        mk.qk_norm_rope(qx, kx, wq, wk, pos, inv)
+        for g in segs:
+            B, S, o = g["block_table"].shape[0], g["S"], g["token_offset"]
+            mk.paged_kv_scatter(kx[o:o + B * S].view(B, S, H, hd), kcache, g["block_table"],
+                                g["seq_len"], g["start_pos"], 0, bs,
+                                v_src=vx[o:o + B * S].view(B, S, H, hd), v_cache=vcache)
+    sec = time_launches(unfused_norm, ns, iters, warmup)
+    out.append(report("qk_norm_rope_kv_scatter_unfused",
+                      "qk_norm_rope launch + 3 per-segment K+V scatters", nbn, sec, T))
     del sets, kcache, vcache
     torch.cuda.synchronize()
     for r in out:

@@ -156,6 +156,22 @@ int mi_rope_kv_scatter_f16(void* q, void* k, const void* v, const void* q_bias,
                            int64_t num_blocks, int64_t block_size,
                            const mi_kv_segment* segments, int num_segments, void* stream);
 
+/* mi_rope_kv_scatter_f16 for a model with Q/K norm (Gemma 3): the per-head
+ * RMSNorm of mi_qk_norm_rope_f16 (q_weight / k_weight [hd], f(w) = w or
+ * 1 + w when add_one, eps), then the rotation, with the normalised, rotated
+ * K rows and the V rows written into the paged caches, one launch.  Equals
+ * mi_qk_norm_rope_f16 followed by mi_paged_kv_scatter_kv_f16 per segment,
+ * bit for bit.  head_dim one of 16, 32, 64, 128, 256, 512, and the other
+ * limits of mi_rope_kv_scatter_f16; otherwise MI_ERR_UNSUPPORTED.  Replaces
+ * src/layers/attention.cpp:754-780 (two norms, RoPE pair) and :823-846. */
+int mi_qk_norm_rope_kv_scatter_f16(void* q, void* k, const void* v, const void* q_weight,
+                                   const void* k_weight, const int64_t* positions,
+                                   const float* inv_freq_host, int64_t T, int64_t Hq,
+                                   int64_t Hkv, int64_t head_dim, float eps, int add_one,
+                                   void* k_cache, void* v_cache, int64_t layer,
+                                   int64_t num_blocks, int64_t block_size,
+                                   const mi_kv_segment* segments, int num_segments, void* stream);
+
 /* Fused per-head RMSNorm + NeoX RoPE, in place, for Q [T, Hq, hd] and
  * K [T, Hkv, hd]: each head is normalised with its weight (q_weight or
  * k_weight, [hd]; f(w) = w, or 1 + w when add_one), rounded to fp16, then

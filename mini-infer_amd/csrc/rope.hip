@@ -760,20 +760,28 @@ struct KvSegs {
     const int* sp[kMaxKvSegs];
 };
 
-template <bool BIAS>
+// NORM (Gemma 3): the per-head Q/K RMSNorm of qk_norm_rope_kernel first --
+// the CPH = hd/16 lanes of a head sum their squares by DPP, the normalised
+// value is rounded to fp16 where the reference stores it, and the rotation
+// takes it from registers.  CPH = 0: head_dim known at run time (no norm).
+template <bool BIAS, bool NORM, int CPH>
 __global__ __launch_bounds__(256) void rope_kv_kernel(half_t* q, half_t* k, const half_t* v,
                                                        int Hq, int Hkv, int hd,
                                                        const int64_t* __restrict__ positions,
                                                        InvFreq inv, const half_t* __restrict__ bq,
                                                        const half_t* __restrict__ bk,
                                                        const half_t* __restrict__ bv,
-                                                       half_t* k_cache, half_t* v_cache, KvSegs sg,
-                                                       int64_t layer, int64_t num_blocks,
-                                                       int64_t bs) {
+                                                       const half_t* __restrict__ wq,
+                                                       const half_t* __restrict__ wk, float eps,
+                                                       float w_bias, half_t* k_cache,
+                                                       half_t* v_cache, KvSegs sg, int64_t layer,
+                                                       int64_t num_blocks, int64_t bs) {
+    static_assert(!(BIAS && NORM), "no model adds a QKV bias before a Q/K norm");
+    static_assert(!NORM || (CPH >= 1 && CPH <= 32), "the norm needs head_dim / 16 at compile time");
     __shared__ float cs[2 * kMaxHalf];
     const int64_t tok = blockIdx.x;
-    const int half = hd >> 1;
-    const int cph = half >> 3;  // 16-byte slices per half head
+    const int half = CPH ? CPH * 8 : hd >> 1;
+    const int cph = CPH ? CPH : half >> 3;  // 16-byte slices per half head
     const int units = (Hq + Hkv) * cph;
     const int tid = threadIdx.x;
 
@@ -781,22 +789,32 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(half_t* q, half_t* k, cons
     half_t* hp = nullptr;
     int h = 0, c = 0;
     if (tid < units) {
-        h = small_div(tid, 1.0f / static_cast<float>(cph));  // units < 2^22: exact
-        c = tid - h * cph;
-        hp = h < Hq ? q + (tok * Hq + h) * hd : k + (tok * Hkv + (h - Hq)) * hd;
+        if constexpr (CPH != 0) {
+            h = tid / CPH;
+            c = tid & (CPH - 1);
+        } else {
+            h = small_div(tid, 1.0f / static_cast<float>(cph));  // units < 2^22: exact
+            c = tid - h * cph;
+        }
+        hp = h < Hq ? q + (tok * Hq + h) * (2 * half) : k + (tok * Hkv + (h - Hq)) * (2 * half);
         x1 = ld8_stream(hp + c * 8);
         x2 = ld8_stream(hp + half + c * 8);
         if constexpr (BIAS) {  // a few KB every token re-reads: plain loads
-            const half_t* bp = h < Hq ? bq + h * hd : bk + (h - Hq) * hd;
+            const half_t* bp = h < Hq ? bq + h * (2 * half) : bk + (h - Hq) * (2 * half);
             b1 = ld8(bp + c * 8);
             b2 = ld8(bp + half + c * 8);
         }
+        if constexpr (NORM) {  // the norm weights [hd], as the biases
+            const half_t* wp = h < Hq ? wq : wk;
+            b1 = ld8(wp + c * 8);
+            b2 = ld8(wp + half + c * 8);
+        }
     }
     const int vj = tid;  // V vector of this lane (Hkv * hd / 8 <= 256)
-    const bool vlane = vj < Hkv * (hd >> 3);
+    const bool vlane = vj < Hkv * (half >> 2);
     h8 vv = h8(0), vb = h8(0);
     if (vlane) {
-        vv = ld8_stream(v + tok * Hkv * hd + vj * 8);
+        vv = ld8_stream(v + tok * Hkv * (2 * half) + vj * 8);
         if constexpr (BIAS) vb = ld8(bv + vj * 8);
     }
     const float fpos = static_cast<float>(positions[tok]);
@@ -819,7 +837,7 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(half_t* q, half_t* k, cons
         if (blk >= sg.mb[i]) break;
         const int64_t phys = sg.bt[i][b * sg.mb[i] + blk];
         if (phys >= 0 && phys < num_blocks)
-            dst_base = (layer * num_blocks + phys) * Hkv * bs * hd + (pos - blk * bs) * hd;
+            dst_base = ((layer * num_blocks + phys) * Hkv * bs + (pos - blk * bs)) * (2 * half);
         break;
     }
     if (tid < half) {
@@ -831,6 +849,18 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(half_t* q, half_t* k, cons
     }
     __syncthreads();
 
+    float rrms = 1.0f;
+    if constexpr (NORM) {  // every lane takes part in the DPP sum (idle lanes add zeros)
+        float ss = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const float f1 = (float)x1[e], f2 = (float)x2[e];
+            ss = fmaf(f1, f1, ss);
+            ss = fmaf(f2, f2, ss);
+        }
+        ss = group_sum<CPH ? CPH : 1>(ss);
+        rrms = rsqrtf(ss / static_cast<float>(CPH * 16) + eps);
+    }
     if (tid < units) {
         h8 y1, y2;
 #pragma unroll
@@ -843,13 +873,17 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(half_t* q, half_t* k, cons
                 a = (float)to_half(a + (float)b1[e]);
                 bb = (float)to_half(bb + (float)b2[e]);
             }
+            if constexpr (NORM) {  // the normalised value as the reference stores it (fp16)
+                a = (float)to_half(a * rrms * ((float)b1[e] + w_bias));
+                bb = (float)to_half(bb * rrms * ((float)b2[e] + w_bias));
+            }
             y1[e] = to_half(fp32_rounded(a * cv - bb * sv));
             y2[e] = to_half(fp32_rounded(bb * cv + a * sv));
         }
-        st8_out<MI_WT_ROPE>(hp + c * 8, y1);
-        st8_out<MI_WT_ROPE>(hp + half + c * 8, y2);
+        st8_out<NORM ? MI_WT_QKNR : MI_WT_ROPE>(hp + c * 8, y1);
+        st8_out<NORM ? MI_WT_QKNR : MI_WT_ROPE>(hp + half + c * 8, y2);
         if (h >= Hq && dst_base >= 0) {
-            half_t* kd = k_cache + dst_base + static_cast<int64_t>(h - Hq) * bs * hd;
+            half_t* kd = k_cache + dst_base + static_cast<int64_t>(h - Hq) * bs * (2 * half);
             st8_stream_wt(kd + c * 8, y1);
             st8_stream_wt(kd + half + c * 8, y2);
         }
@@ -859,10 +893,10 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(half_t* q, half_t* k, cons
 #pragma unroll
             for (int e = 0; e < 8; ++e) vv[e] = to_half((float)vv[e] + (float)vb[e]);
         }
-        const int per_head = hd >> 3;
-        const int vh = small_div(vj, 1.0f / static_cast<float>(per_head));
+        const int per_head = half >> 2;
+        const int vh = CPH ? vj / (CPH * 2) : small_div(vj, 1.0f / static_cast<float>(per_head));
         const int vd = (vj - vh * per_head) * 8;
-        st8_stream_wt(v_cache + dst_base + static_cast<int64_t>(vh) * bs * hd + vd, vv);
+        st8_stream_wt(v_cache + dst_base + static_cast<int64_t>(vh) * bs * (2 * half) + vd, vv);
     }
 }
 
@@ -971,42 +1005,47 @@ extern "C" int mi_bias_rope_neox_qk_f16(void* q, void* k, const void* q_bias, co
                            static_cast<const half_t*>(q_bias), static_cast<const half_t*>(k_bias));
 }
 
-extern "C" int mi_rope_kv_scatter_f16(void* q, void* k, const void* v, const void* q_bias,
-                                      const void* k_bias, const void* v_bias,
-                                      const int64_t* positions, const float* inv_freq_host,
-                                      int64_t T, int64_t Hq, int64_t Hkv, int64_t head_dim,
-                                      void* k_cache, void* v_cache, int64_t layer,
-                                      int64_t num_blocks, int64_t block_size,
-                                      const mi_kv_segment* segments, int num_segments,
-                                      void* stream) {
+namespace mi {
+namespace {
+
+// Shared checks and launch of rope_kv_kernel.  q_bias / k_bias / v_bias (all
+// or none) and q_weight / k_weight (NORM) exclude each other.
+int rope_kv_launch(void* q, void* k, const void* v, const void* q_bias, const void* k_bias,
+                   const void* v_bias, const void* q_weight, const void* k_weight, float eps,
+                   int add_one, const int64_t* positions, const float* inv_freq_host, int64_t T,
+                   int64_t Hq, int64_t Hkv, int64_t head_dim, void* k_cache, void* v_cache,
+                   int64_t layer, int64_t num_blocks, int64_t block_size,
+                   const mi_kv_segment* segments, int num_segments, void* stream) {
     if (T < 0 || Hq < 0 || Hkv < 0 || head_dim < 0 || layer < 0 || num_blocks < 0 ||
         block_size <= 0 || num_segments < 0)
         return MI_ERR_INVALID_ARGUMENT;
     if (T == 0) return MI_OK;
     const bool bias = q_bias || k_bias || v_bias;
+    const bool norm = q_weight || k_weight;
     if (!q || !k || !v || !positions || !k_cache || !v_cache || Hq < 1 || Hkv < 1 ||
-        (num_segments > 0 && !segments) ||
-        (bias && (!q_bias || !k_bias || !v_bias)))
+        (num_segments > 0 && !segments) || (bias && (!q_bias || !k_bias || !v_bias)) ||
+        (norm && (!q_weight || !k_weight)) || (bias && norm))
         return MI_ERR_INVALID_ARGUMENT;
     // one 256-lane workgroup per token: its Q/K slices and V's vectors one
     // per lane (both <= 256), 16-byte vectors, few segments
-    if (head_dim % 16 != 0 || head_dim / 2 > mi::kMaxHalf || (Hq + Hkv) * (head_dim / 16) > 256 ||
-        Hkv * head_dim / 8 > 256 || num_segments > mi::kMaxKvSegs || T > mi::kMaxGridX ||
+    if (head_dim % 16 != 0 || head_dim / 2 > kMaxHalf || (Hq + Hkv) * (head_dim / 16) > 256 ||
+        Hkv * head_dim / 8 > 256 || num_segments > kMaxKvSegs || T > kMaxGridX ||
         block_size > INT32_MAX)
         return MI_ERR_UNSUPPORTED;
     for (const void* p : {static_cast<const void*>(q), static_cast<const void*>(k), v,
                           static_cast<const void*>(k_cache), static_cast<const void*>(v_cache)})
-        if (!mi::aligned16(p)) return MI_ERR_UNSUPPORTED;
-    if (bias && !(mi::aligned16(q_bias) && mi::aligned16(k_bias) && mi::aligned16(v_bias)))
+        if (!aligned16(p)) return MI_ERR_UNSUPPORTED;
+    if (bias && !(aligned16(q_bias) && aligned16(k_bias) && aligned16(v_bias)))
         return MI_ERR_UNSUPPORTED;
+    if (norm && !(aligned16(q_weight) && aligned16(k_weight))) return MI_ERR_UNSUPPORTED;
     const int64_t qb = T * Hq * head_dim * 2, kb = T * Hkv * head_dim * 2;
     const int64_t cb = (layer + 1) * num_blocks * Hkv * block_size * head_dim * 2;
     const void* bufs[5] = {q, k, v, k_cache, v_cache};
     const int64_t lens[5] = {qb, kb, kb, cb, cb};
     for (int i = 0; i < 5; ++i)
         for (int j = i + 1; j < 5; ++j)
-            if (mi::overlaps(bufs[i], lens[i], bufs[j], lens[j])) return MI_ERR_ALIASING;
-    mi::KvSegs sg{};
+            if (overlaps(bufs[i], lens[i], bufs[j], lens[j])) return MI_ERR_ALIASING;
+    KvSegs sg{};
     sg.n = num_segments;
     for (int i = 0; i < num_segments; ++i) {
         const mi_kv_segment& g = segments[i];
@@ -1023,27 +1062,74 @@ extern "C" int mi_rope_kv_scatter_f16(void* q, void* k, const void* v, const voi
         sg.sl[i] = g.seq_len;
         sg.sp[i] = g.start_pos;
     }
-    mi::InvFreq inv;
-    if (!mi::load_inv_freq(inv_freq_host, head_dim / 2, inv)) return MI_ERR_INVALID_ARGUMENT;
+    InvFreq inv;
+    if (!load_inv_freq(inv_freq_host, head_dim / 2, inv)) return MI_ERR_INVALID_ARGUMENT;
     const dim3 g(static_cast<unsigned>(T)), b(256);
     auto* qh = static_cast<half_t*>(q);
     auto* kh = static_cast<half_t*>(k);
     const auto* vh = static_cast<const half_t*>(v);
+    const auto* bqh = static_cast<const half_t*>(q_bias);
+    const auto* bkh = static_cast<const half_t*>(k_bias);
+    const auto* bvh = static_cast<const half_t*>(v_bias);
+    const auto* wqh = static_cast<const half_t*>(q_weight);
+    const auto* wkh = static_cast<const half_t*>(k_weight);
     auto* kc = static_cast<half_t*>(k_cache);
     auto* vc = static_cast<half_t*>(v_cache);
-    const hipStream_t s = mi::as_stream(stream);
+    const hipStream_t s = as_stream(stream);
     const int hq = static_cast<int>(Hq), hk = static_cast<int>(Hkv), d = static_cast<int>(head_dim);
-    if (bias)
-        mi::rope_kv_kernel<true><<<g, b, 0, s>>>(qh, kh, vh, hq, hk, d, positions, inv,
-                                                 static_cast<const half_t*>(q_bias),
-                                                 static_cast<const half_t*>(k_bias),
-                                                 static_cast<const half_t*>(v_bias), kc, vc, sg,
-                                                 layer, num_blocks, block_size);
-    else
-        mi::rope_kv_kernel<false><<<g, b, 0, s>>>(qh, kh, vh, hq, hk, d, positions, inv, nullptr,
-                                                  nullptr, nullptr, kc, vc, sg, layer, num_blocks,
-                                                  block_size);
-    return mi::launch_status();
+    const float wb = add_one ? 1.0f : -0.0f;  // w + (-0) == w, also for w = -0
+#define MI_RKV_ARGS                                                                           \
+    qh, kh, vh, hq, hk, d, positions, inv, bqh, bkh, bvh, wqh, wkh, eps, wb, kc, vc, sg, layer, \
+        num_blocks, block_size
+    if (norm) {
+        switch (head_dim / 16) {
+            case 1: rope_kv_kernel<false, true, 1><<<g, b, 0, s>>>(MI_RKV_ARGS); break;
+            case 2: rope_kv_kernel<false, true, 2><<<g, b, 0, s>>>(MI_RKV_ARGS); break;
+            case 4: rope_kv_kernel<false, true, 4><<<g, b, 0, s>>>(MI_RKV_ARGS); break;
+            case 8: rope_kv_kernel<false, true, 8><<<g, b, 0, s>>>(MI_RKV_ARGS); break;
+            case 16: rope_kv_kernel<false, true, 16><<<g, b, 0, s>>>(MI_RKV_ARGS); break;
+            case 32: rope_kv_kernel<false, true, 32><<<g, b, 0, s>>>(MI_RKV_ARGS); break;
+            default: return MI_ERR_UNSUPPORTED;  // head_dim not 16 * 2^k
+        }
+    } else if (bias) {
+        rope_kv_kernel<true, false, 0><<<g, b, 0, s>>>(MI_RKV_ARGS);
+    } else {
+        rope_kv_kernel<false, false, 0><<<g, b, 0, s>>>(MI_RKV_ARGS);
+    }
+#undef MI_RKV_ARGS
+    return launch_status();
+}
+
+}  // namespace
+}  // namespace mi
+
+extern "C" int mi_rope_kv_scatter_f16(void* q, void* k, const void* v, const void* q_bias,
+                                      const void* k_bias, const void* v_bias,
+                                      const int64_t* positions, const float* inv_freq_host,
+                                      int64_t T, int64_t Hq, int64_t Hkv, int64_t head_dim,
+                                      void* k_cache, void* v_cache, int64_t layer,
+                                      int64_t num_blocks, int64_t block_size,
+                                      const mi_kv_segment* segments, int num_segments,
+                                      void* stream) {
+    return mi::rope_kv_launch(q, k, v, q_bias, k_bias, v_bias, nullptr, nullptr, 0.0f, 0,
+                              positions, inv_freq_host, T, Hq, Hkv, head_dim, k_cache, v_cache,
+                              layer, num_blocks, block_size, segments, num_segments, stream);
+}
+
+extern "C" int mi_qk_norm_rope_kv_scatter_f16(void* q, void* k, const void* v,
+                                              const void* q_weight, const void* k_weight,
+                                              const int64_t* positions,
+                                              const float* inv_freq_host, int64_t T, int64_t Hq,
+                                              int64_t Hkv, int64_t head_dim, float eps,
+                                              int add_one, void* k_cache, void* v_cache,
+                                              int64_t layer, int64_t num_blocks,
+                                              int64_t block_size, const mi_kv_segment* segments,
+                                              int num_segments, void* stream) {
+    if (!q_weight || !k_weight) return MI_ERR_INVALID_ARGUMENT;
+    return mi::rope_kv_launch(q, k, v, nullptr, nullptr, nullptr, q_weight, k_weight, eps,
+                              add_one, positions, inv_freq_host, T, Hq, Hkv, head_dim, k_cache,
+                              v_cache, layer, num_blocks, block_size, segments, num_segments,
+                              stream);
 }
 
 extern "C" int mi_qk_norm_rope_f16(void* q, void* k, const void* q_weight, const void* k_weight,

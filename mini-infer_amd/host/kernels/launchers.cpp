@@ -195,6 +195,30 @@ void launch_rope_kv_scatter(__half* q, __half* k, const __half* v, const __half*
                                     max_blocks_per_seq, stream);
 }
 
+void launch_qk_norm_rope_kv_scatter(__half* q, __half* k, const __half* v,
+                                    const __half* q_weight, const __half* k_weight,
+                                    const int64_t* positions_d, const float* inv_freq_h, int B,
+                                    int S, int Hq, int Hkv, int head_dim, float eps, int add_one,
+                                    __half* k_cache, __half* v_cache, const int* block_table,
+                                    const int* seq_len, const int* start_pos, int layer,
+                                    int num_blocks, int block_size, int max_blocks_per_seq,
+                                    hipStream_t stream) {
+    const mi_kv_segment seg{0, B, S, block_table, seq_len, start_pos, max_blocks_per_seq};
+    const int64_t T = static_cast<int64_t>(B) * S;
+    const int st = mi_qk_norm_rope_kv_scatter_f16(
+        q, k, v, q_weight, k_weight, positions_d, inv_freq_h, T, Hq, Hkv, head_dim, eps, add_one,
+        k_cache, v_cache, layer, num_blocks, block_size, &seg, T > 0 ? 1 : 0, sv(stream));
+    if (st != MI_ERR_UNSUPPORTED) {
+        check(st, "launch_qk_norm_rope_kv_scatter");
+        return;
+    }
+    launch_qk_norm_rope(q, k, q_weight, k_weight, positions_d, inv_freq_h, B * S, Hq, Hkv,
+                        head_dim, eps, add_one, stream);
+    launch_paged_kv_scatter_kv(k, v, k_cache, v_cache, block_table, seq_len, start_pos, B, S,
+                               layer, num_blocks, Hkv, head_dim, block_size, max_blocks_per_seq,
+                               stream);
+}
+
 void launch_qk_norm_rope(__half* q, __half* k, const __half* q_weight, const __half* k_weight,
                          const int64_t* positions_d, const float* inv_freq_h, int T, int Hq,
                          int Hkv, int head_dim, float eps, int add_one, hipStream_t stream) {

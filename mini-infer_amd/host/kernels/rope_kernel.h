@@ -53,6 +53,19 @@ void launch_rope_kv_scatter(__half* q, __half* k, const __half* v, const __half*
                             int layer, int num_blocks, int block_size, int max_blocks_per_seq,
                             hipStream_t stream);
 
+// launch_rope_kv_scatter for a model with Q/K norm: launch_qk_norm_rope's
+// per-head RMSNorm (q_weight / k_weight [head_dim], eps, add_one) before the
+// rotation, then the scatter of the rotated K and of V, one launch where the
+// shape allows (else the separate launches; the same results bit for bit).
+void launch_qk_norm_rope_kv_scatter(__half* q, __half* k, const __half* v,
+                                    const __half* q_weight, const __half* k_weight,
+                                    const int64_t* positions_d, const float* inv_freq_h, int B,
+                                    int S, int Hq, int Hkv, int head_dim, float eps, int add_one,
+                                    __half* k_cache, __half* v_cache, const int* block_table,
+                                    const int* seq_len, const int* start_pos, int layer,
+                                    int num_blocks, int block_size, int max_blocks_per_seq,
+                                    hipStream_t stream);
+
 // In place: per-head RMSNorm of q / k with q_weight / k_weight [head_dim]
 // (f(w) = w, or 1 + w when add_one), rounded to fp16, then the NeoX rotation
 // of launch_rope_qk -- the Q/K-norm + RoPE sequence in one pass.

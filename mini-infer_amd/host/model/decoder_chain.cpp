@@ -97,13 +97,15 @@ void DecoderChain::validate_() const {
     }
 }
 
-// Steps 3 and 4 in one launch when the model has no Q/K norm: the rotation
-// pass also writes the rotated K rows and the V rows (+ V bias) into the
-// paged cache, so K is not re-read.  False (nothing launched) for shapes the
-// one-launch kernel does not take; the caller then runs the two steps.
+// Steps 3 and 4 in one launch: the (Q/K-norm +) rotation pass also writes
+// the rotated K rows and the V rows (+ V bias) into the paged cache, so K is
+// not re-read.  False (nothing launched) for shapes the one-launch kernel
+// does not take, and for a QKV bias together with Q/K norm; the caller then
+// runs the two steps.
 bool DecoderChain::rope_kv_fused(hipStream_t s) const {
     const mi_chain_desc& d = d_;
-    if (d.use_qk_norm || d.num_heads <= 0 || d.num_kv_heads <= 0) return false;
+    const bool bias = d.q_bias != nullptr;
+    if ((d.use_qk_norm && bias) || d.num_heads <= 0 || d.num_kv_heads <= 0) return false;
     mi_kv_segment fs[8];
     int n = 0;
     for (const mi_chain_kv_segment& g : segs_) {
@@ -112,12 +114,20 @@ bool DecoderChain::rope_kv_fused(hipStream_t s) const {
         fs[n++] = mi_kv_segment{g.token_offset, g.B, g.S, g.block_table, g.seq_len,
                                 g.start_pos, g.max_blocks_per_seq};
     }
-    const int st = mi_rope_kv_scatter_f16(d.q, d.k, d.v, d.q_bias, d.k_bias, d.v_bias,
-                                          d.positions, inv_freq_.data(), d.T, d.num_heads,
-                                          d.num_kv_heads, d.head_dim, d.k_cache, d.v_cache,
-                                          d.layer, d.num_blocks, d.block_size, fs, n, sv(s));
+    const int st =
+        d.use_qk_norm
+            ? mi_qk_norm_rope_kv_scatter_f16(d.q, d.k, d.v, d.q_norm, d.k_norm, d.positions,
+                                             inv_freq_.data(), d.T, d.num_heads, d.num_kv_heads,
+                                             d.head_dim, d.qk_norm_eps, /*add_one=*/0, d.k_cache,
+                                             d.v_cache, d.layer, d.num_blocks, d.block_size, fs,
+                                             n, sv(s))
+            : mi_rope_kv_scatter_f16(d.q, d.k, d.v, d.q_bias, d.k_bias, d.v_bias, d.positions,
+                                     inv_freq_.data(), d.T, d.num_heads, d.num_kv_heads,
+                                     d.head_dim, d.k_cache, d.v_cache, d.layer, d.num_blocks,
+                                     d.block_size, fs, n, sv(s));
     if (st == MI_ERR_UNSUPPORTED) return false;
-    check(st, d.q_bias ? "bias + rope + kv scatter" : "rope + kv scatter");
+    check(st, d.use_qk_norm ? "qk norm + rope + kv scatter"
+                            : (bias ? "bias + rope + kv scatter" : "rope + kv scatter"));
     return true;
 }
 
@@ -149,8 +159,8 @@ void DecoderChain::run(hipStream_t s, DecoderChainHooks* hooks) const {
     // 3. QKV GEMMs, then Q/K-norm + RoPE in one in-place pass
     //    (attention.cpp:717-780: Qwen2's bias adds, two copies, two norms,
     //    two RoPE forwards); with the bias and no Q/K norm (Qwen2) the bias
-    //    add rides in the rotation pass, and without Q/K norm a chain that
-    //    runs to the KV scatter does steps 3 and 4 in one launch
+    //    add rides in the rotation pass; a chain that runs to the KV scatter
+    //    does steps 3 and 4 in one launch
     h.qkv(d, s);
     const bool bias = d.q_bias != nullptr || d.k_bias != nullptr;
     if (last_ >= MI_CHAIN_KV_SCATTER && rope_kv_fused(s)) {

@@ -49,6 +49,9 @@ SIGNATURES = {
     "mi_paged_kv_scatter_kv_bias_f16": [_c_void_p] * 9 + [_i64] * 8 + [_c_void_p],
     "mi_rope_kv_scatter_f16": [_c_void_p] * 8 + [_i64] * 4 + [_c_void_p, _c_void_p] + [_i64] * 3
                               + [_c_void_p, _int, _c_void_p],
+    "mi_qk_norm_rope_kv_scatter_f16": [_c_void_p] * 6 + [_c_void_p] + [_i64] * 4 + [_f32, _int]
+                                      + [_c_void_p, _c_void_p] + [_i64] * 3
+                                      + [_c_void_p, _int, _c_void_p],
     "mi_softmax_f16": [_c_void_p, _c_void_p, _i64, _i64, _c_void_p],
     "mi_embedding_gather_f16": [_c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64, _c_void_p],
     "mi_embedding_rmsnorm_f16": [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64,
@@ -299,13 +302,7 @@ class KvSegment(ctypes.Structure):
                 ("seq_len", _c_void_p), ("start_pos", _c_void_p), ("max_blocks_per_seq", _i64)]
 
 
-def rope_kv_scatter(q, k, v, positions, inv_freq, k_cache, v_cache, layer: int, block_size: int,
-                    segments, q_bias=None, k_bias=None, v_bias=None, stream=None):
-    """One launch: NeoX RoPE of q [T, Hq, hd] and k [T, Hkv, hd] in place and
-    the rotated K and V [T, Hkv, hd] rows written into k_cache / v_cache
-    [L, num_blocks, Hkv, bs, hd] for the tokens of `segments` (dicts with
-    token_offset, S, block_table [B, max_blocks], seq_len [B], start_pos [B]).
-    With q_bias / k_bias / v_bias (all three) the biases are added first."""
+def _rope_kv_checks(q, k, v, positions, k_cache, v_cache, layer, block_size):
     torch = _torch()
     _need(q, _f16(), "q"); _need(k, _f16(), "k"); _need(v, _f16(), "v")
     _need(positions, torch.int64, "positions")
@@ -321,14 +318,13 @@ def rope_kv_scatter(q, k, v, positions, inv_freq, k_cache, v_cache, layer: int, 
     L, NB, Hc, bs, Dc = k_cache.shape
     if Hc != Hkv or Dc != hd or bs != block_size or not 0 <= layer < L:
         raise ValueError("cache shape does not match k / block_size / layer")
-    biases = (q_bias, k_bias, v_bias)
-    if any(b is not None for b in biases):
-        for b, n, h in zip(biases, ("q_bias", "k_bias", "v_bias"), (Hq, Hkv, Hkv)):
-            if b is None:
-                raise ValueError("set q_bias, k_bias and v_bias together")
-            _need(b, _f16(), n)
-            if b.numel() != h * hd:
-                raise ValueError(f"{n} must hold {h} * head_dim entries")
+    return T, Hq, Hkv, hd, NB
+
+
+def _kv_segments(segments):
+    """ctypes mi_kv_segment array from segment dicts (token_offset, S, and int32
+    device block_table [B, max_blocks], seq_len [B], start_pos [B])."""
+    torch = _torch()
     segs = (KvSegment * max(1, len(segments)))()
     for i, g in enumerate(segments):
         bt = g["block_table"]
@@ -345,6 +341,27 @@ def rope_kv_scatter(q, k, v, positions, inv_freq, k_cache, v_cache, layer: int, 
         segs[i].seq_len = _ptr(g["seq_len"]).value
         segs[i].start_pos = _ptr(g["start_pos"]).value
         segs[i].max_blocks_per_seq = bt.shape[1]
+    return segs
+
+
+def rope_kv_scatter(q, k, v, positions, inv_freq, k_cache, v_cache, layer: int, block_size: int,
+                    segments, q_bias=None, k_bias=None, v_bias=None, stream=None):
+    """One launch: NeoX RoPE of q [T, Hq, hd] and k [T, Hkv, hd] in place and
+    the rotated K and V [T, Hkv, hd] rows written into k_cache / v_cache
+    [L, num_blocks, Hkv, bs, hd] for the tokens of `segments` (dicts with
+    token_offset, S, block_table [B, max_blocks], seq_len [B], start_pos [B]).
+    With q_bias / k_bias / v_bias (all three) the biases are added first."""
+    T, Hq, Hkv, hd, NB = _rope_kv_checks(q, k, v, positions, k_cache, v_cache, layer,
+                                         block_size)
+    biases = (q_bias, k_bias, v_bias)
+    if any(b is not None for b in biases):
+        for b, n, h in zip(biases, ("q_bias", "k_bias", "v_bias"), (Hq, Hkv, Hkv)):
+            if b is None:
+                raise ValueError("set q_bias, k_bias and v_bias together")
+            _need(b, _f16(), n)
+            if b.numel() != h * hd:
+                raise ValueError(f"{n} must hold {h} * head_dim entries")
+    segs = _kv_segments(segments)
     arr, p = _inv_freq_buffer(inv_freq)
     if arr.size != hd // 2:
         raise ValueError("inv_freq must hold head_dim/2 entries")
@@ -354,6 +371,27 @@ def rope_kv_scatter(q, k, v, positions, inv_freq, k_cache, v_cache, layer: int, 
         _ptr(q), _ptr(k), _ptr(v), bp[0], bp[1], bp[2], _ptr(positions), p, T, Hq, Hkv, hd,
         _ptr(k_cache), _ptr(v_cache), layer, NB, block_size, segs, len(segments),
         _stream(stream)), "mi_rope_kv_scatter_f16")
+    return q, k
+
+
+def qk_norm_rope_kv_scatter(q, k, v, q_weight, k_weight, positions, inv_freq, k_cache, v_cache,
+                            layer: int, block_size: int, segments, eps: float = 1e-6,
+                            add_one: bool = False, stream=None):
+    """rope_kv_scatter with the per-head Q/K RMSNorm (q_weight / k_weight
+    [hd]) applied first, as qk_norm_rope does."""
+    T, Hq, Hkv, hd, NB = _rope_kv_checks(q, k, v, positions, k_cache, v_cache, layer,
+                                         block_size)
+    _need(q_weight, _f16(), "q_weight"); _need(k_weight, _f16(), "k_weight")
+    if q_weight.numel() != hd or k_weight.numel() != hd:
+        raise ValueError("q_weight / k_weight must hold head_dim entries")
+    segs = _kv_segments(segments)
+    arr, p = _inv_freq_buffer(inv_freq)
+    if arr.size != hd // 2:
+        raise ValueError("inv_freq must hold head_dim/2 entries")
+    _check(load_library().mi_qk_norm_rope_kv_scatter_f16(
+        _ptr(q), _ptr(k), _ptr(v), _ptr(q_weight), _ptr(k_weight), _ptr(positions), p, T, Hq,
+        Hkv, hd, float(eps), int(add_one), _ptr(k_cache), _ptr(v_cache), layer, NB, block_size,
+        segs, len(segments), _stream(stream)), "mi_qk_norm_rope_kv_scatter_f16")
     return q, k
 
 

@@ -448,6 +448,37 @@ void gpu_checks() {
                             bit_equal(kcb, bits(kcah), "launch_rope_kv_scatter (K cache)") &&
                             bit_equal(vcb, bits(vcah), "launch_rope_kv_scatter (V cache)");
             EXPECT(ok, Hq == 8 ? "rope + kv scatter, one launch" : "rope + kv scatter, fallback");
+
+            // the same with the per-head Q/K norm, against launch_qk_norm_rope + scatter
+            Tensor wt = reftest_f16({D}, 0.1f, 48);
+            Tensor wd = wt.to(Device::cuda(0));
+            const auto* w = static_cast<const __half*>(wd.data());
+            Tensor qc = q.to(Device::cuda(0)), kc2 = src.to(Device::cuda(0));
+            Tensor kcc = cache.to(Device::cuda(0)), vcc = vcache.to(Device::cuda(0));
+            mini_infer::kernels::launch_qk_norm_rope(static_cast<__half*>(qc.data()),
+                                                     static_cast<__half*>(kc2.data()), w, w, pp,
+                                                     inv.data(), T, Hq, Hk, D, 1e-6f, 1, 0);
+            mini_infer::kernels::launch_paged_kv_scatter_kv(
+                static_cast<const __half*>(kc2.data()), static_cast<const __half*>(vsd.data()),
+                static_cast<__half*>(kcc.data()), static_cast<__half*>(vcc.data()),
+                static_cast<const int*>(btd.data()), static_cast<const int*>(sld.data()),
+                static_cast<const int*>(spd.data()), B, S, 1, NB, Hk, D, BS, MB, 0);
+            Tensor qn = q.to(Device::cuda(0)), kn = src.to(Device::cuda(0));
+            Tensor kcn = cache.to(Device::cuda(0)), vcn = vcache.to(Device::cuda(0));
+            mini_infer::kernels::launch_qk_norm_rope_kv_scatter(
+                static_cast<__half*>(qn.data()), static_cast<__half*>(kn.data()),
+                static_cast<const __half*>(vsd.data()), w, w, pp, inv.data(), B, S, Hq, Hk, D,
+                1e-6f, 1, static_cast<__half*>(kcn.data()), static_cast<__half*>(vcn.data()),
+                static_cast<const int*>(btd.data()), static_cast<const int*>(sld.data()),
+                static_cast<const int*>(spd.data()), 1, NB, BS, MB, 0);
+            Tensor qch = qc.to(Device::cpu()), kch = kc2.to(Device::cpu());
+            Tensor kcch = kcc.to(Device::cpu()), vcch = vcc.to(Device::cpu());
+            const bool okn = bit_equal(qn, bits(qch), "launch_qk_norm_rope_kv_scatter (Q)") &&
+                             bit_equal(kn, bits(kch), "launch_qk_norm_rope_kv_scatter (K)") &&
+                             bit_equal(kcn, bits(kcch), "launch_qk_norm_rope_kv_scatter (K cache)") &&
+                             bit_equal(vcn, bits(vcch), "launch_qk_norm_rope_kv_scatter (V cache)");
+            EXPECT(okn, Hq == 8 ? "qk norm + rope + kv scatter, one launch"
+                                : "qk norm + rope + kv scatter, fallback");
         }
 
         const int R = 3, V = 152064;

@@ -1,6 +1,7 @@
 """GPU parity: RoPE of Q/K with the K and V rows written into the paged KV
 cache in the same launch (mi_rope_kv_scatter_f16), with and without Qwen2's
-q/k/v bias.
+q/k/v bias, and with Gemma 3's per-head Q/K RMSNorm before the rotation
+(mi_qk_norm_rope_kv_scatter_f16).
 
 The reference does this as the bias adds, the RoPE pair and one
 launch_paged_kv_scatter per tensor and sequence group
@@ -11,12 +12,17 @@ against this library's own separate launches.  Cases: the decoder chain's
 continuous batch (64 decode tokens + two 3000-token prefills), head_dims
 16..256, ragged segments (a token past its seq_len, unmapped or out-of-range
 block ids, tokens outside every segment, an empty segment), no segment at
-all, and the refusals (unsupported shapes, partial bias, aliasing).
+all, and the refusals (unsupported shapes, partial bias, aliasing).  The
+norm form is bit-exact against this library's qk_norm_rope followed by the
+scatters, its Q/K within the norm + RoPE tolerance of the oracle's
+composition (tests/helpers.py), and its caches bit-exact against the oracle's
+scatter of its own rotated K.
 """
 import numpy as np
 import pytest
 
-from helpers import assert_bits_equal, normal_f16, to_dev, to_host
+from helpers import (assert_bits_equal, assert_norm_rope_close, normal_f16, qk_norm_rope_ref,
+                     to_dev, to_host)
 
 pytestmark = pytest.mark.gpu
 
@@ -184,4 +190,85 @@ def test_rope_kv_scatter_refusals(mk, orc, dev):
     with pytest.raises(ValueError, match="together"):
         mk.rope_kv_scatter(q, k, v, pos, inv, kc, vc, 0, bs, segs, q_bias=bq)
     # nothing written by a refused call
+    assert int(torch.count_nonzero(kc)) == 0 and int(torch.count_nonzero(vc)) == 0
+
+
+@pytest.mark.parametrize("T,Hq,Hkv,hd,kind", [
+    (6064, 28, 4, 128, "chain"),   # config 5: Qwen2.5-7B heads with Gemma-3-style Q/K norm
+    (48, 16, 8, 64, "ragged"),
+    (48, 8, 4, 256, "ragged"),
+    (48, 4, 2, 16, "ragged"),
+    (48, 2, 1, 512, "ragged"),     # 32 lanes per head
+    (20, 8, 8, 128, "none"),
+])
+@pytest.mark.parametrize("add_one", [False, True])
+def test_qk_norm_rope_kv_scatter(mk, orc, dev, T, Hq, Hkv, hd, kind, add_one):
+    _case(f"qk norm + rope + kv scatter T={T} Hq={Hq} Hkv={Hkv} hd={hd} {kind} "
+          f"add_one={add_one}")
+    rng = np.random.default_rng(T + Hq * 3 + hd + add_one)
+    bs, L, layer = 16, 2, 1
+    NB = 2100 if kind == "chain" else 40
+    segs = _segments(rng, kind, T, bs, NB)
+    q = normal_f16(rng, (T, Hq, hd), 0, 3)
+    k = normal_f16(rng, (T, Hkv, hd), 0, 3)
+    v = normal_f16(rng, (T, Hkv, hd))
+    kc = normal_f16(rng, (L, NB, Hkv, bs, hd))
+    vc = normal_f16(rng, (L, NB, Hkv, bs, hd))
+    wq = normal_f16(rng, (hd,), 0 if add_one else 1, 0.1)
+    wk = normal_f16(rng, (hd,), 0 if add_one else 1, 0.1)
+    wq[3] = np.float16(-0.0)  # a -0 weight keeps the sign of zero through the norm
+    pos = rng.integers(0, 32000, T).astype(np.int64)
+    inv = orc.rope_inv_freq(hd, 1e6)
+    posd, wqd, wkd = to_dev(pos, dev), to_dev(wq, dev), to_dev(wk, dev)
+    dsegs = _dev_segs(segs, dev)
+    # this library's two steps
+    qa, ka, va, kca, vca = (to_dev(x, dev) for x in (q, k, v, kc, vc))
+    mk.qk_norm_rope(qa, ka, wqd, wkd, posd, inv, eps=1e-6, add_one=add_one)
+    for g in dsegs:
+        B, S, o = g["block_table"].shape[0], g["S"], g["token_offset"]
+        if B * S == 0:
+            continue
+        mk.paged_kv_scatter(ka[o:o + B * S].reshape(B, S, Hkv, hd), kca, g["block_table"],
+                            g["seq_len"], g["start_pos"], layer, bs,
+                            v_src=va[o:o + B * S].reshape(B, S, Hkv, hd), v_cache=vca)
+    # one launch
+    qb, kb, vb, kcb, vcb = (to_dev(x, dev) for x in (q, k, v, kc, vc))
+    mk.qk_norm_rope_kv_scatter(qb, kb, vb, wqd, wkd, posd, inv, kcb, vcb, layer, bs, dsegs,
+                               eps=1e-6, add_one=add_one)
+    for name, a, b in (("q", qa, qb), ("k", ka, kb), ("k cache", kca, kcb),
+                       ("v cache", vca, vcb)):
+        assert_bits_equal(to_host(b), to_host(a), what=f"{name} vs qk_norm_rope + scatter")
+    assert_bits_equal(to_host(vb), v, what="v source untouched")
+    # the oracle: norm + RoPE within tolerance, cache placement bit-exact
+    kh = to_host(kb)
+    for x, w, got, what in ((q, wq, to_host(qb), "q"), (k, wk, kh, "k")):
+        ref, n16 = qk_norm_rope_ref(orc, x, w, pos, inv, 1e-6, add_one)
+        assert_norm_rope_close(got, ref, n16, what=f"{what} vs oracle")
+    kcr, vcr = kc, vc
+    for g in segs:
+        B, S, o = g["block_table"].shape[0], g["S"], g["token_offset"]
+        if B * S == 0:
+            continue
+        args = (g["block_table"], g["seq_len"], g["start_pos"], layer, bs)
+        kcr = orc.paged_kv_scatter(kh[o:o + B * S].reshape(B, S, Hkv, hd), kcr, *args)
+        vcr = orc.paged_kv_scatter(v[o:o + B * S].reshape(B, S, Hkv, hd), vcr, *args)
+    assert_bits_equal(to_host(kcb), kcr, what="k cache vs oracle scatter")
+    assert_bits_equal(to_host(vcb), vcr, what="v cache vs oracle scatter")
+
+
+def test_qk_norm_rope_kv_scatter_refusals(mk, orc, dev):
+    import torch
+    _case("qk norm + rope + kv scatter refusals")
+    rng = np.random.default_rng(10)
+    bs, NB, T = 16, 40, 48
+    segs = _dev_segs(_segments(rng, "ragged", T, bs, NB), dev)
+    pos = to_dev(rng.integers(0, 1000, T).astype(np.int64), dev)
+    hd = 48  # a multiple of 16 but not 16 * 2^k: no compile-time lane group
+    q, k, v = (to_dev(normal_f16(rng, (T, h, hd)), dev) for h in (4, 2, 2))
+    kc = torch.zeros((1, NB, 2, bs, hd), dtype=torch.float16, device=dev)
+    vc = torch.zeros_like(kc)
+    w = to_dev(normal_f16(rng, (hd,), 1, 0.1), dev)
+    with pytest.raises(RuntimeError, match="status -2"):
+        mk.qk_norm_rope_kv_scatter(q, k, v, w, w, pos, orc.rope_inv_freq(hd), kc, vc, 0, bs,
+                                   segs)
     assert int(torch.count_nonzero(kc)) == 0 and int(torch.count_nonzero(vc)) == 0
