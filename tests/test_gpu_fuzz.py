@@ -8,7 +8,8 @@ tests pin one at a time:
 * in-place and out-of-place calls;
 * split and whole rows for softmax / argmax, and many long softmax rows
   (the persistent one-launch form, rows in rounds);
-* invalid ids and KV blocks;
+* invalid ids and KV blocks, and random segment tables for the one-launch
+  RoPE + K/V scatter;
 * ties, NaN and -inf in argmax rows.
 The bar is the same as everywhere: bit-exact for copies, RoPE and argmax;
 rtol = atol = 1e-3 for the fp32-math outputs (norm-then-rope with its
@@ -280,3 +281,84 @@ def test_fuzz_bias_paths(mk, orc, dev, seed):
     if Hkv2:
         assert_close(to_host(kd2).reshape(-1, hd2),
                      orc.rmsnorm(k2.reshape(-1, hd2), wk, add_one=add_one), what="k norm")
+
+
+def _fuzz_segments(rng, T, bs):
+    """Up to 8 segments over disjoint token ranges of [0, T) (gaps between
+    them), ragged sequences (some stop before S), distinct blocks with a few
+    unmapped (-1) or out-of-range ids; returns (segments, num_blocks)."""
+    nseg = int(rng.integers(0, 9))
+    cuts = np.sort(rng.choice(np.arange(T + 1), size=min(2 * nseg, T + 1), replace=False))
+    segs, nxt, raw = [], 0, []
+    for a, b in zip(cuts[0::2], cuts[1::2]):
+        n = int(b - a)
+        S = int(rng.integers(1, min(n, 48) + 1))  # small caches: B <= 6, positions < 88
+        B = int(rng.integers(1, min(n // S, 6) + 1))
+        start = rng.integers(0, 40, B)
+        sl = start + S - rng.integers(0, 3, B)
+        mb = max(1, -(-int(sl.max()) // bs))
+        raw.append((int(a), B, S, start, sl, mb, nxt))
+        nxt += B * mb
+    NB = max(1, nxt)
+    perm = rng.permutation(NB)
+    for a, B, S, start, sl, mb, off in raw:
+        bt = perm[off:off + B * mb].reshape(B, mb).astype(np.int32)
+        for _ in range(int(rng.integers(0, 3))):
+            bt[rng.integers(0, B), rng.integers(0, mb)] = rng.choice([-1, NB + 3])
+        segs.append(dict(token_offset=a, S=S, block_table=bt, seq_len=sl.astype(np.int32),
+                         start_pos=start.astype(np.int32)))
+    return segs, NB
+
+
+@pytest.mark.parametrize("seed", range(CASES))
+def test_fuzz_rope_kv_scatter(mk, orc, dev, seed):
+    """RoPE + K/V into the paged cache in one launch (plain, QKV bias, Q/K
+    norm) against this library's separate launches, bit for bit, over random
+    head layouts, head_dims and segment tables."""
+    import torch
+    rng = np.random.default_rng(12000 + seed)
+    mode = ("plain", "bias", "norm")[seed % 3]
+    while True:
+        hd = int(rng.choice([16, 32, 64, 128, 256]))
+        Hkv = int(rng.integers(1, 9))
+        Hq = Hkv * int(rng.integers(1, 8))
+        if (Hq + Hkv) * hd // 16 <= 256:
+            break
+    T, bs, L = int(rng.integers(1, 300)), int(rng.choice([1, 4, 16, 32])), 2
+    layer = int(rng.integers(0, L))
+    segs, NB = _fuzz_segments(rng, T, bs)
+    _case(f"rope_kv seed={seed} {mode} T={T} Hq={Hq} Hkv={Hkv} hd={hd} bs={bs} "
+          f"segments={len(segs)} NB={NB}")
+    q, k, v = (normal_f16(rng, (T, h, hd)) for h in (Hq, Hkv, Hkv))
+    kc, vc = (normal_f16(rng, (L, NB, Hkv, bs, hd)) for _ in range(2))
+    pos = rng.integers(0, 1 << int(rng.integers(4, 20)), T).astype(np.int64)
+    inv = orc.rope_inv_freq(hd, 1e6)
+    posd = _dev_array(pos, dev)
+    dsegs = [dict(g, block_table=_dev_array(g["block_table"], dev),
+                  seq_len=_dev_array(g["seq_len"], dev), start_pos=_dev_array(g["start_pos"], dev))
+             for g in segs]
+    bias = [_dev_array(normal_f16(rng, (h * hd,), 0, 1), dev) for h in (Hq, Hkv, Hkv)]
+    w = [_dev_array(normal_f16(rng, (hd,), 1, 0.1), dev) for _ in range(2)]
+    qa, ka, va, kca, vca = (_dev_array(x, dev) for x in (q, k, v, kc, vc))
+    if mode == "plain":
+        mk.rope_neox_qk(qa, ka, posd, inv)
+    elif mode == "bias":
+        mk.bias_rope_neox_qk(qa, ka, bias[0], bias[1], posd, inv)
+    else:
+        mk.qk_norm_rope(qa, ka, w[0], w[1], posd, inv)
+    for g in dsegs:
+        B, S, o = g["block_table"].shape[0], g["S"], g["token_offset"]
+        mk.paged_kv_scatter(ka[o:o + B * S].reshape(B, S, Hkv, hd), kca, g["block_table"],
+                            g["seq_len"], g["start_pos"], layer, bs,
+                            v_src=va[o:o + B * S].reshape(B, S, Hkv, hd), v_cache=vca,
+                            v_bias=bias[2] if mode == "bias" else None)
+    qb, kb, vb, kcb, vcb = (_dev_array(x, dev) for x in (q, k, v, kc, vc))
+    if mode == "norm":
+        mk.qk_norm_rope_kv_scatter(qb, kb, vb, w[0], w[1], posd, inv, kcb, vcb, layer, bs, dsegs)
+    else:
+        extra = bias if mode == "bias" else ()
+        mk.rope_kv_scatter(qb, kb, vb, posd, inv, kcb, vcb, layer, bs, dsegs, *extra)
+    torch.cuda.synchronize()
+    for name, a, b in (("q", qa, qb), ("k", ka, kb), ("k cache", kca, kcb),
+                       ("v cache", vca, vcb), ("v", va, vb)):
+        assert_bits_equal(to_host(b), to_host(a), what=name)
