@@ -752,7 +752,7 @@ def chain_bytes(s, segments_tokens):
             + (2 * N * V * 2 + N * 4))                                # softmax + argmax
 
 
-def decoder_chain(mk, dev, iters, warmup, qwen2=False):
+def decoder_chain(mk, dev, iters, warmup, qwen2=False, prefills=(3000, 3000)):
     """BASELINE config 5 as one step: the C++ decoder chain (include/mi_chain.h)
     over one non-GEMM decoder layer at T = 6064 (64 decode tokens at random
     positions + two 3000-token prefills), then the sampling step:
@@ -769,6 +769,8 @@ def decoder_chain(mk, dev, iters, warmup, qwen2=False):
     fused step's algorithmic bytes.  Two workloads alternate, so consecutive
     steps stream from HBM rather than the Infinity Cache.
 
+    prefills=(): the decode-only step (T = 64), rows named decoder_chain_decode64.
+
     qwen2: Qwen2.5-7B's own attention pre-processing instead of config 5's
     Gemma-3-style Q/K norm -- the q/k/v_proj bias and no Q/K norm
     (attention.cpp:717-780): the chain adds the Q/K bias in the rotation pass
@@ -779,7 +781,8 @@ def decoder_chain(mk, dev, iters, warmup, qwen2=False):
     import torch
     import mi_chain
     extra = dict(use_qk_norm=0, qkv_bias=1) if qwen2 else {}
-    ws = [mi_chain.Workload(dev, seed=5 + i, host=False, **extra) for i in range(2)]
+    ws = [mi_chain.Workload(dev, seed=5 + i, host=False, prefills=prefills, **extra)
+          for i in range(2)]
     s = ws[0].shapes
     T, D, V, N = s["T"], s["hidden_size"], s["vocab"], s["logit_rows"]
     Hq, Hkv, hd = s["num_heads"], s["num_kv_heads"], s["head_dim"]
@@ -832,8 +835,10 @@ def decoder_chain(mk, dev, iters, warmup, qwen2=False):
     if qwen2:
         cfg = ("gather&norm+qkv-bias&rope+kv(v-bias)+add&norm+swiglu+add&norm+softmax&argmax "
                f"T={T} (64 decode + 2x3000 prefill)")
+    if not prefills:
+        cfg = cfg.replace(f"T={T} (64 decode + 2x3000 prefill)", f"T={T} (decode only)")
     rows = []
-    suffix = "_qwen2" if qwen2 else ""
+    suffix = ("_qwen2" if qwen2 else "") + ("" if prefills else f"_decode{T}")
     for name, fn in (("decoder_chain" + suffix, fused), ("decoder_chain" + suffix + "_unfused",
                                                           unfused)):
         sec = time_launches(fn, len(ws), iters, warmup)
@@ -985,6 +990,10 @@ def main():
             kernels += decoder_chain(mk, dev, max(10, args.steps // 8), max(3, args.warmup // 4))
             kernels += decoder_chain(mk, dev, max(10, args.steps // 8), max(3, args.warmup // 4),
                                      qwen2=True)
+            # the decode-only step of the same model (64 sequences, one token each):
+            # launch-latency territory, where the fusion's saved launches show most
+            kernels += decoder_chain(mk, dev, max(10, args.steps // 8), max(3, args.warmup // 4),
+                                     prefills=())
         for k in kernels:
             floor = ""
             if "frac_of_floor" in k:
