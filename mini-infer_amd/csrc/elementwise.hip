@@ -101,6 +101,7 @@ int ew_launch(const void* av, const void* bv, void* outv, int64_t n, float scale
     if (n < 0) return MI_ERR_INVALID_ARGUMENT;
     if (n == 0) return MI_OK;
     if (!av || !outv || (binary<OP>() && !bv)) return MI_ERR_INVALID_ARGUMENT;
+    if (!product_fits({n, 2})) return MI_ERR_INVALID_ARGUMENT;
     const int64_t bytes = n * 2;
     if (outv != av && overlaps(outv, bytes, av, bytes)) return MI_ERR_ALIASING;
     if (binary<OP>() && outv != bv && overlaps(outv, bytes, bv, bytes)) return MI_ERR_ALIASING;
@@ -164,6 +165,8 @@ int add_bias(void* yv, const void* biasv, int64_t M, int64_t N, int64_t batch_st
     if (M < 0 || N < 0 || batch_stride < 0) return MI_ERR_INVALID_ARGUMENT;
     if (M == 0) return MI_OK;  // the reference returns before launching
     if (N == 0 || !yv || !biasv) return MI_ERR_INVALID_ARGUMENT;
+    if (!product_fits({M, N, 2})) return MI_ERR_INVALID_ARGUMENT;
+    if (!product_fits({batch_stride, 2})) return MI_ERR_INVALID_ARGUMENT;
     const int64_t per = M * N;
     const int64_t batches = batch_stride / per;
     if (batches < 1) return MI_ERR_INVALID_ARGUMENT;  // a grid with no batch: no launch

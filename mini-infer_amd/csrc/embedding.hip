@@ -204,6 +204,8 @@ extern "C" int mi_embedding_rmsnorm_f16(const int64_t* ids, const void* table, v
     if (T == 0 || D == 0) return MI_OK;
     if (!ids || !table || !hidden || !weight || !y) return MI_ERR_INVALID_ARGUMENT;
     if (T > mi::kMaxGridX) return MI_ERR_UNSUPPORTED;
+    if (!mi::product_fits({T, D, 2})) return MI_ERR_INVALID_ARGUMENT;
+    if (!mi::product_fits({vocab, D, 2})) return MI_ERR_INVALID_ARGUMENT;
     const int64_t bytes = T * D * 2;
     if (mi::overlaps(hidden, bytes, y, bytes)) return MI_ERR_ALIASING;
     if (vocab > 0 && (mi::overlaps(hidden, bytes, table, vocab * D * 2) ||
@@ -237,6 +239,8 @@ extern "C" int mi_embedding_gather_f16(const int64_t* ids, const void* table, vo
     if (T < 0 || H < 0) return MI_ERR_INVALID_ARGUMENT;
     if (T == 0 || H == 0) return MI_OK;
     if (!ids || !table || !out) return MI_ERR_INVALID_ARGUMENT;
+    if (!mi::product_fits({T, H, 2})) return MI_ERR_INVALID_ARGUMENT;
+    if (!mi::product_fits({vocab, H, 2})) return MI_ERR_INVALID_ARGUMENT;
     const bool vec = H % 8 == 0 && mi::aligned16(table) && mi::aligned16(out);
     const int L = mi::gather_lanes(vec ? H / 8 : H);
     if (mi::ceil_div(T, 256 / L) > mi::kMaxGridX) return MI_ERR_UNSUPPORTED;

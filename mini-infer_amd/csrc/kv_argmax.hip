@@ -166,14 +166,17 @@ int kv_scatter(const void* src0, void* cache0, const void* src1, void* cache1,
                int64_t S, int64_t layer, int64_t num_blocks, int64_t H_kv, int64_t D,
                int64_t block_size, int64_t max_blocks_per_seq, void* stream,
                const void* bias0v = nullptr, const void* bias1v = nullptr) {
-    if (B < 0 || S < 0 || layer < 0 || num_blocks < 0 || H_kv < 0 || D < 0 || block_size <= 0 ||
-        max_blocks_per_seq < 0)
+    if (B < 0 || S < 0 || layer < 0 || layer >= (int64_t{1} << 62) || num_blocks < 0 ||
+        H_kv < 0 || D < 0 || block_size <= 0 || max_blocks_per_seq < 0)
         return MI_ERR_INVALID_ARGUMENT;
     if (B == 0 || S == 0 || H_kv == 0 || D == 0 || num_blocks == 0 || max_blocks_per_seq == 0)
         return MI_OK;
     if (!src0 || !cache0 || !block_table || !seq_len || !start_pos) return MI_ERR_INVALID_ARGUMENT;
     if ((src1 == nullptr) != (cache1 == nullptr)) return MI_ERR_INVALID_ARGUMENT;
     if (bias1v && !src1) return MI_ERR_INVALID_ARGUMENT;
+    if (!product_fits({B, S, H_kv, D, 2})) return MI_ERR_INVALID_ARGUMENT;
+    if (!product_fits({layer + 1, num_blocks, H_kv, block_size, D, 2})) return MI_ERR_INVALID_ARGUMENT;
+    if (!product_fits({B, max_blocks_per_seq, 4})) return MI_ERR_INVALID_ARGUMENT;
     const int64_t tokens = B * S;
     const bool vec = D % 8 == 0 && aligned16(src0) && aligned16(cache0) &&
                      (!src1 || (aligned16(src1) && aligned16(cache1))) &&

@@ -5,6 +5,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <initializer_list>
 #include <map>
 #include <mutex>
 #include <utility>
@@ -19,6 +20,19 @@ inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 
 inline bool overlaps(const void* a, int64_t abytes, const void* b, int64_t bbytes) {
     const uintptr_t a0 = reinterpret_cast<uintptr_t>(a), b0 = reinterpret_cast<uintptr_t>(b);
     return a0 < b0 + static_cast<uintptr_t>(bbytes) && b0 < a0 + static_cast<uintptr_t>(abytes);
+}
+
+// True when every factor is non-negative and their product stays within
+// 2^62 (byte counts formed from it, and sums of two such, cannot overflow
+// int64).  Entry points check their size products with it before forming
+// them and return MI_ERR_INVALID_ARGUMENT otherwise: no real buffer is that
+// large.
+inline bool product_fits(std::initializer_list<int64_t> factors) {
+    int64_t p = 1;
+    for (int64_t f : factors) {
+        if (f < 0 || __builtin_mul_overflow(p, f, &p) || p > (int64_t{1} << 62)) return false;
+    }
+    return true;
 }
 
 // Maps the outcome of the launches just issued to the ABI's status code.

@@ -340,6 +340,7 @@ int rmsnorm_dispatch(const void* xv, void* rv, const void* wv, void* yv, int64_t
     if (N == 0 || D == 0) return MI_OK;
     if (!xv || !wv || !yv || (FUSED && !rv)) return MI_ERR_INVALID_ARGUMENT;
     if (N > kMaxGridX) return MI_ERR_UNSUPPORTED;
+    if (!product_fits({N, D, 2})) return MI_ERR_INVALID_ARGUMENT;
     const int64_t bytes = N * D * 2;
     if (xv != yv && overlaps(xv, bytes, yv, bytes)) return MI_ERR_ALIASING;
     if (FUSED && (overlaps(rv, bytes, xv, bytes) || overlaps(rv, bytes, yv, bytes)))
@@ -369,6 +370,7 @@ int qk_rmsnorm(void* qv, void* kv, const void* wqv, const void* wkv, int64_t T, 
     if (T < 0 || Hq < 0 || Hkv < 0 || D < 0) return MI_ERR_INVALID_ARGUMENT;
     if (T == 0 || Hq + Hkv == 0 || D == 0) return MI_OK;
     if ((Hq > 0 && (!qv || !wqv)) || (Hkv > 0 && (!kv || !wkv))) return MI_ERR_INVALID_ARGUMENT;
+    if (!product_fits({T, Hq + Hkv, D, 2})) return MI_ERR_INVALID_ARGUMENT;
     const int64_t Nq = T * Hq, Nk = T * Hkv;
     if (Hq > 0 && Hkv > 0 && overlaps(qv, Nq * D * 2, kv, Nk * D * 2)) return MI_ERR_ALIASING;
     const bool vec = D % 8 == 0 && D <= 512 && (Hq == 0 || (aligned16(qv) && aligned16(wqv))) &&

@@ -914,6 +914,7 @@ using mi::half_t;
 extern "C" int mi_rope_neox_f16(const void* x, const void* cos_t, const void* sin_t, void* y,
                                 int64_t B, int64_t S, int64_t H, int64_t D, void* stream) {
     if (B < 0 || S < 0 || H < 0 || D < 0) return MI_ERR_INVALID_ARGUMENT;
+    if (!mi::product_fits({B, S, H, D, 2})) return MI_ERR_INVALID_ARGUMENT;
     const int64_t T = B * S;
     if (T == 0 || H == 0) return MI_OK;
     if (!x || !y || !cos_t || !sin_t) return MI_ERR_INVALID_ARGUMENT;
@@ -935,6 +936,7 @@ extern "C" int mi_rope_tables_f16(const float* inv_freq_host, const int64_t* pos
     if (!positions || !cos_t || !sin_t) return MI_ERR_INVALID_ARGUMENT;
     mi::InvFreq inv;
     if (!mi::load_inv_freq(inv_freq_host, half, inv)) return MI_ERR_INVALID_ARGUMENT;
+    if (!mi::product_fits({N, half, 4})) return MI_ERR_INVALID_ARGUMENT;
     const int64_t total = N * half;
     const int64_t grid = mi::ceil_div(total, 256);
     if (grid > mi::kMaxGridX) return MI_ERR_UNSUPPORTED;
@@ -954,6 +956,7 @@ extern "C" int mi_rope_neox_qk_f16(void* q, void* k, const int64_t* positions,
     if (T == 0 || Hq + Hkv == 0) return MI_OK;
     if (!positions || (Hq > 0 && !q) || (Hkv > 0 && !k)) return MI_ERR_INVALID_ARGUMENT;
     if (!mi::heads_ok(Hq, Hkv, head_dim)) return MI_ERR_UNSUPPORTED;
+    if (!mi::product_fits({T, Hq + Hkv, head_dim, 2})) return MI_ERR_INVALID_ARGUMENT;
     if (Hq > 0 && Hkv > 0 &&
         mi::overlaps(q, T * Hq * head_dim * 2, k, T * Hkv * head_dim * 2))
         return MI_ERR_ALIASING;
@@ -981,6 +984,7 @@ extern "C" int mi_bias_rope_neox_qk_f16(void* q, void* k, const void* q_bias, co
     if (!positions || (Hq > 0 && (!q || !q_bias)) || (Hkv > 0 && (!k || !k_bias)))
         return MI_ERR_INVALID_ARGUMENT;
     if (!mi::heads_ok(Hq, Hkv, head_dim)) return MI_ERR_UNSUPPORTED;
+    if (!mi::product_fits({T, Hq + Hkv, head_dim, 2})) return MI_ERR_INVALID_ARGUMENT;
     const int64_t qb = T * Hq * head_dim * 2, kb = T * Hkv * head_dim * 2;
     if (Hq > 0 && Hkv > 0 && mi::overlaps(q, qb, k, kb)) return MI_ERR_ALIASING;
     if ((Hq > 0 && (mi::overlaps(q_bias, Hq * head_dim * 2, q, qb) ||
@@ -1016,8 +1020,8 @@ int rope_kv_launch(void* q, void* k, const void* v, const void* q_bias, const vo
                    int64_t Hq, int64_t Hkv, int64_t head_dim, void* k_cache, void* v_cache,
                    int64_t layer, int64_t num_blocks, int64_t block_size,
                    const mi_kv_segment* segments, int num_segments, void* stream) {
-    if (T < 0 || Hq < 0 || Hkv < 0 || head_dim < 0 || layer < 0 || num_blocks < 0 ||
-        block_size <= 0 || num_segments < 0)
+    if (T < 0 || Hq < 0 || Hkv < 0 || head_dim < 0 || layer < 0 || layer >= (int64_t{1} << 62) ||
+        num_blocks < 0 || block_size <= 0 || num_segments < 0)
         return MI_ERR_INVALID_ARGUMENT;
     if (T == 0) return MI_OK;
     const bool bias = q_bias || k_bias || v_bias;
@@ -1038,6 +1042,8 @@ int rope_kv_launch(void* q, void* k, const void* v, const void* q_bias, const vo
     if (bias && !(aligned16(q_bias) && aligned16(k_bias) && aligned16(v_bias)))
         return MI_ERR_UNSUPPORTED;
     if (norm && !(aligned16(q_weight) && aligned16(k_weight))) return MI_ERR_UNSUPPORTED;
+    if (!product_fits({layer + 1, num_blocks, Hkv, block_size, head_dim, 2}))
+        return MI_ERR_INVALID_ARGUMENT;
     const int64_t qb = T * Hq * head_dim * 2, kb = T * Hkv * head_dim * 2;
     const int64_t cb = (layer + 1) * num_blocks * Hkv * block_size * head_dim * 2;
     const void* bufs[5] = {q, k, v, k_cache, v_cache};
@@ -1049,7 +1055,9 @@ int rope_kv_launch(void* q, void* k, const void* v, const void* q_bias, const vo
     sg.n = num_segments;
     for (int i = 0; i < num_segments; ++i) {
         const mi_kv_segment& g = segments[i];
-        if (g.token_offset < 0 || g.B < 0 || g.S < 0 || g.token_offset + g.B * g.S > T)
+        // B and S bounded before their product is formed
+        if (g.token_offset < 0 || g.token_offset > T || g.B < 0 || g.S < 0 ||
+            (g.B > 0 && g.S > 0 && (g.B > T || g.S > T || g.B * g.S > T - g.token_offset)))
             return MI_ERR_INVALID_ARGUMENT;
         if (g.B * g.S > 0 && (!g.block_table || !g.seq_len || !g.start_pos ||
                               g.max_blocks_per_seq <= 0))
@@ -1141,6 +1149,7 @@ extern "C" int mi_qk_norm_rope_f16(void* q, void* k, const void* q_weight, const
     if (!positions || (Hq > 0 && (!q || !q_weight)) || (Hkv > 0 && (!k || !k_weight)))
         return MI_ERR_INVALID_ARGUMENT;
     if (!mi::heads_ok(Hq, Hkv, head_dim)) return MI_ERR_UNSUPPORTED;
+    if (!mi::product_fits({T, Hq + Hkv, head_dim, 2})) return MI_ERR_INVALID_ARGUMENT;
     if (Hq > 0 && Hkv > 0 &&
         mi::overlaps(q, T * Hq * head_dim * 2, k, T * Hkv * head_dim * 2))
         return MI_ERR_ALIASING;

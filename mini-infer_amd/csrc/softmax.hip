@@ -861,6 +861,7 @@ int softmax_checked(const void* x, void* y, int64_t N, int64_t D, void* ws, int6
     if (N == 0 || D == 0) return MI_OK;
     if (!x || !y) return MI_ERR_INVALID_ARGUMENT;
     if (N > kMaxGridX) return MI_ERR_UNSUPPORTED;
+    if (!product_fits({N, D, 2})) return MI_ERR_INVALID_ARGUMENT;
     const int64_t bytes = N * D * 2;
     if (x != y && overlaps(x, bytes, y, bytes)) return MI_ERR_ALIASING;
     int64_t splits, chunk;
@@ -1041,6 +1042,7 @@ extern "C" int mi_softmax_argmax_ws_f16(const void* logits, void* probs, int32_t
     if (N == 0 || V == 0) return MI_OK;
     if (!logits || !probs || !out || !workspace) return MI_ERR_INVALID_ARGUMENT;
     if (N > 65535) return MI_ERR_UNSUPPORTED;  // the argmax grid's rows
+    if (!mi::product_fits({N, V, 2})) return MI_ERR_INVALID_ARGUMENT;
     const int64_t need = mi_softmax_argmax_workspace_bytes(N, V);
     if (workspace_bytes < need || reinterpret_cast<uintptr_t>(workspace) % 16 != 0)
         return MI_ERR_INVALID_ARGUMENT;

@@ -85,6 +85,36 @@ def test_host_side_argument_rejection(lib):
     assert lib.mi_rope_tables_f16(None, a, b, c, 4, 32, None) == -1
 
 
+def test_size_products_that_overflow_are_rejected(lib):
+    """Sizes whose byte counts would overflow int64 are argument errors,
+    decided before any HIP call (fake pointers)."""
+    a, b, c, d, e = (P(0x10000 * i) for i in range(1, 6))
+    big = 1 << 40
+    assert lib.mi_rmsnorm_f16(a, b, c, 1 << 30, big, 1e-6, 0, None) == -1
+    assert lib.mi_softmax_f16(a, c, 1 << 30, big, None) == -1
+    assert lib.mi_swiglu_f16(a, b, c, 1 << 62, None) == -1
+    assert lib.mi_embedding_gather_f16(a, b, c, 1 << 30, big, 0, None) == -1
+    assert lib.mi_add_bias_f16(a, b, big, big, big, None) == -1
+    # B * S past int64 (and a layer whose + 1 would overflow)
+    assert lib.mi_paged_kv_scatter_f16(a, b, c, d, e, 1 << 40, 1 << 40, 0, 8, 4, 128, 16, 4,
+                                       None) == -1
+    assert lib.mi_paged_kv_scatter_f16(a, b, c, d, e, 1, 1, (1 << 63) - 1, 8, 4, 128, 16, 4,
+                                       None) == -1
+    # a segment of the one-launch RoPE + KV scatter whose B * S would overflow
+    import mi_kernels
+    inv = (ctypes.c_float * 64)()
+    seg = (mi_kernels.KvSegment * 1)()
+    seg[0].token_offset, seg[0].B, seg[0].S = 0, 1 << 40, 1 << 40
+    seg[0].block_table, seg[0].seq_len, seg[0].start_pos = 0x60000, 0x70000, 0x80000
+    seg[0].max_blocks_per_seq = 4
+    q, k, v, kc, vc = (P(0x1000000 * i) for i in range(1, 6))
+    assert lib.mi_rope_kv_scatter_f16(q, k, v, None, None, None, P(0x90000), inv, 100, 28, 4,
+                                      128, kc, vc, 0, 8, 16, seg, 1, None) == -1
+    seg[0].B, seg[0].S = 0, 1 << 62  # an empty segment is fine; nothing launched for T = 0
+    assert lib.mi_rope_kv_scatter_f16(q, k, v, None, None, None, P(0x90000), inv, 0, 28, 4,
+                                      128, kc, vc, 0, 8, 16, seg, 1, None) == 0
+
+
 def test_binding_validates_on_host():
     import torch
     x = torch.zeros(4, 8, dtype=torch.float16)
