@@ -145,9 +145,9 @@ typedef struct mi_kv_segment {
  * (v itself is not written).  Equals mi_rope_neox_qk_f16 (or
  * mi_bias_rope_neox_qk_f16) followed by mi_paged_kv_scatter_kv_f16 (or its
  * bias form) per segment, bit for bit.  hd a multiple of 16 (<= 512),
- * (Hq + Hkv) * hd / 16 <= 256, Hkv * hd <= 2048, at most 8 segments,
- * 16-byte-aligned buffers; otherwise MI_ERR_UNSUPPORTED (use the separate
- * entry points).  Replaces src/layers/attention.cpp:717-780 (bias adds,
+ * (Hq + Hkv) * hd / 16 <= 256, Hkv * hd <= 2048, at most 8 segments over
+ * disjoint token ranges, 16-byte-aligned buffers; otherwise
+ * MI_ERR_UNSUPPORTED (use the separate entry points).  Replaces src/layers/attention.cpp:717-780 (bias adds,
  * copies, RoPE pair) and :823-846 (the two scatters). */
 int mi_rope_kv_scatter_f16(void* q, void* k, const void* v, const void* q_bias,
                            const void* k_bias, const void* v_bias, const int64_t* positions,

@@ -1062,6 +1062,15 @@ int rope_kv_launch(void* q, void* k, const void* v, const void* q_bias, const vo
         if (g.B * g.S > 0 && (!g.block_table || !g.seq_len || !g.start_pos ||
                               g.max_blocks_per_seq <= 0))
             return MI_ERR_INVALID_ARGUMENT;
+        // disjoint token ranges: the kernel scatters a token through the first
+        // segment holding it, where separate scatters would write it once per
+        // segment
+        for (int j = 0; j < i && g.B * g.S > 0; ++j) {
+            const mi_kv_segment& o = segments[j];
+            if (o.B * o.S > 0 && g.token_offset < o.token_offset + o.B * o.S &&
+                o.token_offset < g.token_offset + g.B * g.S)
+                return MI_ERR_UNSUPPORTED;
+        }
         sg.off[i] = g.token_offset;
         sg.B[i] = g.B;
         sg.S[i] = g.S;

@@ -110,6 +110,15 @@ def test_size_products_that_overflow_are_rejected(lib):
     q, k, v, kc, vc = (P(0x1000000 * i) for i in range(1, 6))
     assert lib.mi_rope_kv_scatter_f16(q, k, v, None, None, None, P(0x90000), inv, 100, 28, 4,
                                       128, kc, vc, 0, 8, 16, seg, 1, None) == -1
+    # overlapping token ranges: unsupported (the separate scatters write such a
+    # token once per segment); refused before any launch
+    two = (mi_kernels.KvSegment * 2)()
+    for i, off in enumerate((0, 30)):
+        two[i].token_offset, two[i].B, two[i].S = off, 2, 20
+        two[i].block_table, two[i].seq_len, two[i].start_pos = 0x60000, 0x70000, 0x80000
+        two[i].max_blocks_per_seq = 4
+    assert lib.mi_rope_kv_scatter_f16(q, k, v, None, None, None, P(0x90000), inv, 100, 28, 4,
+                                      128, kc, vc, 0, 8, 16, two, 2, None) == -2
     seg[0].B, seg[0].S = 0, 1 << 62  # an empty segment is fine; nothing launched for T = 0
     assert lib.mi_rope_kv_scatter_f16(q, k, v, None, None, None, P(0x90000), inv, 0, 28, 4,
                                       128, kc, vc, 0, 8, 16, seg, 1, None) == 0
