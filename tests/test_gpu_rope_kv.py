@@ -183,7 +183,8 @@ def test_rope_kv_scatter_refusals(mk, orc, dev):
     with pytest.raises(RuntimeError, match="status -2"):  # nine segments
         mk.rope_kv_scatter(q, k, v, pos, inv, kc, vc, 0, bs, [segs[0]] * 9)
     with pytest.raises(RuntimeError, match="status -2"):  # overlapping token ranges
-        mk.rope_kv_scatter(q, k, v, pos, inv, kc, vc, 0, bs, [segs[0], dict(segs[0], token_offset=2)])
+        mk.rope_kv_scatter(q, k, v, pos, inv, kc, vc, 0, bs,
+                           [segs[0], dict(segs[0], token_offset=2)])
     with pytest.raises(RuntimeError, match="status -3"):  # K and V caches the same buffer
         mk.rope_kv_scatter(q, k, v, pos, inv, kc, kc, 0, bs, segs)
     with pytest.raises(RuntimeError, match="status -1"):  # segment past T
