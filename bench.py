@@ -447,6 +447,14 @@ def all_kernels(mk, dev, iters, warmup):
     sec = time_launches(lambda i: mk.greedy_argmax(xs[i], out=outi, workspace=wsa), ns, iters,
                         warmup)
     out.append(report("greedy_argmax", "[64,152064]", nb, sec, N))
+    # 5g''. top-p sampling of 64 rows of 30000 logits (the largest vocabulary
+    # that takes the nucleus path; larger ones are greedy): latency-bound
+    xt = [randn16((N, 30000), gen, dev, 0.0, 4.0) for _ in range(4)]
+    sec = time_launches(lambda i: mk.top_p_sample(xt[i], 0.9, 0.8, 7, out=outi), 4, iters,
+                        warmup)
+    out.append(report("top_p_sample", "[64,30000] p=0.9 T=0.8", N * 30000 * 2 + N * 4, sec,
+                      N))
+    del xt
     # 5g'. softmax and argmax of the same logits in one pass
     nb = 2 * N * V * 2 + N * 4
     ysm = [torch.empty((N, V), dtype=f16, device=dev) for _ in range(ns)]

@@ -382,6 +382,24 @@ int mi_greedy_argmax_ws_f16(const void* logits, int64_t B, int64_t V, int32_t* o
  * that fallback everywhere.  Returns the previous bound. */
 int mi_greedy_argmax_test_poll_limit(int limit);
 
+/* Nucleus (top-p) sampling of one row of `vocab` fp16 logits into out[0]
+ * (int32, device), with the reference's rule (launch_top_p_sample,
+ * src/kernels/sampling_kernel.cu:86-221): above 30000 logits the greedy
+ * argmax of mi_greedy_argmax_f16; otherwise, with q_i = exp(x_i/T - max) /
+ * sum, the candidates at indices 0, 128, 256, ... in q-descending order
+ * (ties: lower index), the first position i whose running sum reaches p, and
+ * the index at slot floor(u * (i + 1)) with u from MurmurHash3's fmix64 of
+ * seed ^ (index_i << 32); -1 when the sum never reaches p.  Finite logits,
+ * temperature > 0. */
+int mi_top_p_sample_f16(const void* logits, int64_t vocab, float p, float temperature,
+                        uint64_t seed, int32_t* out, void* stream);
+
+/* mi_top_p_sample_f16 over B rows of [B, vocab] logits into out[B], row b
+ * with seed + b.  (The reference's launch_top_p_sample_batched,
+ * sampling_kernel.cu:223-227, is an empty stub.) */
+int mi_top_p_sample_batched_f16(const void* logits, int64_t B, int64_t vocab, float p,
+                                float temperature, uint64_t seed, int32_t* out, void* stream);
+
 /* Test hook (no counterpart in the reference): how the one-launch softmax,
  * argmax and softmax + argmax kernels read their row records.  0 (default):
  * the copy in the row's XCD L2 first, then the device-scope mirror; 1: the

@@ -312,5 +312,19 @@ void launch_greedy_sample_batched(const __half* logits, int B, int vocab, int* o
           "launch_greedy_sample_batched");
 }
 
+void launch_top_p_sample(const __half* logits, int vocab, float p, float temperature,
+                         unsigned long long seed, int* out, hipStream_t stream) {
+    check(mi_top_p_sample_f16(logits, vocab, p, temperature, seed, out, sv(stream)),
+          "launch_top_p_sample");
+}
+
+void launch_top_p_sample_batched(const __half* logits, int B, int vocab, float p,
+                                 float temperature, unsigned long long seed, int* out,
+                                 hipStream_t stream) {
+    if (B <= 0) return;
+    check(mi_top_p_sample_batched_f16(logits, B, vocab, p, temperature, seed, out, sv(stream)),
+          "launch_top_p_sample_batched");
+}
+
 }  // namespace kernels
 }  // namespace mini_infer

@@ -52,6 +52,9 @@ SIGNATURES = {
     "mi_qk_norm_rope_kv_scatter_f16": [_c_void_p] * 6 + [_c_void_p] + [_i64] * 4 + [_f32, _int]
                                       + [_c_void_p, _c_void_p] + [_i64] * 3
                                       + [_c_void_p, _int, _c_void_p],
+    "mi_top_p_sample_f16": [_c_void_p, _i64, _f32, _f32, ctypes.c_uint64, _c_void_p, _c_void_p],
+    "mi_top_p_sample_batched_f16": [_c_void_p, _i64, _i64, _f32, _f32, ctypes.c_uint64,
+                                    _c_void_p, _c_void_p],
     "mi_softmax_f16": [_c_void_p, _c_void_p, _i64, _i64, _c_void_p],
     "mi_embedding_gather_f16": [_c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64, _c_void_p],
     "mi_embedding_rmsnorm_f16": [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64,
@@ -749,6 +752,24 @@ def greedy_argmax_test_poll_limit(limit: int) -> int:
     if prev < 0:
         raise ValueError("limit must be >= 0")
     return prev
+
+
+def top_p_sample(logits, p: float, temperature: float, seed: int, out=None, stream=None):
+    """int32 [B] top-p samples of logits [B, V] (or [V]) with the reference's
+    rule (greedy above 30000 logits); row b draws with seed + b."""
+    torch = _torch()
+    _need(logits, _f16(), "logits")
+    x = logits if logits.dim() == 2 else logits.view(1, -1)
+    B, V = x.shape
+    if out is None:
+        out = torch.empty(B, dtype=torch.int32, device=logits.device)
+    _need(out, torch.int32, "out")
+    if out.numel() != B:
+        raise ValueError("out must hold B entries")
+    _check(load_library().mi_top_p_sample_batched_f16(
+        _ptr(x), B, V, float(p), float(temperature), int(seed) & 0xFFFFFFFFFFFFFFFF, _ptr(out),
+        _stream(stream)), "mi_top_p_sample_batched_f16")
+    return out
 
 
 def greedy_argmax(logits, out=None, workspace=None, stream=None):

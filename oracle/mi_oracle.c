@@ -485,3 +485,79 @@ void mio_greedy_argmax(const uint16_t* logits, int64_t B, int64_t V, int32_t* ou
         out[r] = best_i[0];
     }
 }
+
+uint64_t mio_fmix64(uint64_t s) {
+    s ^= s >> 33;
+    s *= 0xff51afd7ed558ccdULL;
+    s ^= s >> 33;
+    s *= 0xc4ceb9fe1a85ec53ULL;
+    s ^= s >> 33;
+    return s;
+}
+
+void mio_top_p_sample(const uint16_t* logits, int64_t B, int64_t vocab, float p,
+                      float temperature, uint64_t seed, int32_t* out) {
+    enum { K = 256, STRIDE = 128 };
+    if (vocab > 30000) {
+        mio_greedy_argmax(logits, B, vocab, out);
+        return;
+    }
+    for (int64_t r = 0; r < B; ++r) {
+        const uint16_t* x = logits + r * vocab;
+        float row_max = -INFINITY;
+        for (int64_t i = 0; i < vocab; ++i) {
+            const float v = mio_f16_to_f32(x[i]) / temperature;
+            if (v > row_max) row_max = v;
+        }
+        double sum = 0.0;
+        for (int64_t i = 0; i < vocab; ++i)
+            sum += (double)expf(mio_f16_to_f32(x[i]) / temperature - row_max);
+        const float row_sum = (float)sum;
+        /* K selection rounds over the first thread's share: indices 0, 128, ... */
+        int32_t top_idx[K];
+        float top_val[K];
+        for (int k = 0; k < K; ++k) {
+            float best_val = -INFINITY;
+            int32_t best_idx = -1;
+            for (int64_t i = 0; i < vocab; i += STRIDE) {
+                int used = 0;
+                for (int j = 0; j < k; ++j)
+                    if (top_idx[j] == (int32_t)i) { used = 1; break; }
+                if (used) continue;
+                const float v = expf(mio_f16_to_f32(x[i]) / temperature - row_max) / row_sum;
+                if (v > best_val) { best_val = v; best_idx = (int32_t)i; }
+            }
+            top_idx[k] = best_idx;
+            top_val[k] = best_val;
+        }
+        /* insertion sort, descending (stable) */
+        for (int i = 1; i < K; ++i) {
+            const float v = top_val[i];
+            const int32_t ix = top_idx[i];
+            int j = i - 1;
+            while (j >= 0 && top_val[j] < v) {
+                top_val[j + 1] = top_val[j];
+                top_idx[j + 1] = top_idx[j];
+                --j;
+            }
+            top_val[j + 1] = v;
+            top_idx[j + 1] = ix;
+        }
+        const uint64_t rs = seed + (uint64_t)r;
+        float cum = 0.0f;
+        int32_t choice = top_idx[K - 1];
+        for (int i = 0; i < K; ++i) {
+            cum += top_val[i];
+            if (cum >= p) {
+                const uint64_t h = mio_fmix64(rs ^ ((uint64_t)(int64_t)top_idx[i] << 32));
+                const float u = (float)(h & 0xFFFFFFu) / (float)0x1000000;
+                int slot = (int)(u * (float)(i + 1));
+                if (slot < 0) slot = 0;
+                if (slot > i) slot = i;
+                choice = top_idx[slot];
+                break;
+            }
+        }
+        out[r] = choice;
+    }
+}

@@ -138,6 +138,22 @@ void mio_paged_kv_scatter(const uint16_t* src, uint16_t* cache, const int32_t* b
  * (src/kernels/sampling_kernel.cu:52-76). */
 void mio_greedy_argmax(const uint16_t* logits, int64_t B, int64_t V, int32_t* out);
 
+/* MurmurHash3's 64-bit finaliser, the slot hash of the reference's top-p
+ * (src/kernels/sampling_kernel.cu:177-180). */
+uint64_t mio_fmix64(uint64_t s);
+
+/* Top-p sampling of B rows, row b with seed + b, following
+ * launch_top_p_sample (src/kernels/sampling_kernel.cu:86-221) step by step:
+ * above 30000 logits the greedy argmax (mio_greedy_argmax); otherwise the
+ * row maximum of x/T, probabilities expf(x/T - max) / sum, K = 256 rounds of
+ * strict-greater selection over the first thread's stride-128 share of the
+ * row (indices 0, 128, ...; empty rounds leave index -1 and -inf), the
+ * insertion sort, the running sum over the 256 slots and the fmix64 slot
+ * draw; when the sum never reaches p, slot 255 (index -1 below 30001
+ * logits). */
+void mio_top_p_sample(const uint16_t* logits, int64_t B, int64_t vocab, float p,
+                      float temperature, uint64_t seed, int32_t* out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -61,6 +61,8 @@ def lib() -> ctypes.CDLL:
             "mio_embedding_gather": ([P, P, P, I64, I64, I64, I], None),
             "mio_paged_kv_scatter": ([P, P, P, P, P] + [I64] * 8, None),
             "mio_greedy_argmax": ([P, I64, I64, P], None),
+            "mio_fmix64": ([ctypes.c_uint64], ctypes.c_uint64),
+            "mio_top_p_sample": ([P, I64, I64, F, F, ctypes.c_uint64, P], None),
         }
         for name, (args, res) in sig.items():
             fn = getattr(L, name)
@@ -262,4 +264,19 @@ def greedy_argmax(logits) -> np.ndarray:
     B, V = x.shape
     out = np.empty(B, dtype=np.int32)
     lib().mio_greedy_argmax(_p(x), B, V, _p(out))
+    return out
+
+
+def fmix64(v: int) -> int:
+    return int(lib().mio_fmix64(v & 0xFFFFFFFFFFFFFFFF))
+
+
+def top_p_sample(logits, p: float, temperature: float, seed: int) -> np.ndarray:
+    """logits [V] or [B, V] fp16; int32 [B] (row b with seed + b)."""
+    x = _h(logits)
+    if x.ndim == 1:
+        x = x.reshape(1, -1)
+    B, V = x.shape
+    out = np.empty(B, dtype=np.int32)
+    lib().mio_top_p_sample(_p(x), B, V, p, temperature, seed & 0xFFFFFFFFFFFFFFFF, _p(out))
     return out

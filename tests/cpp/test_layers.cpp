@@ -497,6 +497,27 @@ void gpu_checks() {
                                                   static_cast<int*>(od.data()), 0);
         oh = od.to(Device::cpu());
         EXPECT(static_cast<const int32_t*>(oh.data())[0] == want[0], "greedy single row");
+
+        // top-p: above 30000 logits the greedy argmax; below, a dominant
+        // candidate (index 384, a multiple of 128) is drawn at any seed
+        mini_infer::kernels::launch_top_p_sample(static_cast<const __half*>(lgd.data()), V, 0.9f,
+                                                 0.8f, 11, static_cast<int*>(od.data()), 0);
+        oh = od.to(Device::cpu());
+        EXPECT(static_cast<const int32_t*>(oh.data())[0] == want[0], "top-p above 30000 = greedy");
+        Tensor small = reftest_f16({2, 1000}, 1.0f, 49);
+        static_cast<uint16_t*>(small.data())[384] = 0x4d00;          // 20.0
+        static_cast<uint16_t*>(small.data())[1000 + 384] = 0x4d00;
+        Tensor smd = small.to(Device::cuda(0));
+        Tensor od2 = Tensor::empty({2}, DType::INT32, Device::cuda(0));
+        mini_infer::kernels::launch_top_p_sample_batched(static_cast<const __half*>(smd.data()), 2,
+                                                         1000, 0.9f, 1.0f, 3,
+                                                         static_cast<int*>(od2.data()), 0);
+        Tensor oh2 = od2.to(Device::cpu());
+        const auto* t2 = static_cast<const int32_t*>(oh2.data());
+        std::vector<int32_t> want2(2);
+        mio_top_p_sample(bits(small), 2, 1000, 0.9f, 1.0f, 3, want2.data());
+        EXPECT(t2[0] == 384 && t2[1] == 384 && want2[0] == 384 && want2[1] == 384,
+               "top-p batched, dominant candidate");
     }
     // --- device Tensor round trip --------------------------------------------
     {

@@ -400,3 +400,93 @@ def test_paged_kv_scatter_brute_force():
             ref[1, bt[b, p // bs], :, p % bs, :] = src[b, s]
     assert (out.view(np.uint16) == ref.view(np.uint16)).all()
     assert (out[0].view(np.uint16) == cache[0].view(np.uint16)).all()  # other layer untouched
+
+
+# --- top-p sampling (launch_top_p_sample, sampling_kernel.cu:86-221) ---------
+
+_M64 = (1 << 64) - 1
+
+
+def _fmix64_inverse(h):
+    """The published inverse of MurmurHash3's fmix64 (its own constants)."""
+    h ^= h >> 33
+    h = (h * 0x9CB4B2F8129337DB) & _M64
+    h ^= h >> 33
+    h = (h * 0x4F74430C22A54005) & _M64
+    h ^= h >> 33
+    return h
+
+
+def test_fmix64_known_answer_and_inverse():
+    # fmix64(1) is MurmurHash3's widely quoted value; the inverse, built from
+    # different constants, undoes it only if both multipliers and all shifts
+    # are right
+    assert O.fmix64(1) == 0xB456BCFC34C2CB2C
+    assert O.fmix64(0) == 0
+    rng = np.random.default_rng(5)
+    for v in [int(a) for a in rng.integers(0, 1 << 63, 200, dtype=np.int64)] + [_M64, 1 << 63]:
+        assert _fmix64_inverse(O.fmix64(v)) == v
+
+
+def _top_p_by_sorting(x, p, T, seed):
+    """The rule restated as a sort (not the reference's K selection rounds):
+    candidates at multiples of 128 in (q descending, index ascending) order,
+    the fp32 running sum, the fmix64 slot."""
+    xf = x.astype(np.float32) / np.float32(T)
+    m = xf.max()
+    e = np.exp((xf - m).astype(np.float64))
+    S = np.float32(e.sum())
+    idx = np.arange(0, x.size, 128)
+    q = (np.exp((xf[idx] - m)).astype(np.float32) / S).astype(np.float32)
+    order = np.lexsort((idx, -q))
+    cum = np.float32(0)
+    for i, o in enumerate(order):
+        cum = np.float32(cum + q[o])
+        if cum >= np.float32(p):
+            h = O.fmix64(seed ^ (int(idx[o]) << 32))
+            u = np.float32(h & 0xFFFFFF) / np.float32(1 << 24)
+            slot = min(max(int(np.float32(u * np.float32(i + 1))), 0), i)
+            return int(idx[order[slot]])
+    return -1
+
+
+def test_top_p_rules():
+    rng = np.random.default_rng(21)
+    # above 30000 logits: the greedy argmax
+    x = normal_f16(rng, (3, 30001), 0, 3)
+    assert (O.top_p_sample(x, 0.9, 0.8, 7) == O.greedy_argmax(x)).all()
+    # a dominant candidate: the running sum passes p at the first slot
+    x = normal_f16(rng, (1000,), 0, 1)
+    x[384] = 30
+    assert O.top_p_sample(x, 0.9, 1.0, 3)[0] == 384
+    # a dominant logit that is not a candidate: the sum never reaches p
+    x[384] = 0
+    x[385] = 30
+    assert O.top_p_sample(x, 0.5, 1.0, 3)[0] == -1
+    # nothing but candidates can be returned; equal logits order by index
+    x = np.zeros(640, dtype=np.float16)
+    x[::128] = 8  # five equal candidates holding 95.9% of the mass
+    seen = set()
+    for seed in range(20):
+        got = O.top_p_sample(x, 0.9, 1.0, seed)[0]
+        assert got == _top_p_by_sorting(x, 0.9, 1.0, seed) and got >= 0 and got % 128 == 0
+        seen.add(int(got))
+    assert len(seen) > 1  # the draw spreads over the nucleus
+
+
+@pytest.mark.parametrize("V", [129, 1000, 4096, 30000])
+def test_top_p_selection_rounds_match_a_sort(V):
+    rng = np.random.default_rng(V)
+    for trial in range(12):
+        x = normal_f16(rng, (V,), 0, 2)
+        hot = rng.choice(np.arange(0, V, 128), size=min(6, (V + 127) // 128), replace=False)
+        x[hot] = (rng.random(hot.size) * 6 + 6).astype(np.float16)  # mass on candidates
+        p, T, seed = float(rng.choice([0.3, 0.6, 0.9])), float(rng.choice([0.7, 1.0])), trial
+        assert O.top_p_sample(x, p, T, seed)[0] == _top_p_by_sorting(x, p, T, seed)
+    # rows of a batch draw with seed + row
+    xb = normal_f16(rng, (4, V), 0, 2)
+    xb[:, 0] = 12
+    xb[:, 128 % V] = 12
+    got = O.top_p_sample(xb, 0.95, 1.0, 100)
+    assert [int(g) for g in got] == [_top_p_by_sorting(xb[b], 0.95, 1.0, 100 + b)
+                                     for b in range(4)]
