@@ -362,3 +362,34 @@ def test_fuzz_rope_kv_scatter(mk, orc, dev, seed):
     for name, a, b in (("q", qa, qb), ("k", ka, kb), ("k cache", kca, kcb),
                        ("v cache", vca, vcb), ("v", va, vb)):
         assert_bits_equal(to_host(b), to_host(a), what=name)
+
+
+@pytest.mark.parametrize("seed", range(CASES))
+def test_fuzz_top_p(mk, orc, dev, seed):
+    """Top-p sampling against the oracle over random batch sizes,
+    vocabularies either side of the 30000 greedy boundary, p, temperature
+    and seeds; rows whose outcome sits near a rounding boundary of the fp32
+    probabilities are redrawn (tests/test_gpu_top_p.py states the screen)."""
+    from test_gpu_top_p import _safe
+    rng = np.random.default_rng(13000 + seed)
+    B = int(rng.integers(1, 40))
+    V = int(rng.choice([int(rng.integers(1, 30001)), int(rng.integers(30001, 160000))]))
+    p = float(rng.choice([0.05, 0.3, 0.7, 0.9, 0.99]))
+    T = float(rng.choice([0.5, 0.8, 1.0, 1.7]))
+    draw = int(rng.integers(0, 1 << 62))
+    _case(f"top-p seed={seed} B={B} V={V} p={p} T={T}")
+    rows = []
+    while len(rows) < B:
+        x = normal_f16(rng, (V,), 0, float(rng.choice([0.5, 2, 6])))
+        if V <= 30000:
+            nc = (V + 127) // 128
+            hot = rng.choice(np.arange(0, V, 128), size=min(int(rng.integers(0, 6)), nc),
+                             replace=False)
+            x[hot] = (rng.random(hot.size) * 10).astype(np.float16)
+            if not _safe(x, p, T):
+                continue
+        rows.append(x)
+    x = np.stack(rows)
+    got = to_host(mk.top_p_sample(_dev_array(x, dev, misalign=bool(rng.integers(0, 2))), p, T,
+                                  draw))
+    np.testing.assert_array_equal(got, orc.top_p_sample(x, p, T, draw))
