@@ -107,3 +107,32 @@ def test_top_p_empty_rows_and_refusals(mk, dev):
     # B = 0: nothing written; negative sizes refused
     assert lib.mi_top_p_sample_batched_f16(None, 0, 10, 0.9, 1.0, 1, mk._ptr(out), None) == 0
     assert lib.mi_top_p_sample_batched_f16(None, -1, 10, 0.9, 1.0, 1, mk._ptr(out), None) == -1
+
+
+def test_top_p_in_a_graph(mk, orc, dev):
+    """Captured once, replayed several times with eager work between the
+    replays; every replay matches the oracle (the launch allocates nothing
+    and clears nothing)."""
+    import torch
+    _case("top-p: graph replays")
+    rng = np.random.default_rng(77)
+    x = _rows(rng, 16, 4096, 0.9, 1.0)
+    xd = to_dev(x, dev)
+    out = torch.empty(16, dtype=torch.int32, device=dev)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        mk.top_p_sample(xd, 0.9, 1.0, 123, out=out)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        mk.top_p_sample(xd, 0.9, 1.0, 123, out=out)
+    want = orc.top_p_sample(x, 0.9, 1.0, 123)
+    for _ in range(4):
+        out.fill_(-7)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(to_host(out), want)
+    del graph
