@@ -275,3 +275,39 @@ def test_qk_norm_rope_kv_scatter_refusals(mk, orc, dev):
         mk.qk_norm_rope_kv_scatter(q, k, v, w, w, pos, orc.rope_inv_freq(hd), kc, vc, 0, bs,
                                    segs)
     assert int(torch.count_nonzero(kc)) == 0 and int(torch.count_nonzero(vc)) == 0
+
+
+@pytest.mark.parametrize("bias", [False, True])
+def test_rope_kv_scatter_in_a_graph(mk, orc, dev, bias):
+    """Captured once and replayed with q / k restored eagerly between the
+    replays (they are rotated in place): every replay equals the eager call."""
+    import torch
+    _case(f"rope + kv scatter graph replays, bias={bias}")
+    rng = np.random.default_rng(91 + bias)
+    T, Hq, Hkv, hd, bs, NB = 48, 16, 8, 64, 16, 40
+    segs = _dev_segs(_segments(rng, "ragged", T, bs, NB), dev)
+    q, k, v = (normal_f16(rng, (T, h, hd)) for h in (Hq, Hkv, Hkv))
+    pos = to_dev(rng.integers(0, 32000, T).astype(np.int64), dev)
+    inv = orc.rope_inv_freq(hd, 1e6)
+    extra = tuple(to_dev(normal_f16(rng, (h * hd,), 0, 0.5), dev) for h in (Hq, Hkv, Hkv)) \
+        if bias else ()
+    q0, k0 = to_dev(q, dev), to_dev(k, dev)
+    qd, kd, vd = q0.clone(), k0.clone(), to_dev(v, dev)
+    kc = torch.zeros((1, NB, Hkv, bs, hd), dtype=torch.float16, device=dev)
+    vc = torch.zeros_like(kc)
+    mk.rope_kv_scatter(qd, kd, vd, pos, inv, kc, vc, 0, bs, segs, *extra)
+    torch.cuda.synchronize()
+    want = [to_host(t) for t in (qd, kd, kc, vc)]
+    qd.copy_(q0); kd.copy_(k0); kc.zero_(); vc.zero_()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        mk.rope_kv_scatter(qd, kd, vd, pos, inv, kc, vc, 0, bs, segs, *extra)
+    for _ in range(3):
+        qd.copy_(q0); kd.copy_(k0); kc.zero_(); vc.zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        for name, a, b in zip(("q", "k", "k cache", "v cache"), (qd, kd, kc, vc), want):
+            assert_bits_equal(to_host(a), b, what=f"replay {name}")
+    del graph
