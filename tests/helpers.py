@@ -75,8 +75,9 @@ def assert_norm_rope_close(ours, ref, n16, what):
     sums in an fp32 tree and uses an fp32 reciprocal square root, so the fp16
     value it hands to the rotation can be one ulp away there.  RoPE then
     carries that ulp into an output that may be much smaller (x1 c - x2 s
-    cancels).  Such elements must be rare (< 1e-5 of the tensor) and within
-    one ulp of each rotated operand plus one output ulp."""
+    cancels).  Such elements must be rare (at most 1e-5 of the
+    tensor, or 2 in a smaller one) and within one ulp of each rotated operand
+    plus one output ulp."""
     ours = np.asarray(ours).astype(np.float32)
     ref = np.asarray(ref, np.float32)
     diff = np.abs(ours - ref)
@@ -90,4 +91,7 @@ def assert_norm_rope_close(ours, ref, n16, what):
     assert (diff[out] <= bound[out]).all(), (
         f"{what}: error beyond one ulp of the normalised operands at {worst}: "
         f"ours={ours[worst]} ref={ref[worst]} bound={bound[worst]}")
-    assert out.mean() < 1e-5, f"{what}: {int(out.sum())} of {out.size} outside tolerance"
+    # rare: at most 1 in 10^5 of the tensor, or 2 elements in a small one
+    # (where one boundary case alone exceeds the fraction)
+    assert out.sum() <= max(2, 1e-5 * out.size), (
+        f"{what}: {int(out.sum())} of {out.size} outside tolerance")
