@@ -3,12 +3,12 @@
 
 Headline (the JSON line's `value`): achieved HBM bandwidth of the fused
 residual-add + RMSNorm kernel at Qwen2.5-7B prefill, x / residual fp16
-[8192, 3584] (BASELINE config 2).  One step = one launch over that batch;
+[8192, 3584] (Qwen2.5-7B prefill).  One step = one launch over that batch;
 inputs are resident in HBM before the timed region.  Buffer sets are rotated
 so the working set of consecutive launches exceeds the 256 MB Infinity Cache
 and every launch streams from HBM.
 
-Also reported, under "kernels": every BASELINE config, each kernel timed the
+Also reported, under "kernels": every benchmark workload, each kernel timed the
 same way (average over back-to-back launches with HIP events on the launch
 stream), as algorithmic GB/s, fraction of the 8 TB/s HBM peak and tokens/s.
 
@@ -284,7 +284,7 @@ def headline(mk, dev, steps, warmup):
 
 
 # ---------------------------------------------------------------------------
-# Every BASELINE config
+# Every benchmark workload
 # ---------------------------------------------------------------------------
 
 def config3_positions(gen_np, total, nseq, max_start):
@@ -541,7 +541,7 @@ def all_kernels(mk, dev, iters, warmup):
         out.append(report("rope_kv_scatter" + tag + "_unfused",
                           "RoPE launch + 3 per-segment K+V scatters" + (", bias" if extra else ""),
                           nb + (len(extra) and 36 * 128 * 2), sec, T))
-    # 5j. config 5's form: Q/K RMSNorm + RoPE + K/V scatter in one launch,
+    # 5j. the Gemma-3 form: Q/K RMSNorm + RoPE + K/V scatter in one launch,
     # against qk_norm_rope then the three per-segment scatters
     nbn = nb + 2 * 128 * 2
     sec = time_launches(lambda i: mk.qk_norm_rope_kv_scatter(sets[i][0], sets[i][1], sets[i][2],
@@ -761,7 +761,7 @@ def chain_bytes(s, segments_tokens):
 
 
 def decoder_chain(mk, dev, iters, warmup, qwen2=False, prefills=(3000, 3000)):
-    """BASELINE config 5 as one step: the C++ decoder chain (include/mi_chain.h)
+    """The decoder-chain workload as one step: the C++ decoder chain (include/mi_chain.h)
     over one non-GEMM decoder layer at T = 6064 (64 decode tokens at random
     positions + two 3000-token prefills), then the sampling step:
       gather + input RMSNorm -> Q/K-norm + RoPE -> paged K+V scatter ->
@@ -779,10 +779,10 @@ def decoder_chain(mk, dev, iters, warmup, qwen2=False, prefills=(3000, 3000)):
 
     prefills=(): the decode-only step (T = 64), rows named decoder_chain_decode64.
 
-    qwen2: Qwen2.5-7B's own attention pre-processing instead of config 5's
+    qwen2: Qwen2.5-7B's own attention pre-processing instead of the chain's
     Gemma-3-style Q/K norm -- the q/k/v_proj bias and no Q/K norm
-    (attention.cpp:717-780): the chain adds the Q/K bias in the rotation pass
-    and V's on its way into the cache; the unfused composition runs
+    (attention.cpp:717-780): the chain adds the q/k/v bias, rotates and writes
+    K and V into the cache in one launch; the unfused composition runs
     launch_add_bias on Q, K and V, the tables and two RoPE launches, then the
     two scatters (like the config-5 composition, without the reference's
     Q/K device copies)."""
@@ -859,7 +859,7 @@ def decoder_chain(mk, dev, iters, warmup, qwen2=False, prefills=(3000, 3000)):
 
 
 def shape_table(mk, dev, iters=40, warmup=5):
-    """Beyond the BASELINE configs (`--shapes`): each kernel across common
+    """Beyond the benchmark workloads (`--shapes`): each kernel across common
     LLM shapes, ~100-260 MB per launch unless the shape is small by nature,
     timed like the kernel table (graph replay, buffers rotated past the
     Infinity Cache).  Rows: kernel, shape, us, % of HBM peak."""

@@ -1,4 +1,4 @@
-"""GPU accuracy margins at the BASELINE shapes: how far inside the parity bar
+"""GPU accuracy margins at the benchmark workloads' shapes (Qwen2.5-7B): how far inside the parity bar
 the fp32-math kernels land.
 
 The parity bar is rtol = atol = 1e-3 against the fp32 oracle

@@ -10,7 +10,7 @@ paged K/V scatter -> [attention] -> residual add + post-attention RMSNorm ->
 -> softmax and greedy argmax.  The bracketed GEMMs are seeded stand-in
 buffers.
 
-BASELINE config 5 is the workload: 64 decode tokens at random positions
+The workload: 64 decode tokens at random positions
 plus two 3000-token prefills (T = 6064), Qwen2.5-7B shapes, embedding table
 [152064, 3584], logits [64, 152064].
 
@@ -150,16 +150,16 @@ def _check_chain(chain_mod, orc, w, what):
 
 
 def test_chain_config5_every_stage(chain_mod, orc, cfg5):
-    """BASELINE config 5 through the whole chain, Gemma-3-style Q/K norm on."""
-    _case("chain config 5: T=6064, qk-norm + rope, SwiGLU [6064,18944], logits [64,152064]")
-    _check_chain(chain_mod, orc, cfg5, "config 5")
+    """The decoder-chain workload through the whole chain, Gemma-3-style Q/K norm on."""
+    _case("chain workload: T=6064, qk-norm + rope, SwiGLU [6064,18944], logits [64,152064]")
+    _check_chain(chain_mod, orc, cfg5, "chain workload")
 
 
 def test_chain_config5_plain_rope(chain_mod, orc, cfg5):
     """Qwen2.5 proper has no Q/K norm: the plain in-place RoPE on the chain's
     positions (64 decode tokens + two 3000-token prefills), bit-exact, and
     the scatter of its rotated K."""
-    _case("chain config 5 without qk-norm: rope_neox_qk on the chain positions")
+    _case("chain workload without qk-norm: rope_neox_qk on the chain positions")
     import copy
     w = copy.copy(cfg5)
     w.shapes = dict(cfg5.shapes, use_qk_norm=0)
@@ -178,11 +178,11 @@ def test_chain_config5_plain_rope(chain_mod, orc, cfg5):
 
 
 def test_chain_config5_qwen2_bias(chain_mod, orc, dev, cfg5):
-    """Qwen2.5 proper: the QKV projection bias and no Q/K norm, at config 5
+    """Qwen2.5 proper: the QKV projection bias and no Q/K norm, at the chain workload
     (T = 6064): Q/K biased and rotated in one pass (bit-exact against
     add_bias then RoPE), V's bias added on its way into the cache
     (bit-exact), then the rest of the step."""
-    _case("chain config 5, Qwen2 QKV bias, no qk-norm")
+    _case("chain workload, Qwen2 QKV bias, no qk-norm")
     import copy
     import torch
     w = copy.copy(cfg5)

@@ -34,7 +34,7 @@ def test_reference_cases(mk, orc, dev):
 
 
 def test_config4_swiglu_full(mk, orc, dev):
-    """BASELINE config 4a: gate/up [4096, 18944] ~N(0,1)."""
+    """The SwiGLU workload: gate/up [4096, 18944] ~N(0,1)."""
     _case("swiglu [4096,18944]")
     rng = np.random.default_rng(41)
     g = normal_f16(rng, (4096, 18944))
@@ -44,7 +44,7 @@ def test_config4_swiglu_full(mk, orc, dev):
 
 
 def test_config4_geglu_full(mk, orc, dev):
-    """BASELINE config 4b: gate/up [4096, 14336] ~N(0,1)."""
+    """The GeGLU workload: gate/up [4096, 14336] ~N(0,1)."""
     _case("geglu [4096,14336]")
     rng = np.random.default_rng(42)
     g = normal_f16(rng, (4096, 14336))

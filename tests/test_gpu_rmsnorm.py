@@ -35,7 +35,7 @@ def test_reference_case_std_and_gemma(mk, orc, dev):
 
 
 def test_config1_16x3584(mk, orc, dev):
-    """x [16,3584] ~N(0,1), w ~N(1,0.1), eps 1e-6."""
+    """The small RMSNorm workload: x [16,3584] ~N(0,1), w ~N(1,0.1), eps 1e-6."""
     _case("rmsnorm [16,3584]")
     rng = np.random.default_rng(1)
     x = normal_f16(rng, (16, 3584))
@@ -98,7 +98,7 @@ def test_qk_norm_chain_shape(mk, orc, dev):
 
 @pytest.mark.parametrize("N,D", [(8192, 3584), (6064, 3584), (37, 128), (5, 3583), (3, 20000)])
 def test_fused_add_rmsnorm(mk, orc, dev, N, D):
-    """BASELINE config 2 ([8192,3584]) and the chain's residual+norm ([6064,3584])."""
+    """The headline workload ([8192,3584]) and the chain's residual+norm ([6064,3584])."""
     _case(f"fused add+rmsnorm [{N},{D}]")
     rng = np.random.default_rng(N + D)
     x = normal_f16(rng, (N, D))

@@ -26,7 +26,7 @@ def _case(msg):
 
 def config3_positions(rng, total=4096, nseq=8, max_start=28000):
     """8 sequences of uniform-random lengths summing to `total`, each starting
-    at a uniform offset in [0, max_start)."""
+    at a uniform offset in [0, max_start) (the RoPE benchmark workload)."""
     cuts = np.sort(rng.choice(np.arange(1, total), nseq - 1, replace=False))
     lengths = np.diff(np.concatenate([[0], cuts, [total]]))
     starts = rng.integers(0, max_start, nseq)
@@ -81,7 +81,7 @@ def test_tables_huge_positions(mk, orc, dev, lo, hi):
 
 
 def test_config3_fused_qk(mk, orc, dev):
-    """Q [4096,28,128], K [4096,4,128] in place, theta 1e6."""
+    """The RoPE benchmark workload: Q [4096,28,128], K [4096,4,128] in place, theta 1e6."""
     _case("rope fused qk [4096,28|4,128]")
     rng = np.random.default_rng(33)
     T, Hq, Hkv, hd = 4096, 28, 4, 128
@@ -237,7 +237,7 @@ def _bias_ref(orc, x, bias):
 def test_bias_rope(mk, orc, dev, T, Hq, Hkv, hd, chain):
     """Qwen2's q_proj / k_proj bias with the rotation in one pass, bit-exact
     against launch_add_bias followed by RoPE (attention.cpp:717-780): at the
-    chain's tokens and positions, config 3's, a head_dim of 6 (scalar path)
+    chain's tokens and positions, the RoPE workload's, a head_dim of 6 (scalar path)
     and K-only."""
     _case(f"bias + rope T={T} Hq={Hq} Hkv={Hkv} hd={hd}")
     rng = np.random.default_rng(T + Hq * 10 + hd)

@@ -197,7 +197,7 @@ def test_rope_kv_scatter_refusals(mk, orc, dev):
 
 
 @pytest.mark.parametrize("T,Hq,Hkv,hd,kind", [
-    (6064, 28, 4, 128, "chain"),   # config 5: Qwen2.5-7B heads with Gemma-3-style Q/K norm
+    (6064, 28, 4, 128, "chain"),   # the chain workload: Qwen2.5-7B heads, Gemma-3-style Q/K norm
     (48, 16, 8, 64, "ragged"),
     (48, 8, 4, 256, "ragged"),
     (48, 4, 2, 16, "ragged"),

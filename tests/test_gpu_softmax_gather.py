@@ -29,7 +29,7 @@ def test_softmax_reference_case(mk, orc, dev):
 
 
 def test_softmax_lm_head_config(mk, orc, dev):
-    """BASELINE config 5 softmax: logits [64, 152064] ~N(0,4) (split-row path)."""
+    """The decoder chain's sampling softmax: logits [64, 152064] ~N(0,4) (split-row path)."""
     _case("softmax [64,152064]")
     rng = np.random.default_rng(51)
     x = normal_f16(rng, (64, 152064), 0, 4)
@@ -62,7 +62,7 @@ def test_softmax_in_place_and_neg_inf(mk, orc, dev):
 
 
 def test_gather_chain_config(mk, orc, dev):
-    """BASELINE config 5 gather: table [152064, 3584] ~N(0, 0.02), 6064 uniform ids."""
+    """The decoder chain's gather: table [152064, 3584] ~N(0, 0.02), 6064 uniform ids."""
     _case("gather [6064] from [152064,3584]")
     import torch
     g = torch.Generator(device=dev).manual_seed(53)
