@@ -11,7 +11,9 @@ device-scope mirror; polls read the L2 copy first.  These tests check that:
   * results match the oracle in both modes;
   * the default mode is served by the L2 copy: a call takes far less than
     the L2 phase's 20 us bound (a launch that fell through to the mirror
-    would take at least that long).
+    would take at least that long);
+  * calls on two streams at once, beside a kernel holding CUs, stay correct
+    and bounded in time.
 """
 import numpy as np
 import pytest
@@ -112,3 +114,54 @@ def test_default_mode_is_served_by_l2(mk, dev):
         us = t0.elapsed_time(t1) * 1e3 / n
         print(f"[case]   {name}: {us:.1f} us per call", flush=True)
         assert us < 16.0, f"{name}: {us:.1f} us per call (L2 exchange not taken?)"
+
+
+def test_one_launch_kernels_on_concurrent_streams(mk, orc, dev):
+    """Softmax, argmax and the fused pass on two streams at once, each call
+    with its own workspace, next to a large SwiGLU holding CUs: a row's chunk
+    workgroups may then not all be resident together, and polls that run out
+    take the bounded fallback.  Every result matches the oracle, and the whole
+    exchange finishes well inside a wall-clock bound."""
+    import time
+    import torch
+    _case("one-launch kernels on two concurrent streams")
+    rng = np.random.default_rng(31)
+    shapes = ((64, 152064), (48, 131072))
+    xs = [normal_f16(rng, s, 0, 4) for s in shapes]
+    xd = [to_dev(x, dev) for x in xs]
+    g = (torch.randn((4096, 18944), device=dev) * 2).half()
+    u = torch.randn((4096, 18944), device=dev).half()
+    act = torch.empty_like(g)
+    ws = [(torch.zeros(mk.softmax_workspace_bytes(*s), dtype=torch.uint8, device=dev),
+           torch.zeros(mk.greedy_argmax_workspace_bytes(*s), dtype=torch.uint8, device=dev),
+           torch.zeros(mk.softmax_argmax_workspace_bytes(*s), dtype=torch.uint8, device=dev))
+          for s in shapes]
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    torch.cuda.synchronize()
+    t0 = time.time()
+    outs = []
+    for rep in range(3):
+        res = []
+        for i, st in enumerate(streams):
+            with torch.cuda.stream(st):
+                if i == 0:
+                    mk.swiglu(g, u, out=act)
+                y = mk.softmax(xd[i], workspace=ws[i][0])
+                a = mk.greedy_argmax(xd[i], workspace=ws[i][1])
+                p, o = mk.softmax_argmax(xd[i], ws[i][2])
+                res.append((y, a, p, o))
+        outs.append(res)
+    torch.cuda.synchronize()
+    wall = time.time() - t0
+    for res in outs:
+        for i, (y, a, p, o) in enumerate(res):
+            x = xs[i]
+            want = orc.greedy_argmax(x)
+            np.testing.assert_array_equal(to_host(a).astype(np.int64), want)
+            np.testing.assert_array_equal(to_host(o).astype(np.int64), want)
+            yh = to_host(y)
+            assert_bits_equal(to_host(p), yh, what=f"fused probs vs softmax {shapes[i]}")
+            assert_close(yh, orc.softmax(x, nthreads=8), what=f"softmax {shapes[i]}")
+    # 18 one-launch calls: even every poll of every call running to its 200 us
+    # bound would stay far below this
+    assert wall < 10.0, f"{wall:.1f} s"
