@@ -603,7 +603,10 @@ int launch_rope_t(const half_t* q_in, half_t* q_out, int hq, const half_t* k_in,
                   int hk, const int64_t* positions, const half_t* cos_t, const half_t* sin_t,
                   int64_t T, int d, const InvFreq& inv, hipStream_t s,
                   const half_t* bq = nullptr, const half_t* bk = nullptr) {
-    const int tpw = fill_tokens_per_wg((hq + hk) * (d / 2 / VEC));
+    int tpw = fill_tokens_per_wg((hq + hk) * (d / 2 / VEC));
+    // the bias form holds twice the registers per token: 8 tokens of 16-byte
+    // units spill (236 bytes of scratch), 4 fit in 122 VGPRs
+    if (BIAS && VEC == 8 && tpw > 4) tpw = 4;
     const int64_t grid = ceil_div(T, tpw);
     if (grid > kMaxGridX) return MI_ERR_UNSUPPORTED;
     if (static_cast<int64_t>(tpw) * (hq + hk) * (d / 2 / VEC) >= (int64_t{1} << 22))
@@ -763,7 +766,9 @@ struct KvSegs {
 // NORM (Gemma 3): the per-head Q/K RMSNorm of qk_norm_rope_kernel first --
 // the CPH = hd/16 lanes of a head sum their squares by DPP, the normalised
 // value is rounded to fp16 where the reference stores it, and the rotation
-// takes it from registers.  CPH = 0: head_dim known at run time (no norm).
+// takes it from registers.  CPH = head_dim / 16 at compile time (shifts for
+// the lane -> (head, slice) split: 0.3-0.4 us less than CPH = 0 at Qwen2.5's
+// shapes); CPH = 0: head_dim known at run time (no norm).
 template <bool BIAS, bool NORM, int CPH>
 __global__ __launch_bounds__(256) void rope_kv_kernel(half_t* q, half_t* k, const half_t* v,
                                                        int Hq, int Hkv, int hd,
@@ -811,7 +816,7 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(half_t* q, half_t* k, cons
         }
     }
     const int vj = tid;  // V vector of this lane (Hkv * hd / 8 <= 256)
-    const bool vlane = vj < Hkv * (half >> 2);
+    const bool vlane = sg.n > 0 && vj < Hkv * (half >> 2);  // no segment: V not read
     h8 vv = h8(0), vb = h8(0);
     if (vlane) {
         vv = ld8_stream(v + tok * Hkv * (2 * half) + vj * 8);
@@ -894,10 +899,62 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(half_t* q, half_t* k, cons
             for (int e = 0; e < 8; ++e) vv[e] = to_half((float)vv[e] + (float)vb[e]);
         }
         const int per_head = half >> 2;
-        const int vh = CPH ? vj / (CPH * 2) : small_div(vj, 1.0f / static_cast<float>(per_head));
+        int vh;
+        if constexpr (CPH != 0)
+            vh = vj / (CPH * 2);
+        else
+            vh = small_div(vj, 1.0f / static_cast<float>(per_head));
         const int vd = (vj - vh * per_head) * 8;
         st8_stream_wt(v_cache + dst_base + static_cast<int64_t>(vh) * bs * (2 * half) + vd, vv);
     }
+}
+
+// RoPE of Q and K from positions (+ the Q/K bias) through rope_kv_kernel
+// with no segment: one token per 256-lane workgroup, head_dim's lane split at
+// compile time.  Against rope_kernel at T = 6064 (plain / with the bias):
+// 256 (head, slice) units per token 17.9 -> 17.6 / 19.2 -> 18.7 us (at T =
+// 4096: 12.8 -> 12.5 us), 192 units 15.1 -> 13.7 / 16.2 -> 14.5, 144 units
+// 13.3 -> 12.1 / 15.4 -> 13.7, 96 units 9.4 -> 9.1; below that plain RoPE is
+// faster in rope_kernel, which packs several tokens per workgroup (64 units
+// 7.3 against 7.6 us), while the bias form there is not (40 units 17.0
+// against 7.4 us).  MI_ERR_UNSUPPORTED: the caller runs rope_kernel.
+#ifndef MI_RKV_MIN_UNITS
+#define MI_RKV_MIN_UNITS 80
+#endif
+int rope_qk_one_token(half_t* q, half_t* k, const half_t* bq, const half_t* bk,
+                      const int64_t* positions, const InvFreq& inv, int64_t T, int64_t Hq,
+                      int64_t Hkv, int64_t head_dim, hipStream_t s) {
+    const int64_t units = (Hq + Hkv) * (head_dim / 16);
+    if (head_dim % 16 != 0 || head_dim / 2 > kMaxHalf || units > 256 ||
+        (!bq && units < MI_RKV_MIN_UNITS) ||
+        T > kMaxGridX || !aligned16(q) || (Hkv > 0 && !aligned16(k)) ||
+        (bq && !aligned16(bq)) || (bk && Hkv > 0 && !aligned16(bk)))
+        return MI_ERR_UNSUPPORTED;
+    KvSegs sg{};
+    sg.n = 0;
+    const dim3 g(static_cast<unsigned>(T)), b(256);
+    const int hq = static_cast<int>(Hq), hk = static_cast<int>(Hkv), d = static_cast<int>(head_dim);
+#define MI_RQ_ARGS                                                                          \
+    q, k, k, hq, hk, d, positions, inv, bq, bk, nullptr, nullptr, nullptr, 0.0f, 0.0f, nullptr, \
+        nullptr, sg, 0, 0, 1
+#define MI_RQ_CPH(BIAS)                                                                     \
+    switch (head_dim / 16) {                                                                \
+        case 1: rope_kv_kernel<BIAS, false, 1><<<g, b, 0, s>>>(MI_RQ_ARGS); break;         \
+        case 2: rope_kv_kernel<BIAS, false, 2><<<g, b, 0, s>>>(MI_RQ_ARGS); break;         \
+        case 4: rope_kv_kernel<BIAS, false, 4><<<g, b, 0, s>>>(MI_RQ_ARGS); break;         \
+        case 8: rope_kv_kernel<BIAS, false, 8><<<g, b, 0, s>>>(MI_RQ_ARGS); break;         \
+        case 16: rope_kv_kernel<BIAS, false, 16><<<g, b, 0, s>>>(MI_RQ_ARGS); break;       \
+        case 32: rope_kv_kernel<BIAS, false, 32><<<g, b, 0, s>>>(MI_RQ_ARGS); break;       \
+        default: rope_kv_kernel<BIAS, false, 0><<<g, b, 0, s>>>(MI_RQ_ARGS);               \
+    }
+    if (bq) {
+        MI_RQ_CPH(true)
+    } else {
+        MI_RQ_CPH(false)
+    }
+#undef MI_RQ_CPH
+#undef MI_RQ_ARGS
+    return launch_status();
 }
 
 // (Hq + Hkv) * hd/2 must fit the int lane arithmetic of rope_kernel.
@@ -969,6 +1026,10 @@ extern "C" int mi_rope_neox_qk_f16(void* q, void* k, const int64_t* positions,
         k = nullptr;
         Hkv = 0;
     }
+    const int st = mi::rope_qk_one_token(static_cast<half_t*>(q), static_cast<half_t*>(k),
+                                         nullptr, nullptr, positions, inv, T, Hq, Hkv, head_dim,
+                                         mi::as_stream(stream));
+    if (st != MI_ERR_UNSUPPORTED) return st;
     return mi::launch_rope(static_cast<const half_t*>(q), static_cast<half_t*>(q), Hq,
                            static_cast<const half_t*>(k), static_cast<half_t*>(k), Hkv,
                            positions, nullptr, nullptr, T, head_dim, inv,
@@ -1003,6 +1064,11 @@ extern "C" int mi_bias_rope_neox_qk_f16(void* q, void* k, const void* q_bias, co
         k_bias = nullptr;
         Hkv = 0;
     }
+    const int st = mi::rope_qk_one_token(
+        static_cast<half_t*>(q), static_cast<half_t*>(k), static_cast<const half_t*>(q_bias),
+        static_cast<const half_t*>(k_bias), positions, inv, T, Hq, Hkv, head_dim,
+        mi::as_stream(stream));
+    if (st != MI_ERR_UNSUPPORTED) return st;
     return mi::launch_rope(static_cast<const half_t*>(q), static_cast<half_t*>(q), Hq,
                            static_cast<const half_t*>(k), static_cast<half_t*>(k), Hkv,
                            positions, nullptr, nullptr, T, head_dim, inv, mi::as_stream(stream),
@@ -1098,21 +1164,26 @@ int rope_kv_launch(void* q, void* k, const void* v, const void* q_bias, const vo
 #define MI_RKV_ARGS                                                                           \
     qh, kh, vh, hq, hk, d, positions, inv, bqh, bkh, bvh, wqh, wkh, eps, wb, kc, vc, sg, layer, \
         num_blocks, block_size
-    if (norm) {
-        switch (head_dim / 16) {
-            case 1: rope_kv_kernel<false, true, 1><<<g, b, 0, s>>>(MI_RKV_ARGS); break;
-            case 2: rope_kv_kernel<false, true, 2><<<g, b, 0, s>>>(MI_RKV_ARGS); break;
-            case 4: rope_kv_kernel<false, true, 4><<<g, b, 0, s>>>(MI_RKV_ARGS); break;
-            case 8: rope_kv_kernel<false, true, 8><<<g, b, 0, s>>>(MI_RKV_ARGS); break;
-            case 16: rope_kv_kernel<false, true, 16><<<g, b, 0, s>>>(MI_RKV_ARGS); break;
-            case 32: rope_kv_kernel<false, true, 32><<<g, b, 0, s>>>(MI_RKV_ARGS); break;
-            default: return MI_ERR_UNSUPPORTED;  // head_dim not 16 * 2^k
-        }
-    } else if (bias) {
-        rope_kv_kernel<true, false, 0><<<g, b, 0, s>>>(MI_RKV_ARGS);
-    } else {
-        rope_kv_kernel<false, false, 0><<<g, b, 0, s>>>(MI_RKV_ARGS);
+#define MI_RKV_CPH(BIAS, NORM)                                                            \
+    switch (head_dim / 16) {                                                              \
+        case 1: rope_kv_kernel<BIAS, NORM, 1><<<g, b, 0, s>>>(MI_RKV_ARGS); break;       \
+        case 2: rope_kv_kernel<BIAS, NORM, 2><<<g, b, 0, s>>>(MI_RKV_ARGS); break;       \
+        case 4: rope_kv_kernel<BIAS, NORM, 4><<<g, b, 0, s>>>(MI_RKV_ARGS); break;       \
+        case 8: rope_kv_kernel<BIAS, NORM, 8><<<g, b, 0, s>>>(MI_RKV_ARGS); break;       \
+        case 16: rope_kv_kernel<BIAS, NORM, 16><<<g, b, 0, s>>>(MI_RKV_ARGS); break;     \
+        case 32: rope_kv_kernel<BIAS, NORM, 32><<<g, b, 0, s>>>(MI_RKV_ARGS); break;     \
+        default:                                                                          \
+            if (NORM) return MI_ERR_UNSUPPORTED; /* head_dim not 16 * 2^k */             \
+            rope_kv_kernel<BIAS, false, 0><<<g, b, 0, s>>>(MI_RKV_ARGS);                 \
     }
+    if (norm) {
+        MI_RKV_CPH(false, true)
+    } else if (bias) {
+        MI_RKV_CPH(true, false)
+    } else {
+        MI_RKV_CPH(false, false)
+    }
+#undef MI_RKV_CPH
 #undef MI_RKV_ARGS
     return launch_status();
 }
