@@ -909,7 +909,7 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(half_t* q, half_t* k, cons
     }
 }
 
-// RoPE of Q and K from positions (+ the Q/K bias) through rope_kv_kernel
+// RoPE of Q and K from positions (+ the Q/K bias, or the Q/K norm) through rope_kv_kernel
 // with no segment: one token per 256-lane workgroup, head_dim's lane split at
 // compile time.  Against rope_kernel at T = 6064 (plain / with the bias):
 // 256 (head, slice) units per token 17.9 -> 17.6 / 19.2 -> 18.7 us (at T =
@@ -918,25 +918,34 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(half_t* q, half_t* k, cons
 // faster in rope_kernel, which packs several tokens per workgroup (64 units
 // 7.3 against 7.6 us), while the bias form there is not (40 units 17.0
 // against 7.4 us).  MI_ERR_UNSUPPORTED: the caller runs rope_kernel.
+// With the Q/K norm (against qk_norm_rope_pipe_kernel, T = 6064): 256 units
+// 19.5 -> 17.9 us (T = 4096: 13.8 -> 12.8, T = 64: 4.2 -> 3.1), 192 units
+// 15.5 -> 14.1, 144 units 14.6 -> 13.0; 96 units 9.5 against 10.1 us, so the
+// norm form takes tokens of 120 units and more.
 #ifndef MI_RKV_MIN_UNITS
 #define MI_RKV_MIN_UNITS 80
 #endif
+constexpr int64_t kRkvMinUnitsNorm = 120;
 int rope_qk_one_token(half_t* q, half_t* k, const half_t* bq, const half_t* bk,
                       const int64_t* positions, const InvFreq& inv, int64_t T, int64_t Hq,
-                      int64_t Hkv, int64_t head_dim, hipStream_t s) {
+                      int64_t Hkv, int64_t head_dim, hipStream_t s,
+                      const half_t* wq = nullptr, const half_t* wk = nullptr, float eps = 0.0f,
+                      float w_bias = 0.0f) {
     const int64_t units = (Hq + Hkv) * (head_dim / 16);
-    if (head_dim % 16 != 0 || head_dim / 2 > kMaxHalf || units > 256 ||
-        (!bq && units < MI_RKV_MIN_UNITS) ||
+    const bool norm = wq != nullptr;
+    const int64_t min_units = norm ? kRkvMinUnitsNorm : (bq ? 1 : MI_RKV_MIN_UNITS);
+    if (head_dim % 16 != 0 || head_dim / 2 > kMaxHalf || units > 256 || units < min_units ||
         T > kMaxGridX || !aligned16(q) || (Hkv > 0 && !aligned16(k)) ||
-        (bq && !aligned16(bq)) || (bk && Hkv > 0 && !aligned16(bk)))
+        (bq && !aligned16(bq)) || (bk && Hkv > 0 && !aligned16(bk)) ||
+        (norm && (!aligned16(wq) || (Hkv > 0 && !aligned16(wk)))))
         return MI_ERR_UNSUPPORTED;
     KvSegs sg{};
     sg.n = 0;
     const dim3 g(static_cast<unsigned>(T)), b(256);
     const int hq = static_cast<int>(Hq), hk = static_cast<int>(Hkv), d = static_cast<int>(head_dim);
 #define MI_RQ_ARGS                                                                          \
-    q, k, k, hq, hk, d, positions, inv, bq, bk, nullptr, nullptr, nullptr, 0.0f, 0.0f, nullptr, \
-        nullptr, sg, 0, 0, 1
+    q, k, k, hq, hk, d, positions, inv, bq, bk, nullptr, wq, wk, eps, w_bias, nullptr, nullptr, \
+        sg, 0, 0, 1
 #define MI_RQ_CPH(BIAS)                                                                     \
     switch (head_dim / 16) {                                                                \
         case 1: rope_kv_kernel<BIAS, false, 1><<<g, b, 0, s>>>(MI_RQ_ARGS); break;         \
@@ -947,7 +956,17 @@ int rope_qk_one_token(half_t* q, half_t* k, const half_t* bq, const half_t* bk,
         case 32: rope_kv_kernel<BIAS, false, 32><<<g, b, 0, s>>>(MI_RQ_ARGS); break;       \
         default: rope_kv_kernel<BIAS, false, 0><<<g, b, 0, s>>>(MI_RQ_ARGS);               \
     }
-    if (bq) {
+    if (norm) {
+        switch (head_dim / 16) {
+            case 1: rope_kv_kernel<false, true, 1><<<g, b, 0, s>>>(MI_RQ_ARGS); break;
+            case 2: rope_kv_kernel<false, true, 2><<<g, b, 0, s>>>(MI_RQ_ARGS); break;
+            case 4: rope_kv_kernel<false, true, 4><<<g, b, 0, s>>>(MI_RQ_ARGS); break;
+            case 8: rope_kv_kernel<false, true, 8><<<g, b, 0, s>>>(MI_RQ_ARGS); break;
+            case 16: rope_kv_kernel<false, true, 16><<<g, b, 0, s>>>(MI_RQ_ARGS); break;
+            case 32: rope_kv_kernel<false, true, 32><<<g, b, 0, s>>>(MI_RQ_ARGS); break;
+            default: return MI_ERR_UNSUPPORTED;
+        }
+    } else if (bq) {
         MI_RQ_CPH(true)
     } else {
         MI_RQ_CPH(false)
@@ -1246,6 +1265,13 @@ extern "C" int mi_qk_norm_rope_f16(void* q, void* k, const void* q_weight, const
         k = nullptr;
         k_weight = nullptr;
         Hkv = 0;
+    }
+    {
+        const int st = mi::rope_qk_one_token(
+            static_cast<half_t*>(q), static_cast<half_t*>(k), nullptr, nullptr, positions, inv,
+            T, Hq, Hkv, head_dim, mi::as_stream(stream), static_cast<const half_t*>(q_weight),
+            static_cast<const half_t*>(k_weight), eps, add_one ? 1.0f : -0.0f);
+        if (st != MI_ERR_UNSUPPORTED) return st;
     }
     return mi::launch_qk_norm_rope(static_cast<half_t*>(q), Hq, static_cast<half_t*>(k), Hkv,
                                    static_cast<const half_t*>(q_weight),
