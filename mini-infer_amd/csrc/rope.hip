@@ -769,7 +769,9 @@ struct KvSegs {
 // takes it from registers.  CPH = head_dim / 16 at compile time (shifts for
 // the lane -> (head, slice) split: 0.3-0.4 us less than CPH = 0 at Qwen2.5's
 // shapes); CPH = 0: head_dim known at run time (no norm).
-template <bool BIAS, bool NORM, int CPH>
+// SEG = false: RoPE (+ bias or norm) alone -- no cache segment, no V, no
+// cache stores (a distinct kernel in traces, with none of that code).
+template <bool BIAS, bool NORM, int CPH, bool SEG = true>
 __global__ __launch_bounds__(256) void rope_kv_kernel(half_t* q, half_t* k, const half_t* v,
                                                        int Hq, int Hkv, int hd,
                                                        const int64_t* __restrict__ positions,
@@ -816,7 +818,7 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(half_t* q, half_t* k, cons
         }
     }
     const int vj = tid;  // V vector of this lane (Hkv * hd / 8 <= 256)
-    const bool vlane = sg.n > 0 && vj < Hkv * (half >> 2);  // no segment: V not read
+    const bool vlane = SEG && sg.n > 0 && vj < Hkv * (half >> 2);  // no segment: V not read
     h8 vv = h8(0), vb = h8(0);
     if (vlane) {
         vv = ld8_stream(v + tok * Hkv * (2 * half) + vj * 8);
@@ -829,7 +831,7 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(half_t* q, half_t* k, cons
     // (token indices and segment sizes fit 32 bits: T <= kMaxGridX)
     int64_t dst_base = -1;
     const int itok = static_cast<int>(tok);
-    for (int i = 0; i < sg.n; ++i) {
+    for (int i = 0; SEG && i < sg.n; ++i) {
         const int r = itok - static_cast<int>(sg.off[i]);
         const int S = static_cast<int>(sg.S[i]);
         if (r < 0 || r >= static_cast<int>(sg.B[i]) * S) continue;
@@ -887,13 +889,13 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(half_t* q, half_t* k, cons
         }
         st8_out<NORM ? MI_WT_QKNR : MI_WT_ROPE>(hp + c * 8, y1);
         st8_out<NORM ? MI_WT_QKNR : MI_WT_ROPE>(hp + half + c * 8, y2);
-        if (h >= Hq && dst_base >= 0) {
+        if (SEG && h >= Hq && dst_base >= 0) {
             half_t* kd = k_cache + dst_base + static_cast<int64_t>(h - Hq) * bs * (2 * half);
             st8_stream_wt(kd + c * 8, y1);
             st8_stream_wt(kd + half + c * 8, y2);
         }
     }
-    if (vlane && dst_base >= 0) {
+    if (SEG && vlane && dst_base >= 0) {
         if constexpr (BIAS) {
 #pragma unroll
             for (int e = 0; e < 8; ++e) vv[e] = to_half((float)vv[e] + (float)vb[e]);
@@ -948,22 +950,22 @@ int rope_qk_one_token(half_t* q, half_t* k, const half_t* bq, const half_t* bk,
         sg, 0, 0, 1
 #define MI_RQ_CPH(BIAS)                                                                     \
     switch (head_dim / 16) {                                                                \
-        case 1: rope_kv_kernel<BIAS, false, 1><<<g, b, 0, s>>>(MI_RQ_ARGS); break;         \
-        case 2: rope_kv_kernel<BIAS, false, 2><<<g, b, 0, s>>>(MI_RQ_ARGS); break;         \
-        case 4: rope_kv_kernel<BIAS, false, 4><<<g, b, 0, s>>>(MI_RQ_ARGS); break;         \
-        case 8: rope_kv_kernel<BIAS, false, 8><<<g, b, 0, s>>>(MI_RQ_ARGS); break;         \
-        case 16: rope_kv_kernel<BIAS, false, 16><<<g, b, 0, s>>>(MI_RQ_ARGS); break;       \
-        case 32: rope_kv_kernel<BIAS, false, 32><<<g, b, 0, s>>>(MI_RQ_ARGS); break;       \
-        default: rope_kv_kernel<BIAS, false, 0><<<g, b, 0, s>>>(MI_RQ_ARGS);               \
+        case 1: rope_kv_kernel<BIAS, false, 1, false><<<g, b, 0, s>>>(MI_RQ_ARGS); break;   \
+        case 2: rope_kv_kernel<BIAS, false, 2, false><<<g, b, 0, s>>>(MI_RQ_ARGS); break;   \
+        case 4: rope_kv_kernel<BIAS, false, 4, false><<<g, b, 0, s>>>(MI_RQ_ARGS); break;   \
+        case 8: rope_kv_kernel<BIAS, false, 8, false><<<g, b, 0, s>>>(MI_RQ_ARGS); break;   \
+        case 16: rope_kv_kernel<BIAS, false, 16, false><<<g, b, 0, s>>>(MI_RQ_ARGS); break; \
+        case 32: rope_kv_kernel<BIAS, false, 32, false><<<g, b, 0, s>>>(MI_RQ_ARGS); break; \
+        default: rope_kv_kernel<BIAS, false, 0, false><<<g, b, 0, s>>>(MI_RQ_ARGS);         \
     }
     if (norm) {
         switch (head_dim / 16) {
-            case 1: rope_kv_kernel<false, true, 1><<<g, b, 0, s>>>(MI_RQ_ARGS); break;
-            case 2: rope_kv_kernel<false, true, 2><<<g, b, 0, s>>>(MI_RQ_ARGS); break;
-            case 4: rope_kv_kernel<false, true, 4><<<g, b, 0, s>>>(MI_RQ_ARGS); break;
-            case 8: rope_kv_kernel<false, true, 8><<<g, b, 0, s>>>(MI_RQ_ARGS); break;
-            case 16: rope_kv_kernel<false, true, 16><<<g, b, 0, s>>>(MI_RQ_ARGS); break;
-            case 32: rope_kv_kernel<false, true, 32><<<g, b, 0, s>>>(MI_RQ_ARGS); break;
+            case 1: rope_kv_kernel<false, true, 1, false><<<g, b, 0, s>>>(MI_RQ_ARGS); break;
+            case 2: rope_kv_kernel<false, true, 2, false><<<g, b, 0, s>>>(MI_RQ_ARGS); break;
+            case 4: rope_kv_kernel<false, true, 4, false><<<g, b, 0, s>>>(MI_RQ_ARGS); break;
+            case 8: rope_kv_kernel<false, true, 8, false><<<g, b, 0, s>>>(MI_RQ_ARGS); break;
+            case 16: rope_kv_kernel<false, true, 16, false><<<g, b, 0, s>>>(MI_RQ_ARGS); break;
+            case 32: rope_kv_kernel<false, true, 32, false><<<g, b, 0, s>>>(MI_RQ_ARGS); break;
             default: return MI_ERR_UNSUPPORTED;
         }
     } else if (bq) {
