@@ -58,6 +58,15 @@ constexpr int kMaxSplits = 1024;    // chunk pairs of a row, folded by one wave
 #endif
 constexpr int64_t kSplitTargetWgs = MI_SOFTMAX_TARGET_WGS;
 
+// exp(x - m) for every element of a row against one m, with m * log2(e)
+// formed once: one fma and the exp per element instead of a subtract, a
+// multiply and the exp (the VALU work sits on the critical path before and
+// after a one-launch row's exchange: 9.5 -> 8.9 us at [64, 152064]).
+constexpr float kLog2e = 1.4426950408889634f;
+__device__ __forceinline__ float exp_shifted(float x, float m_log2e) {
+    return __builtin_amdgcn_exp2f(fmaf(x, kLog2e, -m_log2e));
+}
+
 // Fold one loaded value group into the lane's online (m, s).
 template <int VEC>
 __device__ __forceinline__ void fold(const float (&v)[VEC], float& m, float& s) {
@@ -67,8 +76,9 @@ __device__ __forceinline__ void fold(const float (&v)[VEC], float& m, float& s) 
     const float mn = fmaxf(m, vm);
     if (mn == -INFINITY) return;  // nothing but -inf so far
     float acc = s * fast_exp(m - mn);
+    const float mnl = mn * kLog2e;
 #pragma unroll
-    for (int k = 0; k < VEC; ++k) acc += fast_exp(v[k] - mn);
+    for (int k = 0; k < VEC; ++k) acc += exp_shifted(v[k], mnl);
     s = acc;
     m = mn;
 }
@@ -130,10 +140,11 @@ __device__ __forceinline__ void tile_stats(const half_t* xr, int64_t begin, int6
         const float mt = (float)__builtin_elementwise_max(m2.x, m2.y);
         if (!(mt > -INFINITY)) continue;  // nothing but -inf (or NaN) in this lane's tile
         float st = 0.0f;
+        const float mtl = mt * kLog2e;
 #pragma unroll
         for (int j = 0; j < U; ++j) {
 #pragma unroll
-            for (int k = 0; k < 8; ++k) st += fast_exp((float)a[j][k] - mt);
+            for (int k = 0; k < 8; ++k) st += exp_shifted((float)a[j][k], mtl);
         }
         const float mn = fmaxf(m, mt);
         s = s * fast_exp(m - mn) + st * fast_exp(mt - mn);
@@ -162,7 +173,8 @@ __device__ __forceinline__ void write_range(const half_t* xr, half_t* yr, int64_
                 if (i < end) {
                     h8 o;
 #pragma unroll
-                    for (int k = 0; k < 8; ++k) o[k] = to_half(fast_exp((float)h[j][k] - m) * inv);
+                    for (int k = 0; k < 8; ++k)
+                        o[k] = to_half(exp_shifted((float)h[j][k], m * kLog2e) * inv);
                     st8_out<MI_WT_SM>(yr + i, o);
                 }
             }
@@ -170,7 +182,7 @@ __device__ __forceinline__ void write_range(const half_t* xr, half_t* yr, int64_
 #pragma unroll
             for (int j = 0; j < kStatUnroll; ++j) {
                 const int64_t i = i0 + j * step;
-                if (i < end) yr[i] = to_half(fast_exp((float)xr[i] - m) * inv);
+                if (i < end) yr[i] = to_half(exp_shifted((float)xr[i], m * kLog2e) * inv);
             }
         }
     }
@@ -237,7 +249,7 @@ __global__ __launch_bounds__(G > 256 ? G : 256) void softmax_reg_kernel(const ha
     for (int j = 0; j < VPT; ++j) {
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
-            const float t = fast_exp((float)a[j][k] - m);
+            const float t = exp_shifted((float)a[j][k], m * kLog2e);
             if constexpr (kKeepExp) e[j][k] = t;
             s += t;
         }
@@ -260,7 +272,8 @@ __global__ __launch_bounds__(G > 256 ? G : 256) void softmax_reg_kernel(const ha
             h8 o;
 #pragma unroll
             for (int k = 0; k < 8; ++k) {
-                const float t = kKeepExp ? e[kKeepExp ? j : 0][k] : fast_exp((float)a[j][k] - mw);
+                const float t =
+                    kKeepExp ? e[kKeepExp ? j : 0][k] : exp_shifted((float)a[j][k], mw * kLog2e);
                 o[k] = to_half(t * inv);
             }
             st8_out<MI_WT_SM>(
@@ -453,10 +466,12 @@ __device__ __forceinline__ void chunk_lane_stats(const h8 (&a)[U], float& m, flo
     m = (float)__builtin_elementwise_max(m2.x, m2.y);
     s = 0.0f;
     if (m > -INFINITY) {
+        const float ml = m * kLog2e;
 #pragma unroll
         for (int j = 0; j < U; ++j) {
 #pragma unroll
-            for (int k = 0; k < 8; ++k) s += fast_exp((float)a[j][k] - m);
+            for (int k = 0; k < 8; ++k)
+                s += exp_shifted((float)a[j][k], ml);
         }
     } else {
         m = -INFINITY;  // NaN-free lane maximum of an all -inf (or NaN) lane
@@ -599,7 +614,8 @@ __device__ __forceinline__ void lane_store(const h8 (&a)[U], half_t* row, uint32
         if (ok[j]) {
             h8 o;
 #pragma unroll
-            for (int k = 0; k < 8; ++k) o[k] = to_half(fast_exp((float)a[j][k] - M) * inv);
+            for (int k = 0; k < 8; ++k)
+                o[k] = to_half(exp_shifted((float)a[j][k], M * kLog2e) * inv);
             st8_out<MI_WT_SM>(reinterpret_cast<half_t*>(base + j * 256 * 16), o);
         }
     }
