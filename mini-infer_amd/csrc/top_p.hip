@@ -32,7 +32,7 @@ namespace {
 constexpr int64_t kTopPMaxVocab = 30000;  // above: greedy
 constexpr int kTopPStride = 128;          // candidate indices are multiples of 128
 constexpr int kTopPMaxCand = static_cast<int>((kTopPMaxVocab + kTopPStride - 1) / kTopPStride);
-constexpr int kTopPWalk = (kTopPMaxCand + 15) / 16 * 16;  // 240
+static_assert(kTopPMaxCand <= 256, "candidate slots");
 
 // MurmurHash3's 64-bit finaliser (fmix64), the reference's slot hash.
 __device__ __forceinline__ uint64_t fmix64(uint64_t s) {
@@ -44,85 +44,116 @@ __device__ __forceinline__ uint64_t fmix64(uint64_t s) {
     return s;
 }
 
-// Lanes per row and logits per lane: 1024 x 32 >= 30000, so each lane issues
-// all of its loads at once and keeps its logits in registers (a strided
-// loop, one load at a time, took 63 us at [64, 30000]).
+// One workgroup of 1024 lanes per row; lane t loads the 16-byte vectors t,
+// t + 1024, ... of the row's 16-byte-aligned window (4 per lane cover 30000
+// logits at any 2-byte alignment), all issued at once and kept in registers.
 constexpr int kTopPLanes = 1024;
-constexpr int kTopPPerLane = 32;
-static_assert(kTopPLanes * kTopPPerLane >= kTopPMaxVocab, "a row must fit the registers");
+constexpr int kTopPVecs = 4;  // vectors per lane
+static_assert(kTopPLanes * kTopPVecs * 8 >= kTopPMaxVocab + 7, "a row must fit the registers");
 constexpr int kTopPRankParts = kTopPLanes / 256;  // lanes that rank one candidate
-static_assert(kTopPWalk / kTopPRankParts % 4 == 0, "rank slices are whole float4s");
+constexpr int kTopPKeys = 256;                    // key slots (>= candidates)
+static_assert(kTopPKeys / kTopPRankParts % 2 == 0, "rank slices are whole 16-byte reads");
+constexpr int kTopPBatch = 32;  // walk: values per batch of LDS reads
 
 __global__ __launch_bounds__(kTopPLanes) void top_p_small_kernel(const half_t* __restrict__ logits,
                                                                  int vocab, float p,
                                                                  float temperature, uint64_t seed,
                                                                  int32_t* out) {
-    __shared__ float slots[kTopPLanes / kWave];
-    // x, then q, of candidate c (index c * 128); zero past the candidates
-    __shared__ __attribute__((aligned(16))) float cand[kTopPWalk];
+    __shared__ float wave_m[kTopPLanes / kWave], wave_s[kTopPLanes / kWave];
+    __shared__ float cand[kTopPKeys];  // x of candidate c (index c * 128)
+    // (q bits << 32) | (255 - c): larger key = earlier in the walk order
+    __shared__ __attribute__((aligned(16))) uint64_t keys[kTopPKeys];
     __shared__ int partial[kTopPRankParts][256];
-    // q in walk order, zero past the candidates, read 16 at a time
-    __shared__ __attribute__((aligned(16))) float sorted_q[kTopPWalk];
-    __shared__ int sorted_i[kTopPMaxCand];
+    // q in walk order, zero past the candidates
+    __shared__ __attribute__((aligned(16))) float sorted_q[kTopPKeys];
+    __shared__ int sorted_i[kTopPKeys];
     const int64_t row = blockIdx.x;
     const half_t* x = logits + row * vocab;
     const int tid = threadIdx.x;
     const int nc = (vocab + kTopPStride - 1) / kTopPStride;
+    const float rT = 1.0f / temperature;
 
-    float xv[kTopPPerLane];
+    // element e of the row sits at window position e + shift
+    const int shift = static_cast<int>((reinterpret_cast<uintptr_t>(x) & 15) >> 1);
+    const half_t* xa = x - shift;
+    h8 v[kTopPVecs];
 #pragma unroll
-    for (int j = 0; j < kTopPPerLane; ++j) {
-        const int i = tid + j * kTopPLanes;
-        xv[j] = i < vocab ? (float)x[i] : -INFINITY;
+    for (int j = 0; j < kTopPVecs; ++j) {
+        const int e0 = (tid + j * kTopPLanes) * 8 - shift;
+        v[j] = e0 < vocab ? ld8_stream(xa + e0 + shift) : h8(-__builtin_huge_valf16());
     }
-    // max of x / T = (max of x) / T: division by T > 0, correctly rounded,
-    // is monotone
+    // the lane's maximum over its valid logits (x / T, correctly rounded, is
+    // monotone in x, so max(x) / T is the maximum of x / T)
     float m = -INFINITY;
 #pragma unroll
-    for (int j = 0; j < kTopPPerLane; ++j) m = fmaxf(m, xv[j]);
-    const float M = block_max(m, slots) / temperature;
-    __syncthreads();  // slots reused by the sum
-    // the normaliser: x / T as x * (1 / T) (within an ulp; the candidates'
-    // own probabilities below use the division)
-    const float rT = 1.0f / temperature;
-    float s = 0.0f;
+    for (int j = 0; j < kTopPVecs; ++j) {
+        const int e0 = (tid + j * kTopPLanes) * 8 - shift;
 #pragma unroll
-    for (int j = 0; j < kTopPPerLane; ++j) s += fast_exp(xv[j] * rT - M);  // -inf -> 0
-    // candidate c sits in lane (c % 8) * 128, register c / 8: those lanes
-    // stage x, then lane c forms q_c
-    if ((tid & (kTopPStride - 1)) == 0) {
+        for (int k = 0; k < 8; ++k) {
+            const int e = e0 + k;
+            if (e < 0 || e >= vocab) v[j][k] = -__builtin_huge_valf16();  // outside the row
+            m = fmaxf(m, (float)v[j][k]);
+        }
+        // the vector holds at most one candidate: element e0 + ((-e0) & 127)
+        const int k0 = (-e0) & (kTopPStride - 1);
+        if (k0 < 8 && e0 + k0 < vocab) {
+            float c = 0.0f;
 #pragma unroll
-        for (int j = 0; j < kTopPPerLane; ++j) {
-            const int c = j * (kTopPLanes / kTopPStride) + tid / kTopPStride;
-            if (c < nc) cand[c] = xv[j];
+            for (int k = 0; k < 8; ++k)
+                if (k == k0) c = (float)v[j][k];
+            cand[(e0 + k0) >> 7] = c;
         }
     }
-    const float S = block_sum(s, slots);  // its barrier also publishes cand
+    // the normaliser, merged as (max, sum) pairs: per lane with its own
+    // maximum, per wave, then across the 16 waves after one barrier (x / T as
+    // x * (1 / T), within an ulp; the candidates' own q below use the division)
+    const float ml = m / temperature;  // -inf for a lane past the row
+    float s = 0.0f;
+    if (ml != -INFINITY) {
+#pragma unroll
+        for (int j = 0; j < kTopPVecs; ++j)
+#pragma unroll
+            for (int k = 0; k < 8; ++k) s += fast_exp((float)v[j][k] * rT - ml);  // -inf -> 0
+    }
+    {
+        const float mw = group_max<kWave>(ml);
+        float part = ml == -INFINITY ? 0.0f : s * fast_exp(ml - mw);
+        part = group_sum<kWave>(part);
+        if ((tid & (kWave - 1)) == 0) {
+            wave_m[tid / kWave] = mw;
+            wave_s[tid / kWave] = part;
+        }
+    }
+    __syncthreads();  // also publishes cand
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kTopPLanes / kWave; ++w) M = fmaxf(M, wave_m[w]);
+    float S = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kTopPLanes / kWave; ++w)
+        S += wave_m[w] == -INFINITY ? 0.0f : wave_s[w] * fast_exp(wave_m[w] - M);
     float qc = 0.0f;
     if (tid < nc) qc = fast_exp(cand[tid] / temperature - M) / S;
-    __syncthreads();  // every lane has read its x
-    if (tid < kTopPWalk) cand[tid] = qc;  // zero past the candidates
+    if (tid < kTopPKeys)  // q >= 0: its bits order as unsigned integers
+        keys[tid] = (static_cast<uint64_t>(__builtin_bit_cast(uint32_t, qc)) << 32) |
+                    static_cast<uint32_t>(kTopPKeys - 1 - tid);
     __syncthreads();
     // rank by (q descending, index ascending), the order the reference's
     // strict-greater selection produces: four lanes per candidate, each
-    // comparing a quarter of the candidates, 16 bytes per LDS read
+    // counting the larger keys in a quarter of the slots, two keys per read.
+    // Slots past the candidates hold q = 0 with a larger index, below every
+    // candidate's key.
     {
         const int c = tid & 255, part = tid >> 8;
         int r = 0;
         if (c < nc) {
-            const float v = cand[c];
-            constexpr int kSlice = kTopPWalk / kTopPRankParts;  // 60
-            const int lo = part * kSlice;
-            const float4* c4 = reinterpret_cast<const float4*>(cand + lo);
+            const uint64_t kc = keys[c];
+            constexpr int kSlice = kTopPKeys / kTopPRankParts;  // 64
+            const ulonglong2* k2 = reinterpret_cast<const ulonglong2*>(keys + part * kSlice);
 #pragma unroll
-            for (int k4 = 0; k4 < kSlice / 4; ++k4) {
-                const float4 t = c4[k4];
-                const float u[4] = {t.x, t.y, t.z, t.w};
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const int o = lo + 4 * k4 + e;
-                    r += (o < nc && (u[e] > v || (u[e] == v && o < c))) ? 1 : 0;
-                }
+            for (int i = 0; i < kSlice / 2; ++i) {
+                const ulonglong2 t = k2[i];
+                r += (t.x > kc ? 1 : 0) + (t.y > kc ? 1 : 0);
             }
         }
         partial[part][c] = r;
@@ -134,36 +165,37 @@ __global__ __launch_bounds__(kTopPLanes) void top_p_small_kernel(const half_t* _
         for (int k = 0; k < kTopPRankParts; ++k) rank += partial[k][tid];
         sorted_q[rank] = qc;
         sorted_i[rank] = tid * kTopPStride;
-    } else if (tid < kTopPWalk) {
+    } else if (tid < kTopPKeys) {
         sorted_q[tid] = 0.0f;
     }
     __syncthreads();
     if (tid == 0) {
-        // the reference's running fp32 sum, in order: 16 values per batch of
-        // vector reads; only the additions are chained, the threshold tests
-        // follow them
-        int hit = -1;
+        // the reference's running fp32 sum, in order.  q >= 0, so the sum
+        // never decreases and the first position whose sum reaches p is the
+        // count of positions whose sum does not: no branch per value.  The
+        // zeros past the candidates leave the sum as it is, so a count >= nc
+        // means p was never reached.
+        int below = 0;
         float cum = 0.0f;
         const float4* q4 = reinterpret_cast<const float4*>(sorted_q);
-        for (int base = 0; base < nc && hit < 0; base += 16) {
-            float v[16], c[16];
+        for (int base = 0; base < nc; base += kTopPBatch) {
+            float4 t[kTopPBatch / 4];
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                const float4 t = q4[base / 4 + k];
-                v[4 * k] = t.x;
-                v[4 * k + 1] = t.y;
-                v[4 * k + 2] = t.z;
-                v[4 * k + 3] = t.w;
+            for (int k = 0; k < kTopPBatch / 4; ++k) t[k] = q4[base / 4 + k];
+#pragma unroll
+            for (int k = 0; k < kTopPBatch / 4; ++k) {
+                cum += t[k].x;
+                below += cum >= p ? 0 : 1;
+                cum += t[k].y;
+                below += cum >= p ? 0 : 1;
+                cum += t[k].z;
+                below += cum >= p ? 0 : 1;
+                cum += t[k].w;
+                below += cum >= p ? 0 : 1;
             }
-#pragma unroll
-            for (int k = 0; k < 16; ++k) {
-                cum += v[k];
-                c[k] = cum;
-            }
-#pragma unroll
-            for (int k = 15; k >= 0; --k)
-                if (base + k < nc && c[k] >= p) hit = base + k;
+            if (cum >= p) break;
         }
+        const int hit = below < nc ? below : -1;
         int choice = -1;
         if (hit >= 0) {
             // row b draws with seed + b (a single row: seed itself)
@@ -188,6 +220,7 @@ int top_p(const void* logits, int64_t B, int64_t vocab, float p, float temperatu
     if (vocab > kTopPMaxVocab) return mi_greedy_argmax_f16(logits, B, vocab, out, stream);
     if (B > kMaxGridX) return MI_ERR_UNSUPPORTED;
     if (overlaps(out, B * 4, logits, B * vocab * 2)) return MI_ERR_ALIASING;
+    if (reinterpret_cast<uintptr_t>(logits) & 1) return MI_ERR_INVALID_ARGUMENT;  // fp16 alignment
     top_p_small_kernel<<<dim3(static_cast<unsigned>(B)), dim3(kTopPLanes), 0,
                          as_stream(stream)>>>(
         static_cast<const half_t*>(logits), static_cast<int>(vocab), p, temperature, seed, out);

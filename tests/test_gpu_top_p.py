@@ -73,6 +73,25 @@ def test_top_p_vs_oracle(mk, orc, dev, V, B):
             assert int(to_host(out)[0]) == int(want[0])
 
 
+@pytest.mark.parametrize("V", [128, 1000, 30000])
+def test_top_p_unaligned_rows(mk, orc, dev, V):
+    """Rows starting 0..7 halves past a 16-byte boundary: the kernel reads
+    each row through an aligned window and masks the elements outside it."""
+    import torch
+    rng = np.random.default_rng(V + 3)
+    B = 3
+    x = _rows(rng, B, V, 0.9, 1.0)
+    flat = torch.empty(B * V + 16, dtype=torch.float16, device=dev)
+    want = orc.top_p_sample(x, 0.9, 1.0, 11)
+    for off in range(8):
+        _case(f"top-p V={V} rows at +{off} halves")
+        flat.fill_(60.0)  # neighbours far above every logit: a stray read would win
+        xs = flat[off:off + B * V].view(B, V)
+        xs.copy_(torch.from_numpy(x).to(dev))
+        got = to_host(mk.top_p_sample(xs, 0.9, 1.0, 11))
+        np.testing.assert_array_equal(got, want)
+
+
 def test_top_p_nucleus_not_reached_and_ties(mk, orc, dev):
     _case("top-p: -1 when the candidates cannot reach p; exact ties")
     x = np.zeros((3, 1000), dtype=np.float16)
