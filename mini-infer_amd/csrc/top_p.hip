@@ -171,31 +171,34 @@ __global__ __launch_bounds__(kTopPLanes) void top_p_small_kernel(const half_t* _
     __syncthreads();
     if (tid == 0) {
         // the reference's running fp32 sum, in order.  q >= 0, so the sum
-        // never decreases and the first position whose sum reaches p is the
-        // count of positions whose sum does not: no branch per value.  The
-        // zeros past the candidates leave the sum as it is, so a count >= nc
-        // means p was never reached.
-        int below = 0;
+        // never decreases: only a batch's last sum is tested, and in the
+        // batch that reaches p the first position that does is the count of
+        // its sums that do not (a test per value costs a vector-to-scalar
+        // round trip each).  The zeros past the candidates leave the sum as
+        // it is, so the sum of the whole walk decides whether p is reached.
+        int hit = -1;
         float cum = 0.0f;
         const float4* q4 = reinterpret_cast<const float4*>(sorted_q);
         for (int base = 0; base < nc; base += kTopPBatch) {
             float4 t[kTopPBatch / 4];
 #pragma unroll
             for (int k = 0; k < kTopPBatch / 4; ++k) t[k] = q4[base / 4 + k];
+            float c[kTopPBatch];
 #pragma unroll
             for (int k = 0; k < kTopPBatch / 4; ++k) {
-                cum += t[k].x;
-                below += cum >= p ? 0 : 1;
-                cum += t[k].y;
-                below += cum >= p ? 0 : 1;
-                cum += t[k].z;
-                below += cum >= p ? 0 : 1;
-                cum += t[k].w;
-                below += cum >= p ? 0 : 1;
+                c[4 * k] = cum += t[k].x;
+                c[4 * k + 1] = cum += t[k].y;
+                c[4 * k + 2] = cum += t[k].z;
+                c[4 * k + 3] = cum += t[k].w;
             }
-            if (cum >= p) break;
+            if (cum >= p) {
+                int below = 0;
+#pragma unroll
+                for (int k = 0; k < kTopPBatch; ++k) below += c[k] >= p ? 0 : 1;
+                hit = base + below < nc ? base + below : -1;
+                break;
+            }
         }
-        const int hit = below < nc ? below : -1;
         int choice = -1;
         if (hit >= 0) {
             // row b draws with seed + b (a single row: seed itself)
