@@ -92,6 +92,34 @@ def test_top_p_unaligned_rows(mk, orc, dev, V):
         np.testing.assert_array_equal(got, want)
 
 
+@pytest.mark.parametrize("V", [1000, 30000])  # serial walk; double prefix + walk
+@pytest.mark.parametrize("k", [3, 7])
+def test_top_p_p_on_a_running_sum(mk, orc, dev, k, V):
+    """p equal to (or one ulp either side of) the fp32 running sum at each
+    position: within the kernel's error bound of its double prefix, so the
+    in-order fp32 sum decides.  k equal candidates and every other logit at
+    fp16's lowest value make q = fl(1/k) exactly on every implementation (exp
+    of 0 is 1, the others underflow to 0), so no screening is needed."""
+    _case(f"top-p: p on the running sums of {k} equal candidates, V={V}")
+    x = np.full((1, V), np.finfo(np.float16).min, dtype=np.float16)
+    x[0, np.arange(k) * 128] = 0.0
+    q = np.float32(1.0) / np.float32(k)
+    cums, c = [], np.float32(0.0)
+    for _ in range(k):
+        c = np.float32(c + q)
+        cums.append(c)
+    ps = set()
+    for c in cums:
+        ps.update((float(c), float(np.nextafter(c, np.float32(0))),
+                   float(np.nextafter(c, np.float32(2)))))
+    xd = to_dev(x, dev)
+    for p in sorted(ps):
+        for seed in (1, 99):
+            got = to_host(mk.top_p_sample(xd, p, 1.0, seed))
+            np.testing.assert_array_equal(got, orc.top_p_sample(x, p, 1.0, seed),
+                                          err_msg=f"p={p!r} seed={seed}")
+
+
 def test_top_p_nucleus_not_reached_and_ties(mk, orc, dev):
     _case("top-p: -1 when the candidates cannot reach p; exact ties")
     x = np.zeros((3, 1000), dtype=np.float16)
