@@ -137,18 +137,22 @@ __global__ __launch_bounds__(kTopPLanes) void top_p_small_kernel(const half_t* _
         const int e0 = (tid + j * kTopPLanes) * 8 - shift;
         v[j] = e0 < vocab ? ld8_stream(xa + e0 + shift) : h8(-__builtin_huge_valf16());
     }
-    // the lane's maximum over its valid logits (x / T, correctly rounded, is
-    // monotone in x, so max(x) / T is the maximum of x / T)
-    float m = -INFINITY;
+    // elements outside the row (only the vectors at its two ends hold any)
+    // become -inf; the lane's maximum over its valid logits in fp16 pairs
+    // (exact).  x / T, correctly rounded, is monotone in x, so max(x) / T is
+    // the maximum of x / T.
+    h2 pm = h2(-__builtin_huge_valf16());
 #pragma unroll
     for (int j = 0; j < kTopPVecs; ++j) {
         const int e0 = (tid + j * kTopPLanes) * 8 - shift;
+        if (e0 < 0 || e0 + 8 > vocab) {
 #pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            const int e = e0 + k;
-            if (e < 0 || e >= vocab) v[j][k] = -__builtin_huge_valf16();  // outside the row
-            m = fmaxf(m, (float)v[j][k]);
+            for (int k = 0; k < 8; ++k)
+                if (e0 + k < 0 || e0 + k >= vocab) v[j][k] = -__builtin_huge_valf16();
         }
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+            pm = __builtin_elementwise_max(pm, h2{v[j][2 * k], v[j][2 * k + 1]});
         // the vector holds at most one candidate: element e0 + ((-e0) & 127)
         const int k0 = (-e0) & (kTopPStride - 1);
         if (k0 < 8 && e0 + k0 < vocab) {
@@ -159,16 +163,21 @@ __global__ __launch_bounds__(kTopPLanes) void top_p_small_kernel(const half_t* _
             cand[(e0 + k0) >> 7] = c;
         }
     }
+    const float m = fmaxf((float)pm[0], (float)pm[1]);
     // the normaliser, merged as (max, sum) pairs: per lane with its own
-    // maximum, per wave, then across the 16 waves after one barrier (x / T as
-    // x * (1 / T), within an ulp; the candidates' own q below use the division)
+    // maximum, per wave, then across the 16 waves after one barrier.  Each
+    // term is exp2(x (log2(e) / T) - max log2(e)), one fma (within a few ulps
+    // of exp(x / T - max) at moderate logits); the candidates' own q below
+    // use the division.
     const float ml = m / temperature;  // -inf for a lane past the row
     float s = 0.0f;
     if (ml != -INFINITY) {
+        const float c1 = rT * 1.4426950408889634f, c0 = ml * 1.4426950408889634f;
 #pragma unroll
         for (int j = 0; j < kTopPVecs; ++j)
 #pragma unroll
-            for (int k = 0; k < 8; ++k) s += fast_exp((float)v[j][k] * rT - ml);  // -inf -> 0
+            for (int k = 0; k < 8; ++k)
+                s += __builtin_amdgcn_exp2f(fmaf((float)v[j][k], c1, -c0));  // -inf -> 0
     }
     {
         const float mw = group_max<kWave>(ml);
