@@ -189,18 +189,22 @@ __global__ __launch_bounds__(kTopPLanes) void top_p_small_kernel(const half_t* _
         }
     }
     __syncthreads();  // also publishes cand
-    float M = -INFINITY;
-#pragma unroll
-    for (int w = 0; w < kTopPLanes / kWave; ++w) M = fmaxf(M, wave_m[w]);
-    float S = 0.0f;
-#pragma unroll
-    for (int w = 0; w < kTopPLanes / kWave; ++w)
-        S += wave_m[w] == -INFINITY ? 0.0f : wave_s[w] * fast_exp(wave_m[w] - M);
+    // the first 256 lanes (the candidates' probabilities and keys) fold the
+    // wave pairs; the other waves wait at the next barrier
     float qc = 0.0f;
-    if (tid < nc) qc = fast_exp(cand[tid] / temperature - M) / S;
-    if (tid < kTopPKeys)  // q >= 0: its bits order as unsigned integers
+    if (tid < kTopPKeys) {
+        float M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < kTopPLanes / kWave; ++w) M = fmaxf(M, wave_m[w]);
+        float S = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kTopPLanes / kWave; ++w)
+            S += wave_m[w] == -INFINITY ? 0.0f : wave_s[w] * fast_exp(wave_m[w] - M);
+        if (tid < nc) qc = fast_exp(cand[tid] / temperature - M) / S;
+        // q >= 0: its bits order as unsigned integers
         keys[tid] = (static_cast<uint64_t>(__builtin_bit_cast(uint32_t, qc)) << 32) |
                     static_cast<uint32_t>(kTopPKeys - 1 - tid);
+    }
     __syncthreads();
     // rank by (q descending, index ascending), the order the reference's
     // strict-greater selection produces: four lanes per candidate, each
