@@ -390,7 +390,7 @@ int mi_greedy_argmax_test_poll_limit(int limit);
  * (ties: lower index), the first position i whose running sum reaches p, and
  * the index at slot floor(u * (i + 1)) with u from MurmurHash3's fmix64 of
  * seed ^ (index_i << 32); -1 when the sum never reaches p.  Finite logits,
- * temperature > 0. */
+ * temperature > 0; logits 2-byte aligned (else MI_ERR_INVALID_ARGUMENT). */
 int mi_top_p_sample_f16(const void* logits, int64_t vocab, float p, float temperature,
                         uint64_t seed, int32_t* out, void* stream);
 

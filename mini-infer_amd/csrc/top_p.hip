@@ -47,6 +47,8 @@ __device__ __forceinline__ uint64_t fmix64(uint64_t s) {
 // One workgroup of 1024 lanes per row; lane t loads the 16-byte vectors t,
 // t + 1024, ... of the row's 16-byte-aligned window (4 per lane cover 30000
 // logits at any 2-byte alignment), all issued at once and kept in registers.
+// The window's bytes outside the row share 16-byte granules with the row's
+// own, so they never reach another page; they are masked to -inf.
 constexpr int kTopPLanes = 1024;
 constexpr int kTopPVecs = 4;  // vectors per lane
 static_assert(kTopPLanes * kTopPVecs * 8 >= kTopPMaxVocab + 7, "a row must fit the registers");
@@ -297,10 +299,10 @@ int top_p(const void* logits, int64_t B, int64_t vocab, float p, float temperatu
     if (B == 0) return MI_OK;
     if (!out || (vocab > 0 && !logits)) return MI_ERR_INVALID_ARGUMENT;
     if (!product_fits({B, vocab, 2})) return MI_ERR_INVALID_ARGUMENT;
+    if (reinterpret_cast<uintptr_t>(logits) & 1) return MI_ERR_INVALID_ARGUMENT;  // fp16 alignment
     if (vocab > kTopPMaxVocab) return mi_greedy_argmax_f16(logits, B, vocab, out, stream);
     if (B > kMaxGridX) return MI_ERR_UNSUPPORTED;
     if (overlaps(out, B * 4, logits, B * vocab * 2)) return MI_ERR_ALIASING;
-    if (reinterpret_cast<uintptr_t>(logits) & 1) return MI_ERR_INVALID_ARGUMENT;  // fp16 alignment
     top_p_small_kernel<<<dim3(static_cast<unsigned>(B)), dim3(kTopPLanes), 0,
                          as_stream(stream)>>>(
         static_cast<const half_t*>(logits), static_cast<int>(vocab), p, temperature, seed, out);

@@ -119,6 +119,9 @@ def test_size_products_that_overflow_are_rejected(lib):
         two[i].max_blocks_per_seq = 4
     assert lib.mi_rope_kv_scatter_f16(q, k, v, None, None, None, P(0x90000), inv, 100, 28, 4,
                                       128, kc, vc, 0, 8, 16, two, 2, None) == -2
+    # fp16 logits at an odd address, on the nucleus and the greedy path
+    assert lib.mi_top_p_sample_f16(P(0x10001), 100, 0.9, 1.0, 1, P(0x20000), None) == -1
+    assert lib.mi_top_p_sample_f16(P(0x10001), 40000, 0.9, 1.0, 1, P(0x20000), None) == -1
     seg[0].B, seg[0].S = 0, 1 << 62  # an empty segment is fine; nothing launched for T = 0
     assert lib.mi_rope_kv_scatter_f16(q, k, v, None, None, None, P(0x90000), inv, 0, 28, 4,
                                       128, kc, vc, 0, 8, 16, seg, 1, None) == 0
