@@ -117,7 +117,6 @@ __global__ __launch_bounds__(kTopPLanes) void top_p_small_kernel(const half_t* _
                                                                  float temperature, uint64_t seed,
                                                                  int32_t* out) {
     __shared__ float wave_m[kTopPLanes / kWave], wave_s[kTopPLanes / kWave];
-    __shared__ float cand[kTopPKeys];  // x of candidate c (index c * 128)
     // (q bits << 32) | (255 - c): larger key = earlier in the walk order
     __shared__ __attribute__((aligned(16))) uint64_t keys[kTopPKeys];
     __shared__ int partial[kTopPRankParts][256];
@@ -139,6 +138,9 @@ __global__ __launch_bounds__(kTopPLanes) void top_p_small_kernel(const half_t* _
         const int e0 = (tid + j * kTopPLanes) * 8 - shift;
         v[j] = e0 < vocab ? ld8_stream(xa + e0 + shift) : h8(-__builtin_huge_valf16());
     }
+    // lane c < nc also reads candidate c (index c * 128) itself, with the
+    // row's loads: it forms that candidate's probability below
+    const float xc = tid < nc ? (float)x[tid * kTopPStride] : 0.0f;
     // elements outside the row (only the vectors at its two ends hold any)
     // become -inf; the lane's maximum over its valid logits in fp16 pairs
     // (exact).  x / T, correctly rounded, is monotone in x, so max(x) / T is
@@ -155,15 +157,6 @@ __global__ __launch_bounds__(kTopPLanes) void top_p_small_kernel(const half_t* _
 #pragma unroll
         for (int k = 0; k < 4; ++k)
             pm = __builtin_elementwise_max(pm, h2{v[j][2 * k], v[j][2 * k + 1]});
-        // the vector holds at most one candidate: element e0 + ((-e0) & 127)
-        const int k0 = (-e0) & (kTopPStride - 1);
-        if (k0 < 8 && e0 + k0 < vocab) {
-            float c = 0.0f;
-#pragma unroll
-            for (int k = 0; k < 8; ++k)
-                if (k == k0) c = (float)v[j][k];
-            cand[(e0 + k0) >> 7] = c;
-        }
     }
     const float m = fmaxf((float)pm[0], (float)pm[1]);
     // the normaliser, merged as (max, sum) pairs: per lane with its own
@@ -190,7 +183,7 @@ __global__ __launch_bounds__(kTopPLanes) void top_p_small_kernel(const half_t* _
             wave_s[tid / kWave] = part;
         }
     }
-    __syncthreads();  // also publishes cand
+    __syncthreads();
     // the first 256 lanes (the candidates' probabilities and keys) fold the
     // wave pairs; the other waves wait at the next barrier
     float qc = 0.0f;
@@ -202,7 +195,7 @@ __global__ __launch_bounds__(kTopPLanes) void top_p_small_kernel(const half_t* _
 #pragma unroll
         for (int w = 0; w < kTopPLanes / kWave; ++w)
             S += wave_m[w] == -INFINITY ? 0.0f : wave_s[w] * fast_exp(wave_m[w] - M);
-        if (tid < nc) qc = fast_exp(cand[tid] / temperature - M) / S;
+        if (tid < nc) qc = fast_exp(xc / temperature - M) / S;
         // q >= 0: its bits order as unsigned integers
         keys[tid] = (static_cast<uint64_t>(__builtin_bit_cast(uint32_t, qc)) << 32) |
                     static_cast<uint32_t>(kTopPKeys - 1 - tid);
