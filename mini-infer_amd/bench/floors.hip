@@ -21,6 +21,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "mi_device.h"
+
 namespace {
 
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
@@ -70,6 +72,108 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(const u4* src, u4* dst
 }
 
 __global__ void empty_kernel() {}
+
+// The in-place RoPE kernels' exact grid and access pattern with no
+// arithmetic: a 256-lane workgroup per token, lane j < (Hq + Hkv) * hd/16
+// taking head j / (hd/16), 16-byte slice j % (hd/16), loading x[i..i+8) and
+// x[h + i .. h + i + 8) of that head (h = hd/2), XOR-ing both and storing
+// them back in place.  WT: write-through stores ("nt sc1") as the RoPE
+// kernels use, else non-temporal stores.  SER: each store waits for the one
+// before it.  PERS: a resident grid walking tokens with a stride, the next
+// token's loads issued before this token's stores.
+template <bool WT>
+__device__ __forceinline__ void rope_shape_store(_Float16* p, u4 v) {
+    if constexpr (WT) mi::st8_stream_wt(p, __builtin_bit_cast(mi::h8, v));
+    else st(reinterpret_cast<u4*>(p), v);
+}
+template <bool WT, bool SER, bool PERS, int TPW, bool CONTIG = false>
+__global__ __launch_bounds__(256) void rope_shape_kernel(_Float16* q, _Float16* k, int64_t T,
+                                                         int Hq, int Hkv, int hd) {
+    const int half = hd >> 1, cph = hd >> 4;
+    const int tid = threadIdx.x;
+    if (tid >= (Hq + Hkv) * cph) return;
+    const int h = tid / cph, c = tid - h * cph;
+    auto addr = [&](int64_t tok) {
+        return h < Hq ? q + (tok * Hq + h) * hd + c * 8 : k + (tok * Hkv + (h - Hq)) * hd + c * 8;
+    };
+    if constexpr (TPW > 1) {  // TPW tokens per workgroup, every load issued first
+        u4 a[TPW], b[TPW];
+        _Float16 *pa[TPW], *pb[TPW];
+        const int qv = Hq * cph * 2;  // 16-byte vectors of a token's Q row
+#pragma unroll
+        for (int t = 0; t < TPW; ++t) {
+            int64_t tok = static_cast<int64_t>(blockIdx.x) * TPW + t;
+            tok = tok < T ? tok : T - 1;
+            if (CONTIG) {  // lane j: vectors j and j + 256 of the token's [Q | K] rows
+                pa[t] = q + (tok * Hq * hd) + tid * 8;
+                const int j2 = tid + 256;
+                pb[t] = j2 < qv ? q + (tok * Hq * hd) + j2 * 8 : k + tok * Hkv * hd + (j2 - qv) * 8;
+            } else {
+                pa[t] = addr(tok);
+                pb[t] = pa[t] + half;
+            }
+            a[t] = __builtin_nontemporal_load(reinterpret_cast<const u4*>(pa[t]));
+            b[t] = __builtin_nontemporal_load(reinterpret_cast<const u4*>(pb[t]));
+        }
+#pragma unroll
+        for (int t = 0; t < TPW; ++t) {
+            if (static_cast<int64_t>(blockIdx.x) * TPW + t >= T) break;
+            rope_shape_store<WT>(pa[t], a[t] ^ 0x3c003c00u);
+            mi::store_gap<SER>();
+            rope_shape_store<WT>(pb[t], b[t] ^ 0x3c003c00u);
+            mi::store_gap<SER>();
+        }
+        return;
+    }
+    int64_t tok = blockIdx.x;
+    _Float16* hp = addr(tok);
+    u4 a = __builtin_nontemporal_load(reinterpret_cast<const u4*>(hp));
+    u4 b = __builtin_nontemporal_load(reinterpret_cast<const u4*>(hp + half));
+    while (true) {
+        const int64_t nt = tok + gridDim.x;
+        const bool more = PERS && nt < T;
+        _Float16* np = hp;
+        u4 na = a, nb = b;
+        if (more) {
+            np = addr(nt);
+            na = __builtin_nontemporal_load(reinterpret_cast<const u4*>(np));
+            nb = __builtin_nontemporal_load(reinterpret_cast<const u4*>(np + half));
+        }
+        rope_shape_store<WT>(hp, a ^ 0x3c003c00u);
+        mi::store_gap<SER>();
+        rope_shape_store<WT>(hp + half, b ^ 0x3c003c00u);
+        mi::store_gap<SER>();
+        if (!more) break;
+        tok = nt;
+        hp = np;
+        a = na;
+        b = nb;
+    }
+}
+
+// RoPE-shaped in-place stream over Q [T, Hq, hd] and K [T, Hkv, hd] (fp16,
+// 16-byte aligned, hd a multiple of 16, (Hq + Hkv) * hd / 16 <= 256).
+// form bit 0: write-through stores (else non-temporal); bit 1: each store
+// waits for the one before; bit 2: a resident grid of `form >> 8` workgroups
+// per CU (0: the occupancy limit) walking the tokens.
+template <bool WT, bool SER, bool PERS, int TPW = 1, bool CONTIG = false>
+int rope_shape_launch(_Float16* q, _Float16* k, int64_t T, int Hq, int Hkv, int hd, int per_cu_req,
+                      hipStream_t s) {
+    const auto kf = rope_shape_kernel<WT, SER, PERS, TPW, CONTIG>;
+    int64_t grid = (T + TPW - 1) / TPW;
+    if (PERS) {
+        int per_cu = 0, cus = 0, dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kf, 256, 0) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+            return -2;
+        if (per_cu_req > 0 && per_cu_req < per_cu) per_cu = per_cu_req;
+        const int64_t cap = static_cast<int64_t>(per_cu) * cus;
+        if (cap > 0 && cap < grid) grid = cap;
+    }
+    kf<<<dim3(static_cast<unsigned>(grid)), dim3(256), 0, s>>>(q, k, T, Hq, Hkv, hd);
+    return hipGetLastError() == hipSuccess ? 0 : 1;
+}
 
 template <int KIND, int VPL, bool NT, bool SER>
 int launch_vpl(const void* src, void* dst, int64_t nvec, int persistent, uint32_t* sink,
@@ -145,6 +249,62 @@ extern "C" int mi_floor_inplace(void* buf, int64_t bytes, int form, void* stream
 extern "C" int mi_floor_read(const void* src, int64_t bytes, int form, uint32_t* sink,
                              int64_t sink_words, void* stream) {
     return launch<kRead>(src, nullptr, bytes, form, sink, sink_words, stream);
+}
+
+extern "C" int mi_floor_rope_inplace(void* q, void* k, int64_t T, int64_t Hq, int64_t Hkv,
+                                     int64_t hd, int form, void* stream) {
+    if (T <= 0 || T > 2147483647 || Hq < 0 || Hkv < 0 || hd <= 0 || hd % 16 != 0 ||
+        (Hq + Hkv) * (hd / 16) > 256 || (Hq + Hkv) * (hd / 16) < 1 || !q || (Hkv > 0 && !k))
+        return -1;
+    if ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k)) & 15u) return -1;
+    const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    auto* qh = static_cast<_Float16*>(q);
+    auto* kh = static_cast<_Float16*>(k);
+    const int a = static_cast<int>(Hq), b = static_cast<int>(Hkv), d = static_cast<int>(hd);
+    const int pc = form >> 8;
+    if (form & 8) {  // bit 3: 2 tokens per workgroup; bit 4: 4 tokens (no persistence)
+        switch (form & 3) {
+            case 0: return rope_shape_launch<false, false, false, 2>(qh, kh, T, a, b, d, 0, s);
+            case 1: return rope_shape_launch<true, false, false, 2>(qh, kh, T, a, b, d, 0, s);
+            case 2: return rope_shape_launch<false, true, false, 2>(qh, kh, T, a, b, d, 0, s);
+            default: return rope_shape_launch<true, true, false, 2>(qh, kh, T, a, b, d, 0, s);
+        }
+    }
+    if (form & 32) {  // bit 5: 4 tokens, lane j on vectors j and j + 256 of a token's [Q | K]
+        if (Hq * hd / 8 < 256 || (Hq + Hkv) * hd / 8 != 512) return -1;
+        switch (form & 3) {
+            case 0: return rope_shape_launch<false, false, false, 4, true>(qh, kh, T, a, b, d, 0, s);
+            case 1: return rope_shape_launch<true, false, false, 4, true>(qh, kh, T, a, b, d, 0, s);
+            case 2: return rope_shape_launch<false, true, false, 4, true>(qh, kh, T, a, b, d, 0, s);
+            default: return rope_shape_launch<true, true, false, 4, true>(qh, kh, T, a, b, d, 0, s);
+        }
+    }
+    if (form & 64) {  // bit 6: 8 tokens per workgroup
+        switch (form & 3) {
+            case 0: return rope_shape_launch<false, false, false, 8>(qh, kh, T, a, b, d, 0, s);
+            case 1: return rope_shape_launch<true, false, false, 8>(qh, kh, T, a, b, d, 0, s);
+            case 2: return rope_shape_launch<false, true, false, 8>(qh, kh, T, a, b, d, 0, s);
+            default: return rope_shape_launch<true, true, false, 8>(qh, kh, T, a, b, d, 0, s);
+        }
+    }
+    if (form & 16) {
+        switch (form & 3) {
+            case 0: return rope_shape_launch<false, false, false, 4>(qh, kh, T, a, b, d, 0, s);
+            case 1: return rope_shape_launch<true, false, false, 4>(qh, kh, T, a, b, d, 0, s);
+            case 2: return rope_shape_launch<false, true, false, 4>(qh, kh, T, a, b, d, 0, s);
+            default: return rope_shape_launch<true, true, false, 4>(qh, kh, T, a, b, d, 0, s);
+        }
+    }
+    switch (form & 7) {
+        case 0: return rope_shape_launch<false, false, false>(qh, kh, T, a, b, d, pc, s);
+        case 1: return rope_shape_launch<true, false, false>(qh, kh, T, a, b, d, pc, s);
+        case 2: return rope_shape_launch<false, true, false>(qh, kh, T, a, b, d, pc, s);
+        case 3: return rope_shape_launch<true, true, false>(qh, kh, T, a, b, d, pc, s);
+        case 4: return rope_shape_launch<false, false, true>(qh, kh, T, a, b, d, pc, s);
+        case 5: return rope_shape_launch<true, false, true>(qh, kh, T, a, b, d, pc, s);
+        case 6: return rope_shape_launch<false, true, true>(qh, kh, T, a, b, d, pc, s);
+        default: return rope_shape_launch<true, true, true>(qh, kh, T, a, b, d, pc, s);
+    }
 }
 
 // An empty one-workgroup launch.

@@ -68,6 +68,23 @@ inline int64_t resident_workgroups(const void* kernel, int threads) {
     return cap;
 }
 
+// Compute units of the current device, queried once per device (0 if the
+// runtime cannot say).
+inline int device_cus() {
+    static std::mutex mu;
+    static std::map<int, int> cache;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 0;
+    std::lock_guard<std::mutex> lock(mu);
+    auto it = cache.find(dev);
+    if (it != cache.end()) return it->second;
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+        cus = 0;
+    cache[dev] = cus;
+    return cus;
+}
+
 // A zeroed device region of `bytes` that the library holds for the current
 // device's legacy default stream (stream 0), one per `tag`: allocated and
 // zeroed on stream 0 at its first use, never freed.  Calls on stream 0 run in

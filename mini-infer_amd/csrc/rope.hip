@@ -911,6 +911,310 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(half_t* q, half_t* k, cons
     }
 }
 
+// ---------------------------------------------------------------------------
+// RoPE of Q and K from positions, in place, TPW tokens per 256-lane
+// workgroup with the token rows walked as contiguous 16-byte vectors: lane j
+// takes vectors j, j + 256, ... (R of them) of the token's [Q heads | K heads]
+// row, so each wave-wide load or store covers 1 KiB of consecutive bytes and
+// a workgroup's TPW tokens lie together.  A head's first-half vector s and
+// second-half vector s + X (X = head_dim / 16) sit in lanes j and j ^ X of one
+// wave; the partner's value comes over DPP (X = 8: row_ror:8) or a lane
+// shuffle.  Every load of the workgroup is issued first, then the TPW x
+// head_dim/2 cos/sin values are built once in LDS (one barrier), then every
+// output is formed, then the stores go out, each waiting for the one before
+// it.  On the same access pattern with no arithmetic (floors.hip,
+// mi_floor_rope_inplace), 4 tokens per workgroup with paced non-temporal
+// stores move 67 MB in place in 11.5 us, one token per workgroup (the
+// rope_kv_kernel shape) in 12.3 us.
+// The arithmetic is rope_kv_kernel's, operation for operation -- the bias add
+// rounded to fp16, the Q/K norm's per-lane sum over (x1[e], x2[e]) pairs and
+// its DPP sum over the X lanes of a half head (the first-half and second-half
+// lanes each form the same sum), the rotation with one rounding to fp32 -- so
+// the outputs equal rope_kv_kernel's bit for bit.  Only plain RoPE takes this
+// kernel by default: with the bias (Qwen2's q/k_proj bias) it measured 21.1
+// against 18.3 us at T = 6064, with the Q/K norm 19.7-21.0 against 18.0 us
+// (MI_ROPE_ROWS_BIAS / MI_ROPE_ROWS_NORM switch them on).
+#ifndef MI_ROPE_ROWS
+#define MI_ROPE_ROWS 1
+#endif
+#ifndef MI_ROPE_ROWS_SER
+#define MI_ROPE_ROWS_SER 1
+#endif
+#ifndef MI_ROPE_ROWS_NORM
+#define MI_ROPE_ROWS_NORM 0
+#endif
+#ifndef MI_ROPE_ROWS_BIAS
+#define MI_ROPE_ROWS_BIAS 0
+#endif
+
+// Lane j's 16-byte vector as seen by lane j ^ X (X = 4, 8, 16).
+template <int X>
+__device__ __forceinline__ h8 partner_vec(h8 v) {
+    typedef uint32_t u4v __attribute__((ext_vector_type(4)));
+    u4v u = __builtin_bit_cast(u4v, v), r;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        if constexpr (X == 8)  // row_ror:8 within a 16-lane row: lane i reads lane i ^ 8
+            r[i] = static_cast<uint32_t>(
+                __builtin_amdgcn_mov_dpp(static_cast<int>(u[i]), 0x128, 0xF, 0xF, false));
+        else
+            r[i] = static_cast<uint32_t>(__shfl_xor(static_cast<int>(u[i]), X, kWave));
+    }
+    return __builtin_bit_cast(h8, r);
+}
+
+// `inv` is the first kernel parameter, so it sits at offset 0 of the
+// kernel-argument block (explicit arguments are laid out in order from 0).
+template <bool BIAS, bool NORM, int X, int R, int TPW>
+__global__ __launch_bounds__(256) void rope_rows_kernel(
+    InvFreq inv, half_t* q, half_t* k, int Hq, int Hkv, int64_t T,
+    const int64_t* __restrict__ positions, const half_t* __restrict__ bq, const half_t* __restrict__ bk,
+    const half_t* __restrict__ wq, const half_t* __restrict__ wk, float eps, float w_bias) {
+    constexpr int HALF = X * 8;  // head_dim / 2
+    constexpr int HV = 2 * X;    // 16-byte vectors per head
+    constexpr int HD = 2 * HALF;
+    __shared__ __attribute__((aligned(16))) float cs[TPW][2][HALF];
+    const int tid = threadIdx.x;
+    const int qv = Hq * HV, nv = (Hq + Hkv) * HV;
+    const int64_t tok0 = static_cast<int64_t>(blockIdx.x) * TPW;
+
+    // this lane's R vectors: Q or K, offset within the token's row, row stride
+    // (the tensor picked where each address is formed, so the compiler keeps
+    // global rather than flat memory instructions)
+    bool inq[R], ok[R];
+    int64_t stride[R];
+    int col[R], sl[R], head[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const int v = tid + 256 * r;
+        ok[r] = v < nv;
+        inq[r] = v < qv || !ok[r];  // idle lanes point at Q's row and never load or store
+        const int vv = v < qv ? v : v - qv;
+        stride[r] = static_cast<int64_t>(inq[r] ? Hq : Hkv) * HD;
+        col[r] = ok[r] ? vv * 8 : 0;
+        sl[r] = vv & (HV - 1);  // slice within the head
+        head[r] = vv / HV;
+    }
+    auto at = [&](int r, int64_t tok) {
+        return (inq[r] ? q : k) + (tok * stride[r] + col[r]);
+    };
+    // The token positions as scalar loads and the bias / norm-weight slices
+    // (a few KB every token re-reads: plain loads) ahead of the data loads:
+    // vector loads complete in issue order, so a small load issued after the
+    // data would wait for all of it.
+    int64_t pos[TPW];
+#pragma unroll
+    for (int t = 0; t < TPW; ++t) pos[t] = positions[tok0 + t < T ? tok0 + t : T - 1];
+    h8 b1[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        b1[r] = h8(0);
+        if constexpr (BIAS) b1[r] = ld8((inq[r] ? bq : bk) + (ok[r] ? head[r] * HD + sl[r] * 8 : 0));
+        if constexpr (NORM) {
+            b1[r] = ld8((inq[r] ? wq : wk) + sl[r] * 8);  // the own slice's weights
+        }
+    }
+    // This lane's inverse frequencies for the cos/sin table below, read from
+    // the kernel-argument block ahead of the data loads.  Vector loads
+    // complete in issue order, so the wait for them below lets the TPW * R
+    // data loads issued after them stay in flight.  Written as asm because
+    // the compiler sinks an argument-block load to its first use, behind the
+    // data loads, where its wait would be a wait for all of them.
+    constexpr int NCS = (TPW * HALF + 255) / 256;
+    float invv[NCS];
+#pragma unroll
+    for (int j = 0; j < NCS; ++j) {
+        const float* ip =
+            reinterpret_cast<const float*>(
+                reinterpret_cast<uintptr_t>(__builtin_amdgcn_kernarg_segment_ptr())) +
+            ((tid + 256 * j) & (HALF - 1));  // inv.v[...]
+        asm volatile("global_load_dword %0, %1, off" : "=v"(invv[j]) : "v"(ip) : "memory");
+    }
+    // Every load is unconditional (idle lanes read Q's first vector, tokens
+    // past T re-read the last token and are never stored), so the loads are
+    // straight-line code and each later wait counts exactly the loads it needs.
+    h8 x[TPW][R];
+#pragma unroll
+    for (int t = 0; t < TPW; ++t) {
+        const int64_t tok = tok0 + t < T ? tok0 + t : T - 1;
+#pragma unroll
+        for (int r = 0; r < R; ++r) x[t][r] = ld8_stream(at(r, tok));
+    }
+    // the inverse frequencies have landed once at most the data loads issued
+    // after them are outstanding
+    asm volatile("s_waitcnt vmcnt(%0)" : : "n"(TPW * R) : "memory");
+#pragma unroll
+    for (int j = 0; j < NCS; ++j) asm volatile("" : "+v"(invv[j]));
+    // the workgroup's cos/sin rows (quad_split layout)
+#pragma unroll
+    for (int j = 0; j < NCS; ++j) {
+        const int i = tid + 256 * j;
+        if (i >= TPW * HALF) break;
+        const int t = i / HALF, e = i - t * HALF;
+        float fp = 0.0f;
+#pragma unroll
+        for (int tt = 0; tt < TPW; ++tt)
+            if (tt == t) fp = static_cast<float>(pos[tt]);
+        half_t hc, hs;
+        cos_sin_half(fp * invv[j], hc, hs);
+        const int li = quad_split(e, HALF);
+        cs[t][0][li] = (float)hc;
+        cs[t][1][li] = (float)hs;
+    }
+    __syncthreads();
+
+#pragma unroll
+    for (int t = 0; t < TPW; ++t) {
+        const int64_t tok = tok0 + t;
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            h8 own = x[t][r];
+            if constexpr (BIAS) {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) own[e] = to_half((float)own[e] + (float)b1[r][e]);
+            }
+            h8 oth = partner_vec<X>(own);  // every lane takes part
+            const bool first = (sl[r] & X) == 0;
+            const int c = sl[r] & (X - 1);
+            float rrms = 1.0f;
+            if constexpr (NORM) {  // the sum over (x1[e], x2[e]) pairs, x1 first
+                const h8 x1 = first ? own : oth, x2 = first ? oth : own;
+                float ss = 0.0f;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const float f1 = (float)x1[e], f2 = (float)x2[e];
+                    ss = fmaf(f1, f1, ss);
+                    ss = fmaf(f2, f2, ss);
+                }
+                ss = group_sum<X>(ss);
+                rrms = rsqrtf(ss / static_cast<float>(X * 16) + eps);
+                // the normalised value as the reference stores it (fp16); the
+                // partner's comes over the same exchange
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                    own[e] = to_half((float)own[e] * rrms * ((float)b1[r][e] + w_bias));
+                oth = partner_vec<X>(own);
+            }
+            // entries 0-3 of slice c at c*4, entries 4-7 at HALF/2 + c*4 (quad_split)
+            typedef float f4 __attribute__((ext_vector_type(4)));
+            const f4 c_lo = *reinterpret_cast<const f4*>(&cs[t][0][c * 4]);
+            const f4 c_hi = *reinterpret_cast<const f4*>(&cs[t][0][(HALF >> 1) + c * 4]);
+            const f4 s_lo = *reinterpret_cast<const f4*>(&cs[t][1][c * 4]);
+            const f4 s_hi = *reinterpret_cast<const f4*>(&cs[t][1][(HALF >> 1) + c * 4]);
+            // y = own * cos + partner * (-sin for a first-half lane, +sin for a
+            // second-half one): x1*c - x2*s and x2*c + x1*s, the negation exact
+            const float sgn = first ? -1.0f : 1.0f;
+            h8 y;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float cv = e < 4 ? c_lo[e & 3] : c_hi[e & 3];
+                const float sv = sgn * (e < 4 ? s_lo[e & 3] : s_hi[e & 3]);
+                const float a = (float)own[e], bb = (float)oth[e];
+                y[e] = to_half(fp32_rounded(a * cv + bb * sv));
+            }
+            x[t][r] = y;
+        }
+    }
+    // every output formed, then the stores, each waiting for the one before
+#pragma unroll
+    for (int t = 0; t < TPW; ++t) {
+        const int64_t tok = tok0 + t;
+        if (tok >= T) break;  // workgroup-uniform
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            if (ok[r]) {
+                st8_stream(at(r, tok), x[t][r]);
+                store_gap<MI_ROPE_ROWS_SER != 0>();
+            }
+        }
+    }
+}
+
+template <bool BI, bool NO, int XX, int RR>
+void rope_rows_go(int tpw, dim3 g, hipStream_t s, const InvFreq& inv, half_t* q, half_t* k,
+                  int hq, int hk, int64_t T, const int64_t* positions, const half_t* bq,
+                  const half_t* bk, const half_t* wq, const half_t* wk, float eps, float w_bias) {
+#define MI_RR_GO(TT)                                                                            \
+    rope_rows_kernel<BI, NO, XX, RR, TT><<<g, dim3(256), 0, s>>>(inv, q, k, hq, hk, T, positions, \
+                                                                 bq, bk, wq, wk, eps, w_bias)
+    switch (tpw) {
+        case 1: MI_RR_GO(1); break;
+        case 2: MI_RR_GO(2); break;
+        case 4: MI_RR_GO(4); break;
+        case 6: if constexpr (RR <= 2) MI_RR_GO(6); break;
+        default: if constexpr (RR <= 2) MI_RR_GO(8); break;
+    }
+#undef MI_RR_GO
+}
+
+// Tokens per workgroup: the fewest of {1, 2, 4, 6, 8} (R <= 2; {1, 2, 4}
+// for R = 3, 4) whose grid fits 4 workgroups per CU -- one resident round
+// with every CU equally loaded -- else the most.  Measured at Qwen2.5's
+// 28 + 4 heads of 128 (R = 2): T = 4096, 4 tokens (1024 workgroups) 11.7 us
+// against 12.6 us for rope_kv_kernel's one token per workgroup; T = 6064,
+// 6 tokens (1011 workgroups) 17.5 us against 17.8 us, while 4 tokens
+// (1516 workgroups, an uneven round) took 20.1 us.
+int rope_rows_tpw(int64_t T, int R) {
+    const int64_t target = 4 * static_cast<int64_t>(device_cus() > 0 ? device_cus() : 256);
+    static const int kCands[] = {1, 2, 4, 6, 8};
+    const int n = R <= 2 ? 5 : 3;
+    for (int i = 0; i < n; ++i)
+        if (ceil_div(T, kCands[i]) <= target) return kCands[i];
+    return kCands[n - 1];
+}
+
+// rope_rows_kernel for head_dim 64 / 128 / 256 and up to 1024 vectors per
+// token; MI_ERR_UNSUPPORTED otherwise (the caller takes rope_kv_kernel).
+int rope_qk_rows(half_t* q, half_t* k, const half_t* bq, const half_t* bk,
+                 const int64_t* positions, const InvFreq& inv, int64_t T, int64_t Hq,
+                 int64_t Hkv, int64_t head_dim, hipStream_t s, const half_t* wq,
+                 const half_t* wk, float eps, float w_bias) {
+    const bool norm = wq != nullptr;
+    if (!MI_ROPE_ROWS || (norm && !MI_ROPE_ROWS_NORM) || (bq && !MI_ROPE_ROWS_BIAS))
+        return MI_ERR_UNSUPPORTED;
+    const int64_t nv = (Hq + Hkv) * head_dim / 8;
+    if ((head_dim != 64 && head_dim != 128 && head_dim != 256) || nv > 1024 || nv < 1 ||
+        !aligned16(q) || (Hkv > 0 && !aligned16(k)) || (bq && !aligned16(bq)) ||
+        (bk && Hkv > 0 && !aligned16(bk)) ||
+        (norm && (!aligned16(wq) || (Hkv > 0 && !aligned16(wk)))))
+        return MI_ERR_UNSUPPORTED;
+    const int R = static_cast<int>((nv + 255) / 256);
+    const int tpw = rope_rows_tpw(T, R);
+    const int64_t grid = ceil_div(T, tpw);
+    if (grid > kMaxGridX) return MI_ERR_UNSUPPORTED;
+    const dim3 g(static_cast<unsigned>(grid));
+    const int hq = static_cast<int>(Hq), hk = static_cast<int>(Hkv);
+#define MI_RR_ARGS tpw, g, s, inv, q, k, hq, hk, T, positions, bq, bk, wq, wk, eps, w_bias
+#define MI_RR_R(BI, NO, XX)                                    \
+    switch (R) {                                               \
+        case 1: rope_rows_go<BI, NO, XX, 1>(MI_RR_ARGS); break; \
+        case 2: rope_rows_go<BI, NO, XX, 2>(MI_RR_ARGS); break; \
+        case 3: rope_rows_go<BI, NO, XX, 3>(MI_RR_ARGS); break; \
+        default: rope_rows_go<BI, NO, XX, 4>(MI_RR_ARGS);      \
+    }
+#define MI_RR_X(BI, NO)                     \
+    switch (head_dim) {                     \
+        case 64: MI_RR_R(BI, NO, 4) break;  \
+        case 128: MI_RR_R(BI, NO, 8) break; \
+        default: MI_RR_R(BI, NO, 16)        \
+    }
+    if (norm) {
+#if MI_ROPE_ROWS_NORM
+        MI_RR_X(false, true)
+#endif
+    } else if (bq) {
+#if MI_ROPE_ROWS_BIAS
+        MI_RR_X(true, false)
+#endif
+    } else {
+        MI_RR_X(false, false)
+    }
+#undef MI_RR_X
+#undef MI_RR_R
+#undef MI_RR_ARGS
+    return launch_status();
+}
+
 // RoPE of Q and K from positions (+ the Q/K bias, or the Q/K norm) through rope_kv_kernel
 // with no segment: one token per 256-lane workgroup, head_dim's lane split at
 // compile time.  Against rope_kernel at T = 6064 (plain / with the bias):
@@ -933,6 +1237,11 @@ int rope_qk_one_token(half_t* q, half_t* k, const half_t* bq, const half_t* bk,
                       int64_t Hkv, int64_t head_dim, hipStream_t s,
                       const half_t* wq = nullptr, const half_t* wk = nullptr, float eps = 0.0f,
                       float w_bias = 0.0f) {
+    {
+        const int st = rope_qk_rows(q, k, bq, bk, positions, inv, T, Hq, Hkv, head_dim, s, wq, wk,
+                                    eps, w_bias);
+        if (st != MI_ERR_UNSUPPORTED) return st;
+    }
     const int64_t units = (Hq + Hkv) * (head_dim / 16);
     const bool norm = wq != nullptr;
     const int64_t min_units = norm ? kRkvMinUnitsNorm : (bq ? 1 : MI_RKV_MIN_UNITS);

@@ -131,6 +131,32 @@ def test_shapes(mk, orc, dev, T, Hq, Hkv, hd):
         assert_bits_equal(to_host(kd), orc.rope_neox(k, c, s).astype(np.float16), what="k")
 
 
+# Shapes for the contiguous-row kernel (rope_rows_kernel): head_dim 64 / 128 /
+# 256; 1-4 rounds of 256 vectors per token (R); every tokens-per-workgroup
+# choice (1, 2, 4, 6, 8 on a 256-CU part) with a partial last workgroup; Q-only
+# and K-only; a grid past 4 workgroups per CU; 1024 vectors (the largest it
+# takes) and 1032 (past it: the one-token kernel).
+@pytest.mark.parametrize("T,Hq,Hkv,hd", [
+    (1, 28, 4, 128), (1029, 28, 4, 128), (2047, 28, 4, 128), (4099, 28, 4, 128),
+    (8191, 28, 4, 128), (9001, 28, 4, 128), (2050, 8, 8, 128), (3000, 32, 8, 128),
+    (700, 56, 8, 128), (1500, 12, 2, 64), (2100, 16, 8, 256), (77, 0, 8, 128),
+    (100, 5, 0, 128), (33, 129, 0, 64)])
+def test_rows_shapes(mk, orc, dev, T, Hq, Hkv, hd):
+    _case(f"rope rows T={T} Hq={Hq} Hkv={Hkv} hd={hd}")
+    rng = np.random.default_rng(T * 7 + Hq * 131 + hd)
+    q = normal_f16(rng, (T, Hq, hd))
+    k = normal_f16(rng, (T, Hkv, hd))
+    pos = rng.integers(0, 40000, T).astype(np.int64)
+    inv = orc.rope_inv_freq(hd, 1e6)
+    qd, kd = to_dev(q, dev), to_dev(k, dev)
+    mk.rope_neox_qk(qd, kd if Hkv else None, to_dev(pos, dev), inv)
+    c, s = orc.rope_tables(inv, pos)
+    if Hq:
+        assert_bits_equal(to_host(qd), orc.rope_neox(q, c, s).astype(np.float16), what="q")
+    if Hkv:
+        assert_bits_equal(to_host(kd), orc.rope_neox(k, c, s).astype(np.float16), what="k")
+
+
 def test_out_of_place_table_path(mk, orc, dev):
     _case("rope table path out of place")
     rng = np.random.default_rng(35)
