@@ -46,6 +46,8 @@ def rotations(set_bytes, min_sets=2, max_sets=64):
 
 
 EAGER = False  # --eager: plain launches (for counter collection), no graph
+KERNEL_ITERS = 100  # launches per kernel-table row (at least)
+CHAIN_ITERS = 40    # decoder-chain steps per chain row (at least)
 
 
 def time_launches(launch, nsets, iters, warmup):
@@ -136,6 +138,7 @@ def floors_lib():
         lib.mi_floor_inplace.argtypes = [vp, i64, ci, vp]
         lib.mi_floor_read.argtypes = [vp, i64, ci, vp, i64, vp]
         lib.mi_floor_empty.argtypes = [vp]
+        lib.mi_floor_rope_inplace.argtypes = [vp, vp, i64, i64, i64, i64, ci, vp]
         _FLOORS_LIB = lib
     return _FLOORS_LIB
 
@@ -185,6 +188,28 @@ def floor_time(dev, kind, nbytes, iters=40, warmup=5, forms=None):
     if forms is None:
         _FLOOR[key] = (best, per)
     return best, per
+
+
+def rope_floor_time(dev, T, Hq, Hkv, hd, form, iters=100, warmup=10):
+    """The in-place RoPE access pattern with no arithmetic (mi_floor_rope_inplace):
+    form 32 = the contiguous-row kernel's (lane j on vectors j, j + 256 of a
+    token's [Q | K] row, its tokens per workgroup, paced stores), 1 = one token
+    per workgroup, lane (head, slice) on both half-head vectors, write-through
+    stores (the one-token kernel's)."""
+    import torch
+    lib = floors_lib()
+    ns = rotations(T * (Hq + Hkv) * hd * 2)
+    bufs = [(torch.zeros((T, Hq, hd), dtype=torch.float16, device=dev),
+             torch.zeros((T, Hkv, hd), dtype=torch.float16, device=dev)) for _ in range(ns)]
+
+    def go(i):
+        rc = lib.mi_floor_rope_inplace(bufs[i][0].data_ptr(), bufs[i][1].data_ptr(), T, Hq, Hkv,
+                                       hd, form, torch.cuda.current_stream().cuda_stream)
+        if rc != 0:
+            raise RuntimeError(f"rope floor failed: {rc}")
+    sec = time_launches(go, ns, iters, warmup)
+    del bufs
+    return sec
 
 
 def empty_launch_time(iters=400, warmup=20):
@@ -303,6 +328,13 @@ def chain_positions(gen_np):
     return np.concatenate([dec] + pre).astype(np.int64)
 
 
+def attach_rope_floors(dev, row, T, Hq, Hkv, hd):
+    """RoPE rows: the time of their own access pattern with no arithmetic."""
+    row["rope_floor_us"] = round(rope_floor_time(dev, T, Hq, Hkv, hd, 32) * 1e6, 3)
+    row["rope_floor_one_token_us"] = round(rope_floor_time(dev, T, Hq, Hkv, hd, 1) * 1e6, 3)
+    row["frac_of_rope_floor"] = round(row["rope_floor_us"] / row["us"], 4)
+
+
 def all_kernels(mk, dev, iters, warmup):
     import numpy as np
     import torch
@@ -346,6 +378,7 @@ def all_kernels(mk, dev, iters, warmup):
     sec = time_launches(lambda i: mk.rope_neox_qk(qs[i], ks[i], pos, inv), ns, iters, warmup)
     out.append(report("rope_neox_qk", "Q[4096,28,128]+K[4096,4,128]", nb, sec, T, "inplace"))
     del qs, ks
+    attach_rope_floors(dev, out[-1], T, Hq, Hkv, hd)
 
     # 4a/4b. SwiGLU [4096,18944], GeGLU [4096,14336]
     for name, fn, I in (("swiglu", mk.swiglu, 18944), ("geglu", mk.geglu, 14336)):
@@ -404,6 +437,7 @@ def all_kernels(mk, dev, iters, warmup):
     sec = time_launches(lambda i: mk.rope_neox_qk(qs[i].view(T, 28, 128), ks[i].view(T, 4, 128),
                                                   pos, inv), ns, iters, warmup)
     out.append(report("rope_neox_qk", "chain Q[6064,28,128]+K[6064,4,128]", nb, sec, T, "inplace"))
+    rope_chain_row = out[-1]
     # 5c+5d fused: Q/K RMSNorm + RoPE in one pass (replaces the two rows above)
     nb = 2 * T * 32 * 128 * 2 + T * 8 + 2 * 128 * 2
     sec = time_launches(lambda i: mk.qk_norm_rope(qs[i].view(T, 28, 128), ks[i].view(T, 4, 128),
@@ -418,6 +452,7 @@ def all_kernels(mk, dev, iters, warmup):
     out.append(report("bias_rope_neox_qk", "chain Q[6064,28,128]+K[6064,4,128]", nb, sec, T,
                       "inplace"))
     del qs, ks
+    attach_rope_floors(dev, rope_chain_row, T, 28, 4, 128)
     # 5e. SwiGLU [6064, 18944]
     nb = 3 * T * I * 2
     ns = rotations(3 * T * I * 2)
@@ -573,12 +608,20 @@ def all_kernels(mk, dev, iters, warmup):
 # CPU baseline: the oracle on the host, bounded sample of the headline config
 # ---------------------------------------------------------------------------
 
+def host_cpus():
+    """The host's processor counts beside the threads a CPU leg used: `nproc`
+    (the CPUs this process may run on, os.sched_getaffinity) and
+    `hardware_concurrency` (the online CPUs, which C++'s
+    std::thread::hardware_concurrency and os.cpu_count both report)."""
+    return {"nproc": len(os.sched_getaffinity(0)), "hardware_concurrency": os.cpu_count()}
+
+
 def cpu_baseline(budget_s=10.0):
     import numpy as np
     sys.path.insert(0, str(ROOT / "oracle"))
     import oracle  # the checker, timed here as the CPU reference implementation
     T, D = 8192, 3584
-    cores = max(1, min(16, os.cpu_count() or 1))
+    cores = max(1, min(16, len(os.sched_getaffinity(0))))
     rng = np.random.default_rng(0)
     x = rng.standard_normal((T, D), dtype=np.float32).astype(np.float16)
     r = rng.standard_normal((T, D), dtype=np.float32).astype(np.float16)
@@ -598,6 +641,7 @@ def cpu_baseline(budget_s=10.0):
         "value": round(nbytes / sec / 1e9, 3),
         "unit": "GB/s",
         "cores": cores,
+        **host_cpus(),
         "kind": "port",
         "sample": (f"oracle fused residual-add + RMSNorm (fp32 math) on the full [8192,3584] "
                    f"workload, {n} passes in {el:.1f} s with {cores} threads over rows; "
@@ -613,7 +657,7 @@ def cpu_torch_baseline(budget_s=5.0):
     reference's add kernel does, then the fp32 RMSNorm of the result.  Threads:
     torch's intra-op pool, capped at 16."""
     import torch
-    cores = max(1, min(16, os.cpu_count() or 1))
+    cores = max(1, min(16, len(os.sched_getaffinity(0))))
     torch.set_num_threads(cores)
     T, D = 8192, 3584
     g = torch.Generator().manual_seed(0)
@@ -650,7 +694,7 @@ def cpu_kernel_table(budget_s=1.0):
     import numpy as np
     sys.path.insert(0, str(ROOT / "oracle"))
     import oracle  # the checker, timed here as the CPU reference implementation
-    cores = max(1, min(16, os.cpu_count() or 1))
+    cores = max(1, min(16, len(os.sched_getaffinity(0))))
     rng = np.random.default_rng(2)
 
     def h(shape, mean=0.0, std=1.0):
@@ -993,15 +1037,18 @@ def main():
     kernels = None
     if not args.no_kernels:
         log("[bench] per-config kernel table")
-        kernels = all_kernels(mk, dev, max(20, args.steps // 2), max(5, args.warmup // 2))
+        # The table's rows average at least KERNEL_ITERS back-to-back launches
+        # per graph replay whatever --steps is, so the replay's fixed start
+        # cost (a few us per graph) stays out of the per-launch figures.
+        kit, kwu = max(KERNEL_ITERS, args.steps // 2), max(10, args.warmup // 2)
+        cit, cwu = max(CHAIN_ITERS, args.steps // 8), max(5, args.warmup // 4)
+        kernels = all_kernels(mk, dev, kit, kwu)
         if not args.no_chain:
-            kernels += decoder_chain(mk, dev, max(10, args.steps // 8), max(3, args.warmup // 4))
-            kernels += decoder_chain(mk, dev, max(10, args.steps // 8), max(3, args.warmup // 4),
-                                     qwen2=True)
+            kernels += decoder_chain(mk, dev, cit, cwu)
+            kernels += decoder_chain(mk, dev, cit, cwu, qwen2=True)
             # the decode-only step of the same model (64 sequences, one token each):
             # launch-latency territory, where the fusion's saved launches show most
-            kernels += decoder_chain(mk, dev, max(10, args.steps // 8), max(3, args.warmup // 4),
-                                     prefills=())
+            kernels += decoder_chain(mk, dev, cit, cwu, prefills=())
         for k in kernels:
             floor = ""
             if "frac_of_floor" in k:
@@ -1010,6 +1057,9 @@ def main():
                          + f" us -> {100 * k['frac_of_floor']:5.1f}% of {k['floor_kind']}")
             elif "empty_launch_us" in k:
                 floor = f"  empty launch {k['empty_launch_us']:.2f} us"
+            if "rope_floor_us" in k:
+                floor += (f"  rope pattern {k['rope_floor_us']:.2f} us (one-token pattern "
+                          f"{k['rope_floor_one_token_us']:.2f})")
             log(f"[bench]   {k['kernel']:<18} {k['config']:<38} {k['us']:>9.2f} us "
                 f"{k['GBps']:>8.1f} GB/s  {100 * k['frac']:5.1f}%{floor}")
 
@@ -1029,7 +1079,8 @@ def main():
         cpu = cpu_baseline(args.cpu_seconds)
         cpu_torch = cpu_torch_baseline(min(5.0, args.cpu_seconds))
         log(f"[bench] CPU oracle {cpu['value']} GB/s, torch CPU {cpu_torch['value']} GB/s "
-            f"({cpu['cores']} threads)")
+            f"({cpu['cores']} threads; nproc {cpu['nproc']}, "
+            f"hardware_concurrency {cpu['hardware_concurrency']})")
         if kernels is not None:
             cores, cpu_rows = cpu_kernel_table(args.cpu_seconds_per_config)
             by_key = {(r["kernel"], r["config"]): r for r in cpu_rows}
@@ -1039,6 +1090,7 @@ def main():
                     continue
                 k.update({kk: v for kk, v in c.items() if kk not in ("kernel", "config")})
                 k["cpu_cores"] = cores
+                k.update({"cpu_" + kk: v for kk, v in host_cpus().items()})
                 k["gpu_over_cpu"] = round(c["cpu_us"] / k["us"], 1)
                 log(f"[bench]   cpu {k['kernel']:<18} {k['config']:<38} {c['cpu_us']:>11.1f} us "
                     f"{c['cpu_GBps']:>8.2f} GB/s  ({cores} threads)")

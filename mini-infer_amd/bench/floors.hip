@@ -86,7 +86,7 @@ __device__ __forceinline__ void rope_shape_store(_Float16* p, u4 v) {
     if constexpr (WT) mi::st8_stream_wt(p, __builtin_bit_cast(mi::h8, v));
     else st(reinterpret_cast<u4*>(p), v);
 }
-template <bool WT, bool SER, bool PERS, int TPW, bool CONTIG = false>
+template <bool WT, bool SER, bool PERS, int TPW, int CONTIG = 0>
 __global__ __launch_bounds__(256) void rope_shape_kernel(_Float16* q, _Float16* k, int64_t T,
                                                          int Hq, int Hkv, int hd) {
     const int half = hd >> 1, cph = hd >> 4;
@@ -96,7 +96,7 @@ __global__ __launch_bounds__(256) void rope_shape_kernel(_Float16* q, _Float16* 
     auto addr = [&](int64_t tok) {
         return h < Hq ? q + (tok * Hq + h) * hd + c * 8 : k + (tok * Hkv + (h - Hq)) * hd + c * 8;
     };
-    if constexpr (TPW > 1) {  // TPW tokens per workgroup, every load issued first
+    if constexpr (TPW > 1 || CONTIG) {  // TPW tokens per workgroup, every load issued first
         u4 a[TPW], b[TPW];
         _Float16 *pa[TPW], *pb[TPW];
         const int qv = Hq * cph * 2;  // 16-byte vectors of a token's Q row
@@ -104,7 +104,15 @@ __global__ __launch_bounds__(256) void rope_shape_kernel(_Float16* q, _Float16* 
         for (int t = 0; t < TPW; ++t) {
             int64_t tok = static_cast<int64_t>(blockIdx.x) * TPW + t;
             tok = tok < T ? tok : T - 1;
-            if (CONTIG) {  // lane j: vectors j and j + 256 of the token's [Q | K] rows
+            if (CONTIG == 2) {
+                // lane j: vectors j + 256 i of the workgroup's TPW Q rows as one
+                // block, then of its TPW K rows as one block
+                const int64_t t0 = static_cast<int64_t>(blockIdx.x) * TPW;
+                const int nq = TPW * qv;
+                const int i0 = tid + 256 * (2 * t), i1 = i0 + 256;
+                pa[t] = i0 < nq ? q + t0 * Hq * hd + i0 * 8 : k + t0 * Hkv * hd + (i0 - nq) * 8;
+                pb[t] = i1 < nq ? q + t0 * Hq * hd + i1 * 8 : k + t0 * Hkv * hd + (i1 - nq) * 8;
+            } else if (CONTIG) {  // lane j: vectors j and j + 256 of the token's [Q | K] rows
                 pa[t] = q + (tok * Hq * hd) + tid * 8;
                 const int j2 = tid + 256;
                 pb[t] = j2 < qv ? q + (tok * Hq * hd) + j2 * 8 : k + tok * Hkv * hd + (j2 - qv) * 8;
@@ -155,8 +163,9 @@ __global__ __launch_bounds__(256) void rope_shape_kernel(_Float16* q, _Float16* 
 // 16-byte aligned, hd a multiple of 16, (Hq + Hkv) * hd / 16 <= 256).
 // form bit 0: write-through stores (else non-temporal); bit 1: each store
 // waits for the one before; bit 2: a resident grid of `form >> 8` workgroups
-// per CU (0: the occupancy limit) walking the tokens.
-template <bool WT, bool SER, bool PERS, int TPW = 1, bool CONTIG = false>
+// per CU (0: the occupancy limit) walking the tokens; bit 3 / 4 / 6: 2 / 4 / 8
+// tokens per workgroup; bit 5: the contiguous-row kernel's pattern (below).
+template <bool WT, bool SER, bool PERS, int TPW = 1, int CONTIG = 0>
 int rope_shape_launch(_Float16* q, _Float16* k, int64_t T, int Hq, int Hkv, int hd, int per_cu_req,
                       hipStream_t s) {
     const auto kf = rope_shape_kernel<WT, SER, PERS, TPW, CONTIG>;
@@ -270,14 +279,36 @@ extern "C" int mi_floor_rope_inplace(void* q, void* k, int64_t T, int64_t Hq, in
             default: return rope_shape_launch<true, true, false, 2>(qh, kh, T, a, b, d, 0, s);
         }
     }
-    if (form & 32) {  // bit 5: 4 tokens, lane j on vectors j and j + 256 of a token's [Q | K]
+    if (form & 32) {
+        // bit 5: the contiguous-row RoPE kernel's pattern -- lane j on vectors j
+        // and j + 256 of a token's [Q | K] row (512 vectors a token), paced
+        // non-temporal stores, its tokens per workgroup: the fewest of 1, 2, 4,
+        // 6, 8 that keep the grid within 4 workgroups per CU
         if (Hq * hd / 8 < 256 || (Hq + Hkv) * hd / 8 != 512) return -1;
-        switch (form & 3) {
-            case 0: return rope_shape_launch<false, false, false, 4, true>(qh, kh, T, a, b, d, 0, s);
-            case 1: return rope_shape_launch<true, false, false, 4, true>(qh, kh, T, a, b, d, 0, s);
-            case 2: return rope_shape_launch<false, true, false, 4, true>(qh, kh, T, a, b, d, 0, s);
-            default: return rope_shape_launch<true, true, false, 4, true>(qh, kh, T, a, b, d, 0, s);
+        int dev = 0, cus = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+            return -2;
+        const int64_t target = 4 * static_cast<int64_t>(cus);
+        int tpw = 8;
+        for (int c : {1, 2, 4, 6, 8})
+            if ((T + c - 1) / c <= target) {
+                tpw = c;
+                break;
+            }
+        switch (tpw) {
+            case 1: return rope_shape_launch<false, true, false, 1, 1>(qh, kh, T, a, b, d, 0, s);
+            case 2: return rope_shape_launch<false, true, false, 2, 1>(qh, kh, T, a, b, d, 0, s);
+            case 4: return rope_shape_launch<false, true, false, 4, 1>(qh, kh, T, a, b, d, 0, s);
+            case 6: return rope_shape_launch<false, true, false, 6, 1>(qh, kh, T, a, b, d, 0, s);
+            default: return rope_shape_launch<false, true, false, 8, 1>(qh, kh, T, a, b, d, 0, s);
         }
+    }
+    if (form & 128) {  // bit 7: 4 tokens, flat over the workgroup's Q block, then its K block
+        if (T % 4 != 0 || (Hq + Hkv) * hd / 8 != 512) return -1;
+        if (form & 2)
+            return rope_shape_launch<false, true, false, 4, 2>(qh, kh, T, a, b, d, 0, s);
+        return rope_shape_launch<false, false, false, 4, 2>(qh, kh, T, a, b, d, 0, s);
     }
     if (form & 64) {  // bit 6: 8 tokens per workgroup
         switch (form & 3) {
