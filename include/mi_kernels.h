@@ -261,14 +261,18 @@ int mi_softmax_ws_f16(const void* x, void* y, int64_t N, int64_t D, void* worksp
 /* mi_softmax_f16 for callers that cannot allocate (no counterpart in the
  * reference; for code under HIP graph capture, tight serving loops and
  * harnesses that forbid hipMalloc): the same kernels as mi_softmax_ws_f16,
- * with the workspace taken from a file-scope device array of 1,318,912 bytes
- * per GPU (row records plus 256 KiB of two-pass pairs) that the library
- * holds from load until the process ends.  Calls no hipMalloc / hipFree; on a
- * device's first call it looks up the array's address and zeroes it with a
- * kernel on `stream`.  Shapes whose workspace would exceed the array return
- * MI_ERR_UNSUPPORTED.  Every call on one GPU shares that GPU's array, so
- * calls that overlap in time on one GPU (different streams, or threads)
- * race; calls in one stream's order do not. */
+ * with the workspace taken from a file-scope device array of 2,424,832 bytes
+ * per GPU (512 row records of 4,224 bytes plus 256 KiB of two-pass pairs)
+ * that the library holds from load until the process ends.  The array is
+ * zero from the library's load and each call leaves it valid for the next;
+ * calls launch nothing but the softmax (a device's first call only looks up
+ * the array's address), so the first call may itself be captured in a
+ * graph.  Calls no hipMalloc / hipFree.  Shapes whose workspace would exceed
+ * the array return MI_ERR_UNSUPPORTED.  Every call on one GPU shares that
+ * GPU's array: calls that overlap in time on one GPU (on different streams,
+ * from different threads, or graph replays concurrent with other calls) are
+ * UNDEFINED -- their results may be wrong, with no error reported.  Calls in
+ * one stream's order, or otherwise ordered one after the other, are safe. */
 int mi_softmax_noalloc_f16(const void* x, void* y, int64_t N, int64_t D, void* stream);
 
 /* The sampling step over one set of logits [N, V] in one pass: probs =

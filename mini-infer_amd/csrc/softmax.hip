@@ -958,18 +958,12 @@ int softmax_checked(const void* x, void* y, int64_t N, int64_t D, void* ws, int6
 // Allocation-free entry (mi_softmax_noalloc_f16): the same plans and kernels
 // as mi_softmax_ws_f16, with the workspace taken from a file-scope device
 // array (`scratch`, below) instead of the caller or the runtime.  Its host
-// address comes from hipGetSymbolAddress once per device; it is zeroed by a
-// fill kernel on that device's first call (the row records must start at
-// zero) and then left to each call, which leaves it valid for the next.
+// address comes from hipGetSymbolAddress once per device; it is zero from
+// the library's load (the row records must start at zero) and then left to
+// each call, which leaves it valid for the next.
 // ---------------------------------------------------------------------------
 constexpr int64_t kNoAllocPairBytes = 256 * 1024;  // two-pass (max, sum) pairs
 constexpr int64_t kScratchBytes = kOnePassRegion + kNoAllocPairBytes;
-
-__global__ __launch_bounds__(256) void zero_kernel(uint4* p, int64_t n) {
-    for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n;
-         i += static_cast<int64_t>(gridDim.x) * 256)
-        p[i] = make_uint4(0, 0, 0, 0);
-}
 
 }  // namespace
 }  // namespace mi
@@ -977,14 +971,20 @@ __global__ __launch_bounds__(256) void zero_kernel(uint4* p, int64_t n) {
 // 2,424,832 bytes per GPU, held from the library's load until the process
 // ends.  Host code never passes this name to a kernel or a copy: it is a
 // host-side stand-in; the device address comes from hipGetSymbolAddress.
+// It starts at zero, as the row records must: an object of static storage
+// with no initializer is zero-initialized, and in the code object it is
+// .bss, which the loader zero-fills on each device when it loads the code.
 static __device__ __align__(256) unsigned char scratch[mi::kScratchBytes];
 
 namespace mi {
 namespace {
 
 // This device's address of `scratch` (nullptr with *err set when the
-// runtime cannot give it), looked up and zeroed on the device's first call.
-void* scratch_for_current_device(hipStream_t s, int* err) {
+// runtime cannot give it), looked up on the device's first call.  Nothing
+// is launched here (the array is zero from load; each call leaves it valid
+// for the next), so a first call under graph capture records only the
+// softmax itself.
+void* scratch_for_current_device(int* err) {
     static std::mutex mu;
     static std::map<int, void*> ptrs;
     int dev = 0;
@@ -1001,12 +1001,6 @@ void* scratch_for_current_device(hipStream_t s, int* err) {
     if (e != hipSuccess || ptr == nullptr) {
         *err = static_cast<int>(e != hipSuccess ? e : hipErrorInvalidSymbol);
         (void)hipGetLastError();
-        return nullptr;
-    }
-    zero_kernel<<<dim3(64), dim3(256), 0, s>>>(static_cast<uint4*>(ptr), kScratchBytes / 16);
-    e = hipGetLastError();
-    if (e != hipSuccess) {
-        *err = static_cast<int>(e);
         return nullptr;
     }
     ptrs[dev] = ptr;
@@ -1026,7 +1020,7 @@ extern "C" int mi_softmax_noalloc_f16(const void* x, void* y, int64_t N, int64_t
     if (need == 0)
         return mi::softmax_checked(x, y, N, D, nullptr, 0, mi::Ws::kRecordsThenPairs, stream);
     int err = MI_OK;
-    void* ptr = mi::scratch_for_current_device(mi::as_stream(stream), &err);
+    void* ptr = mi::scratch_for_current_device(&err);
     if (!ptr) return err;
     return mi::softmax_checked(x, y, N, D, ptr, mi::kScratchBytes, mi::Ws::kRecordsThenPairs,
                                stream);

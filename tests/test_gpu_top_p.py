@@ -73,6 +73,36 @@ def test_top_p_vs_oracle(mk, orc, dev, V, B):
             assert int(to_host(out)[0]) == int(want[0])
 
 
+@pytest.mark.parametrize("V", [1000, 30000])
+def test_top_p_large_logits_small_temperature(mk, orc, dev, V):
+    """Logits far from zero (1e3 .. 6e4) at temperatures 0.1-0.5, where x / T
+    reaches ~6e5 and its fp32 rounding is ~0.03: the normaliser and the
+    candidate numerators must be formed consistently, or q moves by a few
+    percent and the nucleus crossing with it.  Candidates sit a few fp16 ulps
+    below the maximum (ties included), the rest 40 ulps below; p is placed
+    1-3% away from a running sum (as q is exact to ~1e-6 in every consistent
+    implementation, the screen still holds)."""
+    rng = np.random.default_rng(V + 17)
+    for base, T in ((1000.0, 0.5), (20000.0, 0.25), (60000.0, 0.1), (-30000.0, 0.2)):
+        ulp = float(np.spacing(np.float16(abs(base))))
+        for p in (0.32, 0.65, 0.9):
+            _case(f"top-p large logits V={V} base={base} T={T} p={p}")
+            rows = []
+            while len(rows) < 8:
+                x = np.full(V, base - 40 * ulp, dtype=np.float32)
+                n = int(rng.integers(2, 6))
+                hot = rng.choice(np.arange(0, V, 128), size=n, replace=False)
+                x[hot] = base - ulp * rng.integers(0, 3, n)
+                x = x.astype(np.float16)
+                if _safe(x, p, T):
+                    rows.append(x)
+            x = np.stack(rows)
+            seed = int(rng.integers(0, 1 << 62))
+            got = to_host(mk.top_p_sample(to_dev(x, dev), p, T, seed))
+            want = orc.top_p_sample(x, p, T, seed)
+            np.testing.assert_array_equal(got, want)
+
+
 @pytest.mark.parametrize("V", [128, 1000, 30000])
 def test_top_p_unaligned_rows(mk, orc, dev, V):
     """Rows starting 0..7 halves past a 16-byte boundary: the kernel reads

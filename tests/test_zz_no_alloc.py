@@ -5,7 +5,8 @@ for each plan that uses the library's device array -- one-launch split rows
 (row records), the two-launch form (in place: (max, sum) pairs) and the
 persistent many-row form -- and for a shape that needs no workspace.  Run
 after the other tests, and alone in a fresh process (the array is looked up
-and zeroed on the device's first call)."""
+on the device's first call and is zero from the library's load); a fresh
+process whose first call is captured in a graph is checked as well."""
 import numpy as np
 import pytest
 
@@ -51,3 +52,55 @@ def test_noalloc_argument_errors(mk):
     assert lib.mi_softmax_noalloc_f16(None, None, -1, 5, None) == -1
     assert lib.mi_softmax_noalloc_f16(None, None, 4, 5, None) == -1
     assert lib.mi_softmax_noalloc_f16(None, None, 0, 5, None) == 0
+
+
+_CAPTURED_FIRST = r"""
+import sys
+import numpy as np
+import torch
+sys.path.insert(0, sys.argv[1])
+import mi_kernels as mk
+mk.load_library()
+dev = torch.device("cuda:0")
+rng = np.random.default_rng(5)
+x = torch.from_numpy((rng.standard_normal((64, 152064), dtype=np.float32) * 4).astype(np.float16)).to(dev)
+ws = torch.zeros(mk.softmax_workspace_bytes(64, 152064), dtype=torch.uint8, device=dev)
+y_graph = torch.empty_like(x)
+side = torch.cuda.Stream()
+side.wait_stream(torch.cuda.current_stream())
+graph = torch.cuda.CUDAGraph()
+with torch.cuda.stream(side):
+    with torch.cuda.graph(graph, stream=side):
+        mk.softmax_noalloc(x, y=y_graph)   # the process's first call: captured
+torch.cuda.current_stream().wait_stream(side)
+torch.cuda.synchronize()
+ref = mk.softmax(x.clone(), workspace=ws)
+torch.cuda.synchronize()
+ref_bits = ref.cpu().numpy().view(np.uint16)
+bad = 0
+for rep in range(3):
+    y_graph.zero_()
+    graph.replay()
+    torch.cuda.synchronize()
+    bad += int((y_graph.cpu().numpy().view(np.uint16) != ref_bits).sum())
+    y_eager = mk.softmax_noalloc(x)  # eager calls between the replays
+    torch.cuda.synchronize()
+    bad += int((y_eager.cpu().numpy().view(np.uint16) != ref_bits).sum())
+print("MISMATCHES", bad, flush=True)
+"""
+
+
+def test_noalloc_first_call_captured(dev):
+    """In a fresh process, the first allocation-free call is captured in a HIP
+    graph (nothing but the softmax is recorded: the array is zero from load);
+    three replays, each followed by an eager call, all equal the workspace
+    entry point bit for bit."""
+    import subprocess
+    import sys
+    from pathlib import Path
+    print("[case] softmax noalloc: first call captured, replays + eager calls", flush=True)
+    pkg = str(Path(__file__).resolve().parent.parent / "mini-infer_amd")
+    r = subprocess.run([sys.executable, "-c", _CAPTURED_FIRST, pkg], capture_output=True,
+                       text=True, timeout=110)
+    assert r.returncode == 0, r.stderr[-2000:]
+    assert "MISMATCHES 0" in r.stdout, r.stdout[-2000:] + r.stderr[-2000:]
