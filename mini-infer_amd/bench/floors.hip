@@ -338,6 +338,43 @@ extern "C" int mi_floor_rope_inplace(void* q, void* k, int64_t T, int64_t Hq, in
     }
 }
 
+// The gather + input-norm pattern with no arithmetic: one wave per token
+// row, four rows per 256-lane workgroup; the wave reads table row ids[t]
+// (plain loads, H / 8 vectors, up to 16 per lane) and writes it to out1[t]
+// and, XOR-ed, to out2[t].  H a multiple of 8, at most 8192; 16-byte
+// aligned buffers.
+__global__ __launch_bounds__(256) void gather2_kernel(const int64_t* __restrict__ ids,
+                                                      const u4* __restrict__ table, u4* out1,
+                                                      u4* out2, int64_t T, int nv) {
+    const int lane = threadIdx.x & 63;
+    const int64_t t = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    if (t >= T) return;
+    const int64_t id = ids[t];
+    u4 v[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+        if (lane + 64 * i < nv) v[i] = table[id * nv + lane + 64 * i];
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+        if (lane + 64 * i < nv) st(out1 + t * nv + lane + 64 * i, v[i]);
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+        if (lane + 64 * i < nv) st(out2 + t * nv + lane + 64 * i, v[i] ^ 0x3c003c00u);
+}
+
+extern "C" int mi_floor_gather2(const int64_t* ids, const void* table, void* out1, void* out2,
+                                int64_t T, int64_t H, void* stream) {
+    if (T <= 0 || H <= 0 || H % 8 != 0 || H > 8192 || !ids || !table || !out1 || !out2) return -1;
+    if ((reinterpret_cast<uintptr_t>(table) | reinterpret_cast<uintptr_t>(out1) |
+         reinterpret_cast<uintptr_t>(out2)) & 15u)
+        return -1;
+    gather2_kernel<<<dim3(static_cast<unsigned>((T + 3) / 4)), dim3(256), 0,
+                     reinterpret_cast<hipStream_t>(stream)>>>(
+        ids, static_cast<const u4*>(table), static_cast<u4*>(out1), static_cast<u4*>(out2), T,
+        static_cast<int>(H / 8));
+    return hipGetLastError() == hipSuccess ? 0 : 1;
+}
+
 // An empty one-workgroup launch.
 extern "C" int mi_floor_empty(void* stream) {
     empty_kernel<<<dim3(1), dim3(64), 0, reinterpret_cast<hipStream_t>(stream)>>>();

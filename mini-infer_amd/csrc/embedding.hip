@@ -11,6 +11,18 @@
 #include "mi_device.h"
 #include "mi_host.h"
 
+#ifndef MI_EMBED_RMS_WAVE
+#define MI_EMBED_RMS_WAVE 1
+#endif
+// Tokens from which gather + input norm runs one wave per row (four rows per
+// workgroup): at T = 6064 of [152064, 3584] 25.4 -> 24.1 us (2 or 8 rows per
+// workgroup: 25.6 / 24.3 us); at T = 64 the one-workgroup-per-row kernel
+// keeps more CUs busy (2.5 against 3.6 us).
+#ifndef MI_EMBED_RMS_WAVE_MIN_T
+#define MI_EMBED_RMS_WAVE_MIN_T 2048
+#endif
+
+
 namespace mi {
 namespace {
 
@@ -167,6 +179,115 @@ __global__ __launch_bounds__(256) void embed_rms_kernel(const int64_t* __restric
     }
 }
 
+// The same, one wave per token row, RPW rows per workgroup (4).  The
+// wave reproduces embed_rms_kernel's reduction bit for bit: its lane j plays
+// the 256-lane kernel's lanes j, j + 64, j + 128, j + 192 (one per wave of
+// that kernel), holding their vectors, forming each one's sum of squares in
+// the same order, reducing each set of 64 with the same DPP pattern, and
+// adding the four wave totals in slot order from 0.0f as block_sum does --
+// so hidden and the normalised rows equal the one-workgroup-per-row kernel's
+// (and the unfused gather + rmsnorm's) exactly.  The weight is staged in LDS
+// once per workgroup (its loads issued before the table rows'; reading it from
+// the L2 per row instead measured 24.1 -> 24.5 us); no barrier follows the one
+// that publishes it, so each wave runs from its loads to its stores on its
+// own.  (Store pacing or non-temporal table loads: 0.1-1.5 us slower.)
+template <int VPT, int RPW>
+__global__ __launch_bounds__(64 * RPW) void embed_rms_wave_kernel(const int64_t* __restrict__ ids,
+                                                                  const half_t* __restrict__ table,
+                                                                  half_t* __restrict__ hidden,
+                                                                  const half_t* __restrict__ w,
+                                                                  half_t* __restrict__ y, int64_t T,
+                                                                  int64_t D, int64_t vocab,
+                                                                  float scale, float eps,
+                                                                  float w_bias) {
+    constexpr int NV = 4 * VPT;           // vectors per lane: 4 virtual lanes x VPT
+    constexpr int NW = 256 * VPT;         // weight vectors staged
+    constexpr int PER = (NW + 64 * RPW - 1) / (64 * RPW);  // of them per lane
+    __shared__ h8 wl[NW];
+    const int tid = threadIdx.x;
+    const int lane = tid & (kWave - 1);
+    const int64_t nv = D >> 3;
+    // the weight's vectors (vector c at wl[c]), loaded before the table rows
+    h8 wv[PER];
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+        const int64_t c = tid + j * 64 * RPW;
+        wv[j] = c < nv && c < NW ? ld8(w + c * 8) : h8(0);
+    }
+    const int64_t t_raw = static_cast<int64_t>(blockIdx.x) * RPW + (tid >> 6);
+    const bool row_ok = t_raw < T;
+    const int64_t t = __builtin_amdgcn_readfirstlane(static_cast<int>(row_ok ? t_raw : T - 1));
+    const int64_t id = ids[t];
+    const bool valid = id >= 0 && (vocab <= 0 || id < vocab);
+    const half_t* src = table + (valid ? id : 0) * D;
+    // slot (u, j): virtual lane L = lane + 64 u, its vector L + 256 j; plain
+    // loads of scattered table rows, as in gather_kernel
+    h8 v[NV];
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int64_t c = lane + 64 * u + j * 256;
+            v[j * 4 + u] = (valid && c < nv) ? ld8(src + c * 8) : h8(0);
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < PER; ++j)
+        if (tid + j * 64 * RPW < NW) wl[tid + j * 64 * RPW] = wv[j];
+    __syncthreads();
+    __builtin_amdgcn_s_waitcnt(kDrainVmem);
+    if (scale != 1.0f) {
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+#pragma unroll
+            for (int k = 0; k < 8; ++k) v[i][k] = to_half((float)v[i][k] * scale);
+        }
+    }
+    float ss[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        ss[u] = 0.0f;
+#pragma unroll
+        for (int j = 0; j < VPT; ++j) {
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const float f = (float)v[j * 4 + u][k];
+                ss[u] = fmaf(f, f, ss[u]);
+            }
+        }
+    }
+    if (row_ok) {
+#pragma unroll
+        for (int j = 0; j < VPT; ++j) {
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int64_t c = lane + 64 * u + j * 256;
+                if (c < nv) st8_stream(hidden + t * D + c * 8, v[j * 4 + u]);
+            }
+        }
+    }
+    float tot = 0.0f;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) tot += group_sum<kWave>(ss[u]);
+    const float rrms = rsqrtf(tot / static_cast<float>(D) + eps);
+    if (!row_ok) return;
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int64_t c = lane + 64 * u + j * 256;
+            if (c < nv) {
+                const h8 wc = wl[c];
+                h8 o;
+#pragma unroll
+                for (int k = 0; k < 8; ++k)
+                    o[k] = to_half((float)v[j * 4 + u][k] * rrms * ((float)wc[k] + w_bias));
+                st8_stream(y + t * D + c * 8, o);
+            }
+        }
+    }
+}
+
 // Any D or alignment: one workgroup per row, two passes over the row (the
 // second re-reads the hidden values this workgroup's own lanes wrote).
 __global__ __launch_bounds__(256) void embed_rms_scalar_kernel(
@@ -221,7 +342,16 @@ extern "C" int mi_embedding_rmsnorm_f16(const int64_t* ids, const void* table, v
     const bool vec = D % 8 == 0 && mi::aligned16(table) && mi::aligned16(hidden) &&
                      mi::aligned16(weight) && mi::aligned16(y);
     const int64_t vpt = mi::ceil_div(D / 8, 256);
-    if (vec && vpt <= 4) {
+    if (vec && vpt <= 4 && MI_EMBED_RMS_WAVE && T >= MI_EMBED_RMS_WAVE_MIN_T) {
+        constexpr int kR = 4;
+        const dim3 gw(static_cast<unsigned>(mi::ceil_div(T, kR))), bw(64 * kR);
+        switch (vpt) {
+            case 1: mi::embed_rms_wave_kernel<1, kR><<<gw, bw, 0, s>>>(ids, tb, h, w, yo, T, D, vocab, scale, eps, bias); break;
+            case 2: mi::embed_rms_wave_kernel<2, kR><<<gw, bw, 0, s>>>(ids, tb, h, w, yo, T, D, vocab, scale, eps, bias); break;
+            case 3: mi::embed_rms_wave_kernel<3, kR><<<gw, bw, 0, s>>>(ids, tb, h, w, yo, T, D, vocab, scale, eps, bias); break;
+            default: mi::embed_rms_wave_kernel<4, kR><<<gw, bw, 0, s>>>(ids, tb, h, w, yo, T, D, vocab, scale, eps, bias); break;
+        }
+    } else if (vec && vpt <= 4) {
         switch (vpt) {
             case 1: mi::embed_rms_kernel<1><<<g, b, 0, s>>>(ids, tb, h, w, yo, D, vocab, scale, eps, bias); break;
             case 2: mi::embed_rms_kernel<2><<<g, b, 0, s>>>(ids, tb, h, w, yo, D, vocab, scale, eps, bias); break;

@@ -89,17 +89,21 @@ def test_gather_shapes_and_bad_ids(mk, orc, dev, H):
     assert (out[0, 0] == 0).all() and (out[1, 5] == 0).all()
 
 
+@pytest.mark.parametrize("T", [613, 2051])
 @pytest.mark.parametrize("D,scale,add_one", [(3584, 1.0, False), (3584, 3584 ** 0.5, True),
                                              (8192, 1.0, False), (2048, 2048 ** 0.5, False),
                                              (1000, 1.0, False), (3585, 59.87, True)])
-def test_embedding_rmsnorm(mk, orc, dev, D, scale, add_one):
+def test_embedding_rmsnorm(mk, orc, dev, D, scale, add_one, T):
     """Gather fused with the input RMSNorm: hidden is the gathered row (scaled
     and rounded as mi_scale_inplace_f16 does), bit for bit, and y the oracle's
     RMSNorm of that fp16 hidden, rtol = atol = 1e-3.  Vector and scalar
-    paths, out-of-range ids (zero rows), Gemma's scale and (1 + w)."""
-    _case(f"embedding+rmsnorm D={D} scale={scale:.3f} add_one={add_one}")
-    rng = np.random.default_rng(D)
-    V, T = 700, 613
+    paths, out-of-range ids (zero rows), Gemma's scale and (1 + w); T = 613
+    runs a workgroup per row, T = 2051 a wave per row (four rows per
+    workgroup, the last one partial); y equals the unfused GPU sequence bit
+    for bit either way."""
+    _case(f"embedding+rmsnorm T={T} D={D} scale={scale:.3f} add_one={add_one}")
+    rng = np.random.default_rng(D + T)
+    V = 700
     table = normal_f16(rng, (V, D), 0, 0.02)
     w = normal_f16(rng, (D,), 0.0 if add_one else 1.0, 0.1)
     ids = rng.integers(0, V, T).astype(np.int64)
