@@ -51,17 +51,31 @@ namespace {
 constexpr int kRowsPerWg = MI_RMS_ROWS_PER_WG;
 constexpr int kRowsPerGroup = MI_RMS_ROWS_PER_GROUP;
 constexpr int kMaxThreads = MI_RMS_MAX_THREADS;
+#ifndef MI_RMS_PACK_ROWS_MAX
+#define MI_RMS_PACK_ROWS_MAX 32
+#endif
+constexpr int64_t kPackRowsMax = MI_RMS_PACK_ROWS_MAX;
 
 // ---------------------------------------------------------------------------
 // Long rows: RPW rows per workgroup, VPT 16-byte vectors per lane per row.
 // ---------------------------------------------------------------------------
+// xcds > 0 (a few rows, RPW = 1): workgroup i runs on XCD i mod 8 (the
+// dispatcher's round robin); only those on the first `xcds` XCDs work, taking
+// rows (i / 8) * xcds + i mod 8, so the weight every row re-reads is fetched
+// into `xcds` L2s instead of all eight.
 template <int VPT, int RPW, bool FUSED>
 __global__ __launch_bounds__(1024) void rms_row_kernel(const half_t* x, half_t* residual,
                                                        const half_t* __restrict__ w, half_t* y,
                                                        int64_t N, int64_t D, float eps,
-                                                       float w_bias) {
+                                                       float w_bias, int xcds) {
     __shared__ float slots[(1024 / kWave) * RPW];
-    const int64_t row0 = static_cast<int64_t>(blockIdx.x) * RPW;
+    int64_t row0 = static_cast<int64_t>(blockIdx.x) * RPW;
+    if (xcds > 0) {  // workgroup-uniform, before any barrier
+        const int xcd = static_cast<int>(blockIdx.x & 7);
+        if (xcd >= xcds) return;
+        row0 = static_cast<int64_t>(blockIdx.x >> 3) * xcds + xcd;
+        if (row0 >= N) return;
+    }
     const int64_t chunks = D >> 3;
     const int nthr = blockDim.x;
 
@@ -298,16 +312,16 @@ int row_vpt(int64_t chunks) {
 
 template <int RPW, bool FUSED>
 int launch_row_rpw(const half_t* x, half_t* r, const half_t* w, half_t* y, int64_t N, int64_t D,
-                   float eps, float bias, hipStream_t s) {
+                   float eps, float bias, hipStream_t s, int xcds = 0) {
     const int64_t chunks = D >> 3;
     const int vpt = row_vpt(chunks);
     const int threads = static_cast<int>(ceil_div(ceil_div(chunks, vpt), kWave) * kWave);
-    const int64_t grid = ceil_div(N, RPW);
+    const int64_t grid = xcds > 0 ? 8 * ceil_div(N, xcds) : ceil_div(N, RPW);
     if (grid > kMaxGridX) return MI_ERR_UNSUPPORTED;
     const dim3 g(static_cast<unsigned>(grid)), b(threads);
     switch (vpt) {
 #define MI_ROW_CASE(V) \
-    case V: rms_row_kernel<V, RPW, FUSED><<<g, b, 0, s>>>(x, r, w, y, N, D, eps, bias); break;
+    case V: rms_row_kernel<V, RPW, FUSED><<<g, b, 0, s>>>(x, r, w, y, N, D, eps, bias, xcds); break;
         MI_ROW_CASE(1)
         MI_ROW_CASE(2)
         MI_ROW_CASE(3)
@@ -330,6 +344,12 @@ int launch_row(const half_t* x, half_t* r, const half_t* w, half_t* y, int64_t N
     const int vpt = row_vpt(D >> 3);
     if (kRowsPerWg > 1 && vpt <= 2 && N >= 2048)
         return launch_row_rpw<kRowsPerWg, FUSED>(x, r, w, y, N, D, eps, bias, s);
+    // A few rows (a decode batch): on ceil(N / 8) XCDs, eight rows each, so
+    // the weight is fetched into that many L2s rather than all eight (the
+    // launch is latency-bound; the extra fetches are what a counter sees).
+    if (N <= kPackRowsMax)
+        return launch_row_rpw<1, FUSED>(x, r, w, y, N, D, eps, bias, s,
+                                        static_cast<int>(ceil_div(N, 8)));
     return launch_row_rpw<1, FUSED>(x, r, w, y, N, D, eps, bias, s);
 }
 

@@ -47,7 +47,7 @@ def test_config1_16x3584(mk, orc, dev):
 @pytest.mark.parametrize("N,D", [(5, 8), (33, 16), (17, 64), (100, 128), (9, 136), (31, 320),
                                  (8, 512), (8, 520), (3, 1000), (7, 4096), (4, 8192),
                                  (2, 16384), (2, 16392), (2, 40000), (2, 70000), (3, 3583),
-                                 (6, 7)])
+                                 (6, 7), (1, 3584), (17, 3584), (32, 3584), (33, 3584)])
 @pytest.mark.parametrize("add_one", [False, True])
 def test_shapes(mk, orc, dev, N, D, add_one):
     _case(f"rmsnorm [{N},{D}] add_one={add_one}")
@@ -96,7 +96,8 @@ def test_qk_norm_chain_shape(mk, orc, dev):
         assert_close(to_host(xd), orc.rmsnorm(x, w, 1e-6, nthreads=8), what=f"qk rows={rows}")
 
 
-@pytest.mark.parametrize("N,D", [(8192, 3584), (6064, 3584), (37, 128), (5, 3583), (3, 20000)])
+@pytest.mark.parametrize("N,D", [(8192, 3584), (6064, 3584), (37, 128), (5, 3583), (3, 20000),
+                                 (9, 3584), (31, 4096)])
 def test_fused_add_rmsnorm(mk, orc, dev, N, D):
     """The headline workload ([8192,3584]) and the chain's residual+norm ([6064,3584])."""
     _case(f"fused add+rmsnorm [{N},{D}]")
