@@ -92,6 +92,35 @@ __device__ __forceinline__ uint64_t lane_best_key(const h8 (&a)[U], int64_t t0) 
     return argmax_key(__builtin_bit_cast(uint16_t, M), i);
 }
 
+// A chunk of one tile (elements t0 .. t0 + 2048 U of a row, t0 a multiple of
+// 2048, end - t0 a multiple of 8 and >= 8): lane j's vectors t0 + (j + 256 u)
+// * 8, those at or past `end` reading the chunk's last in-range vector and
+// then set to -inf.  Every load is unconditional -- straight-line code, so
+// the compiler's later waits count exactly the loads issued before them.
+template <int U>
+__device__ __forceinline__ void chunk_load(const half_t* xr, int64_t t0, int64_t end, h8 (&a)[U]) {
+#pragma unroll
+    for (int j = 0; j < U; ++j) {
+        const int64_t i = t0 + (threadIdx.x + j * 256) * 8;
+        a[j] = ld8_stream(xr + (i < end ? i : end - 8));
+    }
+#pragma unroll
+    for (int j = 0; j < U; ++j)
+        if (t0 + (threadIdx.x + j * 256) * 8 >= end) a[j] = h8(-__builtin_huge_valf16());
+}
+
+// The workgroup's best key of a chunk loaded by chunk_load (one barrier).
+template <int U>
+__device__ __forceinline__ uint64_t chunk_best_of(const h8 (&a)[U], int64_t t0, uint64_t* slots) {
+    uint64_t best = wave_max_u64(lane_best_key<U>(a, t0));
+    const int wave = threadIdx.x / kWave;
+    if ((threadIdx.x & (kWave - 1)) == 0) slots[wave] = best;
+    __syncthreads();
+    uint64_t t = 0;
+    for (int w = 0; w < static_cast<int>(blockDim.x / kWave); ++w) t = max_u64(t, slots[w]);
+    return t;
+}
+
 // Best key of elements [begin, end) of a row, over the workgroup.  The range
 // is walked in tiles of 256 * VEC * U elements; every load of a tile is
 // issued before any arithmetic, so a workgroup whose chunk is one tile waits
