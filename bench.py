@@ -139,6 +139,8 @@ def floors_lib():
         lib.mi_floor_read.argtypes = [vp, i64, ci, vp, i64, vp]
         lib.mi_floor_empty.argtypes = [vp]
         lib.mi_floor_rope_inplace.argtypes = [vp, vp, i64, i64, i64, i64, ci, vp]
+        lib.mi_floor_gather2.argtypes = [vp, vp, vp, vp, i64, i64, vp]
+        lib.mi_floor_read_rows.argtypes = [vp, i64, i64, ci, vp, i64, vp]
         _FLOORS_LIB = lib
     return _FLOORS_LIB
 
@@ -328,6 +330,11 @@ def chain_positions(gen_np):
     return np.concatenate([dec] + pre).astype(np.int64)
 
 
+def _floor_ok(rc):
+    if rc != 0:
+        raise RuntimeError(f"floor kernel failed: {rc}")
+
+
 def attach_rope_floors(dev, row, T, Hq, Hkv, hd):
     """RoPE rows: the time of their own access pattern with no arithmetic."""
     row["rope_floor_us"] = round(rope_floor_time(dev, T, Hq, Hkv, hd, 32) * 1e6, 3)
@@ -409,6 +416,14 @@ def all_kernels(mk, dev, iters, warmup):
     sec = time_launches(lambda i: mk.embedding_rmsnorm(ids[i], table, w_in, hidden=outs[i],
                                                        y=nrm[i]), ns, iters, warmup)
     out.append(report("embedding_rmsnorm", "T=6064 from [152064,3584]", nb, sec, T))
+    # its access pattern with no arithmetic: the gathered rows read, written twice
+    fl = floors_lib()
+    out[-1]["pattern_floor_us"] = round(time_launches(
+        lambda i: _floor_ok(fl.mi_floor_gather2(ids[i].data_ptr(), table.data_ptr(),
+                                                outs[i].data_ptr(), nrm[i].data_ptr(), T, D,
+                                                torch.cuda.current_stream().cuda_stream)),
+        ns, iters, warmup) * 1e6, 3)
+    out[-1]["pattern_floor"] = "gather + two row writes, one wave per row (floors.hip)"
     del table, ids, outs, nrm
     # 5b. residual + RMSNorm
     nb = 4 * T * D * 2 + D * 2
@@ -482,6 +497,19 @@ def all_kernels(mk, dev, iters, warmup):
     sec = time_launches(lambda i: mk.greedy_argmax(xs[i], out=outi, workspace=wsa), ns, iters,
                         warmup)
     out.append(report("greedy_argmax", "[64,152064]", nb, sec, N))
+    # its access pattern with no arithmetic: one workgroup per 8192-element
+    # chunk, a row's chunks on one XCD (rows padded to whole chunks)
+    fl = floors_lib()
+    vp = -(-V // 8192) * 8192
+    fbuf = [torch.ones(N * vp, dtype=f16, device=dev) for _ in range(rotations(N * vp * 2))]
+    sink = torch.zeros(1 << 20, dtype=torch.int32, device=dev)
+    out[-1]["pattern_floor_us"] = round(time_launches(
+        lambda i: _floor_ok(fl.mi_floor_read_rows(fbuf[i].data_ptr(), N, vp, 1, sink.data_ptr(),
+                                                  sink.numel(),
+                                                  torch.cuda.current_stream().cuda_stream)),
+        len(fbuf), iters, warmup) * 1e6, 3)
+    out[-1]["pattern_floor"] = "8192-element chunk reads, a row's chunks on one XCD (floors.hip)"
+    del fbuf
     # 5g''. top-p sampling of 64 rows of 30000 logits (the largest vocabulary
     # that takes the nucleus path; larger ones are greedy): latency-bound
     xt = [randn16((N, 30000), gen, dev, 0.0, 4.0) for _ in range(4)]
@@ -1057,6 +1085,8 @@ def main():
                          + f" us -> {100 * k['frac_of_floor']:5.1f}% of {k['floor_kind']}")
             elif "empty_launch_us" in k:
                 floor = f"  empty launch {k['empty_launch_us']:.2f} us"
+            if "pattern_floor_us" in k:
+                floor += f"  pattern {k['pattern_floor_us']:.2f} us"
             if "rope_floor_us" in k:
                 floor += (f"  rope pattern {k['rope_floor_us']:.2f} us (one-token pattern "
                           f"{k['rope_floor_one_token_us']:.2f})")

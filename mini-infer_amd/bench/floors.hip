@@ -375,6 +375,48 @@ extern "C" int mi_floor_gather2(const int64_t* ids, const void* table, void* out
     return hipGetLastError() == hipSuccess ? 0 : 1;
 }
 
+// The one-launch argmax's read pattern with no arithmetic: rows of V fp16
+// (V a multiple of 8192), one 256-lane workgroup per 8192-element chunk (4
+// vectors per lane), the workgroups of a row either on one XCD (grouped: the
+// row_exchange.h order, chunk c of row 8g + q at index g * 8 * splits + 8c +
+// q) or row-major (chunk c of row r at r * splits + c).  Every word feeds a
+// store that the 0x01-filled buffers never trigger.
+__global__ __launch_bounds__(256) void read_rows_kernel(const u4* __restrict__ x, int64_t B,
+                                                        int splits, int64_t V, int grouped,
+                                                        uint32_t* sink) {
+    int split, row;
+    if (grouped) {
+        const int per = 8 * splits;
+        const int g = blockIdx.x / per, j = blockIdx.x - g * per;
+        split = j / 8;
+        row = g * 8 + (j - split * 8);
+    } else {
+        row = blockIdx.x / splits;
+        split = blockIdx.x - row * splits;
+    }
+    if (row >= B) return;
+    const u4* p = x + (row * V + static_cast<int64_t>(split) * 8192) / 8 + threadIdx.x;
+    u4 v[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[j] = __builtin_nontemporal_load(p + j * 256);
+    uint32_t acc = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc ^= v[j].x ^ v[j].y ^ v[j].z ^ v[j].w;
+    if (acc == 0x3c003c00u) sink[blockIdx.x] = acc;
+}
+
+extern "C" int mi_floor_read_rows(const void* x, int64_t B, int64_t V, int grouped,
+                                  uint32_t* sink, int64_t sink_words, void* stream) {
+    if (B <= 0 || V <= 0 || V % 8192 != 0 || !x || !sink) return -1;
+    const int64_t splits = V / 8192;
+    const int64_t rows = grouped ? (B + 7) / 8 * 8 : B;
+    if (splits * rows > sink_words) return -1;
+    read_rows_kernel<<<dim3(static_cast<unsigned>(splits * rows)), dim3(256), 0,
+                       reinterpret_cast<hipStream_t>(stream)>>>(
+        static_cast<const u4*>(x), B, static_cast<int>(splits), V, grouped, sink);
+    return hipGetLastError() == hipSuccess ? 0 : 1;
+}
+
 // An empty one-workgroup launch.
 extern "C" int mi_floor_empty(void* stream) {
     empty_kernel<<<dim3(1), dim3(64), 0, reinterpret_cast<hipStream_t>(stream)>>>();

@@ -104,9 +104,11 @@ __device__ __forceinline__ void chunk_load(const half_t* xr, int64_t t0, int64_t
         const int64_t i = t0 + (threadIdx.x + j * 256) * 8;
         a[j] = ld8_stream(xr + (i < end ? i : end - 8));
     }
+    if (t0 + 2048 * U > end) {  // workgroup-uniform: only a row's last chunk
 #pragma unroll
-    for (int j = 0; j < U; ++j)
-        if (t0 + (threadIdx.x + j * 256) * 8 >= end) a[j] = h8(-__builtin_huge_valf16());
+        for (int j = 0; j < U; ++j)
+            if (t0 + (threadIdx.x + j * 256) * 8 >= end) a[j] = h8(-__builtin_huge_valf16());
+    }
 }
 
 // The workgroup's best key of a chunk loaded by chunk_load (one barrier).

@@ -302,9 +302,6 @@ int64_t argmax_splits(int64_t B, int64_t V, int64_t& chunk) {
 // first use.
 // ---------------------------------------------------------------------------
 constexpr int kArgmaxOnePassMaxSplits = 64;
-#ifndef MI_ARGMAX_PROBE
-#define MI_ARGMAX_PROBE 0
-#endif
 #ifndef MI_ARGMAX_ONEPASS_U
 #define MI_ARGMAX_ONEPASS_U 4
 #endif
@@ -361,10 +358,6 @@ __global__ __launch_bounds__(256) void argmax_onepass_kernel(const half_t* __res
     const half_t* xr = x + row * V;
     const int64_t b = split * kArgmaxOnePassChunk;
     const int64_t e = b + kArgmaxOnePassChunk < V ? b + kArgmaxOnePassChunk : V;
-#if MI_ARGMAX_PROBE  // timing probe of a measurement build (never in the library)
-    uint64_t* probe = reinterpret_cast<uint64_t*>(ws + 256 * kArgmaxRecordBytes) + blockIdx.x * 4;
-    if (threadIdx.x == 0) probe[0] = __builtin_amdgcn_s_memrealtime();
-#endif
     // The row's epoch, read by every lane (one request per wave) ahead of the
     // chunk's loads and with no branch around it, so its first wait comes at
     // the publish: a lane-0 load followed by its store to LDS made wave 0
@@ -375,9 +368,6 @@ __global__ __launch_bounds__(256) void argmax_onepass_kernel(const half_t* __res
     h8 a[kArgmaxOnePassU];
     chunk_load<kArgmaxOnePassU>(xr, b, e, a);
     const uint64_t best = chunk_best_of<kArgmaxOnePassU>(a, b, slots);  // barrier inside
-#if MI_ARGMAX_PROBE
-    if (threadIdx.x == 0) probe[1] = __builtin_amdgcn_s_memrealtime();
-#endif
     const uint32_t tag = static_cast<uint32_t>(E + 1);
     if (threadIdx.x == 0) {
         const uint64_t w0 = (static_cast<uint64_t>(tag) << 32) | (best >> 32);
@@ -387,9 +377,6 @@ __global__ __launch_bounds__(256) void argmax_onepass_kernel(const half_t* __res
         device_store(&slot[kArgmaxMirror + 2 * split], w0);
         device_store(&slot[kArgmaxMirror + 2 * split + 1], w1);
     }
-#if MI_ARGMAX_PROBE
-    if (threadIdx.x == 0) probe[2] = __builtin_amdgcn_s_memrealtime();
-#endif
     if (split != 0) return;  // whole workgroup
     if (threadIdx.x < kWave) {
         const int lane = threadIdx.x;
@@ -407,9 +394,6 @@ __global__ __launch_bounds__(256) void argmax_onepass_kernel(const half_t* __res
             k = wave_max_u64(k);
             if (lane == 0) out[row] = key_index(k);
         }
-#if MI_ARGMAX_PROBE
-        if (lane == 0) probe[3] = __builtin_amdgcn_s_memrealtime();
-#endif
         if (lane == 0) fallback_sh = all ? 0 : 1;
     }
     __syncthreads();
