@@ -217,6 +217,37 @@ __device__ __forceinline__ float block_max(float v, float* slots) {
     return t;
 }
 
+// Sum of squares of a head's slice pair, x1 (first half) and x2 (second half)
+// of 8 halves each, as every fused Q/K-norm + RoPE kernel forms it (they must
+// agree bit for bit: the one-launch attention pre-processing is checked
+// against the separate launches).  MI_SUMSQ_FORM 2 (default): packed fp16
+// dot products accumulated in fp32 (v_dot2_f32_f16) over x1 then x2 -- 8
+// instructions instead of 16 conversions and 16 fma, Q/K-norm + RoPE at
+// T = 6064 18.0 -> 17.8 us; the products of fp16 values are exact and the
+// hardware accumulation's rounding differs from an fma chain's by an fp32
+// ulp or so, far inside the norm's tolerance.  0: one fma chain over
+// (x1[e], x2[e]) pairs.
+#ifndef MI_SUMSQ_FORM
+#define MI_SUMSQ_FORM 2
+#endif
+__device__ __forceinline__ float pair_sumsq(const h8& x1, const h8& x2) {
+    float ss = 0.0f;
+#if MI_SUMSQ_FORM == 2
+#pragma unroll
+    for (int e = 0; e < 8; e += 2) ss = __builtin_amdgcn_fdot2(h2{x1[e], x1[e + 1]}, h2{x1[e], x1[e + 1]}, ss, false);
+#pragma unroll
+    for (int e = 0; e < 8; e += 2) ss = __builtin_amdgcn_fdot2(h2{x2[e], x2[e + 1]}, h2{x2[e], x2[e + 1]}, ss, false);
+#else
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const float f1 = (float)x1[e], f2 = (float)x2[e];
+        ss = fmaf(f1, f1, ss);
+        ss = fmaf(f2, f2, ss);
+    }
+#endif
+    return ss;
+}
+
 // floor(u / d) for integers 0 <= u < 2^22 and d >= 1, given inv_d = 1.0f / d
 // (correctly rounded): (u + 0.5) * inv_d lies within (u + 0.5) * 2^-23 of
 // (u + 0.5) / d, which is less than the 0.5 / d separating that value from

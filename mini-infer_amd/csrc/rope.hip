@@ -333,13 +333,7 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(half_t* q, int Hq, ha
     // whole wave); lanes past `units` contribute zeros and store nothing.
     auto process = [&](int u, const h8& a1, const h8& a2) {
         const bool valid = u < units;
-        float ss = 0.0f;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const float f1 = (float)a1[e], f2 = (float)a2[e];
-            ss = fmaf(f1, f1, ss);
-            ss = fmaf(f2, f2, ss);
-        }
+        float ss = pair_sumsq(a1, a2);
         ss = group_sum<CPH>(ss);
         if (!valid) return;
         bool is_k;
@@ -477,13 +471,7 @@ __global__ __launch_bounds__(256) void qk_norm_rope_pipe_kernel(
         const int64_t tok0 = g * G;
 #pragma unroll
         for (int p = 0; p < P; ++p) {
-            float ss = 0.0f;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const float f1 = (float)a1[p][e], f2 = (float)a2[p][e];
-                ss = fmaf(f1, f1, ss);
-                ss = fmaf(f2, f2, ss);
-            }
+            float ss = pair_sumsq(a1[p], a2[p]);
             ss = group_sum<CPH>(ss);
             if (!slot_on[p] || tok0 + slot_t[p] >= T) continue;
             const float rrms = rsqrtf(ss / static_cast<float>(HD) + eps);
@@ -858,13 +846,7 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(half_t* q, half_t* k, cons
 
     float rrms = 1.0f;
     if constexpr (NORM) {  // every lane takes part in the DPP sum (idle lanes add zeros)
-        float ss = 0.0f;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const float f1 = (float)x1[e], f2 = (float)x2[e];
-            ss = fmaf(f1, f1, ss);
-            ss = fmaf(f2, f2, ss);
-        }
+        float ss = pair_sumsq(x1, x2);
         ss = group_sum<CPH ? CPH : 1>(ss);
         rrms = rsqrtf(ss / static_cast<float>(CPH * 16) + eps);
     }
@@ -1034,6 +1016,9 @@ __global__ __launch_bounds__(256) void rope_rows_kernel(
     // past T re-read the last token and are never stored), so the loads are
     // straight-line code and each later wait counts exactly the loads it needs.
     h8 x[TPW][R];
+    // NORM: the weights as the rotation uses them, w + w_bias in fp32, formed
+    // once (a lane's slice of the head is the same in every token)
+    float wf[NORM ? R : 1][8];
 #pragma unroll
     for (int t = 0; t < TPW; ++t) {
         const int64_t tok = tok0 + t < T ? tok0 + t : T - 1;
@@ -1062,6 +1047,13 @@ __global__ __launch_bounds__(256) void rope_rows_kernel(
         cs[t][1][li] = (float)hs;
     }
     __syncthreads();
+    if constexpr (NORM) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) wf[r][e] = (float)b1[r][e] + w_bias;
+        }
+    }
 
 #pragma unroll
     for (int t = 0; t < TPW; ++t) {
@@ -1079,20 +1071,13 @@ __global__ __launch_bounds__(256) void rope_rows_kernel(
             float rrms = 1.0f;
             if constexpr (NORM) {  // the sum over (x1[e], x2[e]) pairs, x1 first
                 const h8 x1 = first ? own : oth, x2 = first ? oth : own;
-                float ss = 0.0f;
-#pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    const float f1 = (float)x1[e], f2 = (float)x2[e];
-                    ss = fmaf(f1, f1, ss);
-                    ss = fmaf(f2, f2, ss);
-                }
+                float ss = pair_sumsq(x1, x2);
                 ss = group_sum<X>(ss);
                 rrms = rsqrtf(ss / static_cast<float>(X * 16) + eps);
                 // the normalised value as the reference stores it (fp16); the
                 // partner's comes over the same exchange
 #pragma unroll
-                for (int e = 0; e < 8; ++e)
-                    own[e] = to_half((float)own[e] * rrms * ((float)b1[r][e] + w_bias));
+                for (int e = 0; e < 8; ++e) own[e] = to_half((float)own[e] * rrms * wf[r][e]);
                 oth = partner_vec<X>(own);
             }
             // entries 0-3 of slice c at c*4, entries 4-7 at HALF/2 + c*4 (quad_split)
