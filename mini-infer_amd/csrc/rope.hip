@@ -759,11 +759,13 @@ struct KvSegs {
 // shapes); CPH = 0: head_dim known at run time (no norm).
 // SEG = false: RoPE (+ bias or norm) alone -- no cache segment, no V, no
 // cache stores (a distinct kernel in traces, with none of that code).
+// `inv` is the first parameter: it sits at offset 0 of the kernel-argument
+// block, which the SEG = false form reads directly (below).
 template <bool BIAS, bool NORM, int CPH, bool SEG = true>
-__global__ __launch_bounds__(256) void rope_kv_kernel(half_t* q, half_t* k, const half_t* v,
-                                                       int Hq, int Hkv, int hd,
+__global__ __launch_bounds__(256) void rope_kv_kernel(InvFreq inv, half_t* q, half_t* k,
+                                                       const half_t* v, int Hq, int Hkv, int hd,
                                                        const int64_t* __restrict__ positions,
-                                                       InvFreq inv, const half_t* __restrict__ bq,
+                                                       const half_t* __restrict__ bq,
                                                        const half_t* __restrict__ bk,
                                                        const half_t* __restrict__ bv,
                                                        const half_t* __restrict__ wq,
@@ -773,7 +775,7 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(half_t* q, half_t* k, cons
                                                        int64_t num_blocks, int64_t bs) {
     static_assert(!(BIAS && NORM), "no model adds a QKV bias before a Q/K norm");
     static_assert(!NORM || (CPH >= 1 && CPH <= 32), "the norm needs head_dim / 16 at compile time");
-    __shared__ float cs[2 * kMaxHalf];
+    __shared__ __attribute__((aligned(16))) float cs[2 * kMaxHalf];
     const int64_t tok = blockIdx.x;
     const int half = CPH ? CPH * 8 : hd >> 1;
     const int cph = CPH ? CPH : half >> 3;  // 16-byte slices per half head
@@ -783,7 +785,45 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(half_t* q, half_t* k, cons
     h8 x1 = h8(0), x2 = h8(0), b1 = h8(0), b2 = h8(0);
     half_t* hp = nullptr;
     int h = 0, c = 0;
-    if (tid < units) {
+    // SEG = false: this lane's inverse frequency read from the kernel-argument
+    // block ahead of the data, and the data loads straight-line (an idle lane
+    // reads head 0's first slice and stores nothing), so the sincos below
+    // waits for that one load only -- not, as when the compiler sinks the
+    // argument load behind the data (the counter is in order), for every
+    // data load first.  Q/K-norm + RoPE at T = 6064: 18.2 -> ... us.
+    float inv_l = 0.0f;
+    if constexpr (!SEG) {
+        const float* ip =
+            reinterpret_cast<const float*>(
+                reinterpret_cast<uintptr_t>(__builtin_amdgcn_kernarg_segment_ptr())) +
+            (tid & (kMaxHalf - 1));  // inv.v[tid] (tid < half <= kMaxHalf uses it)
+        asm volatile("global_load_dword %0, %1, off" : "=v"(inv_l) : "v"(ip) : "memory");
+        const bool act = tid < units;
+        const int u = act ? tid : 0;
+        if constexpr (CPH != 0) {
+            h = u / CPH;
+            c = u & (CPH - 1);
+        } else {
+            h = small_div(u, 1.0f / static_cast<float>(cph));  // units < 2^22: exact
+            c = u - h * cph;
+        }
+        hp = h < Hq ? q + (tok * Hq + h) * (2 * half) : k + (tok * Hkv + (h - Hq)) * (2 * half);
+        x1 = ld8_stream(hp + c * 8);
+        x2 = ld8_stream(hp + half + c * 8);
+        if constexpr (BIAS) {
+            const half_t* bp = h < Hq ? bq + h * (2 * half) : bk + (h - Hq) * (2 * half);
+            b1 = ld8(bp + c * 8);
+            b2 = ld8(bp + half + c * 8);
+        }
+        if constexpr (NORM) {
+            const half_t* wp = h < Hq ? wq : wk;
+            b1 = ld8(wp + c * 8);
+            b2 = ld8(wp + half + c * 8);
+        }
+        // the inverse frequency has landed once only the loads after it remain
+        asm volatile("s_waitcnt vmcnt(%0)" : : "n"((BIAS || NORM) ? 4 : 2) : "memory");
+        asm volatile("" : "+v"(inv_l));
+    } else if (tid < units) {
         if constexpr (CPH != 0) {
             h = tid / CPH;
             c = tid & (CPH - 1);
@@ -837,7 +877,7 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(half_t* q, half_t* k, cons
     }
     if (tid < half) {
         half_t hc, hs;
-        cos_sin_half(fpos * inv.v[tid], hc, hs);
+        cos_sin_half(fpos * (SEG ? inv.v[tid] : inv_l), hc, hs);
         const int li = quad_split(tid, half);
         cs[li] = (float)hc;
         cs[kMaxHalf + li] = (float)hs;
@@ -851,12 +891,17 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(half_t* q, half_t* k, cons
         rrms = rsqrtf(ss / static_cast<float>(CPH * 16) + eps);
     }
     if (tid < units) {
+        // quad_split layout: entries 0-3 of slice c at c*4, 4-7 at half/2 + c*4
+        typedef float f4 __attribute__((ext_vector_type(4)));
+        const f4 c_lo = *reinterpret_cast<const f4*>(&cs[c * 4]);
+        const f4 c_hi = *reinterpret_cast<const f4*>(&cs[(half >> 1) + c * 4]);
+        const f4 s_lo = *reinterpret_cast<const f4*>(&cs[kMaxHalf + c * 4]);
+        const f4 s_hi = *reinterpret_cast<const f4*>(&cs[kMaxHalf + (half >> 1) + c * 4]);
         h8 y1, y2;
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-            // quad_split layout: entry e of slice c at c*4 + (e & 3), + half/2 for e >= 4
-            const int le = ((e & 4) ? (half >> 1) : 0) + c * 4 + (e & 3);
-            const float cv = cs[le], sv = cs[kMaxHalf + le];
+            const float cv = e < 4 ? c_lo[e & 3] : c_hi[e & 3];
+            const float sv = e < 4 ? s_lo[e & 3] : s_hi[e & 3];
             float a = (float)x1[e], bb = (float)x2[e];
             if constexpr (BIAS) {
                 a = (float)to_half(a + (float)b1[e]);
@@ -1240,7 +1285,7 @@ int rope_qk_one_token(half_t* q, half_t* k, const half_t* bq, const half_t* bk,
     const dim3 g(static_cast<unsigned>(T)), b(256);
     const int hq = static_cast<int>(Hq), hk = static_cast<int>(Hkv), d = static_cast<int>(head_dim);
 #define MI_RQ_ARGS                                                                          \
-    q, k, k, hq, hk, d, positions, inv, bq, bk, nullptr, wq, wk, eps, w_bias, nullptr, nullptr, \
+    inv, q, k, k, hq, hk, d, positions, bq, bk, nullptr, wq, wk, eps, w_bias, nullptr, nullptr, \
         sg, 0, 0, 1
 #define MI_RQ_CPH(BIAS)                                                                     \
     switch (head_dim / 16) {                                                                \
@@ -1477,7 +1522,7 @@ int rope_kv_launch(void* q, void* k, const void* v, const void* q_bias, const vo
     const int hq = static_cast<int>(Hq), hk = static_cast<int>(Hkv), d = static_cast<int>(head_dim);
     const float wb = add_one ? 1.0f : -0.0f;  // w + (-0) == w, also for w = -0
 #define MI_RKV_ARGS                                                                           \
-    qh, kh, vh, hq, hk, d, positions, inv, bqh, bkh, bvh, wqh, wkh, eps, wb, kc, vc, sg, layer, \
+    inv, qh, kh, vh, hq, hk, d, positions, bqh, bkh, bvh, wqh, wkh, eps, wb, kc, vc, sg, layer, \
         num_blocks, block_size
 #define MI_RKV_CPH(BIAS, NORM)                                                            \
     switch (head_dim / 16) {                                                              \
