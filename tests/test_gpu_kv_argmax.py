@@ -133,6 +133,36 @@ def test_greedy_argmax_specials(mk, orc, dev):
     assert got[0] == -1 and got[1] == 5 and got[3] == 17
 
 
+def test_greedy_argmax_onepass_specials(mk, orc, dev):
+    """The one-launch shape [64, 152064] with values that steer the wave-level
+    search: signalling and quiet NaNs (a lane of only NaNs, an sNaN beside the
+    row's maximum), rows of -inf, -0/+0 maxima in many lanes, the maximum tied
+    in several lanes of one wave and across waves, and +inf."""
+    _case("argmax one-launch specials [64,152064]")
+    rng = np.random.default_rng(31)
+    V = 152064
+    x = normal_f16(rng, (64, V), 0, 1)
+    bits = x.view(np.uint16)
+    bits[0, :] = 0xfc00                          # all -inf -> -1
+    bits[1, ::3] = 0x7d00                        # signalling NaNs everywhere
+    bits[2, 8000:8032] = 0x7e00                  # one lane's 32 elements all quiet NaN
+    bits[3, 100] = 0x7d01; x[3, 101] = 20.0      # sNaN next to the maximum
+    x[4, :] = -1.0; bits[4, ::5] = 0x8000; bits[4, 7::11] = 0x0000   # -0 / +0 maxima
+    x[5, :] = 0.0; bits[5, :] = 0x8000           # only -0
+    x[6, :] = -3.0; x[6, [5, 6, 13, 77, 200, 2048 + 9, 8000, 150000]] = 7.0  # ties in a wave
+    x[7, :] = -3.0; x[7, 1::257] = 7.0           # ties over every wave and chunk
+    x[8, 123456] = np.inf
+    x[9, :] = np.inf                             # every element ties
+    bits[10, :] = 0x7e00; x[10, 99999] = -65504.0  # one finite value among NaNs
+    x[11] = rng.integers(-1, 2, V).astype(np.float16)   # heavy ties
+    bits[12, :] = 0x7e00                         # only NaN -> -1
+    got = to_host(mk.greedy_argmax(to_dev(x, dev)))
+    ref = orc.greedy_argmax(x)
+    assert (got == ref).all(), f"rows {np.nonzero(got != ref)[0].tolist()} differ"
+    assert got[0] == -1 and got[12] == -1 and got[3] == 101 and got[8] == 123456
+    assert got[10] == 99999
+
+
 def test_greedy_argmax_workspace_graph(mk, orc, dev):
     _case("argmax with workspace in a graph")
     import torch
