@@ -156,6 +156,9 @@ def test_greedy_argmax_onepass_specials(mk, orc, dev):
     bits[10, :] = 0x7e00; x[10, 99999] = -65504.0  # one finite value among NaNs
     x[11] = rng.integers(-1, 2, V).astype(np.float16)   # heavy ties
     bits[12, :] = 0x7e00                         # only NaN -> -1
+    bits[13, :] = rng.integers(0x8001, 0x8400, V)  # negative subnormals ...
+    bits[13, 4000:4100] = rng.integers(1, 0x400, 100)  # ... and positive ones, max subnormal
+    bits[14, :] = rng.integers(1, 0x400, V); x[14, 777] = 6e-5   # smallest normal beside subnormals
     got = to_host(mk.greedy_argmax(to_dev(x, dev)))
     ref = orc.greedy_argmax(x)
     assert (got == ref).all(), f"rows {np.nonzero(got != ref)[0].tolist()} differ"
