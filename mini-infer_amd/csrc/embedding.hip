@@ -208,12 +208,16 @@ __global__ __launch_bounds__(64 * RPW) void embed_rms_wave_kernel(const int64_t*
     const int lane = tid & (kWave - 1);
     const int64_t nv = D >> 3;
     // the weight's vectors (vector c at wl[c]), loaded before the table rows
+    // Every load below is unconditional (indices clamped into range, values
+    // masked afterwards): a load under a branch made the compiler wait for it
+    // inside the branch, which serialised the row's loads.
     h8 wv[PER];
 #pragma unroll
     for (int j = 0; j < PER; ++j) {
         const int64_t c = tid + j * 64 * RPW;
-        wv[j] = c < nv && c < NW ? ld8(w + c * 8) : h8(0);
+        wv[j] = ld8(w + (c < nv ? c : nv - 1) * 8);
     }
+    __builtin_amdgcn_sched_barrier(0);  // keep them ahead of the table rows' loads
     const int64_t t_raw = static_cast<int64_t>(blockIdx.x) * RPW + (tid >> 6);
     const bool row_ok = t_raw < T;
     const int64_t t = __builtin_amdgcn_readfirstlane(static_cast<int>(row_ok ? t_raw : T - 1));
@@ -228,14 +232,22 @@ __global__ __launch_bounds__(64 * RPW) void embed_rms_wave_kernel(const int64_t*
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
             const int64_t c = lane + 64 * u + j * 256;
-            v[j * 4 + u] = (valid && c < nv) ? ld8(src + c * 8) : h8(0);
+            v[j * 4 + u] = ld8(src + (c < nv ? c : nv - 1) * 8);
         }
     }
 #pragma unroll
     for (int j = 0; j < PER; ++j)
-        if (tid + j * 64 * RPW < NW) wl[tid + j * 64 * RPW] = wv[j];
+        if (NW % (64 * RPW) == 0 || tid + j * 64 * RPW < NW) wl[tid + j * 64 * RPW] = wv[j];
     __syncthreads();
     __builtin_amdgcn_s_waitcnt(kDrainVmem);
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int64_t c = lane + 64 * u + j * 256;
+            if (!(valid && c < nv)) v[j * 4 + u] = h8(0);
+        }
+    }
     if (scale != 1.0f) {
 #pragma unroll
         for (int i = 0; i < NV; ++i) {
