@@ -381,14 +381,14 @@ __global__ __launch_bounds__(256) void argmax_onepass_kernel(const half_t* __res
     if (threadIdx.x < kWave) {
         const int lane = threadIdx.x;
         uint64_t k = 0;
-        // also bounded by 20000 ticks (200 us) of the 100 MHz constant clock;
+        // also bounded by kPollTicks (50 us) of the 100 MHz constant clock;
         // the L2 copy for the first kLocalPollTicks, then the mirror
         const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
         int it = 0;
         bool all = local != 0 && argmax_poll<true>(slot, splits, tag, it, poll_limit, t0,
                                                    kLocalPollTicks, k);
         if (!all)
-            all = argmax_poll<false>(slot + kArgmaxMirror, splits, tag, it, poll_limit, t0, 20000,
+            all = argmax_poll<false>(slot + kArgmaxMirror, splits, tag, it, poll_limit, t0, kPollTicks,
                                      k);
         if (all) {
             k = wave_max_u64(k);

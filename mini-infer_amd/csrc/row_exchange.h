@@ -46,6 +46,13 @@ constexpr int64_t kRecordHeaderBytes = 128;
 // constant clock (20 us), several times a normal exchange.
 constexpr uint64_t kLocalPollTicks = 2000;
 
+// Wall-clock bound of a row's whole poll, both phases: 5000 ticks (50 us),
+// some 10 times a normal exchange.  A poll that runs out costs only time
+// (its row is computed from x), so the bound is what a call pays when a
+// row-mate cannot run -- the grid not resident because other work holds
+// CUs.
+constexpr uint64_t kPollTicks = 5000;
+
 // Chunk `split` and row slot `slot` of workgroup L in a 1-D grid of
 // splits * R workgroups (R a multiple of kXcds): rows in groups of kXcds,
 // chunk c of slot g * kXcds + q at index g * kXcds * splits + c * kXcds + q.

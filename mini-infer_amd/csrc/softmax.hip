@@ -443,9 +443,6 @@ constexpr int64_t kRowRecordBytesAM = kRecordHeaderBytes + 4 * kOnePassMaxSplits
 template <bool AM>
 constexpr int64_t record_bytes() { return AM ? kRowRecordBytesAM : kRowRecordBytes; }
 constexpr int kPollLimit = 1 << 16;
-// Wall-clock bound of one row's polling: 20000 ticks of the 100 MHz
-// constant clock (s_memrealtime) = 200 us, some 100 times a normal exchange.
-constexpr uint64_t kPollTicks = 20000;
 std::atomic<int> g_poll_limit{kPollLimit};  // mi_softmax_test_poll_limit
 
 __device__ __forceinline__ uint64_t tagged(uint32_t tag, float v) {

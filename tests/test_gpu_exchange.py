@@ -74,8 +74,8 @@ def test_default_mode_is_served_by_l2(mk, dev):
     with events.  Printed for the log (normally ~7-11 us, well under the 20 us
     the L2 phase may last before polls move to the mirror); asserted only
     against a bound loose enough that a loaded box or lowered clocks cannot
-    trip it: 100 us per call, which a call reaches only when its polls run to
-    the 200 us fallback bound."""
+    trip it: 40 us per call, which a call reaches only when its polls run to
+    the 50 us fallback bound."""
     import torch
     _case("exchange: L2 phase serves the default mode")
     N, D = 64, 152064
@@ -115,7 +115,7 @@ def test_default_mode_is_served_by_l2(mk, dev):
         del graph
         us = t0.elapsed_time(t1) * 1e3 / n
         print(f"[case]   {name}: {us:.1f} us per call", flush=True)
-        assert us < 100.0, f"{name}: {us:.1f} us per call (polls ran to their bound?)"
+        assert us < 40.0, f"{name}: {us:.1f} us per call (polls ran to their bound?)"
 
 
 def test_one_launch_kernels_on_concurrent_streams(mk, orc, dev):
@@ -164,6 +164,6 @@ def test_one_launch_kernels_on_concurrent_streams(mk, orc, dev):
             yh = to_host(y)
             assert_bits_equal(to_host(p), yh, what=f"fused probs vs softmax {shapes[i]}")
             assert_close(yh, orc.softmax(x, nthreads=8), what=f"softmax {shapes[i]}")
-    # 18 one-launch calls: even every poll of every call running to its 200 us
+    # 18 one-launch calls: even every poll of every call running to its 50 us
     # bound would stay far below this
     assert wall < 10.0, f"{wall:.1f} s"
